@@ -1,0 +1,118 @@
+/*
+ * convnd_hip.h — C ABI of the MI355X (gfx950) N-d dense convolution library.
+ *
+ * Plain pointers, sizes and a stream handle: no torch types cross this boundary.
+ * Every tensor argument is a dense, row-major (C-contiguous) device buffer:
+ *   input        [batch, channels, input[0], ..., input[rank-1]]
+ *   weight       [output_channels, channels / groups, kernel[0], ..., kernel[rank-1]]
+ *   bias         [output_channels]                      (nullable)
+ *   output       [batch, output_channels, out[0], ..., out[rank-1]]
+ * with out[a] = (input[a] + 2*padding[a] - dilation[a]*(kernel[a]-1) - 1) / stride[a] + 1.
+ * All tensors share one element type (convnd_hip_dtype). Work is enqueued on `stream`
+ * (a hipStream_t; NULL is the default stream) and nothing synchronises the host.
+ * Results are deterministic: no floating-point atomics are used anywhere.
+ *
+ * Each entry point names the reference interface it replaces (lyehe/torch-convnd,
+ * paths relative to the reference repository).
+ */
+#ifndef CONVND_HIP_H
+#define CONVND_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* PyTorch tensors have at most 64 dimensions: batch, channels and 62 spatial axes
+ * (src/torch_convnd/csrc/convnd.h:10-11). */
+#define CONVND_HIP_MAX_RANK 62
+
+typedef enum convnd_hip_dtype {
+  CONVND_HIP_FLOAT32 = 0,
+  CONVND_HIP_FLOAT64 = 1,
+  CONVND_HIP_FLOAT16 = 2,
+  CONVND_HIP_BFLOAT16 = 3
+} convnd_hip_dtype;
+
+typedef enum convnd_hip_status {
+  CONVND_HIP_SUCCESS = 0,
+  CONVND_HIP_INVALID_ARGUMENT = 1, /* geometry/shape/dtype rejected; see convnd_hip_last_error */
+  CONVND_HIP_WORKSPACE_TOO_SMALL = 2,
+  CONVND_HIP_LAUNCH_FAILED = 3,    /* a HIP call failed; message holds hipGetErrorString */
+  CONVND_HIP_UNSUPPORTED = 4
+} convnd_hip_status;
+
+/* Convolution problem description. Replaces the `Geometry` struct and the tensor
+ * metadata that `make_geometry` reads (src/torch_convnd/csrc/convnd.h:13-27,
+ * src/torch_convnd/csrc/convnd.cpp:33-87). Only the first `rank` entries of each array
+ * are read. */
+typedef struct convnd_hip_problem {
+  int64_t rank;            /* spatial rank, 1..62 */
+  int64_t batch;           /* N >= 0 */
+  int64_t channels;        /* input channels C */
+  int64_t output_channels; /* Co */
+  int64_t groups;          /* G; C and Co divisible by G */
+  int64_t input[CONVND_HIP_MAX_RANK];
+  int64_t kernel[CONVND_HIP_MAX_RANK];
+  int64_t stride[CONVND_HIP_MAX_RANK];
+  int64_t padding[CONVND_HIP_MAX_RANK]; /* symmetric zero padding */
+  int64_t dilation[CONVND_HIP_MAX_RANK];
+} convnd_hip_problem;
+
+/* Human-readable message of the last failure on the calling thread ("" if none).
+ * Messages reuse the reference's wording, e.g. "groups must be positive",
+ * "kernel exceeds padded input", "workspace_bytes is too small for one output position". */
+const char* convnd_hip_last_error(void);
+
+/* Validates the geometry and the workspace_bytes contract and writes the output
+ * spatial sizes (`rank` entries) to `output_sizes` (nullable).
+ * Replaces make_geometry + tile_size (src/torch_convnd/csrc/convnd.cpp:33-100):
+ * workspace_bytes must be >= max(element_size, 4) * channels * prod(kernel), as in the
+ * reference, although the implicit GEMM below needs no patch buffer.
+ * Touches no device; safe to call on a machine without a GPU. */
+int convnd_hip_validate(const convnd_hip_problem* problem, int64_t element_size,
+                        int64_t workspace_bytes, int64_t* output_sizes);
+
+/* Device scratch bytes convnd_hip_forward needs for this problem (0 is possible). */
+size_t convnd_hip_forward_workspace_size(const convnd_hip_problem* problem,
+                                         convnd_hip_dtype dtype);
+
+/* output = conv(input, weight) + bias. Replaces the CUDA forward driver `conv_nd`
+ * (src/torch_convnd/csrc/convnd.cpp:305-343) together with its unfold kernels
+ * (src/torch_convnd/csrc/convnd_cuda.cu:91-145,173-191) and GEMM call (convnd.cpp:334):
+ * an implicit GEMM on MFMA for bf16/fp16/fp32 when the channel layout allows, a direct
+ * kernel otherwise. `workspace` must hold convnd_hip_forward_workspace_size bytes. */
+int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                       const void* input, const void* weight, const void* bias, void* output,
+                       void* workspace, size_t workspace_size, void* stream);
+
+/* Device scratch bytes convnd_hip_backward needs for the requested gradients. */
+size_t convnd_hip_backward_workspace_size(const convnd_hip_problem* problem,
+                                          convnd_hip_dtype dtype, int need_grad_input,
+                                          int need_grad_weight, int need_grad_bias);
+
+/* Gradients of conv(input, weight) + bias for a cotangent grad_output. A NULL
+ * grad_input / grad_weight / grad_bias skips that gradient (the reference's
+ * output_mask). Every requested gradient buffer is fully overwritten (no accumulation).
+ * Low-precision gradients accumulate in fp32 and are rounded once to the element type.
+ * Replaces `conv_nd_backward` and `mixed_backward_cuda`
+ * (src/torch_convnd/csrc/convnd.cpp:345-415, src/torch_convnd/csrc/convnd_mixed.cpp:11-60)
+ * with their fold kernels (src/torch_convnd/csrc/convnd_cuda.cu:147-169,193-213). */
+int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                        const void* grad_output, const void* input, const void* weight,
+                        void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
+                        size_t workspace_size, void* stream);
+
+/* Which kernel family convnd_hip_forward / convnd_hip_backward would use, as a short
+ * string ("mfma", "direct", ...) for diagnostics and tests. `which`: 0 forward,
+ * 1 input gradient, 2 weight gradient. No reference counterpart (diagnostic only). */
+const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                                 int which);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* CONVND_HIP_H */

@@ -1,0 +1,790 @@
+// C ABI entry points: validation, planning and launch sequences of the gfx950 kernels.
+//
+// Validation mirrors the reference's make_geometry and tile_size
+// (src/torch_convnd/csrc/convnd.cpp:19-100), including its error wording, so callers see
+// the same failures. Planning chooses, per problem, between the MFMA implicit GEMM and the
+// direct kernels, and picks the output box, channel chunk and tile counts that fit LDS.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+
+#include "convnd_internal.h"
+
+namespace convnd {
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int status, const std::string& message) {
+  g_error = message;
+  return status;
+}
+
+constexpr int64_t kI64Max = std::numeric_limits<int64_t>::max();
+constexpr int64_t kI32Safe = (int64_t{1} << 31) - 1;
+// LDS per workgroup on gfx950 is 160 KiB; keep a margin for the compiler's own use.
+constexpr int64_t kLdsBudget = 160 * 1024 - 1024;
+
+bool mul_ok(int64_t a, int64_t b, int64_t* out) {
+  if (a < 0 || b < 0 || (b != 0 && a > kI64Max / b)) return false;
+  *out = a * b;
+  return true;
+}
+bool add_ok(int64_t a, int64_t b, int64_t* out) {
+  if (a < 0 || b < 0 || a > kI64Max - b) return false;
+  *out = a + b;
+  return true;
+}
+
+struct Geom {
+  int rank = 0;
+  int64_t batch = 0, channels = 0, out_channels = 0, groups = 1, cin_g = 0, cout_g = 0;
+  int64_t in_vol = 1, out_vol = 1, k_vol = 1;
+  int64_t in[kMaxRank] = {}, out[kMaxRank] = {}, k[kMaxRank] = {}, s[kMaxRank] = {},
+          p[kMaxRank] = {}, d[kMaxRank] = {};
+};
+
+// make_geometry (src/torch_convnd/csrc/convnd.cpp:33-87) over plain integers.
+int build_geometry(const convnd_hip_problem* pr, Geom* g) {
+  if (pr == nullptr) return fail(CONVND_HIP_INVALID_ARGUMENT, "problem must not be null");
+  if (pr->rank < 1 || pr->rank > kMaxRank)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "conv_nd requires 1 to 62 spatial dimensions");
+  if (pr->groups <= 0) return fail(CONVND_HIP_INVALID_ARGUMENT, "groups must be positive");
+  if (pr->batch < 0) return fail(CONVND_HIP_INVALID_ARGUMENT, "batch must be nonnegative");
+  if (pr->channels <= 0 || pr->output_channels <= 0 || pr->channels % pr->groups != 0 ||
+      pr->output_channels % pr->groups != 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT,
+                "input/weight channels must match and be divisible by groups");
+  g->rank = static_cast<int>(pr->rank);
+  g->batch = pr->batch;
+  g->channels = pr->channels;
+  g->out_channels = pr->output_channels;
+  g->groups = pr->groups;
+  g->cin_g = pr->channels / pr->groups;
+  g->cout_g = pr->output_channels / pr->groups;
+  for (int a = 0; a < g->rank; ++a) {
+    if (pr->input[a] <= 0 || pr->kernel[a] <= 0)
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "spatial and kernel dimensions must be positive");
+    if (pr->stride[a] <= 0 || pr->dilation[a] <= 0 || pr->padding[a] < 0)
+      return fail(CONVND_HIP_INVALID_ARGUMENT,
+                  "stride and dilation must be positive; padding must be nonnegative");
+    int64_t dk, eff, twop, padded;
+    if (!mul_ok(pr->dilation[a], pr->kernel[a] - 1, &dk) || !add_ok(dk, 1, &eff))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "dilated kernel overflows int64");
+    if (!mul_ok(2, pr->padding[a], &twop))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "padding overflows int64");
+    if (!add_ok(pr->input[a], twop, &padded))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "padded input overflows int64");
+    if (padded < eff) return fail(CONVND_HIP_INVALID_ARGUMENT, "kernel exceeds padded input");
+    g->in[a] = pr->input[a];
+    g->k[a] = pr->kernel[a];
+    g->s[a] = pr->stride[a];
+    g->p[a] = pr->padding[a];
+    g->d[a] = pr->dilation[a];
+    g->out[a] = (padded - eff) / pr->stride[a] + 1;
+    if (!mul_ok(g->in_vol, g->in[a], &g->in_vol))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "input spatial volume overflows int64");
+    if (!mul_ok(g->out_vol, g->out[a], &g->out_vol))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "output spatial volume overflows int64");
+    if (!mul_ok(g->k_vol, g->k[a], &g->k_vol))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "kernel volume overflows int64");
+  }
+  return CONVND_HIP_SUCCESS;
+}
+
+// Axes with one sample, one tap and no padding contribute coordinate 0 only; dropping
+// them changes no volume or layout (the reference does the same,
+// src/torch_convnd/csrc/convnd.h:29-48). One axis is always kept.
+Geom drop_unit_axes(const Geom& g) {
+  Geom r = g;
+  r.rank = 0;
+  for (int a = 0; a < g.rank; ++a) {
+    const bool unit = g.in[a] == 1 && g.k[a] == 1 && g.p[a] == 0;
+    if (unit && (r.rank > 0 || a + 1 < g.rank)) continue;
+    r.in[r.rank] = g.in[a];
+    r.out[r.rank] = g.out[a];
+    r.k[r.rank] = g.k[a];
+    r.s[r.rank] = g.s[a];
+    r.p[r.rank] = g.p[a];
+    r.d[r.rank] = g.d[a];
+    ++r.rank;
+  }
+  return r;
+}
+
+DirectGeom to_direct(const Geom& g) {
+  DirectGeom dg;
+  std::memset(&dg, 0, sizeof(dg));
+  dg.rank = g.rank;
+  dg.batch = g.batch;
+  dg.channels = g.channels;
+  dg.out_channels = g.out_channels;
+  dg.groups = g.groups;
+  dg.cin_g = g.cin_g;
+  dg.cout_g = g.cout_g;
+  dg.in_vol = g.in_vol;
+  dg.out_vol = g.out_vol;
+  dg.k_vol = g.k_vol;
+  for (int a = 0; a < g.rank; ++a) {
+    dg.in[a] = g.in[a];
+    dg.out[a] = g.out[a];
+    dg.k[a] = g.k[a];
+    dg.s[a] = g.s[a];
+    dg.p[a] = g.p[a];
+    dg.d[a] = g.d[a];
+  }
+  return dg;
+}
+
+int64_t element_size(convnd_hip_dtype dt) {
+  switch (dt) {
+    case CONVND_HIP_FLOAT32:
+      return 4;
+    case CONVND_HIP_FLOAT64:
+      return 8;
+    case CONVND_HIP_FLOAT16:
+    case CONVND_HIP_BFLOAT16:
+      return 2;
+  }
+  return 0;
+}
+
+bool is_half(convnd_hip_dtype dt) {
+  return dt == CONVND_HIP_FLOAT16 || dt == CONVND_HIP_BFLOAT16;
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~size_t{255}; }
+
+// Bytes per halo position in LDS: channels*2 rounded to an odd number of 16-byte chunks,
+// so the sixteen-lane 16-byte reads of consecutive positions hit distinct bank groups.
+int halo_pstride(int channels) {
+  int chunks = (channels * 2 + 15) / 16;
+  if (chunks % 2 == 0) ++chunks;
+  return chunks * 16;
+}
+
+// Everything in the fast kernels is int32: check the element counts they index.
+bool fits_int32(const Geom& g) {
+  int64_t v;
+  if (!mul_ok(g.batch, g.channels, &v) || !mul_ok(v, g.in_vol, &v) || v > kI32Safe / 2)
+    return false;
+  if (!mul_ok(g.batch, g.out_channels, &v) || !mul_ok(v, g.out_vol, &v) || v > kI32Safe / 2)
+    return false;
+  if (!mul_ok(g.out_channels, g.cin_g, &v) || !mul_ok(v, g.k_vol, &v) || v > kI32Safe / 4)
+    return false;
+  for (int a = 0; a < g.rank; ++a) {
+    if (g.k[a] > 64 || g.s[a] > 16 || g.d[a] > 64 || g.p[a] > 4096 || g.in[a] > 65536 ||
+        g.out[a] > 65536)
+      return false;
+  }
+  return true;
+}
+
+// ---- implicit GEMM plan (forward and input gradient) -----------------------------------
+
+struct AxisPhaseHost {
+  int ntap = 0, emin = 0, emax = 0, J = 0;
+};
+
+int gcd_int(int a, int b) {
+  while (b != 0) {
+    const int t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// Host twin of the device axis_taps for the input-gradient phases.
+AxisPhaseHost grad_axis(const Geom& g, int a, int r) {
+  AxisPhaseHost t;
+  const int s = static_cast<int>(g.s[a]), d = static_cast<int>(g.d[a]),
+            k = static_cast<int>(g.k[a]), p = static_cast<int>(g.p[a]);
+  const int st = s / gcd_int(s, d);
+  int first = -1;
+  for (int c = 0; c < k && c < st; ++c) {
+    int m = (r + p - c * d) % s;
+    if (m < 0) m += s;
+    if (m == 0) {
+      first = c;
+      break;
+    }
+  }
+  t.ntap = first < 0 ? 0 : (k - 1 - first) / st + 1;
+  if (t.ntap > 0) {
+    t.emax = (r + p - first * d) / s;
+    t.emin = (r + p - (first + (t.ntap - 1) * st) * d) / s;
+  }
+  t.J = static_cast<int>((g.in[a] - r + s - 1) / s);
+  return t;
+}
+
+struct IgemmPlan {
+  bool ok = false;
+  int mb = 1, nb = 4;
+  IgemmArgs args{};
+  size_t lds = 0;
+  size_t wpk_elems = 0;
+  size_t staged_elems = 0;  // channels-last copy of the GEMM's input operand
+};
+
+// mode 0: forward over x; mode 1: input gradient over grad_output.
+IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
+  IgemmPlan plan;
+  if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g)) return plan;
+  const int R = g.rank;
+  const int gemm_cin = static_cast<int>(mode == 0 ? g.cin_g : g.cout_g);
+  const int gemm_cout = static_cast<int>(mode == 0 ? g.cout_g : g.cin_g);
+  if (gemm_cin % 8 != 0) return plan;
+  int nphase = 1;
+  if (mode == 1) {
+    for (int a = 0; a < R; ++a) nphase *= static_cast<int>(g.s[a]);
+    if (nphase > 256) return plan;
+  }
+  // Per axis: j extent, input step sigma, and the widest tap span over the phases.
+  int J[kFastRank], sigma[kFastRank], span[kFastRank];
+  int64_t ntaps_max = 1;
+  for (int a = 0; a < R; ++a) {
+    if (mode == 0) {
+      J[a] = static_cast<int>(g.out[a]);
+      sigma[a] = static_cast<int>(g.s[a]);
+      span[a] = static_cast<int>((g.k[a] - 1) * g.d[a]);
+      ntaps_max *= g.k[a];
+    } else {
+      J[a] = 0;
+      sigma[a] = 1;
+      span[a] = 0;
+      int nt = 0;
+      for (int r = 0; r < g.s[a]; ++r) {
+        const AxisPhaseHost t = grad_axis(g, a, r);
+        J[a] = std::max(J[a], t.J);
+        span[a] = std::max(span[a], t.emax - t.emin);
+        nt = std::max(nt, t.ntap);
+      }
+      ntaps_max *= nt;
+    }
+  }
+  const int mtiles = (gemm_cout + 15) / 16;
+  const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
+  const int mgroups = (mtiles + mb - 1) / mb;
+  const int64_t es = 2;
+
+  // Channel chunk: the largest multiple of 8 dividing gemm_cin, at most 64.
+  std::vector<int> chunk_options;
+  for (int cc = std::min(gemm_cin, 64); cc >= 8; cc -= 8)
+    if (gemm_cin % cc == 0) chunk_options.push_back(cc);
+
+  double best = -1.0;
+  for (int cc : chunk_options) {
+    const int pstride = halo_pstride(cc);
+    const int64_t kc = (ntaps_max * cc + 31) / 32;
+    const int64_t table_bytes = kc * 4 * 4;
+    for (int nb : {4, 2, 1}) {
+      const int box_vol = 64 * nb;
+      // Enumerate power-of-two boxes with product box_vol.
+      int b[kFastRank];
+      int limit[kFastRank];
+      for (int a = 0; a < R; ++a) {
+        int l = 1;
+        while (l < J[a] && l < box_vol) l *= 2;
+        limit[a] = l;
+      }
+      // Odometer over the power-of-two exponents of each axis.
+      std::vector<int> e(R, 0);
+      while (true) {
+        int prod = 1;
+        for (int a = 0; a < R; ++a) {
+          b[a] = 1 << e[a];
+          prod *= b[a];
+        }
+        bool valid = prod == box_vol;
+        for (int a = 0; a < R && valid; ++a) valid = b[a] <= limit[a];
+        if (valid) {
+          int64_t hvol = 1, boxes = 1;
+          for (int a = 0; a < R; ++a) {
+            hvol *= (int64_t)(b[a] - 1) * sigma[a] + span[a] + 1;
+            boxes *= (J[a] + b[a] - 1) / b[a];
+          }
+          const int64_t halo_bytes = hvol * pstride;
+          const bool grid_ok = boxes <= (int64_t{1} << 30) && g.groups * mgroups <= 65535 &&
+                               g.batch * nphase <= 65535;
+          if (halo_bytes + table_bytes <= kLdsBudget && grid_ok) {
+            const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
+            const int64_t nchunk = gemm_cin / cc;
+            const double mfma_clk = double(nchunk) * kc * mb * nb * 16.0;
+            const double load_clk = double(nchunk) * hvol * (cc * es) / 64.0;
+            const double waves_of_wgs = double((wgs + 255) / 256);
+            const double cost = waves_of_wgs * (mfma_clk + load_clk);
+            if (best < 0 || cost < best) {
+              best = cost;
+              plan.ok = true;
+              plan.mb = mb;
+              plan.nb = nb;
+              IgemmArgs& A = plan.args;
+              std::memset(&A, 0, sizeof(A));
+              A.rank = R;
+              A.mode = mode;
+              A.batch = static_cast<int>(g.batch);
+              A.groups = static_cast<int>(g.groups);
+              A.nphase = nphase;
+              A.cin_g = gemm_cin;
+              A.cout_g = gemm_cout;
+              A.cin_total = static_cast<int>(gemm_cin * g.groups);
+              A.cout_total = static_cast<int>(gemm_cout * g.groups);
+              A.wk_cin_g = static_cast<int>(g.cin_g);
+              A.wk_cout_g = static_cast<int>(g.cout_g);
+              A.cc = cc;
+              A.nchunk = static_cast<int>(nchunk);
+              A.kc_max = static_cast<int>(kc);
+              A.mtiles = mtiles;
+              A.mgroups = mgroups;
+              A.mtiles_padded = mgroups * mb;
+              A.pstride = pstride;
+              A.halo_bytes = static_cast<int>(align_up(halo_bytes));
+              int ivol = 1, ovol = 1;
+              for (int a = 0; a < R; ++a) {
+                A.in_size[a] = static_cast<int>(mode == 0 ? g.in[a] : g.out[a]);
+                A.out_size[a] = static_cast<int>(mode == 0 ? g.out[a] : g.in[a]);
+                ivol *= A.in_size[a];
+                ovol *= A.out_size[a];
+                A.box[a] = b[a];
+                A.nbox[a] = (J[a] + b[a] - 1) / b[a];
+                A.k[a] = static_cast<int>(g.k[a]);
+                A.s[a] = static_cast<int>(g.s[a]);
+                A.p[a] = static_cast<int>(g.p[a]);
+                A.d[a] = static_cast<int>(g.d[a]);
+              }
+              A.in_vol = ivol;
+              A.out_vol = ovol;
+              A.box_vol = box_vol;
+              A.boxes = static_cast<int>(boxes);
+              A.k_vol = static_cast<int>(g.k_vol);
+              plan.lds = A.halo_bytes + align_up(table_bytes);
+            }
+          }
+        }
+        // next exponent vector
+        int a = R - 1;
+        for (; a >= 0; --a) {
+          if ((1 << (e[a] + 1)) <= limit[a] && (1 << (e[a] + 1)) <= box_vol) {
+            ++e[a];
+            break;
+          }
+          e[a] = 0;
+        }
+        if (a < 0) break;
+      }
+    }
+  }
+  if (plan.ok) {
+    const IgemmArgs& A = plan.args;
+    plan.wpk_elems = (size_t)A.nphase * A.groups * A.nchunk * A.kc_max * A.mtiles_padded * 64 * 8;
+    plan.staged_elems = (size_t)A.batch * A.in_vol * A.cin_total;
+  }
+  return plan;
+}
+
+// ---- weight-gradient plan ---------------------------------------------------------------
+
+struct WgradPlan {
+  bool ok = false;
+  int mb = 1;
+  WgradArgs args{};
+  size_t lds = 0;
+  size_t staged_elems = 0;
+  size_t partial_elems = 0;
+};
+
+WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
+  WgradPlan plan;
+  if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g) || g.cin_g % 8 != 0 ||
+      g.batch == 0)
+    return plan;
+  const int R = g.rank;
+  const int cin_g = static_cast<int>(g.cin_g), cout_g = static_cast<int>(g.cout_g);
+  const int mtiles = (cout_g + 15) / 16;
+  const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
+  const int mgroups = (mtiles + mb - 1) / mb;
+  const int pstride = halo_pstride(cin_g);
+  const int npairs = static_cast<int>(g.k_vol * (cin_g / 8));
+  const int ncg = (npairs + 15) / 16;
+  const int ncq = (ncg + 3) / 4;
+  if (ncq > 65535 || g.groups * mgroups > 65535) return plan;
+  double best = -1.0;
+  for (int box_vol : {256, 128, 64, 32}) {
+    const int dyrow = box_vol * 2 + 16;
+    int limit[kFastRank];
+    for (int a = 0; a < R; ++a) {
+      int l = 1;
+      while (l < g.out[a] && l < box_vol) l *= 2;
+      limit[a] = l;
+    }
+    std::vector<int> e(R, 0);
+    while (true) {
+      int b[kFastRank];
+      int prod = 1;
+      for (int a = 0; a < R; ++a) {
+        b[a] = 1 << e[a];
+        prod *= b[a];
+      }
+      bool valid = prod == box_vol;
+      for (int a = 0; a < R && valid; ++a) valid = b[a] <= limit[a];
+      if (valid) {
+        int64_t hvol = 1, boxes = 1;
+        int halo[kFastRank];
+        for (int a = 0; a < R; ++a) {
+          halo[a] = static_cast<int>((b[a] - 1) * g.s[a] + (g.k[a] - 1) * g.d[a] + 1);
+          hvol *= halo[a];
+          boxes *= (g.out[a] + b[a] - 1) / b[a];
+        }
+        const int64_t halo_bytes = align_up(hvol * pstride);
+        const int64_t lds = halo_bytes + align_up((int64_t)mb * 16 * dyrow) + box_vol * 4;
+        if (lds <= kLdsBudget) {
+          const int64_t items = boxes * g.batch;
+          // Position chunks: about two workgroups per CU overall.
+          const int64_t per_chunk_wgs = ncq * g.groups * mgroups;
+          int64_t npc = std::max<int64_t>(1, (512 + per_chunk_wgs - 1) / per_chunk_wgs);
+          npc = std::min<int64_t>(npc, items);
+          const int64_t ipc = (items + npc - 1) / npc;
+          npc = (items + ipc - 1) / ipc;
+          const double per_box = double(box_vol / 32) * 8 * mb * 16.0 +
+                                 double(hvol) * cin_g * 2 / 64.0 +
+                                 double(mb * 16) * box_vol * 2 / 64.0;
+          const int64_t wgs = npc * per_chunk_wgs;
+          const double cost = double((wgs + 255) / 256) * ipc * per_box +
+                              double(npc) * g.out_channels * cin_g * g.k_vol * 8 / 4.0e3;
+          if (best < 0 || cost < best) {
+            best = cost;
+            plan.ok = true;
+            plan.mb = mb;
+            WgradArgs& A = plan.args;
+            std::memset(&A, 0, sizeof(A));
+            A.rank = R;
+            A.batch = static_cast<int>(g.batch);
+            A.groups = static_cast<int>(g.groups);
+            A.cin_g = cin_g;
+            A.cout_g = cout_g;
+            A.cin_total = static_cast<int>(g.channels);
+            A.cout_total = static_cast<int>(g.out_channels);
+            int ivol = 1, ovol = 1;
+            for (int a = 0; a < R; ++a) {
+              A.in_size[a] = static_cast<int>(g.in[a]);
+              A.out_size[a] = static_cast<int>(g.out[a]);
+              ivol *= A.in_size[a];
+              ovol *= A.out_size[a];
+              A.k[a] = static_cast<int>(g.k[a]);
+              A.s[a] = static_cast<int>(g.s[a]);
+              A.p[a] = static_cast<int>(g.p[a]);
+              A.d[a] = static_cast<int>(g.d[a]);
+              A.box[a] = b[a];
+              A.nbox[a] = static_cast<int>((g.out[a] + b[a] - 1) / b[a]);
+              A.halo[a] = halo[a];
+            }
+            A.in_vol = ivol;
+            A.out_vol = ovol;
+            A.k_vol = static_cast<int>(g.k_vol);
+            A.box_vol = box_vol;
+            A.boxes = static_cast<int>(boxes);
+            A.halo_vol = static_cast<int>(hvol);
+            A.pstride = pstride;
+            A.halo_bytes = static_cast<int>(halo_bytes);
+            A.dyrow = dyrow;
+            A.mtiles = mtiles;
+            A.mgroups = mgroups;
+            A.npairs = npairs;
+            A.ncg = ncg;
+            A.ncq = ncq;
+            A.npc = static_cast<int>(npc);
+            A.items = static_cast<int>(items);
+            A.items_per_pc = static_cast<int>(ipc);
+            plan.lds = static_cast<size_t>(lds);
+          }
+        }
+      }
+      int a = R - 1;
+      for (; a >= 0; --a) {
+        if ((1 << (e[a] + 1)) <= limit[a] && (1 << (e[a] + 1)) <= box_vol) {
+          ++e[a];
+          break;
+        }
+        e[a] = 0;
+      }
+      if (a < 0) break;
+    }
+  }
+  if (plan.ok) {
+    plan.staged_elems = (size_t)g.batch * g.in_vol * g.channels;
+    plan.partial_elems = (size_t)plan.args.npc * g.out_channels * g.cin_g * g.k_vol;
+  }
+  return plan;
+}
+
+constexpr int64_t kBiasChunks = 32;
+
+// Workspace layout helper: a sequence of 256-byte aligned regions.
+struct Layout {
+  size_t total = 0;
+  size_t take(size_t bytes) {
+    const size_t at = total;
+    total += align_up(bytes);
+    return at;
+  }
+};
+
+struct ForwardSetup {
+  IgemmPlan ig;
+  size_t off_stage = 0, off_wpk = 0;
+  size_t bytes = 0;
+};
+
+ForwardSetup setup_forward(const Geom& g, convnd_hip_dtype dt) {
+  ForwardSetup f;
+  f.ig = plan_igemm(g, dt, 0);
+  Layout L;
+  if (f.ig.ok) {
+    const int64_t es = element_size(dt);
+    f.off_stage = L.take(f.ig.staged_elems * es);
+    f.off_wpk = L.take(f.ig.wpk_elems * es);
+  }
+  f.bytes = L.total;
+  return f;
+}
+
+struct BackwardSetup {
+  IgemmPlan dg;
+  WgradPlan wg;
+  size_t off_dy_stage = 0, off_wpk = 0, off_x_stage = 0, off_partial = 0, off_bias = 0;
+  size_t bytes = 0;
+};
+
+BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw, bool gb) {
+  BackwardSetup b;
+  const int64_t es = element_size(dt);
+  Layout L;
+  if (gi && g.batch > 0) {
+    b.dg = plan_igemm(g, dt, 1);
+    if (b.dg.ok) {
+      b.off_dy_stage = L.take(b.dg.staged_elems * es);
+      b.off_wpk = L.take(b.dg.wpk_elems * es);
+    }
+  }
+  if (gw && g.batch > 0) {
+    b.wg = plan_wgrad(g, dt);
+    if (b.wg.ok) {
+      b.off_x_stage = L.take(b.wg.staged_elems * es);
+      b.off_partial = L.take(b.wg.partial_elems * sizeof(float));
+    }
+  }
+  if (gb) b.off_bias = L.take((size_t)g.out_channels * kBiasChunks * sizeof(double));
+  b.bytes = L.total;
+  return b;
+}
+
+int hip_check(hipError_t err, const char* what) {
+  if (err == hipSuccess) return CONVND_HIP_SUCCESS;
+  return fail(CONVND_HIP_LAUNCH_FAILED,
+              std::string(what) + " failed: " + hipGetErrorString(err));
+}
+
+int prepare(const convnd_hip_problem* problem, convnd_hip_dtype dtype, Geom* g) {
+  if (element_size(dtype) == 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT,
+                "native conv_nd supports float16, bfloat16, float32 and float64");
+  Geom full;
+  const int st = build_geometry(problem, &full);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  *g = drop_unit_axes(full);
+  return CONVND_HIP_SUCCESS;
+}
+
+}  // namespace
+}  // namespace convnd
+
+using namespace convnd;
+
+extern "C" {
+
+const char* convnd_hip_last_error(void) { return g_error.c_str(); }
+
+int convnd_hip_validate(const convnd_hip_problem* problem, int64_t element_sz,
+                        int64_t workspace_bytes, int64_t* output_sizes) {
+  Geom g;
+  const int st = build_geometry(problem, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  // tile_size (src/torch_convnd/csrc/convnd.cpp:89-100).
+  int64_t rows, per_position;
+  if (!mul_ok(g.channels, g.k_vol, &rows))
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "patch rows overflows int64");
+  if (!mul_ok(std::max<int64_t>(element_sz, 4), rows, &per_position))
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "workspace bytes per position overflows int64");
+  if (workspace_bytes < per_position)
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "workspace_bytes is too small for one output position; requires at least " +
+                    std::to_string(per_position));
+  if (output_sizes != nullptr)
+    for (int a = 0; a < g.rank; ++a) output_sizes[a] = g.out[a];
+  g_error.clear();
+  return CONVND_HIP_SUCCESS;
+}
+
+size_t convnd_hip_forward_workspace_size(const convnd_hip_problem* problem,
+                                         convnd_hip_dtype dtype) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
+  return setup_forward(g, dtype).bytes;
+}
+
+size_t convnd_hip_backward_workspace_size(const convnd_hip_problem* problem,
+                                          convnd_hip_dtype dtype, int need_grad_input,
+                                          int need_grad_weight, int need_grad_bias) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
+  return setup_backward(g, dtype, need_grad_input != 0, need_grad_weight != 0,
+                        need_grad_bias != 0)
+      .bytes;
+}
+
+const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                                 int which) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return "invalid";
+  if (which == 0) return plan_igemm(g, dtype, 0).ok ? "mfma" : "direct";
+  if (which == 1) return plan_igemm(g, dtype, 1).ok ? "mfma" : "direct";
+  if (which == 2) return plan_wgrad(g, dtype).ok ? "mfma" : "direct";
+  return "invalid";
+}
+
+int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                       const void* input, const void* weight, const void* bias, void* output,
+                       void* workspace, size_t workspace_size, void* stream_ptr) {
+  Geom g;
+  int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (g.batch == 0) return CONVND_HIP_SUCCESS;
+  const ForwardSetup f = setup_forward(g, dtype);
+  if (workspace_size < f.bytes || (f.bytes > 0 && workspace == nullptr))
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "device workspace is smaller than convnd_hip_forward_workspace_size");
+  if (!f.ig.ok) {
+    return hip_check(launch_direct_forward(dtype, to_direct(g), input, weight, bias, output,
+                                           stream),
+                     "direct forward kernel");
+  }
+  char* ws = static_cast<char*>(workspace);
+  IgemmArgs A = f.ig.args;
+  void* staged = ws + f.off_stage;
+  void* wpk = ws + f.off_wpk;
+  st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels, g.in_vol,
+                                         stream),
+                 "channels-last staging");
+  if (st != CONVND_HIP_SUCCESS) return st;
+  st = hip_check(launch_pack_weights(dtype, A, weight, wpk, stream), "weight packing");
+  if (st != CONVND_HIP_SUCCESS) return st;
+  A.in = staged;
+  A.wpk = wpk;
+  A.bias = bias;
+  A.out = output;
+  return hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
+                   "implicit GEMM forward");
+}
+
+int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                        const void* grad_output, const void* input, const void* weight,
+                        void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
+                        size_t workspace_size, void* stream_ptr) {
+  Geom g;
+  int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const bool gi = grad_input != nullptr, gw = grad_weight != nullptr,
+             gb = grad_bias != nullptr;
+  const BackwardSetup b = setup_backward(g, dtype, gi, gw, gb);
+  if (workspace_size < b.bytes || (b.bytes > 0 && workspace == nullptr))
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "device workspace is smaller than convnd_hip_backward_workspace_size");
+  char* ws = static_cast<char*>(workspace);
+  const int64_t es = element_size(dtype);
+  if (g.batch == 0) {
+    // Gradients of an empty batch: dX is empty, dW and db are zero.
+    if (gw) {
+      st = hip_check(launch_fill_zero(grad_weight, g.out_channels * g.cin_g * g.k_vol * es,
+                                      stream),
+                     "zero weight gradient");
+      if (st != CONVND_HIP_SUCCESS) return st;
+    }
+    if (gb) {
+      st = hip_check(launch_fill_zero(grad_bias, g.out_channels * es, stream),
+                     "zero bias gradient");
+      if (st != CONVND_HIP_SUCCESS) return st;
+    }
+    return CONVND_HIP_SUCCESS;
+  }
+  if (gb) {
+    st = hip_check(launch_grad_bias(dtype, g.batch, g.out_channels, g.out_vol, grad_output,
+                                    grad_bias, reinterpret_cast<float*>(ws + b.off_bias),
+                                    kBiasChunks, stream),
+                   "bias gradient");
+    if (st != CONVND_HIP_SUCCESS) return st;
+  }
+  if (gi) {
+    if (b.dg.ok) {
+      IgemmArgs A = b.dg.args;
+      void* staged = ws + b.off_dy_stage;
+      void* wpk = ws + b.off_wpk;
+      st = hip_check(launch_to_channels_last(dtype, grad_output, staged, g.batch,
+                                             g.out_channels, g.out_vol, stream),
+                     "channels-last staging of grad_output");
+      if (st != CONVND_HIP_SUCCESS) return st;
+      st = hip_check(launch_pack_weights(dtype, A, weight, wpk, stream),
+                     "input-gradient weight packing");
+      if (st != CONVND_HIP_SUCCESS) return st;
+      A.in = staged;
+      A.wpk = wpk;
+      A.bias = nullptr;
+      A.out = grad_input;
+      st = hip_check(launch_igemm(dtype, b.dg.mb, b.dg.nb, A, b.dg.lds, stream),
+                     "implicit GEMM input gradient");
+    } else {
+      st = hip_check(launch_direct_grad_input(dtype, to_direct(g), grad_output, weight,
+                                              grad_input, stream),
+                     "direct input-gradient kernel");
+    }
+    if (st != CONVND_HIP_SUCCESS) return st;
+  }
+  if (gw) {
+    if (b.wg.ok) {
+      WgradArgs A = b.wg.args;
+      void* staged = ws + b.off_x_stage;
+      float* partial = reinterpret_cast<float*>(ws + b.off_partial);
+      st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels,
+                                             g.in_vol, stream),
+                     "channels-last staging of input");
+      if (st != CONVND_HIP_SUCCESS) return st;
+      A.x = staged;
+      A.dy = grad_output;
+      A.partial = partial;
+      st = hip_check(launch_wgrad_mfma(dtype, b.wg.mb, A, b.wg.lds, stream),
+                     "MFMA weight gradient");
+      if (st != CONVND_HIP_SUCCESS) return st;
+      st = hip_check(launch_reduce_partials(dtype, partial, grad_weight,
+                                            (int64_t)g.out_channels * g.cin_g * g.k_vol,
+                                            A.npc, stream),
+                     "weight-gradient reduction");
+    } else {
+      st = hip_check(launch_direct_grad_weight(dtype, to_direct(g), grad_output, input,
+                                               grad_weight, stream),
+                     "direct weight-gradient kernel");
+    }
+    if (st != CONVND_HIP_SUCCESS) return st;
+  }
+  return CONVND_HIP_SUCCESS;
+}
+
+}  // extern "C"

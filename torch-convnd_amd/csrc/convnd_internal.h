@@ -1,0 +1,100 @@
+// Internal declarations shared by the gfx950 kernels and the C ABI host code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "convnd_hip.h"
+
+namespace convnd {
+
+constexpr int kMaxRank = CONVND_HIP_MAX_RANK;
+// Ranks the MFMA kernels unroll over (after axes with one sample, one tap and no
+// padding are dropped).
+constexpr int kFastRank = 8;
+constexpr int kThreads = 256;
+
+// Geometry of the direct (generic, 64-bit index) kernels. Only `rank` entries of the
+// arrays are meaningful. Passed by value as a kernel argument (about 3 KB).
+struct DirectGeom {
+  int32_t rank;
+  int32_t unused;
+  int64_t batch, channels, out_channels, groups, cin_g, cout_g;
+  int64_t in_vol, out_vol, k_vol;
+  int64_t in[kMaxRank], out[kMaxRank], k[kMaxRank], s[kMaxRank], p[kMaxRank], d[kMaxRank];
+};
+
+// Arguments of the box-tiled implicit GEMM (forward, or one family of stride phases of
+// the input gradient). All sizes fit int32; the planner checks that.
+struct IgemmArgs {
+  const void* in;    // channels-last staged operand [N][in_vol][cin_total]
+  const void* wpk;   // packed A fragments [phase][group][chunk][kc][mtile][64 lanes][8]
+  const void* bias;  // [cout_total] or null (forward only)
+  void* out;         // [N][cout_total][out_vol], channels-first
+  int rank;
+  int mode;          // 0: forward convolution, 1: input gradient of a forward convolution
+  int batch, groups, nphase;
+  int cin_g, cout_g;          // GEMM reduction channels / output channels per group
+  int cin_total, cout_total;
+  int wk_cin_g, wk_cout_g;    // channels per group of the original weight tensor
+  int cc, nchunk, kc_max;     // channels per LDS halo chunk, chunks, K32 steps per chunk
+  int mtiles, mgroups, mtiles_padded;
+  int pstride;                // LDS bytes per halo position
+  int halo_bytes;             // LDS bytes reserved for the halo
+  int in_size[kFastRank], out_size[kFastRank];
+  int in_vol, out_vol;
+  int box[kFastRank], nbox[kFastRank];
+  int box_vol, boxes;
+  int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
+  int k_vol;
+};
+
+// Arguments of the MFMA weight-gradient kernel.
+struct WgradArgs {
+  const void* x;      // channels-last input [N][in_vol][cin_total]
+  const void* dy;     // grad_output [N][cout_total][out_vol]
+  float* partial;     // [npc][cout_total][cin_g][k_vol]
+  int rank;
+  int batch, groups, cin_g, cout_g, cin_total, cout_total;
+  int in_size[kFastRank], out_size[kFastRank];
+  int in_vol, out_vol, k_vol;
+  int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
+  int box[kFastRank], nbox[kFastRank];
+  int box_vol, boxes;
+  int halo[kFastRank];
+  int halo_vol, pstride, halo_bytes;
+  int dyrow;          // LDS bytes per grad_output row of the box tile
+  int mtiles, mgroups;
+  int npairs, ncg, ncq;
+  int npc, items, items_per_pc;
+};
+
+// ---- kernel launchers (defined in the .hip files) -------------------------------------
+hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void* dst,
+                                   int64_t batch, int64_t channels, int64_t volume,
+                                   hipStream_t stream);
+hipError_t launch_direct_forward(convnd_hip_dtype dtype, const DirectGeom& g, const void* x,
+                                 const void* w, const void* b, void* y, hipStream_t stream);
+hipError_t launch_direct_grad_input(convnd_hip_dtype dtype, const DirectGeom& g,
+                                    const void* dy, const void* w, void* dx,
+                                    hipStream_t stream);
+hipError_t launch_direct_grad_weight(convnd_hip_dtype dtype, const DirectGeom& g,
+                                     const void* dy, const void* x, void* dw,
+                                     hipStream_t stream);
+hipError_t launch_grad_bias(convnd_hip_dtype dtype, int64_t batch, int64_t channels,
+                            int64_t volume, const void* dy, void* db, float* scratch,
+                            int64_t chunks, hipStream_t stream);
+hipError_t launch_pack_weights(convnd_hip_dtype dtype, const IgemmArgs& a, const void* w,
+                               void* wpk, hipStream_t stream);
+hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,
+                        size_t lds_bytes, hipStream_t stream);
+hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, const WgradArgs& a,
+                             size_t lds_bytes, hipStream_t stream);
+hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream);
+hipError_t launch_reduce_partials(convnd_hip_dtype dtype, const float* partial, void* out,
+                                  int64_t count, int64_t parts, hipStream_t stream);
+
+}  // namespace convnd

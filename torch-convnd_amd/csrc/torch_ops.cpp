@@ -1,0 +1,252 @@
+// PyTorch dispatcher kernels for the torch_convnd::conv_nd / conv_nd_backward schemas.
+//
+// The schemas themselves are defined from Python (torch_convnd/_operators.py) exactly as in
+// the reference (src/torch_convnd/_operators.py:47-56); this library only implements them
+// for the CUDA dispatch key (the ROCm/HIP device), AutocastCUDA and CPU, as the reference's
+// registration block does (src/torch_convnd/csrc/convnd.cpp:435-452). Tensor checks keep
+// the reference's order and wording (convnd.cpp:33-44,310-315,351-355); geometry checks
+// and all device work go through the C ABI in convnd_hip.h.
+
+#include <ATen/ATen.h>
+#include <ATen/autocast_mode.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <array>
+#include <limits>
+#include <optional>
+#include <tuple>
+#include <vector>
+
+#include "convnd_hip.h"
+
+namespace torch_convnd_hip {
+namespace {
+
+using Grads = std::tuple<std::optional<at::Tensor>, std::optional<at::Tensor>,
+                         std::optional<at::Tensor>>;
+
+convnd_hip_dtype to_dtype(at::ScalarType type) {
+  switch (type) {
+    case at::kFloat:
+      return CONVND_HIP_FLOAT32;
+    case at::kDouble:
+      return CONVND_HIP_FLOAT64;
+    case at::kHalf:
+      return CONVND_HIP_FLOAT16;
+    default:
+      return CONVND_HIP_BFLOAT16;
+  }
+}
+
+void raise_status(int status) {
+  TORCH_CHECK(status == CONVND_HIP_SUCCESS, convnd_hip_last_error());
+}
+
+// Tensor-level checks of make_geometry, then the integer geometry checks of the C ABI.
+convnd_hip_problem make_problem(const at::Tensor& input, const at::Tensor& weight,
+                                at::IntArrayRef stride, at::IntArrayRef padding,
+                                at::IntArrayRef dilation, int64_t groups) {
+  TORCH_CHECK(input.layout() == at::kStrided && weight.layout() == at::kStrided,
+              "conv_nd requires strided tensors");
+  TORCH_CHECK(input.device().is_cpu() || input.device().is_cuda(),
+              "conv_nd supports CPU and CUDA tensors");
+  const auto type = input.scalar_type();
+  TORCH_CHECK(type == at::kFloat || type == at::kDouble || type == at::kHalf ||
+                  type == at::kBFloat16,
+              "native conv_nd supports float16, bfloat16, float32 and float64");
+  TORCH_CHECK(weight.device() == input.device() && weight.scalar_type() == type,
+              "input and weight must have the same device and dtype");
+  TORCH_CHECK(input.dim() >= 3 && input.dim() <= CONVND_HIP_MAX_RANK + 2,
+              "conv_nd requires 1 to 62 spatial dimensions");
+  TORCH_CHECK(weight.dim() == input.dim(), "input and weight ranks must match");
+  const int64_t rank = input.dim() - 2;
+  TORCH_CHECK(static_cast<int64_t>(stride.size()) == rank &&
+                  static_cast<int64_t>(padding.size()) == rank &&
+                  static_cast<int64_t>(dilation.size()) == rank,
+              "stride, padding and dilation must match the spatial rank");
+  TORCH_CHECK(groups > 0, "groups must be positive");
+  TORCH_CHECK(input.size(1) > 0 && weight.size(0) > 0 && input.size(1) % groups == 0 &&
+                  weight.size(0) % groups == 0 && weight.size(1) == input.size(1) / groups,
+              "input/weight channels must match and be divisible by groups");
+  convnd_hip_problem problem{};
+  problem.rank = rank;
+  problem.batch = input.size(0);
+  problem.channels = input.size(1);
+  problem.output_channels = weight.size(0);
+  problem.groups = groups;
+  for (int64_t a = 0; a < rank; ++a) {
+    problem.input[a] = input.size(a + 2);
+    problem.kernel[a] = weight.size(a + 2);
+    problem.stride[a] = stride[a];
+    problem.padding[a] = padding[a];
+    problem.dilation[a] = dilation[a];
+  }
+  raise_status(convnd_hip_validate(&problem, input.element_size(),
+                                   std::numeric_limits<int64_t>::max(), nullptr));
+  return problem;
+}
+
+std::vector<int64_t> output_shape(const convnd_hip_problem& problem,
+                                  const at::Tensor& input) {
+  std::vector<int64_t> out(problem.rank);
+  raise_status(convnd_hip_validate(&problem, input.element_size(),
+                                   std::numeric_limits<int64_t>::max(), out.data()));
+  std::vector<int64_t> shape = {problem.batch, problem.output_channels};
+  shape.insert(shape.end(), out.begin(), out.end());
+  return shape;
+}
+
+void check_workspace(const convnd_hip_problem& problem, int64_t element_size,
+                     int64_t workspace_bytes) {
+  raise_status(convnd_hip_validate(&problem, element_size, workspace_bytes, nullptr));
+}
+
+void* current_stream(const at::Tensor& tensor) {
+  return static_cast<void*>(c10::hip::getCurrentHIPStream(tensor.device().index()).stream());
+}
+
+at::Tensor conv_nd_device(const at::Tensor& input, const at::Tensor& weight,
+                          const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                          at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                          int64_t workspace_bytes) {
+  const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
+                    bias->size(0) == problem.output_channels &&
+                    bias->device() == input.device() &&
+                    bias->scalar_type() == input.scalar_type(),
+                "bias must match output channels, device and dtype");
+  }
+  const auto shape = output_shape(problem, input);
+  check_workspace(problem, input.element_size(), workspace_bytes);
+  const c10::OptionalDeviceGuard guard(input.device());
+  auto output = at::empty(shape, input.options());
+  if (problem.batch == 0) return output;
+  const auto x = input.contiguous();
+  const auto w = weight.contiguous();
+  std::optional<at::Tensor> b;
+  if (bias.has_value()) b = bias->contiguous();
+  const auto dtype = to_dtype(input.scalar_type());
+  const size_t ws_bytes = convnd_hip_forward_workspace_size(&problem, dtype);
+  auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
+  raise_status(convnd_hip_forward(&problem, dtype, x.const_data_ptr(), w.const_data_ptr(),
+                                  b.has_value() ? b->const_data_ptr() : nullptr,
+                                  output.mutable_data_ptr(),
+                                  ws_bytes ? workspace.mutable_data_ptr() : nullptr, ws_bytes,
+                                  current_stream(input)));
+  return output;
+}
+
+Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& input,
+                              const at::Tensor& weight, at::IntArrayRef stride,
+                              at::IntArrayRef padding, at::IntArrayRef dilation,
+                              int64_t groups, int64_t workspace_bytes,
+                              std::array<bool, 3> output_mask) {
+  const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
+  const auto shape = output_shape(problem, input);
+  TORCH_CHECK(grad_output.sizes().vec() == shape && grad_output.device() == input.device() &&
+                  grad_output.scalar_type() == input.scalar_type() &&
+                  grad_output.layout() == at::kStrided,
+              "grad_output must match the convolution output shape, device and dtype");
+  // Low-precision backward accumulates in fp32, so the reference sizes its patch buffer
+  // with four-byte elements (src/torch_convnd/csrc/convnd.cpp:361).
+  check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
+  const c10::OptionalDeviceGuard guard(input.device());
+  std::optional<at::Tensor> grad_input, grad_weight, grad_bias;
+  if (problem.batch == 0) {
+    if (output_mask[0]) grad_input = at::zeros(input.sizes(), input.options());
+    if (output_mask[1]) grad_weight = at::zeros(weight.sizes(), weight.options());
+    if (output_mask[2]) grad_bias = at::zeros({problem.output_channels}, input.options());
+    return {grad_input, grad_weight, grad_bias};
+  }
+  if (output_mask[0]) grad_input = at::empty(input.sizes(), input.options());
+  if (output_mask[1]) grad_weight = at::empty(weight.sizes(), weight.options());
+  if (output_mask[2]) grad_bias = at::empty({problem.output_channels}, input.options());
+  if (!output_mask[0] && !output_mask[1] && !output_mask[2]) return {};
+  const auto dy = grad_output.contiguous();
+  const auto x = input.contiguous();
+  const auto w = weight.contiguous();
+  const auto dtype = to_dtype(input.scalar_type());
+  const size_t ws_bytes = convnd_hip_backward_workspace_size(
+      &problem, dtype, output_mask[0], output_mask[1], output_mask[2]);
+  auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
+  raise_status(convnd_hip_backward(
+      &problem, dtype, dy.const_data_ptr(), x.const_data_ptr(), w.const_data_ptr(),
+      grad_input.has_value() ? grad_input->mutable_data_ptr() : nullptr,
+      grad_weight.has_value() ? grad_weight->mutable_data_ptr() : nullptr,
+      grad_bias.has_value() ? grad_bias->mutable_data_ptr() : nullptr,
+      ws_bytes ? workspace.mutable_data_ptr() : nullptr, ws_bytes, current_stream(input)));
+  return {grad_input, grad_weight, grad_bias};
+}
+
+// CPU tensors reach the native op only with backend="native": validate like the reference,
+// then refuse — this build's native kernels are the gfx950 ones.
+at::Tensor conv_nd_cpu(const at::Tensor& input, const at::Tensor& weight,
+                       const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                       at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                       int64_t workspace_bytes) {
+  const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
+                    bias->size(0) == problem.output_channels &&
+                    bias->device() == input.device() &&
+                    bias->scalar_type() == input.scalar_type(),
+                "bias must match output channels, device and dtype");
+  }
+  check_workspace(problem, input.element_size(), workspace_bytes);
+  TORCH_CHECK(false,
+              "native torch_convnd kernels in this build run on ROCm GPUs (gfx950); "
+              "use backend='torch' or backend='auto' for CPU tensors");
+}
+
+Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& input,
+                           const at::Tensor& weight, at::IntArrayRef stride,
+                           at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                           int64_t workspace_bytes, std::array<bool, 3> output_mask) {
+  const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
+  (void)grad_output;
+  (void)output_mask;
+  check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
+  TORCH_CHECK(false,
+              "native torch_convnd kernels in this build run on ROCm GPUs (gfx950); "
+              "use backend='torch' or backend='auto' for CPU tensors");
+}
+
+// Autocast: cast the operands once to the autocast dtype and redispatch below autocast,
+// as the reference's autocast_conv_nd does (src/torch_convnd/csrc/convnd.cpp:417-431).
+at::Tensor conv_nd_autocast(const at::Tensor& input, const at::Tensor& weight,
+                            const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                            at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                            int64_t workspace_bytes) {
+  const c10::impl::ExcludeDispatchKeyGuard no_autocast(c10::DispatchKey::AutocastCUDA);
+  const auto dtype = at::autocast::get_autocast_dtype(at::kCUDA);
+  static const auto op = c10::Dispatcher::singleton()
+                             .findSchemaOrThrow("torch_convnd::conv_nd", "")
+                             .typed<decltype(conv_nd_device)>();
+  const auto cast = [&](const at::Tensor& t) {
+    return at::autocast::cached_cast(dtype, t, c10::DeviceType::CUDA);
+  };
+  std::optional<at::Tensor> b;
+  if (bias.has_value()) b = cast(*bias);
+  return op.call(cast(input), cast(weight), b, stride, padding, dilation, groups,
+                 workspace_bytes);
+}
+
+}  // namespace
+}  // namespace torch_convnd_hip
+
+TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_device);
+  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_device);
+}
+
+TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autocast);
+}
+
+TORCH_LIBRARY_IMPL(torch_convnd, CPU, library) {
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_cpu);
+  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_cpu);
+}

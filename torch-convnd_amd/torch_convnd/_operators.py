@@ -1,0 +1,71 @@
+"""The ``torch_convnd`` operator schemas, defined without any compiler or GPU.
+
+Schemas are byte-identical to the reference's (src/torch_convnd/_operators.py:47-56) so
+scripted/exported graphs and callers of ``torch.ops.torch_convnd`` are interchangeable.
+The CompositeExplicitAutograd kernels load the native library on a graph's first real
+call; once it is loaded its CUDA/CPU kernels take precedence.
+"""
+
+import threading
+
+import torch
+
+from ._compat import HAS_LIBRARY, HAS_NATIVE_AUTOGRAD
+
+_LIBRARY = None
+_LOCK = threading.Lock()
+
+
+def _load_for(input):
+    from . import _build
+
+    if input.device.type not in {"cpu", "cuda"} or (
+        input.device.type == "cuda" and torch.version.hip is None
+    ):
+        raise RuntimeError("Native operators in this build support ROCm GPUs")
+    if _build._LOADED:
+        raise RuntimeError(
+            f"no native torch_convnd kernel is registered for device {input.device.type!r}"
+        )
+    _build.load_native()
+
+
+def _lazy_forward(input, weight, bias, stride, padding, dilation, groups, workspace_bytes):
+    _load_for(input)
+    return torch.ops.torch_convnd.conv_nd.default(
+        input, weight, bias, stride, padding, dilation, groups, workspace_bytes
+    )
+
+
+def _lazy_backward(
+    grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
+):
+    _load_for(input)
+    return torch.ops.torch_convnd.conv_nd_backward.default(
+        grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
+    )
+
+
+def ensure_native_definitions():
+    """Define the schemas once per process (idempotent, thread-safe)."""
+    global _LIBRARY
+    with _LOCK:
+        if _LIBRARY is not None or not HAS_LIBRARY:
+            return
+        library = torch.library.Library("torch_convnd", "DEF")
+        library.define(
+            "conv_nd(Tensor input, Tensor weight, Tensor? bias, int[] stride, int[] padding, "
+            "int[] dilation, int groups, int workspace_bytes) -> Tensor"
+        )
+        library.define(
+            "conv_nd_backward(Tensor grad_output, Tensor input, Tensor weight, int[] stride, "
+            "int[] padding, int[] dilation, int groups, int workspace_bytes, "
+            "bool[3] output_mask) -> (Tensor?, Tensor?, Tensor?)"
+        )
+        library.impl("conv_nd", _lazy_forward, "CompositeExplicitAutograd")
+        library.impl("conv_nd_backward", _lazy_backward, "CompositeExplicitAutograd")
+        if HAS_NATIVE_AUTOGRAD:
+            from ._autograd import register_training
+
+            register_training()
+        _LIBRARY = library

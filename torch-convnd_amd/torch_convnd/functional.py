@@ -1,0 +1,122 @@
+"""Functional frontend: ``conv_nd`` with Conv2d/Conv3d-style semantics for 1-62 axes.
+
+Argument handling follows the reference (src/torch_convnd/functional.py:65-185):
+batched or unbatched input, int/sequence/'same'/'valid' padding, zero/reflect/replicate/
+circular padding modes, complex dtypes, AMP and every backend. Symmetric zero padding is
+passed to the operator as implicit padding; anything else is padded explicitly first.
+"""
+
+from collections.abc import Sequence
+
+import torch
+from torch import Tensor
+
+from ._compat import HAS_LIBRARY, is_autocast_enabled
+from ._dispatch import BACKENDS, convolution, ensure_compatible_operator
+from ._geometry import DEFAULT_WORKSPACE_BYTES, _tuple, any_true, has_rank
+from ._padding import apply_padding, padding_pairs
+
+_CASTABLE = (torch.float16, torch.bfloat16, torch.float32)
+_PADDING_MODES = ("zeros", "reflect", "replicate", "circular", "partial")
+
+
+def _check_options(padding_mode, workspace_bytes, backend):
+    if backend not in BACKENDS:
+        raise ValueError(f"Invalid backend {backend!r}; expected 'auto', 'native' or 'torch'")
+    if workspace_bytes <= 0:
+        raise ValueError("workspace_bytes must be positive")
+    if padding_mode not in _PADDING_MODES:
+        raise ValueError(f"Invalid padding_mode {padding_mode!r}")
+
+
+def _check_arguments(input, weight, stride, padding, dilation, groups):
+    """Geometry, device and dtype checks; returns whether autocast applies."""
+    if min(*stride, *dilation) <= 0 or (not isinstance(padding, str) and min(padding) < 0):
+        raise RuntimeError("stride and dilation must be positive; padding must be nonnegative")
+    if groups <= 0:
+        raise RuntimeError("groups must be positive")
+    in_channels, out_channels = input.shape[1], weight.shape[0]
+    if (
+        in_channels <= 0
+        or out_channels <= 0
+        or in_channels % groups
+        or out_channels % groups
+        or weight.shape[1] != in_channels // groups
+    ):
+        raise RuntimeError("input/weight channels must match and be divisible by groups")
+    if any_true([size <= 0 for size in (*input.shape[2:], *weight.shape[2:])]):
+        raise RuntimeError("spatial and kernel dimensions must be positive")
+    if input.device != weight.device:
+        raise RuntimeError("input and weight must have the same device and dtype")
+    amp = input.device.type in {"cpu", "cuda"} and is_autocast_enabled(input.device.type)
+    if input.dtype != weight.dtype and not (amp and input.dtype in _CASTABLE and weight.dtype in _CASTABLE):
+        raise RuntimeError("input and weight must have the same device and dtype")
+    return amp
+
+
+def _check_bias(input, weight, bias, amp):
+    if bias is None:
+        return
+    dtype_ok = bias.dtype == input.dtype or (amp and bias.dtype in _CASTABLE and input.dtype in _CASTABLE)
+    if bias.ndim != 1 or bias.shape[0] != weight.shape[0] or bias.device != input.device or not dtype_ok:
+        raise RuntimeError("bias must match output channels, device and dtype")
+
+
+def conv_nd(
+    input: Tensor,
+    weight: Tensor,
+    bias: Tensor | None = None,
+    stride: int | Sequence[int] = 1,
+    padding: str | int | Sequence[int] = 0,
+    dilation: int | Sequence[int] = 1,
+    groups: int = 1,
+    *,
+    padding_mode: str = "zeros",
+    workspace_bytes: int = DEFAULT_WORKSPACE_BYTES,
+    backend: str = "auto",
+) -> Tensor:
+    """Full (non-separable) dense convolution over ``weight.ndim - 2`` spatial axes.
+
+    ``backend="auto"`` uses PyTorch convolutions for ranks 1-3 and the gfx950 kernels for
+    rank >= 4 on a ROCm GPU; ``native`` forces the gfx950 kernels, ``torch`` the portable
+    decomposition. Low-precision (bf16/fp16) native results accumulate in fp32.
+    ``workspace_bytes`` keeps the reference's validation contract (at least
+    max(element size, 4) * channels * kernel volume bytes); the implicit-GEMM kernels
+    allocate their own small scratch instead of a patch buffer.
+    """
+    rank = weight.ndim - 2
+    if not 1 <= rank <= 62:
+        raise ValueError("weight must have output/input channels and 1-62 spatial dimensions")
+    if not has_rank(input.ndim, rank):
+        raise ValueError(f"expected {rank + 1} unbatched or {rank + 2} batched dimensions")
+    unbatched = input.ndim == rank + 1
+    if unbatched:
+        input = input.unsqueeze(0)
+    stride = _tuple(stride, rank, "stride")
+    dilation = _tuple(dilation, rank, "dilation")
+    if not isinstance(padding, str):
+        padding = _tuple(padding, rank, "padding")
+    _check_options(padding_mode, workspace_bytes, backend)
+    if padding_mode == "partial":
+        raise NotImplementedError(
+            "padding_mode='partial' (partial convolution) is not part of this build yet"
+        )
+    amp = _check_arguments(input, weight, stride, padding, dilation, groups)
+    _check_bias(input, weight, bias, amp)
+    pairs = padding_pairs(padding, weight.shape[2:], stride, dilation)
+    output = _execute(input, weight, bias, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend)
+    return output.squeeze(0) if unbatched else output
+
+
+def _execute(input, weight, bias, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend):
+    """Pad (when the padding is not symmetric zeros) and dispatch a validated batched call."""
+    if padding_mode != "zeros" or any_true([left != right for left, right in pairs]):
+        input = apply_padding(input, pairs, padding_mode)
+        implicit = (0,) * len(pairs)
+    else:
+        implicit = tuple(left for left, _ in pairs)
+    operation = convolution
+    if torch.jit.is_tracing() and HAS_LIBRARY:
+        ensure_compatible_operator()
+        operation = torch.ops.torch_convnd.compatible_conv_nd
+    return operation(input, weight, bias, stride, implicit, dilation, groups, workspace_bytes, backend)
