@@ -1,0 +1,274 @@
+"""Benchmark of the gfx950 N-d convolution hot path (BASELINE.json metric).
+
+Workload ("C2"): Conv4d bf16 with fp32 accumulation, in=32 out=64,
+kernel 3, padding 'same', stride 1, bias; x[2,32,16,16,16,16] ~ N(0,1) (seed 0), weight and
+bias ~ U(+-1/sqrt(32*81)). A step is one forward plus the full backward (dx, dW, db) of
+y.float().square().mean() through ``torch_convnd.conv_nd(..., backend="native")`` — the
+measurement recipe of the reference's benchmark (src/torch_convnd/benchmark.py:36-70).
+Inputs are resident in HBM before the timed region.
+
+Prints ONE JSON line. ``value`` is forward+backward TFLOP/s (algorithmic FLOPs: 3x the
+forward's 2*N*P*Co*(C/g)*taps; db and the loss are not counted) over wall-clock time
+between synchronisations. ``roofline`` is the dominant kernel's algorithmic FLOPs per launch
+over its average launch time, measured with HIP events around every launch in the timed
+region. ``cpu_baseline`` times this repo's restatement of the reference's backend="torch"
+CPU path (oracle/torch_path.py) on the host cores.
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "torch-convnd_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "Conv4d fwd & fwd+bwd TFLOP/s at 1 GPU (bf16) + % of MFMA/HBM roofline"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD published)
+PEAK_HBM_GBS = 8000.0
+
+X_SHAPE = (2, 32, 16, 16, 16, 16)
+W_SHAPE = (64, 32, 3, 3, 3, 3)
+STRIDE, PADDING, DILATION, GROUPS = (1,) * 4, (1,) * 4, (1,) * 4, 1
+
+
+def forward_flops(x_shape=X_SHAPE, w_shape=W_SHAPE):
+    positions = math.prod(x_shape[2:])  # 'same' padding, stride 1
+    return 2 * x_shape[0] * positions * w_shape[0] * w_shape[1] * math.prod(w_shape[2:])
+
+
+def make_inputs(torch, dtype, device, x_shape=X_SHAPE, w_shape=W_SHAPE, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    bound = 1.0 / math.sqrt(w_shape[1] * math.prod(w_shape[2:]))
+    x = torch.randn(x_shape, generator=g)
+    w = (torch.rand(w_shape, generator=g) * 2 - 1) * bound
+    b = (torch.rand((w_shape[0],), generator=g) * 2 - 1) * bound
+    return [t.to(dtype).to(device) for t in (x, w, b)]
+
+
+def correctness_gate(torch, np, conv, x, w, b):
+    """Check sampled outputs and gradients of the full-size problem against float64 sums
+    computed directly from the definition (check, then time)."""
+    xs, ws, bs = (t.detach().requires_grad_() for t in (x, w, b))
+    y = conv(xs, ws, bs)
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(7)).to(y.dtype).to(y.device)
+    gx, gw, gb = torch.autograd.grad(y, (xs, ws, bs), dy)
+    torch.cuda.synchronize()
+    X = x.double().cpu().numpy()
+    W = w.double().cpu().numpy()
+    B = b.double().cpu().numpy()
+    DY = dy.double().cpu().numpy()
+    Xp = np.pad(X, ((0, 0), (0, 0)) + ((1, 1),) * 4)
+    DYp = np.pad(DY, ((0, 0), (0, 0)) + ((1, 1),) * 4)
+    rng = np.random.default_rng(3)
+    Y, GX, GW = (t.detach().double().cpu().numpy() for t in (y, gx, gw))
+    worst = 0.0
+    for _ in range(64):
+        n, co = rng.integers(2), rng.integers(64)
+        o = rng.integers(16, size=4)
+        ref = B[co] + np.sum(W[co] * Xp[n, :, o[0]:o[0] + 3, o[1]:o[1] + 3, o[2]:o[2] + 3, o[3]:o[3] + 3])
+        worst = max(worst, abs(Y[n, co, o[0], o[1], o[2], o[3]] - ref) / (2e-2 * (abs(ref) + 0.05)))
+        ci = rng.integers(32)
+        # dX[x] = sum_{co,t} W[co,ci,t] * dY[x + 1 - t] (stride 1, pad 1): flipped window.
+        win = DYp[n, :, o[0]:o[0] + 3, o[1]:o[1] + 3, o[2]:o[2] + 3, o[3]:o[3] + 3]
+        ref = np.sum(W[:, ci, ::-1, ::-1, ::-1, ::-1] * win)
+        worst = max(worst, abs(GX[n, ci, o[0], o[1], o[2], o[3]] - ref) / (2e-2 * (abs(ref) + 0.5)))
+    for _ in range(8):
+        co, ci = rng.integers(64), rng.integers(32)
+        t = rng.integers(3, size=4)
+        patch = Xp[:, ci, t[0]:t[0] + 16, t[1]:t[1] + 16, t[2]:t[2] + 16, t[3]:t[3] + 16]
+        ref = np.sum(DY[:, co] * patch)
+        worst = max(worst, abs(GW[co, ci, t[0], t[1], t[2], t[3]] - ref) / (2e-2 * (abs(ref) + 20.0)))
+    ref_db = DY.sum(axis=(0, 2, 3, 4, 5))
+    worst = max(worst, float(np.max(np.abs(gb.detach().double().cpu().numpy() - ref_db) / (2e-2 * (np.abs(ref_db) + 20.0)))))
+    if worst > 1.0:
+        raise SystemExit(f"correctness gate failed (worst normalised error {worst:.3f})")
+    return worst
+
+
+def cpu_baseline(torch):
+    """The reference's backend="torch" CPU path (restated in oracle/torch_path.py) on the
+    same C2 problem, bf16 with fp32 partial accumulation; median of timed fwd+bwd runs."""
+    from oracle import torch_path
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    previous = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        x, w, b = make_inputs(torch, torch.bfloat16, "cpu")
+        x, w, b = (t.requires_grad_() for t in (x, w, b))
+
+        def run():
+            y = torch_path.torch_backend_conv(x, w, b, STRIDE, PADDING, DILATION, GROUPS)
+            torch.autograd.grad(y.float().square().mean(), (x, w, b))
+
+        start = time.perf_counter()
+        run()  # warmup
+        first = time.perf_counter() - start
+        iterations = max(3, min(50, int(10.0 / max(first, 1e-3))))
+        times = []
+        for _ in range(iterations):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        median = statistics.median(times)
+        return {
+            "value": round(3 * forward_flops() / median / 1e12, 6),
+            "unit": "TFLOP/s",
+            "cores": cores,
+            "kind": "port",
+            "sample": (
+                f"full C2 problem, fwd+bwd of y.float().square().mean(), bf16, median of "
+                f"{iterations} runs after 1 warmup ({median * 1e3:.0f} ms each); "
+                f"torch {torch.__version__}, {_cpu_model()}"
+            ),
+        }
+    finally:
+        torch.set_num_threads(previous)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.partition(":")[2].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: this build's hot path is a single-GPU kernel set "
+            f"(requested --gpus {args.gpus}); run with --gpus 1",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import torch_convnd
+    from torch_convnd import _build, _capi
+
+    if not (torch.cuda.is_available() and torch.version.hip is not None):
+        raise SystemExit("bench.py needs a ROCm GPU")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch_convnd.load_native()
+    lib = _build.hip_library()
+    device = torch.device("cuda", 0)
+    x, w, b = make_inputs(torch, torch.bfloat16, device)
+
+    def conv(xx, ww, bb):
+        return torch_convnd.conv_nd(xx, ww, bb, STRIDE, "same", DILATION, GROUPS, backend="native")
+
+    plans = _capi.plan_names(lib, X_SHAPE, W_SHAPE, STRIDE, PADDING, DILATION, GROUPS, torch.bfloat16)
+    gate = correctness_gate(torch, np, conv, x, w, b)
+
+    xs, ws, bs = (t.detach().requires_grad_() for t in (x, w, b))
+
+    def step():
+        y = conv(xs, ws, bs)
+        torch.autograd.grad(y.float().square().mean(), (xs, ws, bs))
+
+    def fwd_only():
+        with torch.no_grad():
+            conv(x, w, b)
+
+    for _ in range(args.warmup):
+        step()
+        fwd_only()
+    torch.cuda.synchronize()
+
+    # Forward alone (the metric's first half).
+    _capi.read_kernel_times(lib)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fwd_only()
+    torch.cuda.synchronize()
+    fwd_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Timed fwd+bwd steps, with every main kernel launch bracketed by HIP events.
+    lib.convnd_hip_timing_enable(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    lib.convnd_hip_timing_enable(0)
+    kernels = _capi.read_kernel_times(lib)
+
+    flops = forward_flops()
+    value = 3 * flops / (step_ms * 1e-3) / 1e12
+    fwd_tflops = flops / (fwd_ms * 1e-3) / 1e12
+    per_kernel = {}
+    for name, (total, count) in kernels.items():
+        if count:
+            avg_ms = total / count
+            per_kernel[name] = {
+                "avg_us": round(avg_ms * 1e3, 2),
+                "launches": count,
+                "tflops": round(flops / (avg_ms * 1e-3) / 1e12, 2),
+                "frac_bf16_peak": round(flops / (avg_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            }
+    dominant = max(per_kernel, key=lambda k: per_kernel[k]["avg_us"])
+    achieved = per_kernel[dominant]["tflops"]
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) input, U(+-1/sqrt(fan_in)) weight/bias)",
+        "config": {
+            "workload": "C2: Conv4d bf16 (fp32 accumulate) 32->64 k3 padding=same x[2,32,16,16,16,16], "
+            "forward + backward (dx, dW, db) of y.float().square().mean()",
+            "global_batch": X_SHAPE[0],
+            "forward_gflop": round(flops / 1e9, 3),
+            "parallelism": "single GPU",
+            "kernels": {"forward": plans[0], "grad_input": plans[1], "grad_weight": plans[2]},
+        },
+        "fwd_ms": round(fwd_ms, 4),
+        "fwd_tflops": round(fwd_tflops, 3),
+        "fwd_frac_bf16_peak": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),
+        "fwd_bwd_frac_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        "kernel_times": per_kernel,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dominant,
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "correctness_gate_worst": round(gate, 4),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

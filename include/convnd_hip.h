@@ -111,6 +111,16 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
 const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                                  int which);
 
+/* Diagnostic kernel timing, no reference counterpart. While enabled, each launch of the
+ * forward implicit GEMM (kernel id 0), the input-gradient implicit GEMM (id 1) and the MFMA
+ * weight-gradient kernel (id 2) is bracketed by HIP events recorded on the launch stream.
+ * Process-global (any thread); not for concurrent use. */
+int convnd_hip_timing_enable(int enable);
+
+/* After the launch streams have synchronised: total milliseconds and number of timed
+ * launches of kernel `kernel` since the previous read; clears that record. */
+int convnd_hip_timing_read(int kernel, double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

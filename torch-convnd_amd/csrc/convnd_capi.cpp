@@ -11,7 +11,9 @@
 #include <cstdint>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "convnd_internal.h"
@@ -232,7 +234,52 @@ struct IgemmPlan {
   size_t lds = 0;
   size_t wpk_elems = 0;
   size_t staged_elems = 0;  // channels-last copy of the GEMM's input operand
+  double cost = 0.0;
 };
+
+// Calls fn(b) for every power-of-two box b (b[a] <= limit[a]) whose volume is box_vol.
+template <typename F>
+void for_each_box(int R, const int* limit, int box_vol, F&& fn) {
+  std::vector<int> e(R, 0);
+  int b[kFastRank];
+  while (true) {
+    int prod = 1;
+    for (int a = 0; a < R; ++a) {
+      b[a] = 1 << e[a];
+      prod *= b[a];
+    }
+    bool valid = prod == box_vol;
+    for (int a = 0; a < R && valid; ++a) valid = b[a] <= limit[a];
+    if (valid) fn(b);
+    int a = R - 1;
+    for (; a >= 0; --a) {
+      if ((1 << (e[a] + 1)) <= limit[a] && (1 << (e[a] + 1)) <= box_vol) {
+        ++e[a];
+        break;
+      }
+      e[a] = 0;
+    }
+    if (a < 0) break;
+  }
+}
+
+// Workgroups resident per CU given their LDS use (at most two: the kernels are compiled
+// for two waves per SIMD).
+int occupancy(int64_t lds) {
+  const int64_t per_cu = 160 * 1024;
+  const int64_t fit = lds > 0 ? per_cu / lds : 2;
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(2, fit)));
+}
+
+// Relative time of `wgs` workgroups on 256 CUs, each needing `mfma_clk` of matrix work
+// and `load_clk` of LDS staging; a second resident workgroup overlaps its staging with
+// the other's MFMAs and hides latency (modelled as 85% vs 60% MFMA issue efficiency).
+double schedule_cost(int64_t wgs, int occ, double mfma_clk, double load_clk) {
+  const double eff = occ >= 2 ? 0.85 : 0.6;
+  const double mfma = mfma_clk / eff;
+  const double per_round = occ >= 2 ? std::max(occ * mfma, mfma + load_clk) : mfma + load_clk;
+  return double((wgs + 256 * occ - 1) / (256 * occ)) * per_round;
+}
 
 // mode 0: forward over x; mode 1: input gradient over grad_output.
 IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
@@ -275,7 +322,7 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
   const int mgroups = (mtiles + mb - 1) / mb;
   const int64_t es = 2;
 
-  // Channel chunk: the largest multiple of 8 dividing gemm_cin, at most 64.
+  // Channel chunk: multiples of 8 dividing gemm_cin, at most 64.
   std::vector<int> chunk_options;
   for (int cc = std::min(gemm_cin, 64); cc >= 8; cc -= 8)
     if (gemm_cin % cc == 0) chunk_options.push_back(cc);
@@ -284,102 +331,80 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
   for (int cc : chunk_options) {
     const int pstride = halo_pstride(cc);
     const int64_t kc = (ntaps_max * cc + 31) / 32;
-    const int64_t table_bytes = kc * 4 * 4;
+    const int64_t table_bytes = align_up(kc * 4 * 4);
+    const int64_t nchunk = gemm_cin / cc;
     for (int nb : {4, 2, 1}) {
       const int box_vol = 64 * nb;
-      // Enumerate power-of-two boxes with product box_vol.
-      int b[kFastRank];
       int limit[kFastRank];
       for (int a = 0; a < R; ++a) {
         int l = 1;
         while (l < J[a] && l < box_vol) l *= 2;
         limit[a] = l;
       }
-      // Odometer over the power-of-two exponents of each axis.
-      std::vector<int> e(R, 0);
-      while (true) {
-        int prod = 1;
+      for_each_box(R, limit, box_vol, [&](const int* b) {
+        int64_t hvol = 1, rows = 1, boxes = 1;
         for (int a = 0; a < R; ++a) {
-          b[a] = 1 << e[a];
-          prod *= b[a];
+          const int64_t h = (int64_t)(b[a] - 1) * sigma[a] + span[a] + 1;
+          hvol *= h;
+          if (a < R - 1) rows *= h;
+          boxes *= (J[a] + b[a] - 1) / b[a];
         }
-        bool valid = prod == box_vol;
-        for (int a = 0; a < R && valid; ++a) valid = b[a] <= limit[a];
-        if (valid) {
-          int64_t hvol = 1, boxes = 1;
-          for (int a = 0; a < R; ++a) {
-            hvol *= (int64_t)(b[a] - 1) * sigma[a] + span[a] + 1;
-            boxes *= (J[a] + b[a] - 1) / b[a];
-          }
-          const int64_t halo_bytes = hvol * pstride;
-          const bool grid_ok = boxes <= (int64_t{1} << 30) && g.groups * mgroups <= 65535 &&
-                               g.batch * nphase <= 65535;
-          if (halo_bytes + table_bytes <= kLdsBudget && grid_ok) {
-            const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
-            const int64_t nchunk = gemm_cin / cc;
-            const double mfma_clk = double(nchunk) * kc * mb * nb * 16.0;
-            const double load_clk = double(nchunk) * hvol * (cc * es) / 64.0;
-            const double waves_of_wgs = double((wgs + 255) / 256);
-            const double cost = waves_of_wgs * (mfma_clk + load_clk);
-            if (best < 0 || cost < best) {
-              best = cost;
-              plan.ok = true;
-              plan.mb = mb;
-              plan.nb = nb;
-              IgemmArgs& A = plan.args;
-              std::memset(&A, 0, sizeof(A));
-              A.rank = R;
-              A.mode = mode;
-              A.batch = static_cast<int>(g.batch);
-              A.groups = static_cast<int>(g.groups);
-              A.nphase = nphase;
-              A.cin_g = gemm_cin;
-              A.cout_g = gemm_cout;
-              A.cin_total = static_cast<int>(gemm_cin * g.groups);
-              A.cout_total = static_cast<int>(gemm_cout * g.groups);
-              A.wk_cin_g = static_cast<int>(g.cin_g);
-              A.wk_cout_g = static_cast<int>(g.cout_g);
-              A.cc = cc;
-              A.nchunk = static_cast<int>(nchunk);
-              A.kc_max = static_cast<int>(kc);
-              A.mtiles = mtiles;
-              A.mgroups = mgroups;
-              A.mtiles_padded = mgroups * mb;
-              A.pstride = pstride;
-              A.halo_bytes = static_cast<int>(align_up(halo_bytes));
-              int ivol = 1, ovol = 1;
-              for (int a = 0; a < R; ++a) {
-                A.in_size[a] = static_cast<int>(mode == 0 ? g.in[a] : g.out[a]);
-                A.out_size[a] = static_cast<int>(mode == 0 ? g.out[a] : g.in[a]);
-                ivol *= A.in_size[a];
-                ovol *= A.out_size[a];
-                A.box[a] = b[a];
-                A.nbox[a] = (J[a] + b[a] - 1) / b[a];
-                A.k[a] = static_cast<int>(g.k[a]);
-                A.s[a] = static_cast<int>(g.s[a]);
-                A.p[a] = static_cast<int>(g.p[a]);
-                A.d[a] = static_cast<int>(g.d[a]);
-              }
-              A.in_vol = ivol;
-              A.out_vol = ovol;
-              A.box_vol = box_vol;
-              A.boxes = static_cast<int>(boxes);
-              A.k_vol = static_cast<int>(g.k_vol);
-              plan.lds = A.halo_bytes + align_up(table_bytes);
-            }
-          }
+        const int64_t halo_bytes = align_up(hvol * pstride);
+        const int64_t lds = halo_bytes + table_bytes + align_up(rows * 4);
+        const bool grid_ok = boxes <= (int64_t{1} << 30) && g.groups * mgroups <= 65535 &&
+                             g.batch * nphase <= 65535;
+        if (lds > kLdsBudget || !grid_ok) return;
+        const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
+        const double mfma_clk = double(nchunk) * kc * mb * nb * 16.0;
+        const double load_clk = double(nchunk) * hvol * (cc * es) / 32.0;
+        const double cost = schedule_cost(wgs, occupancy(lds), mfma_clk, load_clk);
+        if (best >= 0 && cost >= best) return;
+        best = cost;
+        plan.ok = true;
+        plan.mb = mb;
+        plan.nb = nb;
+        plan.cost = cost;
+        IgemmArgs& A = plan.args;
+        std::memset(&A, 0, sizeof(A));
+        A.rank = R;
+        A.mode = mode;
+        A.batch = static_cast<int>(g.batch);
+        A.groups = static_cast<int>(g.groups);
+        A.nphase = nphase;
+        A.cin_g = gemm_cin;
+        A.cout_g = gemm_cout;
+        A.cin_total = static_cast<int>(gemm_cin * g.groups);
+        A.cout_total = static_cast<int>(gemm_cout * g.groups);
+        A.wk_cin_g = static_cast<int>(g.cin_g);
+        A.wk_cout_g = static_cast<int>(g.cout_g);
+        A.cc = cc;
+        A.nchunk = static_cast<int>(nchunk);
+        A.kc_max = static_cast<int>(kc);
+        A.mtiles = mtiles;
+        A.mgroups = mgroups;
+        A.mtiles_padded = mgroups * mb;
+        A.pstride = pstride;
+        A.halo_bytes = static_cast<int>(halo_bytes);
+        int ivol = 1, ovol = 1;
+        for (int a = 0; a < R; ++a) {
+          A.in_size[a] = static_cast<int>(mode == 0 ? g.in[a] : g.out[a]);
+          A.out_size[a] = static_cast<int>(mode == 0 ? g.out[a] : g.in[a]);
+          ivol *= A.in_size[a];
+          ovol *= A.out_size[a];
+          A.box[a] = b[a];
+          A.nbox[a] = (J[a] + b[a] - 1) / b[a];
+          A.k[a] = static_cast<int>(g.k[a]);
+          A.s[a] = static_cast<int>(g.s[a]);
+          A.p[a] = static_cast<int>(g.p[a]);
+          A.d[a] = static_cast<int>(g.d[a]);
         }
-        // next exponent vector
-        int a = R - 1;
-        for (; a >= 0; --a) {
-          if ((1 << (e[a] + 1)) <= limit[a] && (1 << (e[a] + 1)) <= box_vol) {
-            ++e[a];
-            break;
-          }
-          e[a] = 0;
-        }
-        if (a < 0) break;
-      }
+        A.in_vol = ivol;
+        A.out_vol = ovol;
+        A.box_vol = box_vol;
+        A.boxes = static_cast<int>(boxes);
+        A.k_vol = static_cast<int>(g.k_vol);
+        plan.lds = static_cast<size_t>(lds);
+      });
     }
   }
   if (plan.ok) {
@@ -399,7 +424,42 @@ struct WgradPlan {
   size_t lds = 0;
   size_t staged_elems = 0;
   size_t partial_elems = 0;
+  double cost = 0.0;
 };
+
+// Per workgroup column range (64 (tap, channel-octet) pairs), the bounding box of its taps:
+// returns the largest halo volume and row count over all workgroups for box b.
+void wgrad_halo_extent(const Geom& g, const int* b, int npairs, int octs, int64_t* hvol_max,
+                       int64_t* rows_max) {
+  const int R = g.rank;
+  *hvol_max = 0;
+  *rows_max = 0;
+  for (int p0 = 0; p0 < npairs; p0 += 64) {
+    const int p1 = std::min(p0 + 64, npairs);
+    int tmin[kFastRank], tmax[kFastRank];
+    for (int a = 0; a < R; ++a) {
+      tmin[a] = 1 << 30;
+      tmax[a] = -1;
+    }
+    for (int tt = p0 / octs; tt <= (p1 - 1) / octs; ++tt) {
+      int rem = tt;
+      for (int a = R - 1; a >= 0; --a) {
+        const int ta = rem % static_cast<int>(g.k[a]);
+        rem /= static_cast<int>(g.k[a]);
+        tmin[a] = std::min(tmin[a], ta);
+        tmax[a] = std::max(tmax[a], ta);
+      }
+    }
+    int64_t hvol = 1, rows = 1;
+    for (int a = 0; a < R; ++a) {
+      const int64_t h = (int64_t)(b[a] - 1) * g.s[a] + (tmax[a] - tmin[a]) * g.d[a] + 1;
+      hvol *= h;
+      if (a < R - 1) rows *= h;
+    }
+    *hvol_max = std::max(*hvol_max, hvol);
+    *rows_max = std::max(*rows_max, rows);
+  }
+}
 
 WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
   WgradPlan plan;
@@ -412,10 +472,12 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
   const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
   const int mgroups = (mtiles + mb - 1) / mb;
   const int pstride = halo_pstride(cin_g);
-  const int npairs = static_cast<int>(g.k_vol * (cin_g / 8));
+  const int octs = cin_g / 8;
+  const int npairs = static_cast<int>(g.k_vol * octs);
   const int ncg = (npairs + 15) / 16;
   const int ncq = (ncg + 3) / 4;
   if (ncq > 65535 || g.groups * mgroups > 65535) return plan;
+  const int out_last = static_cast<int>(g.out[R - 1]);
   double best = -1.0;
   for (int box_vol : {256, 128, 64, 32}) {
     const int dyrow = box_vol * 2 + 16;
@@ -425,98 +487,82 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       while (l < g.out[a] && l < box_vol) l *= 2;
       limit[a] = l;
     }
-    std::vector<int> e(R, 0);
-    while (true) {
-      int b[kFastRank];
-      int prod = 1;
+    for_each_box(R, limit, box_vol, [&](const int* b) {
+      int64_t hvol, rows;
+      wgrad_halo_extent(g, b, npairs, octs, &hvol, &rows);
+      int64_t boxes = 1;
+      for (int a = 0; a < R; ++a) boxes *= (g.out[a] + b[a] - 1) / b[a];
+      const int64_t box_rows = box_vol / b[R - 1];
+      const int64_t halo_bytes = align_up(hvol * pstride);
+      const int64_t lds = halo_bytes + align_up((int64_t)mb * 16 * dyrow) +
+                          align_up((box_vol + rows + box_rows) * 4);
+      if (lds > kLdsBudget) return;
+      const int occ = occupancy(lds);
+      const int64_t items = boxes * g.batch;
+      // Position chunks: enough workgroups to fill every CU once at this occupancy.
+      const int64_t per_chunk_wgs = (int64_t)ncq * g.groups * mgroups;
+      int64_t npc = std::max<int64_t>(1, (256 * occ + per_chunk_wgs - 1) / per_chunk_wgs);
+      npc = std::min<int64_t>(npc, items);
+      const int64_t ipc = (items + npc - 1) / npc;
+      npc = (items + ipc - 1) / ipc;
+      const double mfma_box = double(box_vol / 32) * 8 * mb * 16.0;
+      const double load_box = double(hvol) * cin_g * 2 / 32.0 + double(mb * 16) * box_vol * 2 / 32.0;
+      const int64_t wgs = npc * per_chunk_wgs;
+      // Partial sums: written once per chunk and read back by the reduction (8 TB/s ~
+      // 3.3 KB per clock at 2.4 GHz spread over the chip).
+      const double partial_clk = double(npc) * g.out_channels * cin_g * g.k_vol * 8 / 3300.0;
+      const double cost = schedule_cost(wgs, occ, ipc * mfma_box, ipc * load_box) + partial_clk;
+      if (best >= 0 && cost >= best) return;
+      best = cost;
+      plan.ok = true;
+      plan.mb = mb;
+      plan.cost = cost;
+      WgradArgs& A = plan.args;
+      std::memset(&A, 0, sizeof(A));
+      A.rank = R;
+      A.batch = static_cast<int>(g.batch);
+      A.groups = static_cast<int>(g.groups);
+      A.cin_g = cin_g;
+      A.cout_g = cout_g;
+      A.cin_total = static_cast<int>(g.channels);
+      A.cout_total = static_cast<int>(g.out_channels);
+      int ivol = 1, ovol = 1;
       for (int a = 0; a < R; ++a) {
-        b[a] = 1 << e[a];
-        prod *= b[a];
+        A.in_size[a] = static_cast<int>(g.in[a]);
+        A.out_size[a] = static_cast<int>(g.out[a]);
+        ivol *= A.in_size[a];
+        ovol *= A.out_size[a];
+        A.k[a] = static_cast<int>(g.k[a]);
+        A.s[a] = static_cast<int>(g.s[a]);
+        A.p[a] = static_cast<int>(g.p[a]);
+        A.d[a] = static_cast<int>(g.d[a]);
+        A.box[a] = b[a];
+        A.nbox[a] = static_cast<int>((g.out[a] + b[a] - 1) / b[a]);
       }
-      bool valid = prod == box_vol;
-      for (int a = 0; a < R && valid; ++a) valid = b[a] <= limit[a];
-      if (valid) {
-        int64_t hvol = 1, boxes = 1;
-        int halo[kFastRank];
-        for (int a = 0; a < R; ++a) {
-          halo[a] = static_cast<int>((b[a] - 1) * g.s[a] + (g.k[a] - 1) * g.d[a] + 1);
-          hvol *= halo[a];
-          boxes *= (g.out[a] + b[a] - 1) / b[a];
-        }
-        const int64_t halo_bytes = align_up(hvol * pstride);
-        const int64_t lds = halo_bytes + align_up((int64_t)mb * 16 * dyrow) + box_vol * 4;
-        if (lds <= kLdsBudget) {
-          const int64_t items = boxes * g.batch;
-          // Position chunks: about two workgroups per CU overall.
-          const int64_t per_chunk_wgs = ncq * g.groups * mgroups;
-          int64_t npc = std::max<int64_t>(1, (512 + per_chunk_wgs - 1) / per_chunk_wgs);
-          npc = std::min<int64_t>(npc, items);
-          const int64_t ipc = (items + npc - 1) / npc;
-          npc = (items + ipc - 1) / ipc;
-          const double per_box = double(box_vol / 32) * 8 * mb * 16.0 +
-                                 double(hvol) * cin_g * 2 / 64.0 +
-                                 double(mb * 16) * box_vol * 2 / 64.0;
-          const int64_t wgs = npc * per_chunk_wgs;
-          const double cost = double((wgs + 255) / 256) * ipc * per_box +
-                              double(npc) * g.out_channels * cin_g * g.k_vol * 8 / 4.0e3;
-          if (best < 0 || cost < best) {
-            best = cost;
-            plan.ok = true;
-            plan.mb = mb;
-            WgradArgs& A = plan.args;
-            std::memset(&A, 0, sizeof(A));
-            A.rank = R;
-            A.batch = static_cast<int>(g.batch);
-            A.groups = static_cast<int>(g.groups);
-            A.cin_g = cin_g;
-            A.cout_g = cout_g;
-            A.cin_total = static_cast<int>(g.channels);
-            A.cout_total = static_cast<int>(g.out_channels);
-            int ivol = 1, ovol = 1;
-            for (int a = 0; a < R; ++a) {
-              A.in_size[a] = static_cast<int>(g.in[a]);
-              A.out_size[a] = static_cast<int>(g.out[a]);
-              ivol *= A.in_size[a];
-              ovol *= A.out_size[a];
-              A.k[a] = static_cast<int>(g.k[a]);
-              A.s[a] = static_cast<int>(g.s[a]);
-              A.p[a] = static_cast<int>(g.p[a]);
-              A.d[a] = static_cast<int>(g.d[a]);
-              A.box[a] = b[a];
-              A.nbox[a] = static_cast<int>((g.out[a] + b[a] - 1) / b[a]);
-              A.halo[a] = halo[a];
-            }
-            A.in_vol = ivol;
-            A.out_vol = ovol;
-            A.k_vol = static_cast<int>(g.k_vol);
-            A.box_vol = box_vol;
-            A.boxes = static_cast<int>(boxes);
-            A.halo_vol = static_cast<int>(hvol);
-            A.pstride = pstride;
-            A.halo_bytes = static_cast<int>(halo_bytes);
-            A.dyrow = dyrow;
-            A.mtiles = mtiles;
-            A.mgroups = mgroups;
-            A.npairs = npairs;
-            A.ncg = ncg;
-            A.ncq = ncq;
-            A.npc = static_cast<int>(npc);
-            A.items = static_cast<int>(items);
-            A.items_per_pc = static_cast<int>(ipc);
-            plan.lds = static_cast<size_t>(lds);
-          }
-        }
-      }
-      int a = R - 1;
-      for (; a >= 0; --a) {
-        if ((1 << (e[a] + 1)) <= limit[a] && (1 << (e[a] + 1)) <= box_vol) {
-          ++e[a];
-          break;
-        }
-        e[a] = 0;
-      }
-      if (a < 0) break;
-    }
+      A.in_vol = ivol;
+      A.out_vol = ovol;
+      A.k_vol = static_cast<int>(g.k_vol);
+      A.box_vol = box_vol;
+      A.boxes = static_cast<int>(boxes);
+      A.pstride = pstride;
+      A.halo_bytes = static_cast<int>(halo_bytes);
+      A.max_rows = static_cast<int>(rows);
+      A.dyrow = dyrow;
+      // Widest load that keeps every run of the box's last axis aligned and either wholly
+      // inside or wholly outside the tensor.
+      int vec = 8;
+      while (vec > 1 && (b[R - 1] % vec != 0 || out_last % vec != 0)) vec /= 2;
+      A.dy_vec = vec;
+      A.mtiles = mtiles;
+      A.mgroups = mgroups;
+      A.npairs = npairs;
+      A.ncg = ncg;
+      A.ncq = ncq;
+      A.npc = static_cast<int>(npc);
+      A.items = static_cast<int>(items);
+      A.items_per_pc = static_cast<int>(ipc);
+      plan.lds = static_cast<size_t>(lds);
+    });
   }
   if (plan.ok) {
     plan.staged_elems = (size_t)g.batch * g.in_vol * g.channels;
@@ -584,6 +630,40 @@ BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool g
   if (gb) b.off_bias = L.take((size_t)g.out_channels * kBiasChunks * sizeof(double));
   b.bytes = L.total;
   return b;
+}
+
+// Diagnostic kernel timing (convnd_hip_timing_enable/read): event pairs recorded around
+// the main kernels. Process-global on purpose — autograd runs backward on its own thread.
+constexpr int kTimedKernels = 3;
+struct TimingState {
+  std::mutex lock;
+  bool enabled = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pairs[kTimedKernels];
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pool;
+};
+TimingState& timing() {
+  static TimingState state;
+  return state;
+}
+
+std::pair<hipEvent_t, hipEvent_t> timing_begin(int kernel, hipStream_t stream) {
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> guard(t.lock);
+  if (!t.enabled) return {nullptr, nullptr};
+  std::pair<hipEvent_t, hipEvent_t> ev{nullptr, nullptr};
+  if (!t.pool.empty()) {
+    ev = t.pool.back();
+    t.pool.pop_back();
+  } else if (hipEventCreate(&ev.first) != hipSuccess || hipEventCreate(&ev.second) != hipSuccess) {
+    return {nullptr, nullptr};
+  }
+  if (hipEventRecord(ev.first, stream) != hipSuccess) return {nullptr, nullptr};
+  t.pairs[kernel].push_back(ev);
+  return ev;
+}
+
+void timing_end(const std::pair<hipEvent_t, hipEvent_t>& ev, hipStream_t stream) {
+  if (ev.second != nullptr) (void)hipEventRecord(ev.second, stream);
 }
 
 int hip_check(hipError_t err, const char* what) {
@@ -691,8 +771,11 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   A.wpk = wpk;
   A.bias = bias;
   A.out = output;
-  return hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
-                   "implicit GEMM forward");
+  const auto ev = timing_begin(0, stream);
+  st = hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
+                 "implicit GEMM forward");
+  timing_end(ev, stream);
+  return st;
 }
 
 int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
@@ -749,8 +832,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       A.wpk = wpk;
       A.bias = nullptr;
       A.out = grad_input;
+      const auto ev = timing_begin(1, stream);
       st = hip_check(launch_igemm(dtype, b.dg.mb, b.dg.nb, A, b.dg.lds, stream),
                      "implicit GEMM input gradient");
+      timing_end(ev, stream);
     } else {
       st = hip_check(launch_direct_grad_input(dtype, to_direct(g), grad_output, weight,
                                               grad_input, stream),
@@ -770,8 +855,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       A.x = staged;
       A.dy = grad_output;
       A.partial = partial;
+      const auto ev = timing_begin(2, stream);
       st = hip_check(launch_wgrad_mfma(dtype, b.wg.mb, A, b.wg.lds, stream),
                      "MFMA weight gradient");
+      timing_end(ev, stream);
       if (st != CONVND_HIP_SUCCESS) return st;
       st = hip_check(launch_reduce_partials(dtype, partial, grad_weight,
                                             (int64_t)g.out_channels * g.cin_g * g.k_vol,
@@ -784,6 +871,34 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     }
     if (st != CONVND_HIP_SUCCESS) return st;
   }
+  return CONVND_HIP_SUCCESS;
+}
+
+int convnd_hip_timing_enable(int enable) {
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> guard(t.lock);
+  t.enabled = enable != 0;
+  return CONVND_HIP_SUCCESS;
+}
+
+int convnd_hip_timing_read(int kernel, double* total_ms, int64_t* launches) {
+  if (kernel < 0 || kernel >= kTimedKernels)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "kernel id must be 0, 1 or 2");
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> guard(t.lock);
+  double total = 0.0;
+  int64_t count = 0;
+  for (const auto& ev : t.pairs[kernel]) {
+    float ms = 0.f;
+    const hipError_t err = hipEventElapsedTime(&ms, ev.first, ev.second);
+    if (err != hipSuccess) return hip_check(err, "hipEventElapsedTime");
+    total += ms;
+    ++count;
+    t.pool.push_back(ev);
+  }
+  t.pairs[kernel].clear();
+  if (total_ms != nullptr) *total_ms = total;
+  if (launches != nullptr) *launches = count;
   return CONVND_HIP_SUCCESS;
 }
 

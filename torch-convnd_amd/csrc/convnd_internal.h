@@ -64,9 +64,10 @@ struct WgradArgs {
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int box[kFastRank], nbox[kFastRank];
   int box_vol, boxes;
-  int halo[kFastRank];
-  int halo_vol, pstride, halo_bytes;
-  int dyrow;          // LDS bytes per grad_output row of the box tile
+  int pstride, halo_bytes;   // LDS bytes per halo position / reserved for the halo
+  int max_rows;              // LDS ints reserved for halo row offsets
+  int dyrow;                 // LDS bytes per grad_output row of the box tile
+  int dy_vec;                // grad_output elements per vector load (8, 4, 2 or 1)
   int mtiles, mgroups;
   int npairs, ncg, ncq;
   int npc, items, items_per_pc;

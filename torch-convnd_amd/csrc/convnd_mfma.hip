@@ -100,6 +100,30 @@ __device__ __forceinline__ int axis_e(const IgemmArgs& A, int a, const AxisTaps&
   return A.mode == 0 ? tap * A.d[a] : (t.r + A.p[a] - tap * A.d[a]) / A.s[a];
 }
 
+// Stages rows of a box halo into LDS, channels-last with `pstride` bytes per position:
+// position (row r, column c) of the halo lands at (r*hlast + c)*pstride. `rowoff[r]` holds
+// the element offset (times the channel count) of the row's first column, or -1 when the
+// row lies outside the tensor; columns are bounds-checked against [0, last_size).
+template <typename T>
+__device__ __forceinline__ void stage_rows(unsigned char* lds, const int* rowoff, int rows,
+                                           int hlast, int corg, int last_size, int nch,
+                                           int pstride, const T* base, int cstride) {
+  const int per_row = hlast * nch;
+  const int items = rows * per_row;
+  for (int it = threadIdx.x; it < items; it += kThreads) {
+    const int r = it / per_row;
+    const int c = it - r * per_row;
+    const int col = c / nch;
+    const int ch = c - col * nch;
+    const int ro = rowoff[r];
+    const int cl = corg + col;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (ro >= 0 && cl >= 0 && cl < last_size)
+      v = *reinterpret_cast<const u32x4*>(base + (size_t)(ro + cl) * cstride + ch * 8);
+    *reinterpret_cast<u32x4*>(lds + (r * hlast + col) * pstride + ch * 16) = v;
+  }
+}
+
 template <typename T, int MB, int NB>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void igemm_kernel(IgemmArgs A) {
@@ -157,9 +181,21 @@ void igemm_kernel(IgemmArgs A) {
     }
   }
   const int KC = (ntaps * A.cc + 31) / 32;
+  int hlast = 1, corg = 0;
+#pragma unroll
+  for (int a = 0; a < kFastRank; ++a) {
+    if (a == R - 1) {
+      hlast = hext[a];
+      corg = horg[a];
+    }
+  }
+  const int rows = hvol / hlast;
+
+  // LDS: [halo | tap table (kc_max*4 ints) | halo row offsets (rows ints)].
+  int* tbl = reinterpret_cast<int*>(lds + A.halo_bytes);
+  int* rowoff = tbl + A.kc_max * 4;
 
   // Tap table: LDS byte offset of (tap, channel) for each K32 step and lane group.
-  int* tbl = reinterpret_cast<int*>(lds + A.halo_bytes);
   for (int idx = tid; idx < KC * 4; idx += kThreads) {
     const int kk = idx * 8;
     const int tau = kk / A.cc;
@@ -178,6 +214,23 @@ void igemm_kernel(IgemmArgs A) {
       off = off * A.pstride + ci * 2;
     }
     tbl[idx] = off;
+  }
+  // Row offsets of the halo (all axes but the last), in input positions.
+  for (int r = tid; r < rows; r += kThreads) {
+    int rem = r, flat = 0, istr = A.in_size[R - 1];
+    bool inb = true;
+#pragma unroll
+    for (int a = kFastRank - 2; a >= 0; --a) {
+      if (a < R - 1) {
+        const int h = rem % hext[a];
+        rem /= hext[a];
+        const int c = horg[a] + h;
+        inb = inb && c >= 0 && c < A.in_size[a];
+        flat += c * istr;
+        istr *= A.in_size[a];
+      }
+    }
+    rowoff[r] = inb ? n * A.in_vol + flat : -1;
   }
 
   // Per-lane position bases (LDS bytes) and output offsets for the NB blocks.
@@ -214,53 +267,64 @@ void igemm_kernel(IgemmArgs A) {
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nch = A.cc / 8;
+  const int lg = lane >> 4;
+  const size_t wstep = (size_t)A.mtiles_padded * 64;  // fragments per K32 step
   for (int ck = 0; ck < A.nchunk; ++ck) {
     __syncthreads();
-    // Stage the halo of this channel chunk, channels-last, zero outside the tensor.
-    const int items = hvol * nch;
-    for (int it = tid; it < items; it += kThreads) {
-      const int hp = it / nch;
-      const int ch = it - hp * nch;
-      int rem = hp, flat = 0, istr = 1;
-      bool inb = true;
-#pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int h = rem % hext[a];
-          rem /= hext[a];
-          const int c = horg[a] + h;
-          inb = inb && c >= 0 && c < A.in_size[a];
-          flat += c * istr;
-          istr *= A.in_size[a];
-        }
-      }
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (inb) {
-        v = *reinterpret_cast<const u32x4*>(
-            in + ((size_t)n * A.in_vol + flat) * A.cin_total + g * A.cin_g + ck * A.cc + ch * 8);
-      }
-      *reinterpret_cast<u32x4*>(lds + hp * A.pstride + ch * 16) = v;
-    }
+    stage_rows<T>(lds, rowoff, rows, hlast, corg, A.in_size[R - 1], nch, A.pstride,
+                  in + g * A.cin_g + ck * A.cc, A.cin_total);
     __syncthreads();
+    if (KC == 0) continue;
 
     const frag* wck = wp +
-                      ((size_t)((phase * A.groups + g) * A.nchunk + ck) * A.kc_max) *
-                          A.mtiles_padded * 64 +
+                      ((size_t)((phase * A.groups + g) * A.nchunk + ck) * A.kc_max) * wstep +
                       (size_t)(mg * MB) * 64 + lane;
-    const int lg = lane >> 4;
-#pragma unroll 2
-    for (int kc = 0; kc < KC; ++kc) {
-      const int toff = tbl[kc * 4 + lg];
-      frag a[MB], b[NB];
+    // Software pipeline: weights two K32 steps ahead (global, L2-resident), B fragments one
+    // step ahead and tap offsets two steps ahead (LDS), so neither latency stalls the MFMAs.
+    frag a0[MB], a1[MB], b0[NB], b1[NB];
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) a[mb] = wck[((size_t)kc * A.mtiles_padded + mb) * 64];
+    for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[mb * 64];
+    int t_next = tbl[lg];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        b[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + toff);
+    for (int nb = 0; nb < NB; ++nb)
+      b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t_next);
+    if (KC > 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[wstep + mb * 64];
+      t_next = tbl[4 + lg];
+    }
+    for (int kc = 0; kc < KC; kc += 2) {
+      // Even step kc: B for kc+1, tap offset for kc+2, then MFMAs on (a0, b0).
+      if (kc + 1 < KC) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          b1[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t_next);
+      }
+      const int t2 = kc + 2 < KC ? tbl[(kc + 2) * 4 + lg] : 0;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a[mb], b[nb], acc[mb][nb]);
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a0[mb], b0[nb], acc[mb][nb]);
+      if (kc + 2 < KC) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[(size_t)(kc + 2) * wstep + mb * 64];
+      }
+      if (kc + 1 >= KC) break;
+      // Odd step kc+1: B for kc+2, tap offset for kc+3, then MFMAs on (a1, b1).
+      if (kc + 2 < KC) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t2);
+      }
+      t_next = kc + 3 < KC ? tbl[(kc + 3) * 4 + lg] : 0;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a1[mb], b1[nb], acc[mb][nb]);
+      if (kc + 3 < KC) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[(size_t)(kc + 3) * wstep + mb * 64];
+      }
     }
   }
 
@@ -353,14 +417,63 @@ __device__ __forceinline__ unsigned hi_pair(unsigned a, unsigned b) {
   return (a >> 16) | (b & 0xffff0000u);
 }
 
+// Loads VEC consecutive 16-bit elements (VEC-aligned) into LDS.
+template <int VEC>
+__device__ __forceinline__ void copy16(unsigned char* dst, const unsigned char* src, bool ok) {
+  if constexpr (VEC == 8) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (ok) v = *reinterpret_cast<const u32x4*>(src);
+    *reinterpret_cast<u32x4*>(dst) = v;
+  } else if constexpr (VEC == 4) {
+    unsigned long long v = 0;
+    if (ok) v = *reinterpret_cast<const unsigned long long*>(src);
+    *reinterpret_cast<unsigned long long*>(dst) = v;
+  } else if constexpr (VEC == 2) {
+    unsigned v = 0;
+    if (ok) v = *reinterpret_cast<const unsigned*>(src);
+    *reinterpret_cast<unsigned*>(dst) = v;
+  } else {
+    unsigned short v = 0;
+    if (ok) v = *reinterpret_cast<const unsigned short*>(src);
+    *reinterpret_cast<unsigned short*>(dst) = v;
+  }
+}
+
+// grad_output box tile [rows channels][box positions] -> LDS, VEC elements per load.
+// `dyrowoff[r]` is the flat output offset of box row r's first position, or -1 outside.
+template <typename T, int VEC>
+__device__ __forceinline__ void stage_dy(unsigned char* dyt, const int* dyrowoff, int rows,
+                                         int box_rows, int blast, int j0last, int out_last,
+                                         const T* dy_base, int out_vol, int co_valid,
+                                         int dyrow) {
+  const int runs = blast / VEC;
+  const int per_ch = box_rows * runs;
+  const int items = rows * per_ch;
+  for (int it = threadIdx.x; it < items; it += kThreads) {
+    const int row = it / per_ch;
+    const int c = it - row * per_ch;
+    const int br = c / runs;
+    const int run = c - br * runs;
+    const int ro = dyrowoff[br];
+    const int col = j0last + run * VEC;
+    const bool ok = row < co_valid && ro >= 0 && col < out_last;
+    const T* src = dy_base + (size_t)row * out_vol + (ok ? ro + col : 0);
+    copy16<VEC>(dyt + row * dyrow + (br * blast + run * VEC) * 2,
+                reinterpret_cast<const unsigned char*>(src), ok);
+  }
+}
+
 template <typename T, int MB>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void wgrad_kernel(WgradArgs A) {
   using M = Mfma16<T>;
   using frag = typename M::frag;
   extern __shared__ __align__(16) unsigned char lds[];
+  // LDS: [halo | grad_output tile | posoff (box_vol) | halo rowoff | dY rowoff]
   unsigned char* dyt = lds + A.halo_bytes;
   int* posoff = reinterpret_cast<int*>(dyt + MB * 16 * A.dyrow);
+  int* rowoff = posoff + A.box_vol;
+  int* dyrowoff = rowoff + A.max_rows;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -376,17 +489,46 @@ void wgrad_kernel(WgradArgs A) {
   const int tap = pair_ok ? pair / octs : 0;
   const int oct = pair_ok ? pair - tap * octs : 0;
 
-  int hstr[kFastRank];
-  {
-    int hv = 1;
+  // Bounding box of this workgroup's taps (a contiguous range of flattened taps).
+  int tmin[kFastRank], tmax[kFastRank];
 #pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        hstr[a] = hv;
-        hv *= A.halo[a];
+  for (int a = 0; a < kFastRank; ++a) {
+    tmin[a] = 1 << 30;
+    tmax[a] = -1;
+  }
+  {
+    const int p0 = blockIdx.y * 64;
+    const int p1 = p0 + 64 < A.npairs ? p0 + 64 : A.npairs;
+    for (int tt = p0 / octs; tt <= (p1 - 1) / octs; ++tt) {
+      int rem = tt;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < R) {
+          const int ta = rem % A.k[a];
+          rem /= A.k[a];
+          tmin[a] = ta < tmin[a] ? ta : tmin[a];
+          tmax[a] = ta > tmax[a] ? ta : tmax[a];
+        }
       }
     }
   }
+  int hext[kFastRank], hstr[kFastRank];
+  int hvol = 1, hlast = 1, blast = 1, box_rows = 1;
+#pragma unroll
+  for (int a = kFastRank - 1; a >= 0; --a) {
+    if (a < R) {
+      hext[a] = (A.box[a] - 1) * A.s[a] + (tmax[a] - tmin[a]) * A.d[a] + 1;
+      hstr[a] = hvol;
+      hvol *= hext[a];
+      if (a == R - 1) {
+        hlast = hext[a];
+        blast = A.box[a];
+      } else {
+        box_rows *= A.box[a];
+      }
+    }
+  }
+  const int rows = hvol / hlast;
   int coloff = 0;
   {
     int rem = tap;
@@ -395,7 +537,7 @@ void wgrad_kernel(WgradArgs A) {
       if (a < R) {
         const int ta = rem % A.k[a];
         rem /= A.k[a];
-        coloff += ta * A.d[a] * hstr[a];
+        coloff += (ta - tmin[a]) * A.d[a] * hstr[a];
       }
     }
     coloff = coloff * A.pstride + oct * 16;
@@ -422,56 +564,49 @@ void wgrad_kernel(WgradArgs A) {
   const T* x = static_cast<const T*>(A.x);
   const T* dy = static_cast<const T*>(A.dy);
   const int nch = A.cin_g / 8;
+  const int co0 = mg * MB * 16;
+  const int co_valid = A.cout_g - co0;
   const int it0 = pc * A.items_per_pc;
   const int it1 = it0 + A.items_per_pc < A.items ? it0 + A.items_per_pc : A.items;
   for (int it = it0; it < it1; ++it) {
     const int n = it / A.boxes;
     int bb = it - n * A.boxes;
     int J0[kFastRank];
+    int j0last = 0, corg = 0;
 #pragma unroll
     for (int a = kFastRank - 1; a >= 0; --a) {
       if (a < R) {
         J0[a] = (bb % A.nbox[a]) * A.box[a];
         bb /= A.nbox[a];
+        if (a == R - 1) {
+          j0last = J0[a];
+          corg = J0[a] * A.s[a] - A.p[a] + tmin[a] * A.d[a];
+        }
       }
     }
     __syncthreads();
-    // Halo of the box (all taps), channels-last.
-    const int items = A.halo_vol * nch;
-    for (int i = tid; i < items; i += kThreads) {
-      const int hp = i / nch;
-      const int ch = i - hp * nch;
-      int rem = hp, flat = 0, istr = 1;
+    for (int r = tid; r < rows; r += kThreads) {
+      int rem = r, flat = 0, istr = A.in_size[R - 1];
       bool inb = true;
 #pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int h = rem % A.halo[a];
-          rem /= A.halo[a];
-          const int c = J0[a] * A.s[a] - A.p[a] + h;
+      for (int a = kFastRank - 2; a >= 0; --a) {
+        if (a < R - 1) {
+          const int h = rem % hext[a];
+          rem /= hext[a];
+          const int c = J0[a] * A.s[a] - A.p[a] + tmin[a] * A.d[a] + h;
           inb = inb && c >= 0 && c < A.in_size[a];
           flat += c * istr;
           istr *= A.in_size[a];
         }
       }
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (inb) {
-        v = *reinterpret_cast<const u32x4*>(
-            x + ((size_t)n * A.in_vol + flat) * A.cin_total + g * A.cin_g + ch * 8);
-      }
-      *reinterpret_cast<u32x4*>(lds + hp * A.pstride + ch * 16) = v;
+      rowoff[r] = inb ? n * A.in_vol + flat : -1;
     }
-    // grad_output tile [MB*16 channels][box positions], zero outside.
-    const int rows = MB * 16;
-    for (int i = tid; i < rows * A.box_vol; i += kThreads) {
-      const int row = i / A.box_vol;
-      const int q = i - row * A.box_vol;
-      const int co = (mg * MB) * 16 + row;
-      int rem = q, flat = 0, ostr = 1;
-      bool ok = co < A.cout_g;
+    for (int r = tid; r < box_rows; r += kThreads) {
+      int rem = r, flat = 0, ostr = A.out_size[R - 1];
+      bool ok = true;
 #pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
+      for (int a = kFastRank - 2; a >= 0; --a) {
+        if (a < R - 1) {
           const int qa = rem % A.box[a];
           rem /= A.box[a];
           const int ja = J0[a] + qa;
@@ -480,9 +615,29 @@ void wgrad_kernel(WgradArgs A) {
           ostr *= A.out_size[a];
         }
       }
-      T v = static_cast<T>(0.f);
-      if (ok) v = dy[((size_t)n * A.cout_total + g * A.cout_g + co) * A.out_vol + flat];
-      *reinterpret_cast<T*>(dyt + row * A.dyrow + q * 2) = v;
+      dyrowoff[r] = ok ? flat : -1;
+    }
+    __syncthreads();
+    stage_rows<T>(lds, rowoff, rows, hlast, corg, A.in_size[R - 1], nch, A.pstride,
+                  x + g * A.cin_g, A.cin_total);
+    const T* dy_base = dy + ((size_t)n * A.cout_total + g * A.cout_g + co0) * A.out_vol;
+    switch (A.dy_vec) {
+      case 8:
+        stage_dy<T, 8>(dyt, dyrowoff, MB * 16, box_rows, blast, j0last, A.out_size[R - 1],
+                       dy_base, A.out_vol, co_valid, A.dyrow);
+        break;
+      case 4:
+        stage_dy<T, 4>(dyt, dyrowoff, MB * 16, box_rows, blast, j0last, A.out_size[R - 1],
+                       dy_base, A.out_vol, co_valid, A.dyrow);
+        break;
+      case 2:
+        stage_dy<T, 2>(dyt, dyrowoff, MB * 16, box_rows, blast, j0last, A.out_size[R - 1],
+                       dy_base, A.out_vol, co_valid, A.dyrow);
+        break;
+      default:
+        stage_dy<T, 1>(dyt, dyrowoff, MB * 16, box_rows, blast, j0last, A.out_size[R - 1],
+                       dy_base, A.out_vol, co_valid, A.dyrow);
+        break;
     }
     __syncthreads();
 
@@ -517,7 +672,7 @@ void wgrad_kernel(WgradArgs A) {
     for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int co = (mg * MB + mb) * 16 + 4 * lg + i;
+        const int co = co0 + mb * 16 + 4 * lg + i;
         if (co < A.cout_g) {
           float* dst = A.partial +
                        (((size_t)pc * A.cout_total + g * A.cout_g + co) * A.cin_g + oct * 8) *

@@ -21,6 +21,8 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_backward_workspace_size",
     "convnd_hip_backward",
     "convnd_hip_plan_name",
+    "convnd_hip_timing_enable",
+    "convnd_hip_timing_read",
 )
 
 
@@ -71,7 +73,25 @@ def bind(library: ctypes.CDLL) -> ctypes.CDLL:
     library.convnd_hip_backward.argtypes = [P, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     library.convnd_hip_plan_name.restype = ctypes.c_char_p
     library.convnd_hip_plan_name.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    library.convnd_hip_timing_enable.restype = ctypes.c_int
+    library.convnd_hip_timing_enable.argtypes = [ctypes.c_int]
+    library.convnd_hip_timing_read.restype = ctypes.c_int
+    library.convnd_hip_timing_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)]
     return library
+
+
+KERNEL_IDS = {"forward_igemm": 0, "grad_input_igemm": 1, "grad_weight_mfma": 2}
+
+
+def read_kernel_times(library):
+    """{kernel name: (total ms, launches)} since the previous read (after a synchronize)."""
+    out = {}
+    for name, kid in KERNEL_IDS.items():
+        total, count = ctypes.c_double(), ctypes.c_int64()
+        if library.convnd_hip_timing_read(kid, ctypes.byref(total), ctypes.byref(count)) != SUCCESS:
+            raise RuntimeError(library.convnd_hip_last_error().decode())
+        out[name] = (total.value, count.value)
+    return out
 
 
 def dtype_code(dtype) -> int:
