@@ -111,6 +111,13 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
 const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                                  int which);
 
+/* JSON description of the launch plan (kernel family, box shape, channel chunk, LDS bytes,
+ * occupancy, workgroups) written to `buffer` (NUL-terminated, truncated to `length`).
+ * `which`: 0 forward, 1 input gradient, 2 weight gradient. Diagnostic only, no reference
+ * counterpart; touches no device. */
+int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                             int which, char* buffer, size_t length);
+
 /* Diagnostic kernel timing, no reference counterpart. While enabled, each launch of the
  * forward implicit GEMM (kernel id 0), the input-gradient implicit GEMM (id 1) and the MFMA
  * weight-gradient kernel (id 2) is bracketed by HIP events recorded on the launch stream.

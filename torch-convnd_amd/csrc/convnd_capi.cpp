@@ -13,6 +13,7 @@
 #include <limits>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -263,22 +264,36 @@ void for_each_box(int R, const int* limit, int box_vol, F&& fn) {
   }
 }
 
-// Workgroups resident per CU given their LDS use (at most two: the kernels are compiled
-// for two waves per SIMD).
-int occupancy(int64_t lds) {
+// Workgroups (of four waves) resident per CU: limited by LDS and by the kernel's register
+// budget in waves per SIMD (see igemm_waves / the wgrad kernel's attribute).
+int occupancy(int64_t lds, int reg_waves = 2) {
   const int64_t per_cu = 160 * 1024;
-  const int64_t fit = lds > 0 ? per_cu / lds : 2;
-  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(2, fit)));
+  const int64_t fit = lds > 0 ? per_cu / lds : reg_waves;
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(reg_waves, fit)));
 }
 
-// Relative time of `wgs` workgroups on 256 CUs, each needing `mfma_clk` of matrix work
-// and `load_clk` of LDS staging; a second resident workgroup overlaps its staging with
-// the other's MFMAs and hides latency (modelled as 85% vs 60% MFMA issue efficiency).
-double schedule_cost(int64_t wgs, int occ, double mfma_clk, double load_clk) {
+// Waves per SIMD the implicit-GEMM kernel is compiled for (igemm_waves in the kernel file).
+int igemm_reg_waves(int mb, int nb) { return mb * nb >= 32 ? 1 : 2; }
+
+// Relative time of `wgs` workgroups on 256 CUs, each needing `core_clk` of main-loop work
+// (MFMA issue, or operand bandwidth when that is the tighter bound) and `load_clk` of LDS
+// staging; a second resident workgroup overlaps its staging with the other's main loop
+// and hides latency (modelled as 85% vs 60% issue efficiency).
+double schedule_cost(int64_t wgs, int occ, double core_clk, double load_clk) {
   const double eff = occ >= 2 ? 0.85 : 0.6;
-  const double mfma = mfma_clk / eff;
-  const double per_round = occ >= 2 ? std::max(occ * mfma, mfma + load_clk) : mfma + load_clk;
+  const double core = core_clk / eff;
+  const double per_round = occ >= 2 ? std::max(occ * core, core + load_clk) : core + load_clk;
   return double((wgs + 256 * occ - 1) / (256 * occ)) * per_round;
+}
+
+// Clocks of one K32 step of a 4-wave workgroup whose waves each run mb x nb 16x16x32 MFMAs
+// (16 clocks each) fed by mb global fragments and nb LDS fragments of 1 KiB: the slowest of
+// MFMA issue, LDS bandwidth (128 B/clk/CU) and vector-L1 bandwidth (64 B/clk/CU).
+double igemm_step_clk(int mb, int nb) {
+  const double mfma = mb * nb * 16.0;
+  const double lds = 4.0 * nb * 1024 / 128.0;
+  const double l1 = 4.0 * mb * 1024 / 64.0;
+  return std::max(mfma, std::max(lds, l1));
 }
 
 // mode 0: forward over x; mode 1: input gradient over grad_output.
@@ -333,7 +348,7 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
     const int64_t kc = (ntaps_max * cc + 31) / 32;
     const int64_t table_bytes = align_up(kc * 4 * 4);
     const int64_t nchunk = gemm_cin / cc;
-    for (int nb : {4, 2, 1}) {
+    for (int nb : {8, 4, 2}) {
       const int box_vol = 64 * nb;
       int limit[kFastRank];
       for (int a = 0; a < R; ++a) {
@@ -355,9 +370,10 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
                              g.batch * nphase <= 65535;
         if (lds > kLdsBudget || !grid_ok) return;
         const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
-        const double mfma_clk = double(nchunk) * kc * mb * nb * 16.0;
+        const double core_clk = double(nchunk) * kc * igemm_step_clk(mb, nb);
         const double load_clk = double(nchunk) * hvol * (cc * es) / 32.0;
-        const double cost = schedule_cost(wgs, occupancy(lds), mfma_clk, load_clk);
+        const double cost =
+            schedule_cost(wgs, occupancy(lds, igemm_reg_waves(mb, nb)), core_clk, load_clk);
         if (best >= 0 && cost >= best) return;
         best = cost;
         plan.ok = true;
@@ -501,7 +517,7 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       const int64_t items = boxes * g.batch;
       // Position chunks: enough workgroups to fill every CU once at this occupancy.
       const int64_t per_chunk_wgs = (int64_t)ncq * g.groups * mgroups;
-      int64_t npc = std::max<int64_t>(1, (256 * occ + per_chunk_wgs - 1) / per_chunk_wgs);
+      int64_t npc = std::max<int64_t>(1, (256 * occ) / per_chunk_wgs);
       npc = std::min<int64_t>(npc, items);
       const int64_t ipc = (items + npc - 1) / npc;
       npc = (items + ipc - 1) / ipc;
@@ -589,7 +605,38 @@ struct ForwardSetup {
   size_t bytes = 0;
 };
 
-ForwardSetup setup_forward(const Geom& g, convnd_hip_dtype dt) {
+// Planning enumerates box shapes and channel chunks; callers repeat the same problem
+// every step, so plans are memoised per (geometry, dtype, request) in a bounded map.
+std::string plan_key(const Geom& g, convnd_hip_dtype dt, int kind) {
+  std::vector<int64_t> key = {g.rank, g.batch, g.channels, g.out_channels, g.groups,
+                              static_cast<int64_t>(dt), kind};
+  for (int a = 0; a < g.rank; ++a) {
+    key.insert(key.end(), {g.in[a], g.k[a], g.s[a], g.p[a], g.d[a]});
+  }
+  return std::string(reinterpret_cast<const char*>(key.data()), key.size() * sizeof(int64_t));
+}
+
+template <typename Setup>
+struct PlanCache {
+  std::mutex lock;
+  std::unordered_map<std::string, Setup> map;
+};
+
+template <typename Setup, typename Make>
+Setup cached_plan(PlanCache<Setup>& cache, const std::string& key, Make&& make) {
+  {
+    std::lock_guard<std::mutex> guard(cache.lock);
+    auto it = cache.map.find(key);
+    if (it != cache.map.end()) return it->second;
+  }
+  Setup setup = make();
+  std::lock_guard<std::mutex> guard(cache.lock);
+  if (cache.map.size() >= 512) cache.map.clear();
+  cache.map.emplace(key, setup);
+  return setup;
+}
+
+ForwardSetup make_forward(const Geom& g, convnd_hip_dtype dt) {
   ForwardSetup f;
   f.ig = plan_igemm(g, dt, 0);
   Layout L;
@@ -609,7 +656,12 @@ struct BackwardSetup {
   size_t bytes = 0;
 };
 
-BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw, bool gb) {
+ForwardSetup setup_forward(const Geom& g, convnd_hip_dtype dt) {
+  static PlanCache<ForwardSetup> cache;
+  return cached_plan(cache, plan_key(g, dt, 0), [&] { return make_forward(g, dt); });
+}
+
+BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw, bool gb) {
   BackwardSetup b;
   const int64_t es = element_size(dt);
   Layout L;
@@ -630,6 +682,12 @@ BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool g
   if (gb) b.off_bias = L.take((size_t)g.out_channels * kBiasChunks * sizeof(double));
   b.bytes = L.total;
   return b;
+}
+
+BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw, bool gb) {
+  static PlanCache<BackwardSetup> cache;
+  const int kind = 1 + (gi ? 1 : 0) + (gw ? 2 : 0) + (gb ? 4 : 0);
+  return cached_plan(cache, plan_key(g, dt, kind), [&] { return make_backward(g, dt, gi, gw, gb); });
 }
 
 // Diagnostic kernel timing (convnd_hip_timing_enable/read): event pairs recorded around
@@ -870,6 +928,61 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                      "direct weight-gradient kernel");
     }
     if (st != CONVND_HIP_SUCCESS) return st;
+  }
+  return CONVND_HIP_SUCCESS;
+}
+
+int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                             int which, char* buffer, size_t length) {
+  Geom g;
+  const int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  std::string text;
+  auto join = [](const int* v, int n) {
+    std::string out = "[";
+    for (int i = 0; i < n; ++i) out += (i ? "," : "") + std::to_string(v[i]);
+    return out + "]";
+  };
+  if (which == 0 || which == 1) {
+    const IgemmPlan p = plan_igemm(g, dtype, which);
+    if (!p.ok) {
+      text = "{\"kernel\":\"direct\"}";
+    } else {
+      const IgemmArgs& A = p.args;
+      text = "{\"kernel\":\"mfma_igemm\",\"mb\":" + std::to_string(p.mb) +
+             ",\"nb\":" + std::to_string(p.nb) + ",\"box\":" + join(A.box, A.rank) +
+             ",\"boxes\":" + std::to_string(A.boxes) + ",\"phases\":" +
+             std::to_string(A.nphase) + ",\"cc\":" + std::to_string(A.cc) +
+             ",\"nchunk\":" + std::to_string(A.nchunk) + ",\"kc_max\":" +
+             std::to_string(A.kc_max) + ",\"mgroups\":" + std::to_string(A.mgroups) +
+             ",\"lds\":" + std::to_string(p.lds) + ",\"occupancy\":" +
+             std::to_string(occupancy(static_cast<int64_t>(p.lds), igemm_reg_waves(p.mb, p.nb))) +
+             ",\"workgroups\":" +
+             std::to_string((int64_t)A.boxes * A.groups * A.mgroups * A.batch * A.nphase) + "}";
+    }
+  } else if (which == 2) {
+    const WgradPlan p = plan_wgrad(g, dtype);
+    if (!p.ok) {
+      text = "{\"kernel\":\"direct\"}";
+    } else {
+      const WgradArgs& A = p.args;
+      text = "{\"kernel\":\"mfma_wgrad\",\"mb\":" + std::to_string(p.mb) +
+             ",\"box\":" + join(A.box, A.rank) + ",\"boxes\":" + std::to_string(A.boxes) +
+             ",\"npc\":" + std::to_string(A.npc) + ",\"items_per_pc\":" +
+             std::to_string(A.items_per_pc) + ",\"ncq\":" + std::to_string(A.ncq) +
+             ",\"mgroups\":" + std::to_string(A.mgroups) + ",\"dy_vec\":" +
+             std::to_string(A.dy_vec) + ",\"lds\":" + std::to_string(p.lds) +
+             ",\"occupancy\":" + std::to_string(occupancy(static_cast<int64_t>(p.lds))) +
+             ",\"workgroups\":" +
+             std::to_string((int64_t)A.npc * A.ncq * A.groups * A.mgroups) + "}";
+    }
+  } else {
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "which must be 0, 1 or 2");
+  }
+  if (buffer != nullptr && length > 0) {
+    const size_t n = std::min(length - 1, text.size());
+    std::memcpy(buffer, text.data(), n);
+    buffer[n] = '\0';
   }
   return CONVND_HIP_SUCCESS;
 }

@@ -124,8 +124,15 @@ __device__ __forceinline__ void stage_rows(unsigned char* lds, const int* rowoff
   }
 }
 
+// Register budget: two waves per SIMD (256 VGPR+AGPR) except the 4x8 tile, which keeps
+// 128 accumulator registers and double-buffered fragments in one wave per SIMD. The
+// planner's occupancy model (igemm_waves_per_simd) must match.
+template <int MB, int NB>
+constexpr int igemm_waves = MB * NB >= 32 ? 1 : 2;
+
 template <typename T, int MB, int NB>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(igemm_waves<MB, NB>, igemm_waves<MB, NB>)))
 void igemm_kernel(IgemmArgs A) {
   using M = Mfma16<T>;
   using frag = typename M::frag;
@@ -234,28 +241,22 @@ void igemm_kernel(IgemmArgs A) {
   }
 
   // Per-lane position bases (LDS bytes) and output offsets for the NB blocks.
-  int pbase[NB], ooff[NB];
-  bool pvalid[NB];
+  // Per-lane LDS byte offsets of the NB position blocks (output offsets are recomputed in
+  // the epilogue so they do not hold registers through the main loop).
+  int pbase[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     int q = wave * NB * 16 + nb * 16 + (lane & 15);
-    int base = 0, oo = 0, ostr = 1;
-    bool ok = true;
+    int base = 0;
 #pragma unroll
     for (int a = kFastRank - 1; a >= 0; --a) {
       if (a < R) {
         const int qa = q % A.box[a];
         q /= A.box[a];
         base += qa * ax[a].sigma * hstr[a];
-        const int ja = J0[a] + qa;
-        ok = ok && ja < ax[a].J;
-        oo += (ax[a].r + ax[a].os * ja) * ostr;
-        ostr *= A.out_size[a];
       }
     }
     pbase[nb] = base * A.pstride;
-    ooff[nb] = oo;
-    pvalid[nb] = ok;
   }
 
   const T* in = static_cast<const T*>(A.in);
@@ -332,17 +333,33 @@ void igemm_kernel(IgemmArgs A) {
   T* out = static_cast<T*>(A.out);
   const T* bias = static_cast<const T*>(A.bias);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
+  for (int nb = 0; nb < NB; ++nb) {
+    int q = wave * NB * 16 + nb * 16 + (lane & 15);
+    int oo = 0, ostr = 1;
+    bool ok = true;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = (mg * MB + mb) * 16 + 4 * (lane >> 4) + i;
-      if (m < A.cout_g) {
-        const int oc = g * A.cout_g + m;
-        const float bv = bias != nullptr ? static_cast<float>(bias[oc]) : 0.f;
-        T* orow = out + ((size_t)n * A.cout_total + oc) * A.out_vol;
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
+        const int qa = q % A.box[a];
+        q /= A.box[a];
+        const int ja = J0[a] + qa;
+        ok = ok && ja < ax[a].J;
+        oo += (ax[a].r + ax[a].os * ja) * ostr;
+        ostr *= A.out_size[a];
+      }
+    }
+    if (!ok) continue;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          if (pvalid[nb]) orow[ooff[nb]] = static_cast<T>(acc[mb][nb][i] + bv);
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = (mg * MB + mb) * 16 + 4 * (lane >> 4) + i;
+        if (m < A.cout_g) {
+          const int oc = g * A.cout_g + m;
+          const float bv = bias != nullptr ? static_cast<float>(bias[oc]) : 0.f;
+          out[((size_t)n * A.cout_total + oc) * A.out_vol + oo] =
+              static_cast<T>(acc[mb][nb][i] + bv);
+        }
       }
     }
   }
@@ -464,7 +481,7 @@ __device__ __forceinline__ void stage_dy(unsigned char* dyt, const int* dyrowoff
 }
 
 template <typename T, int MB>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void wgrad_kernel(WgradArgs A) {
   using M = Mfma16<T>;
   using frag = typename M::frag;
@@ -648,21 +665,30 @@ void wgrad_kernel(WgradArgs A) {
       for (int mb = 0; mb < MB; ++mb)
         a[mb] = *reinterpret_cast<const frag*>(dyt + (mb * 16 + nl) * A.dyrow + q0 * 2);
       const int* po = posoff + q0;
-      u32x4 v[8];
+      int offs[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4*>(lds + po[i] + coloff);
+      for (int i = 0; i < 8; ++i) offs[i] = po[i] + coloff;
+      // Two halves of four channels: 8 positions x 4 channels (8 bytes each) per read, then
+      // an in-register transpose into four B fragments (8 positions of one channel each).
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        u32x4 t;
+      for (int half = 0; half < 2; ++half) {
+        uint2 v[8];
 #pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2) {
-          const unsigned lo = v[2 * w2][u >> 1];
-          const unsigned hi = v[2 * w2 + 1][u >> 1];
-          t[w2] = (u & 1) ? hi_pair(lo, hi) : lo_pair(lo, hi);
+        for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint2*>(lds + offs[i] + half * 8);
+#pragma unroll
+        for (int uu = 0; uu < 4; ++uu) {
+          u32x4 t;
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) {
+            const unsigned lo = (uu >> 1) ? v[2 * w2].y : v[2 * w2].x;
+            const unsigned hi = (uu >> 1) ? v[2 * w2 + 1].y : v[2 * w2 + 1].x;
+            t[w2] = (uu & 1) ? hi_pair(lo, hi) : lo_pair(lo, hi);
+          }
+          const frag b = __builtin_bit_cast(frag, t);
+          const int u = half * 4 + uu;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[mb][u] = M::run(a[mb], b, acc[mb][u]);
         }
-        const frag b = __builtin_bit_cast(frag, t);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb][u] = M::run(a[mb], b, acc[mb][u]);
       }
     }
   }
@@ -699,15 +725,15 @@ hipError_t igemm_dispatch(int mb, int nb, const IgemmArgs& a, size_t lds, hipStr
     hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                             \
     return hipGetLastError();                                                            \
   }
-  CONVND_IGEMM_CASE(1, 1)
   CONVND_IGEMM_CASE(1, 2)
   CONVND_IGEMM_CASE(1, 4)
-  CONVND_IGEMM_CASE(2, 1)
+  CONVND_IGEMM_CASE(1, 8)
   CONVND_IGEMM_CASE(2, 2)
   CONVND_IGEMM_CASE(2, 4)
-  CONVND_IGEMM_CASE(4, 1)
+  CONVND_IGEMM_CASE(2, 8)
   CONVND_IGEMM_CASE(4, 2)
   CONVND_IGEMM_CASE(4, 4)
+  CONVND_IGEMM_CASE(4, 8)
 #undef CONVND_IGEMM_CASE
   return hipErrorInvalidValue;
 }

@@ -21,6 +21,7 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_backward_workspace_size",
     "convnd_hip_backward",
     "convnd_hip_plan_name",
+    "convnd_hip_plan_describe",
     "convnd_hip_timing_enable",
     "convnd_hip_timing_read",
 )
@@ -73,6 +74,8 @@ def bind(library: ctypes.CDLL) -> ctypes.CDLL:
     library.convnd_hip_backward.argtypes = [P, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     library.convnd_hip_plan_name.restype = ctypes.c_char_p
     library.convnd_hip_plan_name.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    library.convnd_hip_plan_describe.restype = ctypes.c_int
+    library.convnd_hip_plan_describe.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_char_p, sz]
     library.convnd_hip_timing_enable.restype = ctypes.c_int
     library.convnd_hip_timing_enable.argtypes = [ctypes.c_int]
     library.convnd_hip_timing_read.restype = ctypes.c_int
@@ -106,3 +109,18 @@ def plan_names(library, x_shape, w_shape, stride, padding, dilation, groups, dty
     p = Problem.make(x_shape, w_shape, stride, padding, dilation, groups)
     code = dtype_code(dtype)
     return tuple(library.convnd_hip_plan_name(ctypes.byref(p), code, which).decode() for which in range(3))
+
+
+def plan_details(library, x_shape, w_shape, stride, padding, dilation, groups, dtype):
+    """Launch plans (forward, input gradient, weight gradient) as dicts."""
+    import json
+
+    p = Problem.make(x_shape, w_shape, stride, padding, dilation, groups)
+    code = dtype_code(dtype)
+    out = []
+    for which in range(3):
+        buffer = ctypes.create_string_buffer(1024)
+        if library.convnd_hip_plan_describe(ctypes.byref(p), code, which, buffer, len(buffer)) != SUCCESS:
+            raise RuntimeError(library.convnd_hip_last_error().decode())
+        out.append(json.loads(buffer.value.decode()))
+    return tuple(out)
