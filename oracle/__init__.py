@@ -49,6 +49,12 @@ def build() -> Path:
     return _LIBRARY_PATH
 
 
+def build_reference() -> Path:
+    """Compile the reference's CPU driver from its sources into oracle/_ref (``make ref``)."""
+    subprocess.run(["make", "-s", "-C", str(_HERE), "ref"], check=True)
+    return _HERE / "_ref" / "libref_convnd_cpu.so"
+
+
 def _library():
     global _LIB
     if _LIB is None:
