@@ -8,9 +8,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstdint>
 #include <cstring>
 #include <limits>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -235,6 +237,7 @@ struct IgemmPlan {
   size_t lds = 0;
   size_t wpk_elems = 0;
   size_t staged_elems = 0;  // channels-last copy of the GEMM's input operand
+  int conflict = 1;         // lanes per 16-byte bank slot in a B-fragment read (1 = none)
   double cost = 0.0;
 };
 
@@ -265,7 +268,7 @@ void for_each_box(int R, const int* limit, int box_vol, F&& fn) {
 }
 
 // Workgroups (of four waves) resident per CU: limited by LDS and by the kernel's register
-// budget in waves per SIMD (see igemm_waves / the wgrad kernel's attribute).
+// budget in waves per SIMD (igemm_waves / the wgrad kernel's attribute).
 int occupancy(int64_t lds, int reg_waves = 2) {
   const int64_t per_cu = 160 * 1024;
   const int64_t fit = lds > 0 ? per_cu / lds : reg_waves;
@@ -275,25 +278,121 @@ int occupancy(int64_t lds, int reg_waves = 2) {
 // Waves per SIMD the implicit-GEMM kernel is compiled for (igemm_waves in the kernel file).
 int igemm_reg_waves(int mb, int nb) { return mb * nb >= 32 ? 1 : 2; }
 
-// Relative time of `wgs` workgroups on 256 CUs, each needing `core_clk` of main-loop work
-// (MFMA issue, or operand bandwidth when that is the tighter bound) and `load_clk` of LDS
-// staging; a second resident workgroup overlaps its staging with the other's main loop
-// and hides latency (modelled as 85% vs 60% issue efficiency).
-double schedule_cost(int64_t wgs, int occ, double core_clk, double load_clk) {
-  const double eff = occ >= 2 ? 0.85 : 0.6;
-  const double core = core_clk / eff;
-  const double per_round = occ >= 2 ? std::max(occ * core, core + load_clk) : core + load_clk;
-  return double((wgs + 256 * occ - 1) / (256 * occ)) * per_round;
+// gfx950 serves a wave-wide 16-byte LDS read in four cycles of sixteen lanes; the lanes of
+// one 16-position block of a B fragment (one k-group) must hit distinct 16-byte slots of
+// the 256-byte bank row. Returns the worst number of lanes sharing a slot over the blocks.
+int block_conflict(int R, const int* box, const int* sigma, const int* hpitch, int box_vol) {
+  int worst = 1;
+  for (int b0 = 0; b0 < box_vol; b0 += 16) {
+    int count[16] = {0};
+    for (int nl = 0; nl < 16; ++nl) {
+      int q = b0 + nl, off = 0;
+      for (int a = R - 1; a >= 0; --a) {
+        const int qa = q % box[a];
+        q /= box[a];
+        off += qa * sigma[a] * hpitch[a];
+      }
+      worst = std::max(worst, ++count[off & 15]);
+    }
+  }
+  return worst;
 }
 
-// Clocks of one K32 step of a 4-wave workgroup whose waves each run mb x nb 16x16x32 MFMAs
-// (16 clocks each) fed by mb global fragments and nb LDS fragments of 1 KiB: the slowest of
-// MFMA issue, LDS bandwidth (128 B/clk/CU) and vector-L1 bandwidth (64 B/clk/CU).
-double igemm_step_clk(int mb, int nb) {
-  const double mfma = mb * nb * 16.0;
-  const double lds = 4.0 * nb * 1024 / 128.0;
-  const double l1 = 4.0 * mb * 1024 / 64.0;
-  return std::max(mfma, std::max(lds, l1));
+// Halo pitches: hpitch[R-1] = 1 and hpitch[a] = hpitch[a+1] * padded extent of axis a+1.
+// The two innermost padded extents are searched (0..15 extra positions each), smallest plane
+// first, for the first layout without bank conflicts (else the fewest). Returns the plane
+// size in positions.
+int64_t choose_pitches(int R, const int* box, const int* sigma, const int* hext, int box_vol,
+                       int* hpitch, int* conflict) {
+  struct Candidate {
+    int64_t size;
+    int p1, p2;
+  };
+  std::vector<Candidate> cands;
+  const int pad_last_max = R >= 2 ? 15 : 0;
+  const int pad_mid_max = R >= 3 ? 15 : 0;
+  auto pitches = [&](int p1, int p2, int* pitch) {
+    pitch[R - 1] = 1;
+    for (int a = R - 2; a >= 0; --a) {
+      int ext = hext[a + 1];
+      if (a + 1 == R - 1) ext += p1;
+      if (a + 1 == R - 2) ext += p2;
+      pitch[a] = pitch[a + 1] * ext;
+    }
+    return (int64_t)pitch[0] * hext[0];
+  };
+  for (int p1 = 0; p1 <= pad_last_max; ++p1)
+    for (int p2 = 0; p2 <= pad_mid_max; ++p2) {
+      int pitch[kFastRank];
+      cands.push_back({pitches(p1, p2, pitch), p1, p2});
+    }
+  std::stable_sort(cands.begin(), cands.end(),
+                   [](const Candidate& x, const Candidate& y) { return x.size < y.size; });
+  int best_conf = 1 << 30;
+  int64_t best_size = 0;
+  for (const Candidate& c : cands) {
+    int pitch[kFastRank];
+    pitches(c.p1, c.p2, pitch);
+    const int conf = block_conflict(R, box, sigma, pitch, box_vol);
+    if (conf < best_conf) {
+      best_conf = conf;
+      best_size = c.size;
+      std::copy(pitch, pitch + R, hpitch);
+      if (conf == 1) break;
+    }
+  }
+  *conflict = best_conf;
+  return best_size;
+}
+
+// Optional launch-plan override for tuning sweeps, read once per process from
+// CONVND_HIP_FWD_PLAN / CONVND_HIP_DGRAD_PLAN, e.g. "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8".
+// Any subset of the keys may be given; the planner then searches only plans matching it and
+// ignores the override when none does.
+struct PlanFilter {
+  int mb = 0, nb = 0, wm = 0, cc = 0;
+  std::vector<int> box;
+  bool active = false;
+};
+
+PlanFilter parse_filter(const char* text) {
+  PlanFilter f;
+  if (text == nullptr || *text == '\0') return f;
+  f.active = true;
+  std::string s(text);
+  size_t pos = 0;
+  while (pos < s.size()) {
+    size_t end = s.find(',', pos);
+    if (end == std::string::npos) end = s.size();
+    const std::string item = s.substr(pos, end - pos);
+    const size_t eq = item.find('=');
+    if (eq != std::string::npos) {
+      const std::string key = item.substr(0, eq), val = item.substr(eq + 1);
+      if (key == "box") {
+        size_t p = 0;
+        while (p < val.size()) {
+          size_t x = val.find('x', p);
+          if (x == std::string::npos) x = val.size();
+          f.box.push_back(std::atoi(val.substr(p, x - p).c_str()));
+          p = x + 1;
+        }
+      } else {
+        const int v = std::atoi(val.c_str());
+        if (key == "mb") f.mb = v;
+        if (key == "nb") f.nb = v;
+        if (key == "wm") f.wm = v;
+        if (key == "cc") f.cc = v;
+      }
+    }
+    pos = end + 1;
+  }
+  return f;
+}
+
+const PlanFilter& plan_filter(int mode) {
+  static const PlanFilter fwd = parse_filter(std::getenv("CONVND_HIP_FWD_PLAN"));
+  static const PlanFilter dgrad = parse_filter(std::getenv("CONVND_HIP_DGRAD_PLAN"));
+  return mode == 0 ? fwd : dgrad;
 }
 
 // mode 0: forward over x; mode 1: input gradient over grad_output.
@@ -333,23 +432,42 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
     }
   }
   const int mtiles = (gemm_cout + 15) / 16;
-  const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
-  const int mgroups = (mtiles + mb - 1) / mb;
-  const int64_t es = 2;
+  const PlanFilter& filter = plan_filter(mode);
 
-  // Channel chunk: multiples of 8 dividing gemm_cin, at most 64.
+  // Channel chunk: 8, 16, 32 or 64 channels dividing gemm_cin (octet planes per chunk are
+  // a power of two).
   std::vector<int> chunk_options;
-  for (int cc = std::min(gemm_cin, 64); cc >= 8; cc -= 8)
-    if (gemm_cin % cc == 0) chunk_options.push_back(cc);
+  for (int cc = 64; cc >= 8; cc /= 2)
+    if (cc <= gemm_cin && gemm_cin % cc == 0) chunk_options.push_back(cc);
 
+  static const int kTiles[][3] = {{1, 2, 1}, {1, 4, 1}, {1, 8, 1}, {2, 2, 1}, {2, 4, 1},
+                                  {2, 8, 1}, {4, 2, 1}, {4, 4, 1}, {4, 8, 1}, {1, 4, 2},
+                                  {1, 8, 2}, {2, 4, 2}, {2, 8, 2}, {1, 4, 4}, {1, 8, 4}};
+  struct PitchMemo {
+    int hpitch[kFastRank];
+    int conflict;
+    int64_t plane_pos;
+  };
+  std::map<std::vector<int>, PitchMemo> pitch_memo;
   double best = -1.0;
-  for (int cc : chunk_options) {
-    const int pstride = halo_pstride(cc);
-    const int64_t kc = (ntaps_max * cc + 31) / 32;
-    const int64_t table_bytes = align_up(kc * 4 * 4);
-    const int64_t nchunk = gemm_cin / cc;
-    for (int nb : {8, 4, 2}) {
-      const int box_vol = 64 * nb;
+  for (const auto& tile : kTiles) {
+    const int mb = tile[0], nb = tile[1], wm = tile[2], wn = 4 / wm;
+    if (!igemm_tile_supported(mb, nb, wm)) continue;
+    // Cover the output channels without idle waves: the waves' M extent may exceed the
+    // channel count by less than one wave's share.
+    if ((wm - 1) * mb >= mtiles || (mb > 1 && (mb / 2) >= mtiles)) continue;
+    if ((filter.mb && filter.mb != mb) || (filter.nb && filter.nb != nb) ||
+        (filter.wm && filter.wm != wm))
+      continue;
+    const int mgroups = (mtiles + wm * mb - 1) / (wm * mb);
+    const int box_vol = wn * nb * 16;
+    const int reg_waves = igemm_reg_waves(mb, nb);
+    for (int cc : chunk_options) {
+      if (filter.cc && filter.cc != cc) continue;
+      const int noct = cc / 8;
+      const int64_t kc = (ntaps_max * cc + 31) / 32;
+      const int64_t table_bytes = align_up(kc * 4 * 4);
+      const int64_t nchunk = gemm_cin / cc;
       int limit[kFastRank];
       for (int a = 0; a < R; ++a) {
         int l = 1;
@@ -357,29 +475,90 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         limit[a] = l;
       }
       for_each_box(R, limit, box_vol, [&](const int* b) {
-        int64_t hvol = 1, rows = 1, boxes = 1;
-        for (int a = 0; a < R; ++a) {
-          const int64_t h = (int64_t)(b[a] - 1) * sigma[a] + span[a] + 1;
-          hvol *= h;
-          if (a < R - 1) rows *= h;
-          boxes *= (J[a] + b[a] - 1) / b[a];
+        if (!filter.box.empty()) {
+          if (static_cast<int>(filter.box.size()) != R) return;
+          for (int a = 0; a < R; ++a)
+            if (filter.box[a] != b[a]) return;
         }
-        const int64_t halo_bytes = align_up(hvol * pstride);
-        const int64_t lds = halo_bytes + table_bytes + align_up(rows * 4);
+        int hext[kFastRank], hpitch[kFastRank];
+        int64_t hvol = 1, rows = 1, boxes = 1, useful = 1;
+        for (int a = 0; a < R; ++a) {
+          hext[a] = (b[a] - 1) * sigma[a] + span[a] + 1;
+          hvol *= hext[a];
+          if (a < R - 1) rows *= hext[a];
+          boxes *= (J[a] + b[a] - 1) / b[a];
+          useful *= J[a];
+        }
+        if (noct * hvol * 16 + table_bytes > kLdsBudget) return;
+        // Row validity masks hold 64 halo coordinates per axis; coordinates are packed in
+        // bytes in the row table.
+        for (int a = 0; a < R; ++a)
+          if ((a < R - 1 && hext[a] > 64) || hext[a] > 255) return;
+        int conflict = 1;
+        // The pitches depend on the box alone (not on the tile or the chunk): memoised.
+        std::vector<int> key(b, b + R);
+        auto hit = pitch_memo.find(key);
+        if (hit == pitch_memo.end()) {
+          PitchMemo m;
+          m.plane_pos = choose_pitches(R, b, sigma, hext, box_vol, m.hpitch, &m.conflict);
+          hit = pitch_memo.emplace(key, m).first;
+        }
+        std::copy(hit->second.hpitch, hit->second.hpitch + R, hpitch);
+        conflict = hit->second.conflict;
+        const int64_t plane_pos = hit->second.plane_pos;
+        const int64_t plane_bytes = align_up(plane_pos * 16);
+        // The epilogue reuses the LDS as a [channels][box positions] tile of 16-bit values.
+        const int64_t tile_bytes = (int64_t)wm * mb * 16 * (box_vol + 8) * 2;
+        const int64_t lds =
+            std::max(noct * plane_bytes + table_bytes + align_up(rows * 8), align_up(tile_bytes));
+        if (rows > (int64_t{1} << 20)) return;
+        // Output positions written per store: consecutive along the last axis (stride 1 in
+        // the output unless an input-gradient phase steps by the stride).
+        int out_vec = 1;
+        {
+          const int out_last = static_cast<int>(mode == 0 ? g.out[R - 1] : g.in[R - 1]);
+          const bool unit_step = mode == 0 || g.s[R - 1] == 1;
+          if (unit_step)
+            for (int v = 8; v > 1; v /= 2)
+              if (b[R - 1] % v == 0 && out_last % v == 0) {
+                out_vec = v;
+                break;
+              }
+        }
         const bool grid_ok = boxes <= (int64_t{1} << 30) && g.groups * mgroups <= 65535 &&
                              g.batch * nphase <= 65535;
         if (lds > kLdsBudget || !grid_ok) return;
+        const int occ = occupancy(lds, reg_waves);
+        // Clocks per K32 step of one workgroup: MFMA issue on each SIMD, B-fragment LDS
+        // reads (4 cycles per wave read when conflict-free; cc == 8 puts four taps of one
+        // plane in a K32 step, which costs a second cycle), A-fragment reads through the
+        // vector L1 (about 64 bytes per clock per CU).
+        const int lds_factor = std::max(conflict, noct == 1 ? 2 : 1);
+        const double mfma = mb * nb * 16.0;
+        const double ldsc = 4.0 * nb * 4.0 * lds_factor;
+        const double l1 = 4.0 * mb * 1024.0 / 64.0;
+        const double step = std::max(mfma * occ, std::max(ldsc, l1) * occ) / occ;
+        const double eff = occ >= 2 ? 0.75 : 0.55;
+        const double core = double(nchunk) * kc * step / eff;
+        const double stage = double(nchunk) * (noct * hvol * 16.0 / 64.0 + 1500.0);
+        // Epilogue: output bytes of the box at 16 bytes per lane-store when out_vec == 8,
+        // proportionally fewer useful bytes per store for shorter runs.
+        const double out_bytes = double(wm) * mb * 16 * box_vol * 2;
+        const double epilogue = out_bytes / (4.0 * out_vec) + 800.0;
+        const double per_wg = core + (occ >= 2 ? 0.25 : 1.0) * stage + epilogue;
         const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
-        const double core_clk = double(nchunk) * kc * igemm_step_clk(mb, nb);
-        const double load_clk = double(nchunk) * hvol * (cc * es) / 32.0;
-        const double cost =
-            schedule_cost(wgs, occupancy(lds, igemm_reg_waves(mb, nb)), core_clk, load_clk);
+        const int64_t slots = 256 * occ;
+        const double rounds = double((wgs + slots - 1) / slots);
+        // Work in padded boxes beyond the tensor is paid for as well (included via boxes).
+        const double cost = rounds * per_wg * (occ >= 2 ? 1.0 : 1.0);
+        (void)useful;
         if (best >= 0 && cost >= best) return;
         best = cost;
         plan.ok = true;
         plan.mb = mb;
         plan.nb = nb;
         plan.cost = cost;
+        plan.conflict = conflict;
         IgemmArgs& A = plan.args;
         std::memset(&A, 0, sizeof(A));
         A.rank = R;
@@ -394,15 +573,24 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.wk_cin_g = static_cast<int>(g.cin_g);
         A.wk_cout_g = static_cast<int>(g.cout_g);
         A.cc = cc;
+        A.noct = noct;
+        A.log2_noct = noct == 8 ? 3 : noct == 4 ? 2 : noct == 2 ? 1 : 0;
+        A.rows = static_cast<int>(rows);
+        A.hlast = hext[R - 1];
         A.nchunk = static_cast<int>(nchunk);
         A.kc_max = static_cast<int>(kc);
+        A.wm = wm;
         A.mtiles = mtiles;
         A.mgroups = mgroups;
-        A.mtiles_padded = mgroups * mb;
-        A.pstride = pstride;
-        A.halo_bytes = static_cast<int>(halo_bytes);
+        A.mtiles_padded = mgroups * wm * mb;
+        A.plane_bytes = static_cast<int>(plane_bytes);
+        A.halo_bytes = static_cast<int>(noct * plane_bytes);
         int ivol = 1, ovol = 1;
         for (int a = 0; a < R; ++a) {
+          A.hpitch[a] = hpitch[a];
+          A.hext[a] = hext[a];
+          A.box_shift[a] = 0;
+          while ((1 << A.box_shift[a]) < b[a]) ++A.box_shift[a];
           A.in_size[a] = static_cast<int>(mode == 0 ? g.in[a] : g.out[a]);
           A.out_size[a] = static_cast<int>(mode == 0 ? g.out[a] : g.in[a]);
           ivol *= A.in_size[a];
@@ -419,6 +607,7 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.box_vol = box_vol;
         A.boxes = static_cast<int>(boxes);
         A.k_vol = static_cast<int>(g.k_vol);
+        A.out_vec = out_vec;
         plan.lds = static_cast<size_t>(lds);
       });
     }
@@ -429,6 +618,17 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
     plan.staged_elems = (size_t)A.batch * A.in_vol * A.cin_total;
   }
   return plan;
+}
+
+// Relative time of `wgs` workgroups on 256 CUs, each needing `core_clk` of main-loop work
+// (MFMA issue, or operand bandwidth when that is the tighter bound) and `load_clk` of LDS
+// staging; a second resident workgroup overlaps its staging with the other's main loop
+// and hides latency (modelled as 85% vs 60% issue efficiency).
+double schedule_cost(int64_t wgs, int occ, double core_clk, double load_clk) {
+  const double eff = occ >= 2 ? 0.85 : 0.6;
+  const double core = core_clk / eff;
+  const double per_round = occ >= 2 ? std::max(occ * core, core + load_clk) : core + load_clk;
+  return double((wgs + 256 * occ - 1) / (256 * occ)) * per_round;
 }
 
 // ---- weight-gradient plan ---------------------------------------------------------------
@@ -823,7 +1023,7 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
                                          stream),
                  "channels-last staging");
   if (st != CONVND_HIP_SUCCESS) return st;
-  st = hip_check(launch_pack_weights(dtype, A, weight, wpk, stream), "weight packing");
+  st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream), "weight packing");
   if (st != CONVND_HIP_SUCCESS) return st;
   A.in = staged;
   A.wpk = wpk;
@@ -883,7 +1083,7 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                                              g.out_channels, g.out_vol, stream),
                      "channels-last staging of grad_output");
       if (st != CONVND_HIP_SUCCESS) return st;
-      st = hip_check(launch_pack_weights(dtype, A, weight, wpk, stream),
+      st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream),
                      "input-gradient weight packing");
       if (st != CONVND_HIP_SUCCESS) return st;
       A.in = staged;
@@ -950,7 +1150,9 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
     } else {
       const IgemmArgs& A = p.args;
       text = "{\"kernel\":\"mfma_igemm\",\"mb\":" + std::to_string(p.mb) +
-             ",\"nb\":" + std::to_string(p.nb) + ",\"box\":" + join(A.box, A.rank) +
+             ",\"nb\":" + std::to_string(p.nb) + ",\"wm\":" + std::to_string(A.wm) +
+             ",\"box\":" + join(A.box, A.rank) + ",\"hpitch\":" + join(A.hpitch, A.rank) +
+             ",\"conflict\":" + std::to_string(p.conflict) +
              ",\"boxes\":" + std::to_string(A.boxes) + ",\"phases\":" +
              std::to_string(A.nphase) + ",\"cc\":" + std::to_string(A.cc) +
              ",\"nchunk\":" + std::to_string(A.nchunk) + ",\"kc_max\":" +

@@ -1,0 +1,635 @@
+// Implicit GEMM (gfx950, 16x16x32 bf16/fp16 MFMA -> fp32) for the forward convolution and
+// for the stride phases of the input gradient.
+//
+//   * A workgroup owns a box of output positions (a power-of-two extent per axis) and a
+//     group of output channels. Its four waves are arranged WM along the channels and 4/WM
+//     along the positions; each wave accumulates MB x NB fragments of 16 x 16.
+//   * The input region the box reads through every tap (the halo) is staged once per
+//     channel chunk into LDS: one plane per octet of 8 channels, 16 bytes per position,
+//     zero outside the tensor, with host-chosen pitches that keep every 16-lane B-fragment
+//     read on distinct bank slots. Every tap then reuses the same LDS bytes.
+//   * K is ordered (channel chunk, tap, channel). A B fragment is one 16-byte LDS read at
+//     pos[q] + tap[k]; A fragments (weights) are packed per call in MFMA lane order and read
+//     from global memory (L2 resident, 16 bytes per lane).
+//   * Per-workgroup index tables (tap offsets, halo rows) are computed into LDS with plain
+//     arithmetic before the first halo load, so no global-memory round trip precedes the
+//     staging; box positions decode with shifts (power-of-two box extents).
+// The input gradient of a strided convolution is split into stride phases: output
+// coordinate x = r + s*j (r the phase residue); the taps that reach phase r are those with
+// (r + pad - t*d) divisible by s, each at the shifted input e(t) = (r + pad - t*d) / s.
+// Every phase is then a stride-1 convolution with per-tap offsets e(t), which the same
+// kernel runs (blockIdx.z covers batch x phase).
+
+#include "convnd_internal.h"
+#include "convnd_types.h"
+
+namespace convnd {
+namespace {
+
+struct AxisTaps {
+  int ntap, first, step;  // taps t = first + i*step for i < ntap
+  int emin, emax;         // range of the input shift e(t)
+  int sigma, cshift;      // input coordinate = j*sigma + cshift + e(t)
+  int J, r, os;           // j extent; output coordinate = r + os*j
+};
+
+__device__ __forceinline__ int gcd_i(int a, int b) {
+  while (b != 0) {
+    const int t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+__device__ __forceinline__ int mod_pos(int a, int b) {
+  const int m = a % b;
+  return m < 0 ? m + b : m;
+}
+
+__device__ __forceinline__ AxisTaps axis_taps(const IgemmArgs& A, int a, int r) {
+  AxisTaps t;
+  if (A.mode == 0) {
+    t.ntap = A.k[a];
+    t.first = 0;
+    t.step = 1;
+    t.emin = 0;
+    t.emax = (A.k[a] - 1) * A.d[a];
+    t.sigma = A.s[a];
+    t.cshift = -A.p[a];
+    t.J = A.out_size[a];
+    t.r = 0;
+    t.os = 1;
+    return t;
+  }
+  const int s = A.s[a], d = A.d[a], k = A.k[a];
+  const int st = s / gcd_i(s, d);
+  int first = -1;
+  for (int c = 0; c < k && c < st; ++c) {
+    if (mod_pos(r + A.p[a] - c * d, s) == 0) {
+      first = c;
+      break;
+    }
+  }
+  t.first = first < 0 ? 0 : first;
+  t.step = st;
+  t.ntap = first < 0 ? 0 : (k - 1 - first) / st + 1;
+  if (t.ntap > 0) {
+    t.emax = (r + A.p[a] - t.first * d) / s;
+    t.emin = (r + A.p[a] - (t.first + (t.ntap - 1) * st) * d) / s;
+  } else {
+    t.emax = 0;
+    t.emin = 0;
+  }
+  t.sigma = 1;
+  t.cshift = 0;
+  t.J = (A.out_size[a] - r + s - 1) / s;
+  t.r = r;
+  t.os = s;
+  return t;
+}
+
+__device__ __forceinline__ int axis_e(const IgemmArgs& A, int a, const AxisTaps& t, int i) {
+  const int tap = t.first + i * t.step;
+  return A.mode == 0 ? tap * A.d[a] : (t.r + A.p[a] - tap * A.d[a]) / A.s[a];
+}
+
+// Axis information of every axis for one phase; returns the phase's tap count.
+__device__ __forceinline__ int phase_axes(const IgemmArgs& A, int phase, AxisTaps* ax) {
+  int rr = phase, ntaps = 1;
+#pragma unroll
+  for (int a = kFastRank - 1; a >= 0; --a) {
+    if (a < A.rank) {
+      const int radix = A.mode ? A.s[a] : 1;
+      ax[a] = axis_taps(A, a, rr % radix);
+      rr /= radix;
+      ntaps *= ax[a].ntap;
+    }
+  }
+  return ntaps;
+}
+
+// ---- weight packing --------------------------------------------------------------------
+
+// Packed weights: unit u = ((((phase*G + g)*nchunk + chunk)*kc_max + kc)*mtiles_padded
+// + mt)*64 + lane holds the 8 A-fragment elements W'[m][k], m = mt*16 + lane%16,
+// k = kc*32 + (lane/16)*8 + i (i < 8), zero where m or k is padding.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const T* w, T* wpk,
+                                                              int64_t units) {
+  const int R = A.rank;
+  {
+    for (int64_t u = blockIdx.x * (int64_t)kThreads + threadIdx.x; u < units;
+         u += (int64_t)gridDim.x * kThreads) {
+      int64_t r = u;
+      const int lane = r & 63;
+      r >>= 6;
+      const int mt = r % A.mtiles_padded;
+      r /= A.mtiles_padded;
+      const int kc = r % A.kc_max;
+      r /= A.kc_max;
+      const int ck = r % A.nchunk;
+      r /= A.nchunk;
+      const int g = r % A.groups;
+      const int phase = (int)(r / A.groups);
+      AxisTaps ax[kFastRank];
+      const int ntaps = phase_axes(A, phase, ax);
+      const int m = mt * 16 + (lane & 15);
+      const int kk = kc * 32 + (lane >> 4) * 8;
+      const int tau = kk / A.cc;
+      const int ci0 = ck * A.cc + (kk - tau * A.cc);
+      T vals[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vals[i] = static_cast<T>(0.f);
+      if (m < A.cout_g && tau < ntaps) {
+        int rem = tau, tflat = 0, kstr = 1;
+#pragma unroll
+        for (int a = kFastRank - 1; a >= 0; --a) {
+          if (a < R) {
+            const int idx = rem % ax[a].ntap;
+            rem /= ax[a].ntap;
+            tflat += (ax[a].first + idx * ax[a].step) * kstr;
+            kstr *= A.k[a];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int ci = ci0 + i;
+          const int64_t widx =
+              A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
+                          : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
+          vals[i] = w[widx];
+        }
+      }
+      T* dst = wpk + u * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dst[i] = vals[i];
+    }
+  }
+}
+
+// ---- main kernel ---------------------------------------------------------------------
+
+// Register budget: two waves per SIMD (256 VGPR+AGPR per wave) for tiles up to 16
+// fragments, one wave per SIMD above. The planner's occupancy model (igemm_reg_waves in
+// the host code) must match.
+template <int MB, int NB>
+constexpr int igemm_waves = MB * NB >= 32 ? 1 : 2;
+
+template <typename T, int MB, int NB, int WM>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(igemm_waves<MB, NB>, igemm_waves<MB, NB>)))
+void igemm_kernel(IgemmArgs A) {
+  using M = Mfma16<T>;
+  using frag = typename M::frag;
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+  const int R = A.rank;
+  const int n = blockIdx.z / A.nphase;
+  const int phase = blockIdx.z % A.nphase;
+  const int g = blockIdx.y / A.mgroups;
+  const int mg = blockIdx.y % A.mgroups;
+
+  // Consecutive workgroup ids go round-robin to the eight XCDs; give each XCD a
+  // contiguous run of boxes so neighbouring halos share its L2.
+  int bx = blockIdx.x;
+  {
+    const int nbx = gridDim.x;
+    if (nbx >= 8) {
+      const int q = nbx >> 3, rem = nbx & 7, x = bx & 7, idx = bx >> 3;
+      bx = x * q + (x < rem ? x : rem) + idx;
+    }
+  }
+
+  AxisTaps ax[kFastRank];
+  const int ntaps = phase_axes(A, phase, ax);
+  int J0[kFastRank], horg[kFastRank];
+  bool outside = false;
+  {
+    int bb = bx;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
+        J0[a] = (bb % A.nbox[a]) * A.box[a];
+        bb /= A.nbox[a];
+        outside |= J0[a] >= ax[a].J;
+        horg[a] = J0[a] * ax[a].sigma + ax[a].cshift + ax[a].emin;
+      }
+    }
+  }
+  if (outside) return;  // uniform over the workgroup (phase with a shorter j extent)
+  const int KC = (ntaps * A.cc + 31) / 32;
+  const int KF = (ntaps * A.cc) / 32;
+
+  // Per axis (all but the last): bit h of valid[a] says halo coordinate h is inside the
+  // tensor. The input position of the halo origin over those axes (may lie outside the
+  // tensor; only rows whose coordinates are all valid use it).
+  unsigned long long valid[kFastRank];
+  int in_base = n * A.in_vol;
+  int istride[kFastRank];
+  {
+    int istr = A.in_size[R - 1];
+#pragma unroll
+    for (int a = kFastRank - 2; a >= 0; --a) {
+      if (a < R - 1) {
+        const int lo = horg[a] < 0 ? -horg[a] : 0;
+        int hi = A.in_size[a] - horg[a];
+        hi = hi < A.hext[a] ? hi : A.hext[a];
+        unsigned long long m = 0;
+        if (hi > lo) {
+          const unsigned long long upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1);
+          m = upto & ~((1ull << lo) - 1);
+        }
+        valid[a] = m;
+        istride[a] = istr;
+        in_base += horg[a] * istr;
+        istr *= A.in_size[a];
+      }
+    }
+  }
+  const int hlast = A.hlast;
+  const int corg = horg[R - 1];
+  const int last_size = A.in_size[R - 1];
+
+  // LDS: [octet planes | tap table (kc_max*4 ints) | rows: input offset (-1 outside), LDS
+  // position offset]. Both tables are computed here, before the first halo load.
+  int* tbl = reinterpret_cast<int*>(lds + A.halo_bytes);
+  int* rowin = tbl + A.kc_max * 4;
+  int* rowlds = rowin + A.rows;
+  for (int idx = tid; idx < KC * 4; idx += kThreads) {
+    // K-group idx: 8 channels of one tap; -1 past the phase's last tap.
+    const int kk = idx * 8;
+    const int tau = kk / A.cc;
+    const int ci = kk - tau * A.cc;
+    int off = -1;
+    if (tau < ntaps) {
+      int rem = tau, t = 0;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < R) {
+          const int i = rem % ax[a].ntap;
+          rem /= ax[a].ntap;
+          t += (axis_e(A, a, ax[a], i) - ax[a].emin) * A.hpitch[a];
+        }
+      }
+      off = t * 16 + (ci >> 3) * A.plane_bytes;
+    }
+    tbl[idx] = off;
+  }
+  for (int r = tid; r < A.rows; r += kThreads) {
+    int rem = r, lds_pos = 0, in_off = 0;
+    bool ok = true;
+#pragma unroll
+    for (int a = kFastRank - 2; a >= 0; --a) {
+      if (a < R - 1) {
+        const int h = rem % A.hext[a];
+        rem /= A.hext[a];
+        lds_pos += h * A.hpitch[a];
+        in_off += h * istride[a];
+        ok = ok && ((valid[a] >> h) & 1ull);
+      }
+    }
+    rowin[r] = ok ? in_base + in_off : -1;
+    rowlds[r] = lds_pos;
+  }
+  // Per-lane LDS byte offsets of this wave's NB position blocks (box extents are powers of
+  // two, so positions decode with shifts).
+  int pbase[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    int q = (wn * NB + nb) * 16 + (lane & 15), off = 0;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
+        off += (q & (A.box[a] - 1)) * ax[a].sigma * A.hpitch[a];
+        q >>= A.box_shift[a];
+      }
+    }
+    pbase[nb] = off * 16;
+  }
+  // Bias of this wave's output channels, loaded now so its latency hides behind the loop.
+  const int mt0 = (mg * WM + wm) * MB;  // first m-tile of this wave
+  const int lg = lane >> 4;
+  float bias_v[MB][4];
+  {
+    const T* bias = static_cast<const T*>(A.bias);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = (mt0 + mb) * 16 + 4 * lg + i;
+        bias_v[mb][i] =
+            (bias != nullptr && m < A.cout_g) ? static_cast<float>(bias[g * A.cout_g + m]) : 0.f;
+      }
+  }
+
+  // Staging walk: item = ((row * noct) + octet) * hlast + column, 256 items apart per
+  // thread; the division happens once and every later item updates incrementally.
+  const int items = A.rows * A.noct * hlast;
+  const int rp0 = tid / hlast, c0 = tid - (tid / hlast) * hlast;
+  const int drp = kThreads / hlast, dc = kThreads - drp * hlast;
+  const int onoct = A.noct - 1;
+
+  const T* in = static_cast<const T*>(A.in);
+  const frag* wp = static_cast<const frag*>(A.wpk);
+  f32x4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const size_t wstep = (size_t)A.mtiles_padded * 64;  // fragments per K32 step
+  const bool tail = KF < KC;
+  // Halo staging in batches of kStageBatch items per thread: the loads of a batch are all
+  // in flight before the first LDS store. The first batch of the next chunk is loaded into
+  // registers before the current chunk's MFMA loop and stored after it, so its latency
+  // hides behind the MFMAs.
+  constexpr int kStageBatch = 8;
+  const T* chunk_base = in + g * A.cin_g;
+  u32x4 pre[kStageBatch];
+  auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v) {
+    const T* base = chunk_base + ck * A.cc;
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+      const int it = it0 + u * kThreads;
+      const int r = rp >> A.log2_noct;
+      const int o = rp & onoct;
+      const int ro = it < items ? rowin[r < A.rows ? r : 0] : -1;
+      const int cl = corg + c;
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      if (ro >= 0 && cl >= 0 && cl < last_size)
+        v[u] = *reinterpret_cast<const u32x4*>(base + (size_t)(ro + cl) * A.cin_total + o * 8);
+      c += dc;
+      rp += drp;
+      if (c >= hlast) {
+        c -= hlast;
+        ++rp;
+      }
+    }
+  };
+  auto stage_store = [&](int it0, int rp, int c, const u32x4* v) {
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+      const int it = it0 + u * kThreads;
+      if (it < items) {
+        const int r = rp >> A.log2_noct;
+        const int o = rp & onoct;
+        *reinterpret_cast<u32x4*>(lds + o * A.plane_bytes + (rowlds[r] + c) * 16) = v[u];
+      }
+      c += dc;
+      rp += drp;
+      if (c >= hlast) {
+        c -= hlast;
+        ++rp;
+      }
+    }
+  };
+  // Position of item it0 + kStageBatch * kThreads in the walk, from the position of it0.
+  auto advance = [&](int& rp, int& c) {
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+      c += dc;
+      rp += drp;
+      if (c >= hlast) {
+        c -= hlast;
+        ++rp;
+      }
+    }
+  };
+  __syncthreads();  // row tables in LDS
+  stage_load(0, tid, rp0, c0, pre);
+  for (int ck = 0; ck < A.nchunk; ++ck) {
+    {
+      // Chunk ck: the first batch is in `pre`; the rest is loaded and stored here.
+      stage_store(tid, rp0, c0, pre);
+      int rp = rp0, c = c0;
+      advance(rp, c);
+      for (int it0 = tid + kStageBatch * kThreads; it0 < items; it0 += kStageBatch * kThreads) {
+        u32x4 v[kStageBatch];
+        stage_load(ck, it0, rp, c, v);
+        stage_store(it0, rp, c, v);
+        advance(rp, c);
+      }
+    }
+    __syncthreads();
+    if (ck + 1 < A.nchunk) stage_load(ck + 1, tid, rp0, c0, pre);
+
+    const frag* wck = wp +
+                      ((size_t)((phase * A.groups + g) * A.nchunk + ck) * A.kc_max) * wstep +
+                      (size_t)mt0 * 64 + lane;
+    if (KF > 0) {
+      // Software pipeline over the full steps: weights two K32 steps ahead (global,
+      // L2-resident), B fragments one step ahead and tap offsets two steps ahead (LDS).
+      // Every prefetch is unconditional (indices clamp to the last full step), so the
+      // compiler's wait counts cover exactly the loads each MFMA group needs.
+      const int last = KF - 1;
+      frag a0[MB], a1[MB], b0[NB], b1[NB];
+      const int s1 = last < 1 ? last : 1;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[mb * 64];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[(size_t)s1 * wstep + mb * 64];
+      const int t0 = tbl[lg];
+      int t1 = tbl[s1 * 4 + lg];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t0);
+      int kc = 0;
+      for (; kc + 1 < KF; kc += 2) {
+        const int n2 = kc + 2 < last ? kc + 2 : last;
+        const int n3 = kc + 3 < last ? kc + 3 : last;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          b1[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t1);
+        const int t2 = tbl[n2 * 4 + lg];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a0[mb], b0[nb], acc[mb][nb]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[(size_t)n2 * wstep + mb * 64];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t2);
+        t1 = tbl[n3 * 4 + lg];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a1[mb], b1[nb], acc[mb][nb]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[(size_t)n3 * wstep + mb * 64];
+      }
+      if (kc < KF) {  // odd number of full steps: the last one is already in (a0, b0)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a0[mb], b0[nb], acc[mb][nb]);
+      }
+    }
+    if (tail) {
+      // The last K32 step holds k-groups past the phase's last tap (table entry -1): their
+      // B fragments are zero, so padding never multiplies a zero weight by a non-finite
+      // input.
+      const int tt = tbl[KF * 4 + lg];
+      frag at[MB], bt[NB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) at[mb] = wck[(size_t)KF * wstep + mb * 64];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        u32x4 v = *reinterpret_cast<const u32x4*>(lds + pbase[nb] + (tt < 0 ? 0 : tt));
+        if (tt < 0) v = u32x4{0u, 0u, 0u, 0u};
+        bt[nb] = __builtin_bit_cast(frag, v);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(at[mb], bt[nb], acc[mb][nb]);
+    }
+    if (ck + 1 < A.nchunk) __syncthreads();  // every wave is done reading this chunk's halo
+  }
+
+  // Epilogue. D[m][n] sits in lane (n + 16*(m/4)), register m%4. The tile (bias added,
+  // rounded to T) goes through LDS as [channel][box position] so that global stores write
+  // A.out_vec consecutive positions (up to 16 bytes) of one channel per lane; box position
+  // q maps to output offset origin + sum_a q_a * ofac[a] and lies inside the output when
+  // q_a < J - J0 on every axis.
+  T* out = static_cast<T*>(A.out);
+  int origin = 0;
+  bool interior = true;
+  int lim[kFastRank], ofac[kFastRank];
+  {
+    int ostr = 1;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
+        origin += (ax[a].r + ax[a].os * J0[a]) * ostr;
+        ofac[a] = ax[a].os * ostr;
+        ostr *= A.out_size[a];
+        lim[a] = ax[a].J - J0[a];
+        interior = interior && lim[a] >= A.box[a];
+      }
+    }
+  }
+  constexpr int kRowsWG = WM * MB * 16;  // output channels of the workgroup
+  const int tstride = A.box_vol + 8;     // elements per tile row (16-byte skew per row)
+  T* tile = reinterpret_cast<T*>(lds);
+  __syncthreads();  // every wave is done with the halo planes and tables
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ml = (wm * MB + mb) * 16 + 4 * lg + i;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int q = (wn * NB + nb) * 16 + (lane & 15);
+        tile[ml * tstride + q] = static_cast<T>(acc[mb][nb][i] + bias_v[mb][i]);
+      }
+    }
+  }
+  __syncthreads();
+  const int vec = A.out_vec;
+  const int per_row = A.box_vol / vec;
+  const int m_valid = A.cout_g - mg * kRowsWG;
+  for (int it = tid; it < kRowsWG * per_row; it += kThreads) {
+    const int ml = it / per_row;
+    const int q = (it - ml * per_row) * vec;
+    if (ml >= m_valid) continue;
+    // Output offset of box position q and, off the interior, whether its row is inside.
+    int qq = q, oo = origin, last_lim = vec;
+    bool ok = true;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
+        const int qa = qq & (A.box[a] - 1);
+        qq >>= A.box_shift[a];
+        oo += qa * ofac[a];
+        if (a == R - 1) {
+          last_lim = lim[a] - qa;
+        } else {
+          ok = ok && qa < lim[a];
+        }
+      }
+    }
+    T* dst = out + ((size_t)n * A.cout_total + g * A.cout_g + mg * kRowsWG + ml) * A.out_vol + oo;
+    const T* src = tile + ml * tstride + q;
+    if (interior) {
+      if (vec == 8) {
+        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+      } else if (vec == 4) {
+        *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
+      } else if (vec == 2) {
+        *reinterpret_cast<unsigned*>(dst) = *reinterpret_cast<const unsigned*>(src);
+      } else {
+        dst[0] = src[0];
+      }
+    } else if (ok) {
+      // Boundary box: the vector's positions share every coordinate but the last.
+      for (int v = 0; v < vec && v < last_lim; ++v) dst[v * ofac[R - 1]] = src[v];
+    }
+  }
+}
+
+// The compiled implicit-GEMM tiles: (MB, NB, WM).
+#define CONVND_IGEMM_TILES(X)                                                             \
+  X(1, 2, 1) X(1, 4, 1) X(1, 8, 1) X(2, 2, 1) X(2, 4, 1) X(2, 8, 1) X(4, 2, 1) X(4, 4, 1) \
+  X(4, 8, 1) X(1, 4, 2) X(1, 8, 2) X(2, 4, 2) X(2, 8, 2) X(1, 4, 4) X(1, 8, 4)
+
+template <typename T>
+hipError_t igemm_dispatch(int mb, int nb, const IgemmArgs& a, size_t lds, hipStream_t s) {
+  const dim3 grid(a.boxes, a.groups * a.mgroups, a.batch * a.nphase);
+#define CONVND_IGEMM_CASE(MBV, NBV, WMV)                                                 \
+  if (mb == MBV && nb == NBV && a.wm == WMV) {                                           \
+    auto fn = igemm_kernel<T, MBV, NBV, WMV>;                                            \
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),              \
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,     \
+                                         static_cast<int>(lds));                         \
+    if (err != hipSuccess) return err;                                                   \
+    hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                             \
+    return hipGetLastError();                                                            \
+  }
+  CONVND_IGEMM_TILES(CONVND_IGEMM_CASE)
+#undef CONVND_IGEMM_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool igemm_tile_supported(int mb, int nb, int wm) {
+#define CONVND_IGEMM_HAS(MBV, NBV, WMV) \
+  if (mb == MBV && nb == NBV && wm == WMV) return true;
+  CONVND_IGEMM_TILES(CONVND_IGEMM_HAS)
+#undef CONVND_IGEMM_HAS
+  return false;
+}
+
+hipError_t launch_igemm_prep(convnd_hip_dtype dtype, const IgemmArgs& a, const void* w,
+                             void* wpk, hipStream_t stream) {
+  const int64_t units = (int64_t)a.nphase * a.groups * a.nchunk * a.kc_max * a.mtiles_padded * 64;
+  if (units == 0) return hipSuccess;
+  const int64_t blocks64 = (units + kThreads - 1) / kThreads;
+  const dim3 grid(static_cast<unsigned>(blocks64 < 4096 ? blocks64 : 4096));
+  if (dtype == CONVND_HIP_BFLOAT16) {
+    hipLaunchKernelGGL((igemm_pack_kernel<__bf16>), grid, dim3(kThreads), 0, stream, a,
+                       static_cast<const __bf16*>(w), static_cast<__bf16*>(wpk), units);
+  } else if (dtype == CONVND_HIP_FLOAT16) {
+    hipLaunchKernelGGL((igemm_pack_kernel<_Float16>), grid, dim3(kThreads), 0, stream, a,
+                       static_cast<const _Float16*>(w), static_cast<_Float16*>(wpk), units);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,
+                        size_t lds_bytes, hipStream_t stream) {
+  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
+  if (dtype == CONVND_HIP_BFLOAT16) return igemm_dispatch<__bf16>(mb, nb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_FLOAT16) return igemm_dispatch<_Float16>(mb, nb, a, lds_bytes, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace convnd

@@ -29,6 +29,12 @@ struct DirectGeom {
 
 // Arguments of the box-tiled implicit GEMM (forward, or one family of stride phases of
 // the input gradient). All sizes fit int32; the planner checks that.
+//
+// LDS halo layout: one plane per octet of 8 channels of the chunk; a plane holds 16 bytes
+// (8 channels) per halo position at position offset sum_a h[a] * hpitch[a]. Plane sizes
+// are multiples of 256 bytes and the pitches are chosen on the host so that the sixteen
+// lanes of every B-fragment read fall on distinct 16-byte bank slots. The halo covers the
+// widest phase (hext is the maximum over the phases).
 struct IgemmArgs {
   const void* in;    // channels-last staged operand [N][in_vol][cin_total]
   const void* wpk;   // packed A fragments [phase][group][chunk][kc][mtile][64 lanes][8]
@@ -40,16 +46,22 @@ struct IgemmArgs {
   int cin_g, cout_g;          // GEMM reduction channels / output channels per group
   int cin_total, cout_total;
   int wk_cin_g, wk_cout_g;    // channels per group of the original weight tensor
-  int cc, nchunk, kc_max;     // channels per LDS halo chunk, chunks, K32 steps per chunk
+  int cc, noct, log2_noct;    // channels and octets per LDS chunk (powers of two)
+  int nchunk, kc_max;         // chunks, K32 steps per chunk (widest phase)
+  int wm;                     // waves along M (output channels); 4 / wm along positions
   int mtiles, mgroups, mtiles_padded;
-  int pstride;                // LDS bytes per halo position
-  int halo_bytes;             // LDS bytes reserved for the halo
+  int plane_bytes;            // LDS bytes of one octet plane (multiple of 256)
+  int halo_bytes;             // noct * plane_bytes
+  int rows, hlast;            // halo rows (all axes but the last) and last-axis extent
+  int hext[kFastRank];        // halo extent per axis (<= 64 on all axes but the last)
+  int hpitch[kFastRank];      // halo position pitch per axis (hpitch[rank-1] == 1)
   int in_size[kFastRank], out_size[kFastRank];
   int in_vol, out_vol;
-  int box[kFastRank], nbox[kFastRank];
+  int box[kFastRank], box_shift[kFastRank], nbox[kFastRank];
   int box_vol, boxes;
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int k_vol;
+  int out_vec;                // output elements per epilogue store (consecutive positions)
 };
 
 // Arguments of the MFMA weight-gradient kernel.
@@ -88,10 +100,14 @@ hipError_t launch_direct_grad_weight(convnd_hip_dtype dtype, const DirectGeom& g
 hipError_t launch_grad_bias(convnd_hip_dtype dtype, int64_t batch, int64_t channels,
                             int64_t volume, const void* dy, void* db, float* scratch,
                             int64_t chunks, hipStream_t stream);
-hipError_t launch_pack_weights(convnd_hip_dtype dtype, const IgemmArgs& a, const void* w,
-                               void* wpk, hipStream_t stream);
+// Packs the weights into the implicit GEMM's A-fragment order.
+hipError_t launch_igemm_prep(convnd_hip_dtype dtype, const IgemmArgs& a, const void* w,
+                             void* wpk, hipStream_t stream);
 hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,
                         size_t lds_bytes, hipStream_t stream);
+// Whether launch_igemm has a compiled kernel for this wave tile (mb x nb fragments) and
+// wave arrangement (wm waves along output channels).
+bool igemm_tile_supported(int mb, int nb, int wm);
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, const WgradArgs& a,
                              size_t lds_bytes, hipStream_t stream);
 hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream);
