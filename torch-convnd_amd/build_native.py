@@ -27,7 +27,13 @@ LIB_DIR = ROOT / "torch_convnd" / "_lib"
 BUILD_DIR = ROOT / "_build"
 HIP_LIBRARY = LIB_DIR / "libconvnd_hip.so"
 OPS_LIBRARY = LIB_DIR / "libtorch_convnd_ops.so"
-HIP_SOURCES = ("convnd_direct.hip", "convnd_igemm.hip", "convnd_mfma.hip", "convnd_capi.cpp")
+HIP_SOURCES = (
+    "convnd_direct.hip",
+    "convnd_layout.hip",
+    "convnd_igemm.hip",
+    "convnd_wgrad.hip",
+    "convnd_capi.cpp",
+)
 OFFLOAD_ARCH = os.environ.get("TORCH_CONVND_OFFLOAD_ARCH", "gfx950")
 
 

@@ -166,14 +166,6 @@ bool is_half(convnd_hip_dtype dt) {
 
 size_t align_up(size_t v) { return (v + 255) & ~size_t{255}; }
 
-// Bytes per halo position in LDS: channels*2 rounded to an odd number of 16-byte chunks,
-// so the sixteen-lane 16-byte reads of consecutive positions hit distinct bank groups.
-int halo_pstride(int channels) {
-  int chunks = (channels * 2 + 15) / 16;
-  if (chunks % 2 == 0) ++chunks;
-  return chunks * 16;
-}
-
 // Everything in the fast kernels is int32: check the element counts they index.
 bool fits_int32(const Geom& g) {
   int64_t v;
@@ -346,7 +338,8 @@ int64_t choose_pitches(int R, const int* box, const int* sigma, const int* hext,
 }
 
 // Optional launch-plan override for tuning sweeps, read once per process from
-// CONVND_HIP_FWD_PLAN / CONVND_HIP_DGRAD_PLAN, e.g. "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8".
+// CONVND_HIP_FWD_PLAN / CONVND_HIP_DGRAD_PLAN / CONVND_HIP_WGRAD_PLAN, e.g.
+// "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8" (the weight gradient reads box only).
 // Any subset of the keys may be given; the planner then searches only plans matching it and
 // ignores the override when none does.
 struct PlanFilter {
@@ -392,6 +385,8 @@ PlanFilter parse_filter(const char* text) {
 const PlanFilter& plan_filter(int mode) {
   static const PlanFilter fwd = parse_filter(std::getenv("CONVND_HIP_FWD_PLAN"));
   static const PlanFilter dgrad = parse_filter(std::getenv("CONVND_HIP_DGRAD_PLAN"));
+  static const PlanFilter wgrad = parse_filter(std::getenv("CONVND_HIP_WGRAD_PLAN"));
+  if (mode == 2) return wgrad;
   return mode == 0 ? fwd : dgrad;
 }
 
@@ -643,40 +638,6 @@ struct WgradPlan {
   double cost = 0.0;
 };
 
-// Per workgroup column range (64 (tap, channel-octet) pairs), the bounding box of its taps:
-// returns the largest halo volume and row count over all workgroups for box b.
-void wgrad_halo_extent(const Geom& g, const int* b, int npairs, int octs, int64_t* hvol_max,
-                       int64_t* rows_max) {
-  const int R = g.rank;
-  *hvol_max = 0;
-  *rows_max = 0;
-  for (int p0 = 0; p0 < npairs; p0 += 64) {
-    const int p1 = std::min(p0 + 64, npairs);
-    int tmin[kFastRank], tmax[kFastRank];
-    for (int a = 0; a < R; ++a) {
-      tmin[a] = 1 << 30;
-      tmax[a] = -1;
-    }
-    for (int tt = p0 / octs; tt <= (p1 - 1) / octs; ++tt) {
-      int rem = tt;
-      for (int a = R - 1; a >= 0; --a) {
-        const int ta = rem % static_cast<int>(g.k[a]);
-        rem /= static_cast<int>(g.k[a]);
-        tmin[a] = std::min(tmin[a], ta);
-        tmax[a] = std::max(tmax[a], ta);
-      }
-    }
-    int64_t hvol = 1, rows = 1;
-    for (int a = 0; a < R; ++a) {
-      const int64_t h = (int64_t)(b[a] - 1) * g.s[a] + (tmax[a] - tmin[a]) * g.d[a] + 1;
-      hvol *= h;
-      if (a < R - 1) rows *= h;
-    }
-    *hvol_max = std::max(*hvol_max, hvol);
-    *rows_max = std::max(*rows_max, rows);
-  }
-}
-
 WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
   WgradPlan plan;
   if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g) || g.cin_g % 8 != 0 ||
@@ -684,50 +645,76 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
     return plan;
   const int R = g.rank;
   const int cin_g = static_cast<int>(g.cin_g), cout_g = static_cast<int>(g.cout_g);
+  const int k_vol = static_cast<int>(g.k_vol);
   const int mtiles = (cout_g + 15) / 16;
   const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
   const int mgroups = (mtiles + mb - 1) / mb;
-  const int pstride = halo_pstride(cin_g);
   const int octs = cin_g / 8;
-  const int npairs = static_cast<int>(g.k_vol * octs);
-  const int ncg = (npairs + 15) / 16;
-  const int ncq = (ncg + 3) / 4;
+  const int npairs = octs * k_vol;
+  const int ncq = (npairs + 63) / 64;
   if (ncq > 65535 || g.groups * mgroups > 65535) return plan;
+  int max_oct = 1;
+  for (int p0 = 0; p0 < npairs; p0 += 64) {
+    const int p1 = std::min(p0 + 64, npairs);
+    max_oct = std::max(max_oct, (p1 - 1) / k_vol - p0 / k_vol + 1);
+  }
   const int out_last = static_cast<int>(g.out[R - 1]);
+  const PlanFilter& filter = plan_filter(2);
   double best = -1.0;
-  for (int box_vol : {256, 128, 64, 32}) {
-    const int dyrow = box_vol * 2 + 16;
+  for (int box_vol : {512, 256, 128}) {
     int limit[kFastRank];
     for (int a = 0; a < R; ++a) {
       int l = 1;
       while (l < g.out[a] && l < box_vol) l *= 2;
       limit[a] = l;
     }
+    // The last axis carries K-groups of 8 consecutive positions.
+    limit[R - 1] = std::max(limit[R - 1], 8);
     for_each_box(R, limit, box_vol, [&](const int* b) {
-      int64_t hvol, rows;
-      wgrad_halo_extent(g, b, npairs, octs, &hvol, &rows);
-      int64_t boxes = 1;
-      for (int a = 0; a < R; ++a) boxes *= (g.out[a] + b[a] - 1) / b[a];
-      const int64_t box_rows = box_vol / b[R - 1];
-      const int64_t halo_bytes = align_up(hvol * pstride);
-      const int64_t lds = halo_bytes + align_up((int64_t)mb * 16 * dyrow) +
-                          align_up((box_vol + rows + box_rows) * 4);
-      if (lds > kLdsBudget) return;
+      if (b[R - 1] < 8) return;
+      if (!filter.box.empty()) {
+        if (static_cast<int>(filter.box.size()) != R) return;
+        for (int a = 0; a < R; ++a)
+          if (filter.box[a] != b[a]) return;
+      }
+      int hext[kFastRank], hpitch[kFastRank];
+      int64_t rows = 1, boxes = 1;
+      for (int a = 0; a < R; ++a) {
+        hext[a] = static_cast<int>((b[a] - 1) * g.s[a] + (g.k[a] - 1) * g.d[a] + 1);
+        if ((a < R - 1 && hext[a] > 64) || hext[a] > 255) return;
+        if (a < R - 1) rows *= hext[a];
+        boxes *= (g.out[a] + b[a] - 1) / b[a];
+      }
+      hpitch[R - 1] = 1;
+      for (int a = R - 2; a >= 0; --a) hpitch[a] = hpitch[a + 1] * hext[a + 1];
+      const int64_t plane_pos = (int64_t)hpitch[0] * hext[0];
+      const int64_t plane_bytes = align_up(plane_pos * 16);
+      const int box_rows = box_vol / b[R - 1];
+      const int dyrow = box_vol * 2 + 32;
+      const int64_t lds_dy = max_oct * plane_bytes;
+      const int64_t lds_pos = lds_dy + align_up((int64_t)mb * 16 * dyrow);
+      const int64_t lds_rows = lds_pos + align_up((int64_t)box_vol * 4);
+      const int64_t lds = lds_rows + align_up((5 * rows + box_rows) * 4);
+      if (lds > kLdsBudget || rows > (int64_t{1} << 20)) return;
       const int occ = occupancy(lds);
       const int64_t items = boxes * g.batch;
-      // Position chunks: enough workgroups to fill every CU once at this occupancy.
       const int64_t per_chunk_wgs = (int64_t)ncq * g.groups * mgroups;
       int64_t npc = std::max<int64_t>(1, (256 * occ) / per_chunk_wgs);
       npc = std::min<int64_t>(npc, items);
       const int64_t ipc = (items + npc - 1) / npc;
       npc = (items + ipc - 1) / ipc;
-      const double mfma_box = double(box_vol / 32) * 8 * mb * 16.0;
-      const double load_box = double(hvol) * cin_g * 2 / 32.0 + double(mb * 16) * box_vol * 2 / 32.0;
+      // Per item: MFMA issue of one wave (8 fragments x MB tiles per K32 step) and the
+      // staging of the octet planes and the grad_output tile (~64 B/clock/CU plus latency).
+      const double mfma_item = double(box_vol / 32) * 8 * mb * 16.0;
+      const double stage_item =
+          (double(max_oct) * plane_pos * 16 + double(mb) * 16 * box_vol * 2) / 64.0 + 2500.0;
+      const double eff = occ >= 2 ? 0.75 : 0.55;
+      const double per_wg = double(ipc) * (mfma_item / eff + stage_item * (occ >= 2 ? 0.4 : 1.0));
       const int64_t wgs = npc * per_chunk_wgs;
-      // Partial sums: written once per chunk and read back by the reduction (8 TB/s ~
-      // 3.3 KB per clock at 2.4 GHz spread over the chip).
-      const double partial_clk = double(npc) * g.out_channels * cin_g * g.k_vol * 8 / 3300.0;
-      const double cost = schedule_cost(wgs, occ, ipc * mfma_box, ipc * load_box) + partial_clk;
+      const double rounds = double((wgs + 256 * occ - 1) / (256 * occ));
+      // Partial sums: written once per position chunk and read back by the reduction.
+      const double partial_clk = double(npc) * g.out_channels * cin_g * k_vol * 8 / 3300.0;
+      const double cost = rounds * per_wg + partial_clk;
       if (best >= 0 && cost >= best) return;
       best = cost;
       plan.ok = true;
@@ -753,30 +740,35 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
         A.p[a] = static_cast<int>(g.p[a]);
         A.d[a] = static_cast<int>(g.d[a]);
         A.box[a] = b[a];
+        A.box_shift[a] = 0;
+        while ((1 << A.box_shift[a]) < b[a]) ++A.box_shift[a];
         A.nbox[a] = static_cast<int>((g.out[a] + b[a] - 1) / b[a]);
+        A.hext[a] = hext[a];
+        A.hpitch[a] = hpitch[a];
       }
       A.in_vol = ivol;
       A.out_vol = ovol;
-      A.k_vol = static_cast<int>(g.k_vol);
+      A.k_vol = k_vol;
       A.box_vol = box_vol;
       A.boxes = static_cast<int>(boxes);
-      A.pstride = pstride;
-      A.halo_bytes = static_cast<int>(halo_bytes);
-      A.max_rows = static_cast<int>(rows);
+      A.rows = static_cast<int>(rows);
+      A.hlast = hext[R - 1];
+      A.plane_bytes = static_cast<int>(plane_bytes);
+      A.max_oct = max_oct;
       A.dyrow = dyrow;
-      // Widest load that keeps every run of the box's last axis aligned and either wholly
-      // inside or wholly outside the tensor.
       int vec = 8;
       while (vec > 1 && (b[R - 1] % vec != 0 || out_last % vec != 0)) vec /= 2;
       A.dy_vec = vec;
       A.mtiles = mtiles;
       A.mgroups = mgroups;
       A.npairs = npairs;
-      A.ncg = ncg;
       A.ncq = ncq;
       A.npc = static_cast<int>(npc);
       A.items = static_cast<int>(items);
       A.items_per_pc = static_cast<int>(ipc);
+      A.lds_dy = static_cast<int>(lds_dy);
+      A.lds_pos = static_cast<int>(lds_pos);
+      A.lds_rows = static_cast<int>(lds_rows);
       plan.lds = static_cast<size_t>(lds);
     });
   }
@@ -787,7 +779,7 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
   return plan;
 }
 
-constexpr int64_t kBiasChunks = 32;
+constexpr size_t kBiasChunks = 32;
 
 // Workspace layout helper: a sequence of 256-byte aligned regions.
 struct Layout {
@@ -879,7 +871,14 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
       b.off_partial = L.take(b.wg.partial_elems * sizeof(float));
     }
   }
-  if (gb) b.off_bias = L.take((size_t)g.out_channels * kBiasChunks * sizeof(double));
+  if (gb) {
+    // Partial sums of the bias gradient: per channel, kBiasChunks doubles on the standalone
+    // path or one float per 64-position tile when they come with the channels-last copy.
+    const size_t fused = (gi && b.dg.ok) ? (size_t)channel_last_sum_blocks(g.batch, g.out_vol) *
+                                               sizeof(float)
+                                         : 0;
+    b.off_bias = L.take((size_t)g.out_channels * std::max(fused, kBiasChunks * sizeof(double)));
+  }
   b.bytes = L.total;
   return b;
 }
@@ -1020,7 +1019,7 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
   st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels, g.in_vol,
-                                         stream),
+                                         nullptr, stream),
                  "channels-last staging");
   if (st != CONVND_HIP_SUCCESS) return st;
   st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream), "weight packing");
@@ -1067,7 +1066,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     }
     return CONVND_HIP_SUCCESS;
   }
-  if (gb) {
+  // The bias gradient rides on the channels-last copy of grad_output when the input
+  // gradient makes one; otherwise it reads grad_output on its own.
+  const bool fused_bias = gb && gi && b.dg.ok;
+  if (gb && !fused_bias) {
     st = hip_check(launch_grad_bias(dtype, g.batch, g.out_channels, g.out_vol, grad_output,
                                     grad_bias, reinterpret_cast<float*>(ws + b.off_bias),
                                     kBiasChunks, stream),
@@ -1079,10 +1081,18 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       IgemmArgs A = b.dg.args;
       void* staged = ws + b.off_dy_stage;
       void* wpk = ws + b.off_wpk;
+      float* sums = fused_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
       st = hip_check(launch_to_channels_last(dtype, grad_output, staged, g.batch,
-                                             g.out_channels, g.out_vol, stream),
+                                             g.out_channels, g.out_vol, sums, stream),
                      "channels-last staging of grad_output");
       if (st != CONVND_HIP_SUCCESS) return st;
+      if (fused_bias) {
+        st = hip_check(launch_grad_bias_from_sums(dtype, sums,
+                                                  channel_last_sum_blocks(g.batch, g.out_vol),
+                                                  g.out_channels, grad_bias, stream),
+                       "bias gradient");
+        if (st != CONVND_HIP_SUCCESS) return st;
+      }
       st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream),
                      "input-gradient weight packing");
       if (st != CONVND_HIP_SUCCESS) return st;
@@ -1107,12 +1117,16 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       void* staged = ws + b.off_x_stage;
       float* partial = reinterpret_cast<float*>(ws + b.off_partial);
       st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels,
-                                             g.in_vol, stream),
+                                             g.in_vol, nullptr, stream),
                      "channels-last staging of input");
       if (st != CONVND_HIP_SUCCESS) return st;
       A.x = staged;
       A.dy = grad_output;
       A.partial = partial;
+      // Vector copies of grad_output rows need the base aligned to the vector width.
+      while (A.dy_vec > 1 &&
+             reinterpret_cast<uintptr_t>(grad_output) % (uintptr_t(A.dy_vec) * 2) != 0)
+        A.dy_vec /= 2;
       const auto ev = timing_begin(2, stream);
       st = hip_check(launch_wgrad_mfma(dtype, b.wg.mb, A, b.wg.lds, stream),
                      "MFMA weight gradient");
@@ -1172,6 +1186,7 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
              ",\"box\":" + join(A.box, A.rank) + ",\"boxes\":" + std::to_string(A.boxes) +
              ",\"npc\":" + std::to_string(A.npc) + ",\"items_per_pc\":" +
              std::to_string(A.items_per_pc) + ",\"ncq\":" + std::to_string(A.ncq) +
+             ",\"max_oct\":" + std::to_string(A.max_oct) +
              ",\"mgroups\":" + std::to_string(A.mgroups) + ",\"dy_vec\":" +
              std::to_string(A.dy_vec) + ",\"lds\":" + std::to_string(p.lds) +
              ",\"occupancy\":" + std::to_string(occupancy(static_cast<int64_t>(p.lds))) +

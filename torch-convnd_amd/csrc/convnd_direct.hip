@@ -259,105 +259,6 @@ __global__ __launch_bounds__(kThreads) void direct_grad_weight_kernel(DirectGeom
   }
 }
 
-// Bias gradient in two deterministic passes: per (channel, chunk) partial sums, then a
-// fixed-order sum of the chunks (the reference's flat_grad.sum({0, 3}),
-// src/torch_convnd/csrc/convnd.cpp:388-390).
-template <typename T>
-__global__ __launch_bounds__(kThreads) void bias_partial_kernel(const T* dy, float* part,
-                                                                int64_t batch,
-                                                                int64_t channels,
-                                                                int64_t volume,
-                                                                int64_t chunks) {
-  using A = typename Acc<T>::type;
-  __shared__ A smem[kThreads];
-  const int64_t c = blockIdx.x;
-  const int64_t chunk = blockIdx.y;
-  const int64_t work = batch * volume;
-  const int64_t per = (work + chunks - 1) / chunks;
-  const int64_t begin = chunk * per;
-  const int64_t end = begin + per < work ? begin + per : work;
-  A acc = 0;
-  for (int64_t i = begin + threadIdx.x; i < end; i += kThreads) {
-    const int64_t n = i / volume;
-    acc += widen<A>(dy[(n * channels + c) * volume + i % volume]);
-  }
-  const A sum = block_sum(acc, smem);
-  if (threadIdx.x == 0) {
-    if constexpr (sizeof(A) == 8) {
-      reinterpret_cast<double*>(part)[c * chunks + chunk] = sum;
-    } else {
-      part[c * chunks + chunk] = sum;
-    }
-  }
-}
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void bias_final_kernel(const float* part, T* db,
-                                                              int64_t channels,
-                                                              int64_t chunks) {
-  using A = typename Acc<T>::type;
-  const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (c >= channels) return;
-  A acc = 0;
-  for (int64_t i = 0; i < chunks; ++i) {
-    if constexpr (sizeof(A) == 8) {
-      acc += reinterpret_cast<const double*>(part)[c * chunks + i];
-    } else {
-      acc += part[c * chunks + i];
-    }
-  }
-  db[c] = narrow<T>(acc);
-}
-
-// [N][C][V] -> [N][V][C] through a 64x64 LDS tile; reads are coalesced along V and
-// writes along C.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void to_channels_last_kernel(const T* src, T* dst,
-                                                                    int64_t batch,
-                                                                    int64_t channels,
-                                                                    int64_t volume) {
-  __shared__ T tile[64][65];
-  const int64_t v0 = (int64_t)blockIdx.x * 64;
-  const int64_t c0 = (int64_t)blockIdx.y * 64;
-  const int tx = threadIdx.x & 63;
-  const int ty = threadIdx.x >> 6;
-  for (int64_t n = blockIdx.z; n < batch; n += gridDim.z) {
-    const T* s = src + n * channels * volume;
-    T* d = dst + n * channels * volume;
-    __syncthreads();
-    for (int r = ty; r < 64; r += 4) {
-      const int64_t c = c0 + r, v = v0 + tx;
-      if (c < channels && v < volume) tile[r][tx] = s[c * volume + v];
-    }
-    __syncthreads();
-    for (int r = ty; r < 64; r += 4) {
-      const int64_t v = v0 + r, c = c0 + tx;
-      if (c < channels && v < volume) d[v * channels + c] = tile[tx][r];
-    }
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void reduce_partials_kernel_f(const float* part,
-                                                                     float* out, int64_t count,
-                                                                     int64_t parts) {
-  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (e >= count) return;
-  float acc = 0.f;
-  for (int64_t i = 0; i < parts; ++i) acc += part[i * count + e];
-  out[e] = acc;
-}
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const float* part, T* out,
-                                                                   int64_t count,
-                                                                   int64_t parts) {
-  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (e >= count) return;
-  float acc = 0.f;
-  for (int64_t i = 0; i < parts; ++i) acc += part[i * count + e];
-  out[e] = static_cast<T>(acc);
-}
-
 __global__ __launch_bounds__(kThreads) void fill_zero_kernel(unsigned char* dst, int64_t bytes) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < bytes;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -448,67 +349,11 @@ hipError_t launch_direct_grad_weight(convnd_hip_dtype dtype, const DirectGeom& g
   });
 }
 
-hipError_t launch_grad_bias(convnd_hip_dtype dtype, int64_t batch, int64_t channels,
-                            int64_t volume, const void* dy, void* db, float* scratch,
-                            int64_t chunks, hipStream_t stream) {
-  if (channels == 0) return hipSuccess;
-  return dispatch_dtype(dtype, [&](auto tag) {
-    using T = decltype(tag);
-    hipLaunchKernelGGL((bias_partial_kernel<T>), dim3(channels, chunks), dim3(kThreads), 0,
-                       stream, static_cast<const T*>(dy), scratch, batch, channels, volume,
-                       chunks);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL((bias_final_kernel<T>), dim3((channels + kThreads - 1) / kThreads),
-                       dim3(kThreads), 0, stream, scratch, static_cast<T*>(db), channels,
-                       chunks);
-    return hipGetLastError();
-  });
-}
-
-hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void* dst,
-                                   int64_t batch, int64_t channels, int64_t volume,
-                                   hipStream_t stream) {
-  if (batch == 0 || channels == 0 || volume == 0) return hipSuccess;
-  if ((volume + 63) / 64 > 0x7fffffff || (channels + 63) / 64 > 65535) return hipErrorInvalidValue;
-  const dim3 grid((volume + 63) / 64, (channels + 63) / 64, batch < 65535 ? batch : 65535);
-  return dispatch_dtype(dtype, [&](auto tag) {
-    using T = decltype(tag);
-    hipLaunchKernelGGL((to_channels_last_kernel<T>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const T*>(src), static_cast<T*>(dst), batch, channels,
-                       volume);
-    return hipGetLastError();
-  });
-}
-
 // A kernel instead of hipMemsetAsync, so callers may capture the sequence in a HIP graph.
 hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream) {
   if (bytes == 0) return hipSuccess;
   hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(bytes)), dim3(kThreads), 0, stream,
                      static_cast<unsigned char*>(dst), bytes);
-  return hipGetLastError();
-}
-
-hipError_t launch_reduce_partials(convnd_hip_dtype dtype, const float* partial, void* out,
-                                  int64_t count, int64_t parts, hipStream_t stream) {
-  if (count == 0) return hipSuccess;
-  const dim3 grid((count + kThreads - 1) / kThreads);
-  switch (dtype) {
-    case CONVND_HIP_FLOAT32:
-      hipLaunchKernelGGL(reduce_partials_kernel_f, grid, dim3(kThreads), 0, stream, partial,
-                         static_cast<float*>(out), count, parts);
-      break;
-    case CONVND_HIP_FLOAT16:
-      hipLaunchKernelGGL((reduce_partials_kernel<_Float16>), grid, dim3(kThreads), 0, stream,
-                         partial, static_cast<_Float16*>(out), count, parts);
-      break;
-    case CONVND_HIP_BFLOAT16:
-      hipLaunchKernelGGL((reduce_partials_kernel<__bf16>), grid, dim3(kThreads), 0, stream,
-                         partial, static_cast<__bf16*>(out), count, parts);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
   return hipGetLastError();
 }
 

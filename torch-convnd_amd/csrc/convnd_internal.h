@@ -64,7 +64,10 @@ struct IgemmArgs {
   int out_vec;                // output elements per epilogue store (consecutive positions)
 };
 
-// Arguments of the MFMA weight-gradient kernel.
+// Arguments of the MFMA weight-gradient kernel. Columns are (octet of 8 input channels,
+// tap) pairs, octet slowest; a workgroup owns 64 consecutive pairs (max_oct octets at most).
+// LDS: [max_oct octet planes | grad_output tile | box position offsets | halo row tables
+// (5 * rows ints) | box row offsets (box_vol / box[rank-1] ints)].
 struct WgradArgs {
   const void* x;      // channels-last input [N][in_vol][cin_total]
   const void* dy;     // grad_output [N][cout_total][out_vol]
@@ -74,21 +77,31 @@ struct WgradArgs {
   int in_size[kFastRank], out_size[kFastRank];
   int in_vol, out_vol, k_vol;
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
-  int box[kFastRank], nbox[kFastRank];
+  int box[kFastRank], box_shift[kFastRank], nbox[kFastRank];
   int box_vol, boxes;
-  int pstride, halo_bytes;   // LDS bytes per halo position / reserved for the halo
-  int max_rows;              // LDS ints reserved for halo row offsets
-  int dyrow;                 // LDS bytes per grad_output row of the box tile
+  int hext[kFastRank], hpitch[kFastRank];  // halo of every tap, plane position pitches
+  int rows, hlast;           // halo rows (all axes but the last) and last-axis extent
+  int plane_bytes;           // LDS bytes per octet plane
+  int max_oct;               // octet planes reserved
+  int dyrow;                 // LDS bytes per grad_output tile row (box_vol*2 + 32)
   int dy_vec;                // grad_output elements per vector load (8, 4, 2 or 1)
   int mtiles, mgroups;
-  int npairs, ncg, ncq;
+  int npairs, ncq;
   int npc, items, items_per_pc;
+  int lds_dy, lds_pos, lds_rows;  // LDS byte offsets of the regions after the planes
 };
 
 // ---- kernel launchers (defined in the .hip files) -------------------------------------
+// [N][C][V] -> [N][V][C] for 16-bit types (C % 8 == 0). With chan_sums non-null it also
+// writes fp32 partial sums per channel and 64-position tile:
+// chan_sums[c * channel_last_sum_blocks(N, V) + block].
 hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void* dst,
                                    int64_t batch, int64_t channels, int64_t volume,
-                                   hipStream_t stream);
+                                   float* chan_sums, hipStream_t stream);
+int64_t channel_last_sum_blocks(int64_t batch, int64_t volume);
+// db[c] = sum of the nsum partial sums of channel c (fixed order).
+hipError_t launch_grad_bias_from_sums(convnd_hip_dtype dtype, const float* sums, int64_t nsum,
+                                      int64_t channels, void* db, hipStream_t stream);
 hipError_t launch_direct_forward(convnd_hip_dtype dtype, const DirectGeom& g, const void* x,
                                  const void* w, const void* b, void* y, hipStream_t stream);
 hipError_t launch_direct_grad_input(convnd_hip_dtype dtype, const DirectGeom& g,
