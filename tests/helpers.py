@@ -93,6 +93,35 @@ def reference_nd(input, weight, bias=None, stride=None, padding=None, dilation=N
     return out
 
 
+def frames_reference(input, weight, bias, stride, padding, dilation, groups):
+    """Rank >= 3 convolution reduced to ``F.conv3d``: for each tap of the first spatial axis,
+    the frames that tap reads are folded into the batch and convolved over the remaining
+    axes, recursively (the reference's frames decomposition, _decomposition.py:11-42 of
+    lyehe/torch-convnd, applied at every rank). Differentiable; used at full BASELINE sizes
+    where the tap-by-tap einsum would be too slow."""
+    rank = input.ndim - 2
+    if rank == 3:
+        out = F.conv3d(input, weight, None, stride, padding, dilation, groups)
+    else:
+        n, c = input.shape[:2]
+        k0, s0, p0, d0 = weight.shape[2], stride[0], padding[0], dilation[0]
+        extent = (input.shape[2] + 2 * p0 - d0 * (k0 - 1) - 1) // s0 + 1
+        pad = [0, 0] * (rank - 1) + [p0, p0]
+        padded = F.pad(input, pad) if p0 else input
+        out = None
+        for tap in range(k0):
+            first = tap * d0
+            frames = padded[:, :, first : first + (extent - 1) * s0 + 1 : s0]
+            frames = frames.movedim(2, 1).reshape(n * extent, c, *input.shape[3:])
+            part = frames_reference(frames, weight[:, :, tap], None, stride[1:], padding[1:],
+                                    dilation[1:], groups)
+            part = part.reshape(n, extent, *part.shape[1:]).movedim(1, 2)
+            out = part if out is None else out + part
+    if bias is not None:
+        out = out + bias.reshape(1, -1, *((1,) * rank))
+    return out
+
+
 def to_numpy64(t):
     return None if t is None else t.detach().double().cpu().numpy()
 

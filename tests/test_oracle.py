@@ -245,6 +245,34 @@ def test_test_helper_reference_matches_oracle():
     np.testing.assert_allclose(ref.numpy(), oracle.forward(x.numpy(), w.numpy(), b.numpy(), *args), rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize(
+    "case",
+    [
+        ((1, 4, 4, 5, 3, 4), (6, 2, 2, 3, 2, 2), (1, 2, 1, 1), (1, 1, 0, 1), (2, 1, 1, 1), 2),
+        ((2, 3, 5, 3, 4, 3, 4), (2, 3, 3, 2, 2, 2, 3), (2, 1, 1, 2, 1), (1, 0, 1, 1, 2), (1, 2, 1, 1, 1), 1),
+        ((1, 4, 3, 4, 3, 3, 4, 3), (4, 1, 2, 3, 2, 2, 2, 2), (1, 1, 2, 1, 1, 1), (1,) * 6, (1, 1, 1, 1, 2, 1), 4),
+    ],
+    ids=["r4", "r5", "r6"],
+)
+def test_frames_helper_matches_oracle(case):
+    """tests/helpers.frames_reference (recursive frames decomposition down to F.conv3d, the
+    full-size GPU checker) agrees with the oracle in value and in all three gradients."""
+    x_shape, w_shape, stride, padding, dilation, groups = case
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(x_shape, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(w_shape, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(w_shape[0], generator=g, dtype=torch.float64, requires_grad=True)
+    y = helpers.frames_reference(x, w, b, stride, padding, dilation, groups)
+    args = (stride, padding, dilation, groups)
+    ref_y = oracle.forward(x.detach().numpy(), w.detach().numpy(), b.detach().numpy(), *args)
+    np.testing.assert_allclose(y.detach().numpy(), ref_y, rtol=1e-11, atol=1e-11)
+    dy = torch.randn(y.shape, generator=g, dtype=torch.float64)
+    dx, dw, db = torch.autograd.grad(y, (x, w, b), dy)
+    ref = oracle.backward(dy.numpy(), x.detach().numpy(), w.detach().numpy(), *args)
+    for got, want in zip((dx, dw, db), ref):
+        np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+
+
 def test_flops_formula():
     assert oracle.flops((2, 32, 16, 16, 16, 16), (64, 32, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4) == \
         2 * 2 * 16**4 * 64 * 32 * 81
