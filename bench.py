@@ -154,6 +154,10 @@ def main():
     parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument(
+        "--calibration-copy-mib", type=int, default=0,
+        help="first run a plain elementwise copy of this many MiB three times (the known-size "
+        "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -175,6 +179,13 @@ def main():
     torch_convnd.load_native()
     lib = _build.hip_library()
     device = torch.device("cuda", 0)
+    if args.calibration_copy_mib > 0:
+        src = torch.ones(args.calibration_copy_mib << 18, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # reads and writes exactly the tensor's bytes
+        torch.cuda.synchronize()
+        del src, dst
     x, w, b = make_inputs(torch, torch.bfloat16, device)
 
     def conv(xx, ww, bb):

@@ -339,11 +339,11 @@ int64_t choose_pitches(int R, const int* box, const int* sigma, const int* hext,
 
 // Optional launch-plan override for tuning sweeps, read once per process from
 // CONVND_HIP_FWD_PLAN / CONVND_HIP_DGRAD_PLAN / CONVND_HIP_WGRAD_PLAN, e.g.
-// "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8" (the weight gradient reads box only).
+// "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8" (the weight gradient reads box and occ).
 // Any subset of the keys may be given; the planner then searches only plans matching it and
 // ignores the override when none does.
 struct PlanFilter {
-  int mb = 0, nb = 0, wm = 0, cc = 0;
+  int mb = 0, nb = 0, wm = 0, cc = 0, occ = 0;
   std::vector<int> box;
   bool active = false;
 };
@@ -375,6 +375,7 @@ PlanFilter parse_filter(const char* text) {
         if (key == "nb") f.nb = v;
         if (key == "wm") f.wm = v;
         if (key == "cc") f.cc = v;
+        if (key == "occ") f.occ = v;
       }
     }
     pos = end + 1;
@@ -631,9 +632,14 @@ double schedule_cost(int64_t wgs, int occ, double core_clk, double load_clk) {
 struct WgradPlan {
   bool ok = false;
   int mb = 1;
+  int stg = 8;         // staging registers per thread, in 16-byte entries
+  bool multi = false;  // items staged in several batches
+  bool exact = true;   // the boxes tile grad_output exactly (no padded copy needed)
   WgradArgs args{};
+  PadArgs pad{};
   size_t lds = 0;
-  size_t staged_elems = 0;
+  size_t staged_elems = 0;   // zero-padded octet-major copy of the input
+  size_t dy_pad_elems = 0;   // grad_output padded to whole boxes (used when needed)
   size_t partial_elems = 0;
   double cost = 0.0;
 };
@@ -677,51 +683,84 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
         for (int a = 0; a < R; ++a)
           if (filter.box[a] != b[a]) return;
       }
-      int hext[kFastRank], hpitch[kFastRank];
-      int64_t rows = 1, boxes = 1;
+      int hext[kFastRank], hpitch[kFastRank], pe[kFastRank];
+      int64_t boxes = 1, pvol = 1;
       for (int a = 0; a < R; ++a) {
-        hext[a] = static_cast<int>((b[a] - 1) * g.s[a] + (g.k[a] - 1) * g.d[a] + 1);
-        if ((a < R - 1 && hext[a] > 64) || hext[a] > 255) return;
-        if (a < R - 1) rows *= hext[a];
-        boxes *= (g.out[a] + b[a] - 1) / b[a];
+        const int64_t h = (b[a] - 1) * g.s[a] + (g.k[a] - 1) * g.d[a] + 1;
+        const int64_t nb = (g.out[a] + b[a] - 1) / b[a];
+        // Padded extent: every box's halo, origin at input coordinate -padding.
+        const int64_t e = (nb - 1) * b[a] * g.s[a] + h;
+        if (h > 4096 || e > kI32Safe) return;
+        hext[a] = static_cast<int>(h);
+        pe[a] = static_cast<int>(e);
+        boxes *= nb;
+        pvol *= e;
+        if (pvol > kI32Safe) return;
       }
+      // The padded copy must stay int32-addressable and not dwarf the input.
+      if (pvol * g.batch * g.channels > kI32Safe / 2 || pvol > 8 * g.in_vol + (1 << 20)) return;
       hpitch[R - 1] = 1;
       for (int a = R - 2; a >= 0; --a) hpitch[a] = hpitch[a + 1] * hext[a + 1];
       const int64_t plane_pos = (int64_t)hpitch[0] * hext[0];
+      if (plane_pos > (1 << 16)) return;
       const int64_t plane_bytes = align_up(plane_pos * 16);
-      const int box_rows = box_vol / b[R - 1];
       const int dyrow = box_vol * 2 + 32;
       const int64_t lds_dy = max_oct * plane_bytes;
       const int64_t lds_pos = lds_dy + align_up((int64_t)mb * 16 * dyrow);
-      const int64_t lds_rows = lds_pos + align_up((int64_t)box_vol * 4);
-      const int64_t lds = lds_rows + align_up((5 * rows + box_rows) * 4);
-      if (lds > kLdsBudget || rows > (int64_t{1} << 20)) return;
-      const int occ = occupancy(lds);
+      const int64_t lds_rel = lds_pos + align_up((int64_t)box_vol * 4);
+      const int64_t lds_items = lds_rel + align_up(plane_pos * 4);
+      if (lds_items > kLdsBudget) return;
+      // grad_output is read in runs of 8 positions along the box's last axis; when the boxes
+      // do not tile the output exactly it is read from a copy padded to whole boxes.
+      int64_t dvol = 1;
+      for (int a = 0; a < R; ++a) dvol *= ((g.out[a] + b[a] - 1) / b[a]) * b[a];
+      if (dvol * g.batch * g.out_channels > kI32Safe / 2) return;
+      // Staging slots per thread (16-byte registers), the next item's held across the MFMAs;
+      // an item needing more than the register budget stages the rest in batches of 8.
+      const int64_t entries = max_oct * plane_pos + (int64_t)mb * 16 * (box_vol / 8);
+      const int stg_max = 24;
+      int stg = static_cast<int>((entries + kThreads - 1) / kThreads);
+      stg = (stg + 7) / 8 * 8;
+      const bool multi = stg > stg_max;
+      if (multi) stg = 8;
+      const int64_t batches = (entries + stg * kThreads - 1) / (stg * kThreads);
       const int64_t items = boxes * g.batch;
       const int64_t per_chunk_wgs = (int64_t)ncq * g.groups * mgroups;
-      int64_t npc = std::max<int64_t>(1, (256 * occ) / per_chunk_wgs);
+      int64_t npc = std::max<int64_t>(1, 256 / per_chunk_wgs);
       npc = std::min<int64_t>(npc, items);
       const int64_t ipc = (items + npc - 1) / npc;
       npc = (items + ipc - 1) / ipc;
-      // Per item: MFMA issue of one wave (8 fragments x MB tiles per K32 step) and the
-      // staging of the octet planes and the grad_output tile (~64 B/clock/CU plus latency).
-      const double mfma_item = double(box_vol / 32) * 8 * mb * 16.0;
-      const double stage_item =
-          (double(max_oct) * plane_pos * 16 + double(mb) * 16 * box_vol * 2) / 64.0 + 2500.0;
-      const double eff = occ >= 2 ? 0.75 : 0.55;
-      const double per_wg = double(ipc) * (mfma_item / eff + stage_item * (occ >= 2 ? 0.4 : 1.0));
+      if (npc * per_chunk_wgs > INT32_MAX) return;
+      // Item table: 8 bytes per item of a workgroup's range.
+      const int64_t lds = lds_items + align_up(ipc * 8);
+      if (lds > kLdsBudget) return;
+      // Per item: MFMA issue of one wave (8 fragments x MB tiles per K32 step) against the
+      // staging of the next item (~64 B/clock/CU of L2 traffic), which overlap only in part,
+      // plus ~1500 clocks of per-item work (barriers, LDS stores); unprefetched batches add
+      // ~3000 clocks of latency each.
+      const double mfma_item = double(box_vol / 32) * 8 * mb * 16.0 / 0.85;
+      const double stage_bw =
+          (double(max_oct) * plane_pos * 16 + double(mb) * 16 * box_vol * 2) / 64.0;
+      const double per_wg =
+          double(ipc) * (std::max(mfma_item, stage_bw) + 0.3 * stage_bw + 1500.0 +
+                         3000.0 * double(batches - 1)) +
+          4000.0;
       const int64_t wgs = npc * per_chunk_wgs;
-      const double rounds = double((wgs + 256 * occ - 1) / (256 * occ));
-      // Partial sums: written once per position chunk and read back by the reduction.
-      const double partial_clk = double(npc) * g.out_channels * cin_g * k_vol * 8 / 3300.0;
+      const double rounds = double((wgs + 255) / 256);
+      // Partial sums: 16-byte lane vectors written once per position chunk, read back by the
+      // reduction (~3 KB/clock across the chip).
+      const double partial_clk = double(npc) * per_chunk_wgs * 4 * mb * 8 * 64 * 16 * 2 / 3000.0;
       const double cost = rounds * per_wg + partial_clk;
       if (best >= 0 && cost >= best) return;
       best = cost;
       plan.ok = true;
       plan.mb = mb;
+      plan.multi = multi;
       plan.cost = cost;
       WgradArgs& A = plan.args;
       std::memset(&A, 0, sizeof(A));
+      PadArgs& P = plan.pad;
+      std::memset(&P, 0, sizeof(P));
       A.rank = R;
       A.batch = static_cast<int>(g.batch);
       A.groups = static_cast<int>(g.groups);
@@ -729,36 +768,45 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       A.cout_g = cout_g;
       A.cin_total = static_cast<int>(g.channels);
       A.cout_total = static_cast<int>(g.out_channels);
-      int ivol = 1, ovol = 1;
+      P.rank = R;
+      P.channels = A.cin_total;
+      int ovol = 1, pstride = 1;
+      for (int a = R - 1; a >= 0; --a) {
+        A.pstride[a] = pstride;
+        pstride *= pe[a];
+      }
       for (int a = 0; a < R; ++a) {
-        A.in_size[a] = static_cast<int>(g.in[a]);
         A.out_size[a] = static_cast<int>(g.out[a]);
-        ivol *= A.in_size[a];
         ovol *= A.out_size[a];
         A.k[a] = static_cast<int>(g.k[a]);
         A.s[a] = static_cast<int>(g.s[a]);
-        A.p[a] = static_cast<int>(g.p[a]);
         A.d[a] = static_cast<int>(g.d[a]);
         A.box[a] = b[a];
         A.box_shift[a] = 0;
         while ((1 << A.box_shift[a]) < b[a]) ++A.box_shift[a];
         A.nbox[a] = static_cast<int>((g.out[a] + b[a] - 1) / b[a]);
+        A.dext[a] = A.nbox[a] * b[a];
         A.hext[a] = hext[a];
         A.hpitch[a] = hpitch[a];
+        P.in[a] = static_cast<int>(g.in[a]);
+        P.pe[a] = pe[a];
+        P.pad[a] = static_cast<int>(g.p[a]);
       }
-      A.in_vol = ivol;
+      P.in_vol = static_cast<int>(g.in_vol);
+      P.pvol = static_cast<int>(pvol);
       A.out_vol = ovol;
+      A.pvol = static_cast<int>(pvol);
       A.k_vol = k_vol;
       A.box_vol = box_vol;
       A.boxes = static_cast<int>(boxes);
-      A.rows = static_cast<int>(rows);
-      A.hlast = hext[R - 1];
+      A.plane_pos = static_cast<int>(plane_pos);
+      A.inv_plane_pos = 1.0f / static_cast<float>(plane_pos);
       A.plane_bytes = static_cast<int>(plane_bytes);
       A.max_oct = max_oct;
       A.dyrow = dyrow;
-      int vec = 8;
-      while (vec > 1 && (b[R - 1] % vec != 0 || out_last % vec != 0)) vec /= 2;
-      A.dy_vec = vec;
+      A.dvol = static_cast<int>(dvol);
+      plan.stg = stg;
+      plan.exact = dvol == g.out_vol;
       A.mtiles = mtiles;
       A.mgroups = mgroups;
       A.npairs = npairs;
@@ -768,13 +816,16 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       A.items_per_pc = static_cast<int>(ipc);
       A.lds_dy = static_cast<int>(lds_dy);
       A.lds_pos = static_cast<int>(lds_pos);
-      A.lds_rows = static_cast<int>(lds_rows);
+      A.lds_rel = static_cast<int>(lds_rel);
+      A.lds_items = static_cast<int>(lds_items);
       plan.lds = static_cast<size_t>(lds);
     });
   }
   if (plan.ok) {
-    plan.staged_elems = (size_t)g.batch * g.in_vol * g.channels;
-    plan.partial_elems = (size_t)plan.args.npc * g.out_channels * g.cin_g * g.k_vol;
+    plan.staged_elems = (size_t)g.batch * plan.args.pvol * g.channels;
+    plan.dy_pad_elems = (size_t)g.batch * plan.args.dvol * g.out_channels;
+    plan.partial_elems =
+        (size_t)plan.args.npc * wgrad_partial_slots(plan.mb, plan.args) * 4;
   }
   return plan;
 }
@@ -845,6 +896,7 @@ struct BackwardSetup {
   IgemmPlan dg;
   WgradPlan wg;
   size_t off_dy_stage = 0, off_wpk = 0, off_x_stage = 0, off_partial = 0, off_bias = 0;
+  size_t off_dy_pad = 0;
   size_t bytes = 0;
 };
 
@@ -869,6 +921,7 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
     if (b.wg.ok) {
       b.off_x_stage = L.take(b.wg.staged_elems * es);
       b.off_partial = L.take(b.wg.partial_elems * sizeof(float));
+      b.off_dy_pad = L.take(b.wg.dy_pad_elems * es);
     }
   }
   if (gb) {
@@ -1116,25 +1169,31 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       WgradArgs A = b.wg.args;
       void* staged = ws + b.off_x_stage;
       float* partial = reinterpret_cast<float*>(ws + b.off_partial);
-      st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels,
-                                             g.in_vol, nullptr, stream),
-                     "channels-last staging of input");
+      st = hip_check(launch_to_octets_padded(dtype, input, staged, g.batch, b.wg.pad, stream),
+                     "padded octet-major staging of input");
       if (st != CONVND_HIP_SUCCESS) return st;
       A.x = staged;
       A.dy = grad_output;
       A.partial = partial;
-      // Vector copies of grad_output rows need the base aligned to the vector width.
-      while (A.dy_vec > 1 &&
-             reinterpret_cast<uintptr_t>(grad_output) % (uintptr_t(A.dy_vec) * 2) != 0)
-        A.dy_vec /= 2;
+      const int64_t es = element_size(dtype);
+      A.x_bytes = static_cast<int>(b.wg.staged_elems * es);
+      A.dy_bytes = static_cast<int>(b.wg.dy_pad_elems * es);
+      // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the
+      // boxes tile it exactly and its base is 16-byte aligned.
+      if (!b.wg.exact || reinterpret_cast<uintptr_t>(grad_output) % 16 != 0) {
+        void* padded = ws + b.off_dy_pad;
+        st = hip_check(launch_pad_grad_output(grad_output, padded, A, stream),
+                       "padded copy of grad_output");
+        if (st != CONVND_HIP_SUCCESS) return st;
+        A.dy = padded;
+      }
       const auto ev = timing_begin(2, stream);
-      st = hip_check(launch_wgrad_mfma(dtype, b.wg.mb, A, b.wg.lds, stream),
-                     "MFMA weight gradient");
+      st = hip_check(
+          launch_wgrad_mfma(dtype, b.wg.mb, b.wg.stg, b.wg.multi, A, b.wg.lds, stream),
+          "MFMA weight gradient");
       timing_end(ev, stream);
       if (st != CONVND_HIP_SUCCESS) return st;
-      st = hip_check(launch_reduce_partials(dtype, partial, grad_weight,
-                                            (int64_t)g.out_channels * g.cin_g * g.k_vol,
-                                            A.npc, stream),
+      st = hip_check(launch_wgrad_reduce(dtype, b.wg.mb, A, grad_weight, stream),
                      "weight-gradient reduction");
     } else {
       st = hip_check(launch_direct_grad_weight(dtype, to_direct(g), grad_output, input,
@@ -1183,14 +1242,15 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
     } else {
       const WgradArgs& A = p.args;
       text = "{\"kernel\":\"mfma_wgrad\",\"mb\":" + std::to_string(p.mb) +
+             ",\"stg\":" + std::to_string(p.stg) +
              ",\"box\":" + join(A.box, A.rank) + ",\"boxes\":" + std::to_string(A.boxes) +
              ",\"npc\":" + std::to_string(A.npc) + ",\"items_per_pc\":" +
              std::to_string(A.items_per_pc) + ",\"ncq\":" + std::to_string(A.ncq) +
              ",\"max_oct\":" + std::to_string(A.max_oct) +
-             ",\"mgroups\":" + std::to_string(A.mgroups) + ",\"dy_vec\":" +
-             std::to_string(A.dy_vec) + ",\"lds\":" + std::to_string(p.lds) +
-             ",\"occupancy\":" + std::to_string(occupancy(static_cast<int64_t>(p.lds))) +
-             ",\"workgroups\":" +
+             ",\"mgroups\":" + std::to_string(A.mgroups) + ",\"lds\":" +
+             std::to_string(p.lds) +
+             ",\"multi\":" + std::to_string(p.multi ? 1 : 0) + ",\"exact\":" +
+             std::to_string(p.exact ? 1 : 0) + ",\"workgroups\":" +
              std::to_string((int64_t)A.npc * A.ncq * A.groups * A.mgroups) + "}";
     }
   } else {

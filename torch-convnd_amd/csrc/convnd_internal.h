@@ -69,26 +69,31 @@ struct IgemmArgs {
 // LDS: [max_oct octet planes | grad_output tile | box position offsets | halo row tables
 // (5 * rows ints) | box row offsets (box_vol / box[rank-1] ints)].
 struct WgradArgs {
-  const void* x;      // channels-last input [N][in_vol][cin_total]
+  const void* x;      // zero-padded octet-major input [N][cin_total/8][pe...][8] (PadArgs)
   const void* dy;     // grad_output [N][cout_total][out_vol]
-  float* partial;     // [npc][cout_total][cin_g][k_vol]
+  float* partial;     // per-lane accumulator vectors, see wgrad_partial_slots
+  int x_bytes, dy_bytes;  // sizes of the two buffers (loads past them read zero)
   int rank;
   int batch, groups, cin_g, cout_g, cin_total, cout_total;
-  int in_size[kFastRank], out_size[kFastRank];
-  int in_vol, out_vol, k_vol;
-  int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
+  int out_size[kFastRank];
+  int out_vol, k_vol;
+  int dext[kFastRank];       // extents of the grad_output buffer read (output, or padded to
+  int dvol;                  // whole boxes), and its per-channel volume
+  int pstride[kFastRank];    // position strides of the padded input
+  int pvol;                  // positions per padded image
+  int k[kFastRank], s[kFastRank], d[kFastRank];
   int box[kFastRank], box_shift[kFastRank], nbox[kFastRank];
   int box_vol, boxes;
-  int hext[kFastRank], hpitch[kFastRank];  // halo of every tap, plane position pitches
-  int rows, hlast;           // halo rows (all axes but the last) and last-axis extent
-  int plane_bytes;           // LDS bytes per octet plane
+  int hext[kFastRank], hpitch[kFastRank];  // halo of every tap, dense plane pitches
+  int plane_pos;             // positions per octet plane (product of hext)
+  float inv_plane_pos;       // 1 / plane_pos (division of staging indices)
+  int plane_bytes;           // LDS bytes per octet plane (plane_pos * 16, 256-aligned)
   int max_oct;               // octet planes reserved
   int dyrow;                 // LDS bytes per grad_output tile row (box_vol*2 + 32)
-  int dy_vec;                // grad_output elements per vector load (8, 4, 2 or 1)
   int mtiles, mgroups;
   int npairs, ncq;
   int npc, items, items_per_pc;
-  int lds_dy, lds_pos, lds_rows;  // LDS byte offsets of the regions after the planes
+  int lds_dy, lds_pos, lds_rel, lds_items;  // LDS byte offsets of the regions after the planes
 };
 
 // ---- kernel launchers (defined in the .hip files) -------------------------------------
@@ -99,6 +104,17 @@ hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void
                                    int64_t batch, int64_t channels, int64_t volume,
                                    float* chan_sums, hipStream_t stream);
 int64_t channel_last_sum_blocks(int64_t batch, int64_t volume);
+
+// Zero-padded octet-major copy: dst[n][c/8][u_0]..[u_{R-1}][c%8] = src[n][c][u - pad] (zero
+// when u - pad lies outside the input), u_a < pe[a]. 16-bit element types, channels % 8 == 0.
+struct PadArgs {
+  int rank, channels;
+  int in[kFastRank], pe[kFastRank], pad[kFastRank];
+  int in_vol, pvol;
+};
+hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void* dst,
+                                          int64_t batch, const PadArgs& args,
+                                          hipStream_t stream);
 // db[c] = sum of the nsum partial sums of channel c (fixed order).
 hipError_t launch_grad_bias_from_sums(convnd_hip_dtype dtype, const float* sums, int64_t nsum,
                                       int64_t channels, void* db, hipStream_t stream);
@@ -121,8 +137,18 @@ hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs&
 // Whether launch_igemm has a compiled kernel for this wave tile (mb x nb fragments) and
 // wave arrangement (wm waves along output channels).
 bool igemm_tile_supported(int mb, int nb, int wm);
-hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, const WgradArgs& a,
-                             size_t lds_bytes, hipStream_t stream);
+// stg: staging slots per thread (8, 16 or 24); multi: the item's staging takes
+// several batches of 8 slots (only the first is prefetched).
+hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
+                             const WgradArgs& a, size_t lds_bytes, hipStream_t stream);
+// grad_output zero-padded to whole boxes (extents a.dext) for the weight gradient.
+hipError_t launch_pad_grad_output(const void* dy, void* dst, const WgradArgs& a,
+                                  hipStream_t stream);
+// Float slots (x4) of one position chunk's partial sums, and the pass that adds the npc
+// chunks in order and writes dW in the weight layout.
+int64_t wgrad_partial_slots(int mb, const WgradArgs& a);
+hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& a, void* dw,
+                               hipStream_t stream);
 hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream);
 hipError_t launch_reduce_partials(convnd_hip_dtype dtype, const float* partial, void* out,
                                   int64_t count, int64_t parts, hipStream_t stream);

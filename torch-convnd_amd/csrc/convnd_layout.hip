@@ -5,6 +5,11 @@
 //     partial sums of every channel over its 64-position tile, which the bias gradient
 //     (the reference's flat_grad.sum({0, 3}), src/torch_convnd/csrc/convnd.cpp:388-390)
 //     then reduces without reading grad_output again.
+//   * to_octets_padded16: [N][C][in...] -> [N][C/8][pe...][8], octet-major (8 channels = 16
+//     bytes per position, one contiguous plane per octet), where padded coordinate u holds
+//     input coordinate u - pad (zero outside the input): every halo a convolution box reads
+//     is then in bounds and each octet's rows are contiguous, so the consumer stages it with
+//     coalesced loads and no validity tests.
 //   * channel_sums: the same partial sums straight from [N][C][V] (bias gradient when no
 //     transposed copy of grad_output is made).
 //   * reduce_channel_sums: db[c] = sum over the partials of channel c in a fixed order.
@@ -87,6 +92,76 @@ __global__ __launch_bounds__(kThreads) void to_channels_last16_kernel(
       v[k] = tile[(cg + 2 * k) * kTileStride + p] |
              ((unsigned)tile[(cg + 2 * k + 1) * kTileStride + p] << 16);
     *reinterpret_cast<u32x4*>(d + (size_t)p * channels + cg) = v;
+  }
+}
+
+// Block (position tile, channel tile, n): 64 consecutive padded positions (flattened,
+// crossing rows) times 64 channels, through an LDS tile. Each position's source offset is
+// decoded once into LDS; loads are 2-byte with lanes along positions (coalesced within a
+// row, any alignment); stores are 16 bytes (one octet) with lanes along positions, so every
+// octet plane of the destination is written contiguously.
+__global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const unsigned short* src,
+                                                                     unsigned short* dst,
+                                                                     PadArgs P) {
+  __shared__ __align__(16) unsigned short tile[kTileC * kTileStride];
+  __shared__ int srcoff[kTileV];
+  const int tid = threadIdx.x;
+  const int R = P.rank;
+  const int p0 = blockIdx.x * kTileV;
+  const int c0 = blockIdx.y * kTileC;
+  const int n = blockIdx.z;
+  const int ct = P.channels - c0 < kTileC ? P.channels - c0 : kTileC;
+  const int vt = P.pvol - p0 < kTileV ? P.pvol - p0 : kTileV;
+  if (tid < kTileV) {
+    int off = -1;
+    if (tid < vt) {
+      int rem = p0 + tid, istr = 1;
+      off = 0;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < R) {
+          const int u = rem % P.pe[a];
+          rem /= P.pe[a];
+          const int i = u - P.pad[a];
+          if (off >= 0 && i >= 0 && i < P.in[a]) {
+            off += i * istr;
+          } else {
+            off = -1;
+          }
+          istr *= P.in[a];
+        }
+      }
+    }
+    srcoff[tid] = off;
+  }
+  __syncthreads();
+  const unsigned short* s = src + ((size_t)n * P.channels + c0) * P.in_vol;
+  unsigned short e[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = tid + j * kThreads;
+    const int c = i >> 6, v = i & 63;
+    const int so = srcoff[v];
+    e[j] = (c < ct && so >= 0) ? s[(size_t)c * P.in_vol + so] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = tid + j * kThreads;
+    tile[(i >> 6) * kTileStride + (i & 63)] = e[j];
+  }
+  __syncthreads();
+  const int octs = P.channels >> 3;
+  const int cgroups = ct >> 3;
+  for (int i = tid; i < cgroups * kTileV; i += kThreads) {
+    const int cg = i >> 6, v = i & 63;
+    if (v >= vt) continue;
+    u32x4 w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = tile[(cg * 8 + 2 * k) * kTileStride + v] |
+             ((unsigned)tile[(cg * 8 + 2 * k + 1) * kTileStride + v] << 16);
+    const size_t plane = (size_t)n * octs + (c0 >> 3) + cg;
+    *reinterpret_cast<u32x4*>(dst + (plane * P.pvol + p0 + v) * 8) = w;
   }
 }
 
@@ -200,6 +275,24 @@ hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void
                      static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst),
                      static_cast<int>(channels), static_cast<int>(volume), chan_sums,
                      static_cast<int>(grid.x * batch), dtype == CONVND_HIP_BFLOAT16);
+  return hipGetLastError();
+}
+
+hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void* dst,
+                                          int64_t batch, const PadArgs& args,
+                                          hipStream_t stream) {
+  if (batch == 0 || args.channels == 0 || args.pvol == 0) return hipSuccess;
+  if (dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16) return hipErrorInvalidValue;
+  if (args.channels % 8 != 0 || args.rank < 1 || args.rank > kFastRank || batch > 65535)
+    return hipErrorInvalidValue;
+  const int64_t blocks = ((int64_t)args.pvol + kTileV - 1) / kTileV;
+  const int64_t ctiles = (args.channels + kTileC - 1) / kTileC;
+  if (blocks > 0x7fffffff || ctiles > 65535) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ctiles),
+                  static_cast<unsigned>(batch));
+  hipLaunchKernelGGL(to_octets_padded16_kernel, grid, dim3(kThreads), 0, stream,
+                     static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst),
+                     args);
   return hipGetLastError();
 }
 

@@ -7,18 +7,24 @@
 //   * Columns are (octet of 8 input channels, tap) pairs, octet slowest. A workgroup owns 64
 //     consecutive pairs (so one or two octets) and all output channels of one M group; each
 //     of its four waves owns 16 pairs, i.e. 128 columns, times MB tiles of 16 channels.
-//   * Per box of positions the workgroup stages, into LDS, the input halo of every tap for
-//     its octets (one plane per octet, 16 bytes = 8 channels per position, zero outside the
-//     tensor) and the grad_output tile [channels][box positions] (rows skewed by 32 bytes so
-//     the 16-lane A-fragment reads hit distinct bank slots).
+//   * Per box of positions (an "item") the workgroup stages into LDS the input halo of every
+//     tap for its octets (one plane per octet, 16 bytes = 8 channels per position) from a
+//     zero-padded octet-major copy of the input, and the grad_output tile [channels][box
+//     positions] (rows skewed by 32 bytes so the 16-lane A-fragment reads hit distinct bank
+//     slots) from grad_output itself when the boxes tile it exactly, else from a zero-padded
+//     copy. Either way every load is in bounds and needs no validity test.
+//   * One workgroup per CU (one wave per SIMD, up to 512 registers per lane): the loads of
+//     the next item are issued into registers before the MFMAs of the current one, so their
+//     latency hides behind the matrix work, and the LDS fragments of the next K step are
+//     read while the current step's MFMAs run. A thread's staging slots have item-invariant
+//     offsets, computed once; per item only two base offsets (from an LDS item table) change.
 //   * A fragments: 8 consecutive positions of one grad_output row (one 16-byte read).
 //     B fragments: a lane reads 8 positions x 8 channels of its pair (eight 16-byte reads at
-//     position offsets + the tap's offset) and transposes them in registers into eight
-//     fragments, one per channel of the octet.
-//   * Each workgroup reduces a fixed range of (image, box) items into fp32 partial sums that
-//     a second pass adds in a fixed order (deterministic, no atomics).
-// All per-workgroup tables (position offsets, halo rows) are built once; per box only the
-// origin, the row validity and the staging change.
+//     position offsets + the tap's offset) and transposes them in registers (v_perm) into
+//     eight fragments, one per channel of the octet.
+//   * Each workgroup reduces a fixed range of items into fp32 partial sums, stored as each
+//     lane's accumulator vectors (16-byte coalesced stores); a second pass adds them in a
+//     fixed order and scatters them into the weight layout (deterministic, no atomics).
 
 #include "convnd_internal.h"
 #include "convnd_types.h"
@@ -26,84 +32,58 @@
 namespace convnd {
 namespace {
 
+// Buffer resource word 3 for raw (unstructured) loads: 32-bit data format, no swizzle.
+constexpr int kRsrcWord3 = 0x00020000;
+// Byte offset past every buffer this kernel reads: such a load returns zero.
+constexpr unsigned kOob = 0x80000000u;
+
+// Low halves of a and b as one dword (a's in the low half): v_perm_b32 byte selection.
 __device__ __forceinline__ unsigned lo_pair(unsigned a, unsigned b) {
-  return (a & 0xffffu) | (b << 16);
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
 }
+// High halves of a and b as one dword (a's in the low half).
 __device__ __forceinline__ unsigned hi_pair(unsigned a, unsigned b) {
-  return (a >> 16) | (b & 0xffff0000u);
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-template <int VEC>
-__device__ __forceinline__ void copy_vec(unsigned char* dst, const unsigned char* src, bool ok) {
-  if constexpr (VEC == 8) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (ok) v = *reinterpret_cast<const u32x4*>(src);
-    *reinterpret_cast<u32x4*>(dst) = v;
-  } else if constexpr (VEC == 4) {
-    uint2 v = {0u, 0u};
-    if (ok) v = *reinterpret_cast<const uint2*>(src);
-    *reinterpret_cast<uint2*>(dst) = v;
-  } else if constexpr (VEC == 2) {
-    unsigned v = 0;
-    if (ok) v = *reinterpret_cast<const unsigned*>(src);
-    *reinterpret_cast<unsigned*>(dst) = v;
-  } else {
-    unsigned short v = 0;
-    if (ok) v = *reinterpret_cast<const unsigned short*>(src);
-    *reinterpret_cast<unsigned short*>(dst) = v;
-  }
-}
-
-// grad_output box tile [rows][box positions] -> LDS with VEC positions per copy.
-// dyrowoff[br]: output offset of box row br's first position (-1 outside the output).
-// runs = blast / VEC and box_rows are powers of two (log2 in runs_shift, rows_shift).
-template <typename T, int VEC>
-__device__ __forceinline__ void stage_dy(unsigned char* dyt, const int* dyrowoff, int rows,
-                                         int rows_shift, int runs_shift, int blast, int j0last,
-                                         int out_last, const T* dy_base, int out_vol,
-                                         int co_valid, int dyrow) {
-  const int per_ch_shift = rows_shift + runs_shift;
-  const int items = rows << per_ch_shift;
-  const int run_mask = (1 << runs_shift) - 1;
-  const int ch_mask = (1 << per_ch_shift) - 1;
-  for (int it = threadIdx.x; it < items; it += kThreads) {
-    const int row = it >> per_ch_shift;
-    const int c = it & ch_mask;
-    const int br = c >> runs_shift;
-    const int run = c & run_mask;
-    const int ro = dyrowoff[br];
-    const int col = j0last + run * VEC;
-    const bool ok = row < co_valid && ro >= 0 && col < out_last;
-    const T* src = dy_base + (size_t)row * out_vol + (ok ? ro + col : 0);
-    copy_vec<VEC>(dyt + row * dyrow + (br * blast + run * VEC) * 2,
-                  reinterpret_cast<const unsigned char*>(src), ok);
-  }
-}
-
-template <typename T, int MB>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// MULTI == false: an item's staging fits one batch of STG slots per thread, prefetched.
+// MULTI == true: the first batch is prefetched, the rest staged synchronously.
+template <typename T, int MB, int STG, bool MULTI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void wgrad_kernel(WgradArgs A) {
   using M = Mfma16<T>;
   using frag = typename M::frag;
   extern __shared__ __align__(16) unsigned char lds[];
-  unsigned char* dyt = lds + A.lds_dy;
+  const unsigned char* dyt = lds + A.lds_dy;
   int* posoff = reinterpret_cast<int*>(lds + A.lds_pos);
-  int* rowlds = reinterpret_cast<int*>(lds + A.lds_rows);
-  int* rowrel = rowlds + A.rows;
-  int* rowh0 = rowrel + A.rows;
-  int* rowh1 = rowh0 + A.rows;
-  int* rowin = rowh1 + A.rows;
-  int* dyrowoff = rowin + A.rows;
+  int* halo_rel = reinterpret_cast<int*>(lds + A.lds_rel);
+  int* itab = reinterpret_cast<int*>(lds + A.lds_items);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int R = A.rank;
-  const int pc = blockIdx.x;
-  const int g = blockIdx.z / A.mgroups;
-  const int mg = blockIdx.z % A.mgroups;
+  // One-dimensional grid. Consecutive workgroup ids go round-robin to the eight XCDs; give
+  // each XCD a contiguous run of logical ids, ordered (position chunk, group, pair chunk)
+  // with the pair chunk fastest, so the workgroups that stage the same grad_output tile and
+  // overlapping input halos share one L2.
+  int wid = blockIdx.x;
+  {
+    const int nb = gridDim.x;
+    if (nb >= 8) {
+      const int q = nb >> 3, rem = nb & 7, x = wid & 7, idx = wid >> 3;
+      wid = x * q + (x < rem ? x : rem) + idx;
+    }
+  }
+  const int ntiles = A.groups * A.mgroups * A.ncq;
+  const int tile = wid % ntiles;
+  const int pc = wid / ntiles;
+  const int cq = tile % A.ncq;
+  const int zq = tile / A.ncq;
+  const int g = zq / A.mgroups;
+  const int mg = zq % A.mgroups;
   const int nl = lane & 15;
   const int lg = lane >> 4;
-  const int p0 = blockIdx.y * 64;
+  const int p0 = cq * 64;
   const int p1 = p0 + 64 < A.npairs ? p0 + 64 : A.npairs;
   const int oct_lo = p0 / A.k_vol;
   const int noct = (p1 - 1) / A.k_vol - oct_lo + 1;
@@ -111,6 +91,10 @@ void wgrad_kernel(WgradArgs A) {
   const bool pair_ok = pair < p1;
   const int oct = pair_ok ? pair / A.k_vol : oct_lo;
   const int tap = pair_ok ? pair - oct * A.k_vol : 0;
+  const int co0 = mg * MB * 16;
+  const int oct0 = (g * A.cin_g >> 3) + oct_lo;  // first octet plane of this workgroup
+  const int it0 = pc * A.items_per_pc;
+  const int nitems = (it0 + A.items_per_pc < A.items ? it0 + A.items_per_pc : A.items) - it0;
 
   // This lane's column offset in the halo: plane of its octet + its tap's position offset.
   int coloff;
@@ -126,19 +110,8 @@ void wgrad_kernel(WgradArgs A) {
     }
     coloff = (oct - oct_lo) * A.plane_bytes + off * 16;
   }
-  // Box-relative tables (the same for every box): LDS offset of each box position's halo
-  // base, and for each halo row its LDS position, input offset and coordinates.
-  int istride[kFastRank];
-  {
-    int istr = A.in_size[R - 1];
-#pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        istride[a] = istr;
-        istr *= A.in_size[a];
-      }
-    }
-  }
+  // Box-relative tables, the same for every box: LDS offset of each box position's halo
+  // base, and the padded-input offset (in positions) of each halo position.
   for (int q = tid; q < A.box_vol; q += kThreads) {
     int qq = q, off = 0;
 #pragma unroll
@@ -150,28 +123,131 @@ void wgrad_kernel(WgradArgs A) {
     }
     posoff[q] = off * 16;
   }
-  for (int r = tid; r < A.rows; r += kThreads) {
-    int rem = r, lp = 0, rel = 0;
-    unsigned h0 = 0, h1 = 0;
+  for (int pp = tid; pp < A.plane_pos; pp += kThreads) {
+    int rem = pp, rel = 0;
 #pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
         const int h = rem % A.hext[a];
         rem /= A.hext[a];
-        lp += h * A.hpitch[a];
-        rel += h * istride[a];
-        if (a < 4) {
-          h0 |= (unsigned)h << (8 * a);
-        } else {
-          h1 |= (unsigned)h << (8 * (a - 4));
-        }
+        rel += h * A.pstride[a];
       }
     }
-    rowlds[r] = lp;
-    rowrel[r] = rel;
-    rowh0[r] = (int)h0;
-    rowh1[r] = (int)h1;
+    halo_rel[pp] = rel;
   }
+  // Item table: byte bases of each item's halo (in the octet-major input) and grad_output
+  // tile (in the buffer read, extents dext).
+  for (int k = tid; k < nitems; k += kThreads) {
+    const int it = it0 + k;
+    const int n = it / A.boxes;
+    int bb = it - n * A.boxes;
+    int base = 0, obase = 0, ostr = 1;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < R) {
+        const int j0 = (bb % A.nbox[a]) * A.box[a];
+        bb /= A.nbox[a];
+        base += j0 * A.s[a] * A.pstride[a];
+        obase += j0 * ostr;
+        ostr *= A.dext[a];
+      }
+    }
+    itab[2 * k] = ((n * (A.cin_total >> 3) + oct0) * A.pvol + base) * 16;
+    itab[2 * k + 1] = ((n * A.cout_total + g * A.cout_g + co0) * A.dvol + obase) * 2;
+  }
+  __syncthreads();
+
+  // Last-axis parameters, selected with constant indices (a runtime index into the kernel
+  // argument arrays would force a private copy of the whole argument block).
+  int shift_last = 0, dlast = 8, blast = 8, s_last = 1;
+#pragma unroll
+  for (int a = 0; a < kFastRank; ++a) {
+    if (a == R - 1) {
+      shift_last = A.box_shift[a];
+      dlast = A.dext[a];
+      blast = A.box[a];
+      s_last = A.s[a];
+    }
+  }
+  // grad_output copies of 8 positions: (channel row, box row br, run along the last axis);
+  // box extents are powers of two so the decode is shifts and masks.
+  const int runs_shift = shift_last - 3;
+  int rows_shift = 0;
+#pragma unroll
+  for (int a = 0; a < kFastRank - 1; ++a)
+    if (a < R - 1) rows_shift += A.box_shift[a];
+  const int per_ch_shift = rows_shift + runs_shift;
+  const int dy_items = (MB * 16) << per_ch_shift;
+  const int halo_items = noct * A.plane_pos;
+  const int nh = (A.max_oct * A.plane_pos + kThreads - 1) / kThreads;
+  const int nslots = nh + (dy_items + kThreads - 1) / kThreads;
+  const int co_valid = A.cout_g - co0;
+
+  // Staging slots J = 0, 1, ...: the first nh hold halo entries e = J*256 + tid, the rest
+  // grad_output copies d = (J - nh)*256 + tid. Offsets are relative to the item's bases.
+  auto slot_offsets = [&](int J, unsigned& off, int& dst) {
+    off = kOob;
+    dst = -1;
+    if (J < nh) {
+      const int e = J * kThreads + tid;
+      if (e < halo_items) {
+        int wo = static_cast<int>(static_cast<float>(e) * A.inv_plane_pos);
+        if (wo * A.plane_pos > e) --wo;
+        if ((wo + 1) * A.plane_pos <= e) ++wo;
+        const int pp = e - wo * A.plane_pos;
+        off = static_cast<unsigned>((wo * A.pvol + halo_rel[pp]) * 16);
+        dst = wo * A.plane_bytes + pp * 16;
+      }
+    } else if (J < nslots) {
+      const int d = (J - nh) * kThreads + tid;
+      if (d < dy_items) {
+        const int row = d >> per_ch_shift;
+        const int c = d & ((1 << per_ch_shift) - 1);
+        const int br = c >> runs_shift;
+        const int run = c & ((1 << runs_shift) - 1);
+        int qoff = run * 8, ostr = dlast, rem = br;
+#pragma unroll
+        for (int a = kFastRank - 2; a >= 0; --a) {
+          if (a < R - 1) {
+            qoff += (rem & (A.box[a] - 1)) * ostr;
+            rem >>= A.box_shift[a];
+            ostr *= A.dext[a];
+          }
+        }
+        if (row < co_valid) off = static_cast<unsigned>((row * A.dvol + qoff) * 2);
+        dst = A.lds_dy + row * A.dyrow + (br * blast + run * 8) * 2;
+      }
+    }
+  };
+
+  const T* x = static_cast<const T*>(A.x);
+  const T* dy = static_cast<const T*>(A.dy);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(x), static_cast<short>(0), A.x_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(dy), static_cast<short>(0), A.dy_bytes, kRsrcWord3);
+  u32x4 pre[STG];
+  // One 16-byte buffer load per slot, no branches: halo and grad_output slots differ only
+  // in the resource and base, selected uniformly.
+  auto load_slots = [&](int k, int jb, const unsigned* off) {
+    const unsigned hbase = static_cast<unsigned>(itab[2 * k]);
+    const unsigned dbase = static_cast<unsigned>(itab[2 * k + 1]);
+#pragma unroll
+    for (int j = 0; j < STG; ++j) {
+      const bool h = jb + j < nh;
+      pre[j] = __builtin_amdgcn_raw_buffer_load_b128(h ? xr : dr, off[j] + (h ? hbase : dbase),
+                                                      0, 0);
+    }
+  };
+  auto store_slots = [&](const int* dst) {
+#pragma unroll
+    for (int j = 0; j < STG; ++j)
+      if (dst[j] >= 0) *reinterpret_cast<u32x4*>(lds + dst[j]) = pre[j];
+  };
+  unsigned soff[STG];
+  int sdst[STG];
+#pragma unroll
+  for (int j = 0; j < STG; ++j) slot_offsets(j, soff[j], sdst[j]);
 
   f32x4 acc[MB][8];
 #pragma unroll
@@ -179,229 +255,251 @@ void wgrad_kernel(WgradArgs A) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[mb][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const T* x = static_cast<const T*>(A.x);
-  const T* dy = static_cast<const T*>(A.dy);
-  const int co0 = mg * MB * 16;
-  const int co_valid = A.cout_g - co0;
-  const int hlast = A.hlast;
-  int box_rows = 1;
+  const int ksteps = A.box_vol / 32;  // 4, 8 or 16
+  const int step = s_last * 16;
+  // LDS fragments of K step kc: A from the grad_output tile, B raw (8 positions x 8
+  // channels of this lane's pair) for the in-register transpose.
+  auto read_frags = [&](int kc, frag* a, u32x4* v) {
+    const int q0 = kc * 32 + lg * 8;
 #pragma unroll
-  for (int a = 0; a < kFastRank - 1; ++a)
-    if (a < R - 1) box_rows *= A.box[a];
-  const int blast = A.box[R - 1];
-  int rows_shift = 0;
+    for (int mb = 0; mb < MB; ++mb)
+      a[mb] = *reinterpret_cast<const frag*>(dyt + (mb * 16 + nl) * A.dyrow + q0 * 2);
+    // Positions q0 .. q0+7 lie on one row of the box's last axis (its extent is a multiple
+    // of 8), so their halo offsets step by stride * 16 bytes.
+    const int b0 = posoff[q0] + coloff;
 #pragma unroll
-  for (int a = 0; a < kFastRank - 1; ++a)
-    if (a < R - 1) rows_shift += A.box_shift[a];
-  // log2(blast / vec): blast and vec are powers of two.
-  auto runs_shift = [&](int vec) { return A.box_shift[R - 1] - (vec == 8 ? 3 : vec == 4 ? 2 : vec == 2 ? 1 : 0); };
-  const int it0 = pc * A.items_per_pc;
-  const int it1 = it0 + A.items_per_pc < A.items ? it0 + A.items_per_pc : A.items;
-  // Halo staging walk: item = (octet * rows + row) * hlast + column.
-  const int halo_items = noct * A.rows * hlast;
-  const int sq0 = tid / hlast, sc0 = tid - sq0 * hlast;  // item tid = (so0*rows + sr0)*hlast + sc0
-  const int so0 = sq0 / A.rows, sr0 = sq0 - so0 * A.rows;
-  const int dsr = kThreads / hlast, dsc = kThreads - dsr * hlast;
-  const T* xg = x + g * A.cin_g + oct_lo * 8;
-  for (int it = it0; it < it1; ++it) {
-    const int n = it / A.boxes;
-    int bb = it - n * A.boxes;
-    int J0[kFastRank], horg[kFastRank];
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4*>(lds + b0 + i * step);
+  };
+  auto mfmas = [&](const frag* a, const u32x4* v) {
 #pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        J0[a] = (bb % A.nbox[a]) * A.box[a];
-        bb /= A.nbox[a];
-        horg[a] = J0[a] * A.s[a] - A.p[a];
+    for (int u = 0; u < 8; ++u) {
+      // Fragment u: channel u of the octet at the 8 positions (two per dword).
+      u32x4 t;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        const unsigned lo = v[2 * w2][u >> 1];
+        const unsigned hi = v[2 * w2 + 1][u >> 1];
+        t[w2] = (u & 1) ? hi_pair(lo, hi) : lo_pair(lo, hi);
       }
-    }
-    // Row validity masks over the halo and the halo origin's input offset.
-    unsigned long long valid[kFastRank];
-    int in_base = n * A.in_vol;
+      const frag b = __builtin_bit_cast(frag, t);
 #pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        const int lo = horg[a] < 0 ? -horg[a] : 0;
-        int hi = A.in_size[a] - horg[a];
-        hi = hi < A.hext[a] ? hi : A.hext[a];
-        unsigned long long m = 0;
-        if (hi > lo) {
-          const unsigned long long upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1);
-          m = upto & ~((1ull << lo) - 1);
-        }
-        valid[a] = m;
-        in_base += horg[a] * istride[a];
-      }
+      for (int mb = 0; mb < MB; ++mb) acc[mb][u] = M::run(a[mb], b, acc[mb][u]);
     }
-    __syncthreads();  // tables ready; the previous item's MFMAs are done with the LDS
-    for (int r = tid; r < A.rows; r += kThreads) {
-      const unsigned h0 = (unsigned)rowh0[r], h1 = (unsigned)rowh1[r];
-      bool ok = true;
-#pragma unroll
-      for (int a = 0; a < kFastRank - 1; ++a) {
-        if (a < R - 1) {
-          const unsigned h = ((a < 4 ? h0 : h1) >> (8 * (a & 3))) & 255u;
-          ok = ok && ((valid[a] >> h) & 1ull);
-        }
-      }
-      rowin[r] = ok ? in_base + rowrel[r] : -1;
-    }
-    for (int r = tid; r < box_rows; r += kThreads) {
-      int rem = r, flat = 0, ostr = A.out_size[R - 1];
-      bool ok = true;
-#pragma unroll
-      for (int a = kFastRank - 2; a >= 0; --a) {
-        if (a < R - 1) {
-          const int qa = rem & (A.box[a] - 1);
-          rem >>= A.box_shift[a];
-          const int ja = J0[a] + qa;
-          ok = ok && ja < A.out_size[a];
-          flat += ja * ostr;
-          ostr *= A.out_size[a];
-        }
-      }
-      dyrowoff[r] = ok ? flat : -1;
-    }
-    __syncthreads();
-    // Halo planes, eight loads in flight per thread. Walk state (octet, row, column) of
-    // item b0 + u*256, advanced incrementally (no division per item).
-    {
-      const int corg = horg[R - 1];
-      const int last_size = A.in_size[R - 1];
-      int wo = so0, wr = sr0, wc = sc0;
-      for (int b0 = tid; b0 < halo_items; b0 += 8 * kThreads) {
-        u32x4 v[8];
-        int dsto[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const bool in_range = b0 + u * kThreads < halo_items;
-          const int ro = in_range ? rowin[wr] : -1;
-          const int cl = corg + wc;
-          v[u] = u32x4{0u, 0u, 0u, 0u};
-          if (ro >= 0 && cl >= 0 && cl < last_size)
-            v[u] = *reinterpret_cast<const u32x4*>(xg + (size_t)(ro + cl) * A.cin_total + wo * 8);
-          dsto[u] = in_range ? wo * A.plane_bytes + (rowlds[wr] + wc) * 16 : -1;
-          wc += dsc;
-          wr += dsr;
-          if (wc >= hlast) {
-            wc -= hlast;
-            ++wr;
-          }
-          while (wr >= A.rows) {
-            wr -= A.rows;
-            ++wo;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (dsto[u] >= 0) *reinterpret_cast<u32x4*>(lds + dsto[u]) = v[u];
-      }
-    }
-    {
-      const T* dy_base = dy + ((size_t)n * A.cout_total + g * A.cout_g + co0) * A.out_vol;
-      const int j0last = J0[R - 1];
-      const int out_last = A.out_size[R - 1];
-      switch (A.dy_vec) {
-        case 8:
-          stage_dy<T, 8>(dyt, dyrowoff, MB * 16, rows_shift, runs_shift(8), blast, j0last,
-                         out_last, dy_base, A.out_vol, co_valid, A.dyrow);
-          break;
-        case 4:
-          stage_dy<T, 4>(dyt, dyrowoff, MB * 16, rows_shift, runs_shift(4), blast, j0last,
-                         out_last, dy_base, A.out_vol, co_valid, A.dyrow);
-          break;
-        case 2:
-          stage_dy<T, 2>(dyt, dyrowoff, MB * 16, rows_shift, runs_shift(2), blast, j0last,
-                         out_last, dy_base, A.out_vol, co_valid, A.dyrow);
-          break;
-        default:
-          stage_dy<T, 1>(dyt, dyrowoff, MB * 16, rows_shift, runs_shift(1), blast, j0last,
-                         out_last, dy_base, A.out_vol, co_valid, A.dyrow);
-          break;
-      }
-    }
-    __syncthreads();
+  };
 
-    {
-      const int ksteps = A.box_vol / 32;
-      for (int kc = 0; kc < ksteps; ++kc) {
-        const int q0 = kc * 32 + lg * 8;
-        frag a[MB];
+  // The first batch starts at slot 0, passed through an opaque register so the compiler
+  // selects each slot's resource inside the loop instead of keeping STG selected resources
+  // live across it.
+  auto opaque_zero = []() {
+    int z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    return z;
+  };
+  if (nitems > 0) load_slots(0, opaque_zero(), soff);
+  for (int k = 0; k < nitems; ++k) {
+    __syncthreads();  // the previous item's MFMAs are done with the LDS
+    store_slots(sdst);
+    if constexpr (MULTI) {
+      for (int jb = STG; jb < nslots; jb += STG) {
+        unsigned xoff[STG];
+        int xdst[STG];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          a[mb] = *reinterpret_cast<const frag*>(dyt + (mb * 16 + nl) * A.dyrow + q0 * 2);
-        // Positions q0 .. q0+7 lie on one row of the box's last axis (its extent is a
-        // multiple of 8), so their halo offsets step by stride * 16 bytes.
-        const int base = posoff[q0] + coloff;
-        const int step = A.s[R - 1] * 16;
-        u32x4 v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4*>(lds + base + i * step);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          // Fragment u: channel u of the octet at the 8 positions (two per dword).
-          u32x4 t;
-#pragma unroll
-          for (int w2 = 0; w2 < 4; ++w2) {
-            const unsigned lo = v[2 * w2][u >> 1];
-            const unsigned hi = v[2 * w2 + 1][u >> 1];
-            t[w2] = (u & 1) ? hi_pair(lo, hi) : lo_pair(lo, hi);
-          }
-          const frag b = __builtin_bit_cast(frag, t);
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) acc[mb][u] = M::run(a[mb], b, acc[mb][u]);
-        }
+        for (int j = 0; j < STG; ++j) slot_offsets(jb + j, xoff[j], xdst[j]);
+        load_slots(k, jb, xoff);
+        store_slots(xdst);
       }
+    }
+    __syncthreads();
+    if (k + 1 < nitems) load_slots(k + 1, opaque_zero(), soff);  // in flight during the MFMAs
+    frag a0[MB], a1[MB];
+    u32x4 v0[8], v1[8];
+    read_frags(0, a0, v0);
+    for (int kc = 0; kc < ksteps; kc += 2) {
+      read_frags(kc + 1, a1, v1);
+      mfmas(a0, v0);
+      read_frags(kc + 2 < ksteps ? kc + 2 : kc + 1, a0, v0);
+      mfmas(a1, v1);
     }
   }
 
-  if (pair_ok) {
+  // Partial sums as each lane's accumulators: [pc][tile][wave][mb][u][lane] x 4 floats.
+  f32x4* part = reinterpret_cast<f32x4*>(A.partial) +
+                ((((size_t)pc * ntiles + tile) * 4 + wave) * MB * 8) * 64 + lane;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int co = co0 + mb * 16 + 4 * lg + i;
-        if (co < A.cout_g) {
-          float* dst = A.partial +
-                       (((size_t)pc * A.cout_total + g * A.cout_g + co) * A.cin_g + oct * 8) *
-                           A.k_vol +
-                       tap;
+    for (int u = 0; u < 8; ++u) part[(mb * 8 + u) * 64] = acc[mb][u];
+}
+
+// dW from the partial sums: slot s = ((tile*4 + wave)*MB + mb)*8 + u)*64 + lane holds four
+// output channels of one (pair, input channel); the npc partials are added in order, eight
+// loads in flight.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* part, T* dw,
+                                                                WgradArgs A, int mbv,
+                                                                int64_t nslots) {
+  const int64_t s = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  if (s >= nslots) return;
+  const int lane = static_cast<int>(s & 63);
+  int64_t r = s >> 6;
+  const int u = static_cast<int>(r % 8);
+  r /= 8;
+  const int mb = static_cast<int>(r % mbv);
+  r /= mbv;
+  const int wave = static_cast<int>(r % 4);
+  const int tile = static_cast<int>(r / 4);
+  const int cq = tile % A.ncq;
+  const int zq = tile / A.ncq;
+  const int g = zq / A.mgroups;
+  const int mg = zq % A.mgroups;
+  const int pair = cq * 64 + wave * 16 + (lane & 15);
+  if (pair >= A.npairs) return;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int i = 0;
+  for (; i + 8 <= A.npc; i += 8) {
+    f32x4 v[8];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) dst[(size_t)u * A.k_vol] = acc[mb][u][i];
-        }
-      }
-    }
+    for (int k = 0; k < 8; ++k) v[k] = part[(int64_t)(i + k) * nslots + s];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc += v[k];
+  }
+  for (; i < A.npc; ++i) acc += part[(int64_t)i * nslots + s];
+  const int oct = pair / A.k_vol;
+  const int tap = pair - oct * A.k_vol;
+  const int co_base = mg * mbv * 16 + mb * 16 + 4 * (lane >> 4);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int co = co_base + k;
+    if (co < A.cout_g)
+      dw[(((int64_t)g * A.cout_g + co) * A.cin_g + oct * 8 + u) * A.k_vol + tap] =
+          static_cast<T>(acc[k]);
   }
 }
 
-template <typename T>
-hipError_t wgrad_dispatch(int mb, const WgradArgs& a, size_t lds, hipStream_t s) {
-  const dim3 grid(a.npc, a.ncq, a.groups * a.mgroups);
-#define CONVND_WGRAD_CASE(MBV)                                                           \
-  if (mb == MBV) {                                                                       \
-    auto fn = wgrad_kernel<T, MBV>;                                                      \
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),              \
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,     \
-                                         static_cast<int>(lds));                         \
-    if (err != hipSuccess) return err;                                                   \
-    hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                             \
-    return hipGetLastError();                                                            \
+// Zero-padded copy of grad_output: dst[nc][u...] = src[nc][u...] for u inside the output
+// extents, else zero; each thread writes 8 consecutive elements of the last axis (whose
+// padded extent is a multiple of 8).
+__global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const unsigned short* src,
+                                                            unsigned short* dst, WgradArgs A,
+                                                            int64_t total_runs) {
+  const int R = A.rank;
+  int dlast = 8, olast = 1;
+#pragma unroll
+  for (int a = 0; a < kFastRank; ++a) {
+    if (a == R - 1) {
+      dlast = A.dext[a];
+      olast = A.out_size[a];
+    }
   }
-  CONVND_WGRAD_CASE(1)
-  CONVND_WGRAD_CASE(2)
-  CONVND_WGRAD_CASE(4)
-#undef CONVND_WGRAD_CASE
+  const int runs = dlast >> 3;
+  const int drows = A.dvol / dlast;
+  for (int64_t t = blockIdx.x * (int64_t)kThreads + threadIdx.x; t < total_runs;
+       t += (int64_t)gridDim.x * kThreads) {
+    const int64_t rowd = t / runs;  // (nc, padded row) index
+    const int u0 = static_cast<int>(t - rowd * runs) * 8;
+    const int64_t nc = rowd / drows;
+    int rem = static_cast<int>(rowd - nc * drows);
+    int srow = 0, istr = olast;
+    bool ok = true;
+#pragma unroll
+    for (int a = kFastRank - 2; a >= 0; --a) {
+      if (a < R - 1) {
+        const int u = rem % A.dext[a];
+        rem /= A.dext[a];
+        ok = ok && u < A.out_size[a];
+        srow += u * istr;
+        istr *= A.out_size[a];
+      }
+    }
+    const unsigned short* s = src + nc * A.out_vol + srow;
+    unsigned w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e0 = u0 + 2 * k, e1 = e0 + 1;
+      const unsigned lo = ok && e0 < olast ? s[e0] : 0u;
+      const unsigned hi = ok && e1 < olast ? s[e1] : 0u;
+      w[k] = lo | (hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst + rowd * dlast + u0) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+template <typename T, int MB, int STG, bool MULTI>
+hipError_t wgrad_launch(const WgradArgs& a, size_t lds, hipStream_t s) {
+  auto fn = wgrad_kernel<T, MB, STG, MULTI>;
+  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds));
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(fn, dim3(a.npc * a.ncq * a.groups * a.mgroups), dim3(kThreads), lds, s, a);
+  return hipGetLastError();
+}
+
+template <typename T, int MB>
+hipError_t wgrad_launch_stg(int stg, bool multi, const WgradArgs& a, size_t lds,
+                            hipStream_t s) {
+  if (multi) return stg == 8 ? wgrad_launch<T, MB, 8, true>(a, lds, s) : hipErrorInvalidValue;
+  if (stg == 8) return wgrad_launch<T, MB, 8, false>(a, lds, s);
+  if (stg == 16) return wgrad_launch<T, MB, 16, false>(a, lds, s);
+  if (stg == 24) return wgrad_launch<T, MB, 24, false>(a, lds, s);
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t wgrad_dispatch(int mb, int stg, bool multi, const WgradArgs& a, size_t lds,
+                          hipStream_t s) {
+  if (mb == 1) return wgrad_launch_stg<T, 1>(stg, multi, a, lds, s);
+  if (mb == 2) return wgrad_launch_stg<T, 2>(stg, multi, a, lds, s);
+  if (mb == 4) return wgrad_launch_stg<T, 4>(stg, multi, a, lds, s);
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, const WgradArgs& a,
-                             size_t lds_bytes, hipStream_t stream) {
+hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
+                             const WgradArgs& a, size_t lds_bytes, hipStream_t stream) {
   if (a.items == 0) return hipSuccess;
-  if (dtype == CONVND_HIP_BFLOAT16) return wgrad_dispatch<__bf16>(mb, a, lds_bytes, stream);
-  if (dtype == CONVND_HIP_FLOAT16) return wgrad_dispatch<_Float16>(mb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_BFLOAT16)
+    return wgrad_dispatch<__bf16>(mb, stg, multi, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_FLOAT16)
+    return wgrad_dispatch<_Float16>(mb, stg, multi, a, lds_bytes, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_pad_grad_output(const void* dy, void* dst, const WgradArgs& a,
+                                  hipStream_t stream) {
+  int dlast = 8;
+  for (int i = 0; i < a.rank; ++i)
+    if (i == a.rank - 1) dlast = a.dext[i];
+  const int64_t total = (int64_t)a.batch * a.cout_total * (a.dvol / dlast) * (dlast / 8);
+  if (total == 0) return hipSuccess;
+  const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, 8192);
+  hipLaunchKernelGGL(pad_dy16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                     stream, static_cast<const unsigned short*>(dy),
+                     static_cast<unsigned short*>(dst), a, total);
+  return hipGetLastError();
+}
+
+int64_t wgrad_partial_slots(int mb, const WgradArgs& a) {
+  return (int64_t)a.groups * a.mgroups * a.ncq * 4 * mb * 8 * 64;
+}
+
+hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& a, void* dw,
+                               hipStream_t stream) {
+  const int64_t nslots = wgrad_partial_slots(mb, a);
+  if (nslots == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((nslots + kThreads - 1) / kThreads));
+  const f32x4* part = reinterpret_cast<const f32x4*>(a.partial);
+  if (dtype == CONVND_HIP_BFLOAT16) {
+    hipLaunchKernelGGL(wgrad_reduce_kernel<__bf16>, grid, dim3(kThreads), 0, stream, part,
+                       static_cast<__bf16*>(dw), a, mb, nslots);
+  } else if (dtype == CONVND_HIP_FLOAT16) {
+    hipLaunchKernelGGL(wgrad_reduce_kernel<_Float16>, grid, dim3(kThreads), 0, stream, part,
+                       static_cast<_Float16*>(dw), a, mb, nslots);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace convnd
