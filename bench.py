@@ -94,6 +94,20 @@ def correctness_gate(torch, np, conv, x, w, b):
     return worst
 
 
+def profiled_traffic():
+    """HBM-side bytes per launch of each MFMA kernel, measured by two rocprofv3 PMC runs
+    (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known size; recorded in
+    profiles/c2_hbm_traffic.md (None when that file is absent)."""
+    path = ROOT / "profiles" / "c2_hbm_traffic.md"
+    try:
+        for line in path.read_text(encoding="utf-8").splitlines():
+            if line.strip().startswith("traffic_bytes_per_launch:"):
+                return json.loads(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return {}
+
+
 def cpu_baseline(torch):
     """The reference's backend="torch" CPU path (restated in oracle/torch_path.py) on the
     same C2 problem, bf16 with fp32 partial accumulation; median of timed fwd+bwd runs."""
@@ -288,7 +302,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic().get(dominant),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
         },
         "correctness_gate_worst": round(gate, 4),
     }
