@@ -132,14 +132,20 @@ def test_half_precision_baseline_configs_plan_mfma(lib, name):
             assert plan["lds"] <= 160 * 1024 and plan["workgroups"] > 0, plan
 
 
-def test_float64_and_odd_channels_plan_direct(lib):
+def test_float64_and_odd_channels_plans(lib):
     import torch
 
     c1 = ((4, 2, 8, 8, 8, 16), (8, 2, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1)
-    # Forward and weight gradient contract over 2 input channels (direct); the input gradient
-    # contracts over 8 output channels, a multiple of the MFMA channel octet.
-    assert _capi.plan_names(lib, *c1, torch.bfloat16) == ("direct", "mfma", "direct")
+    # bf16: the forward contracts over 2 input channels (direct); the input gradient over 8
+    # output channels (an MFMA octet); the weight gradient stages the input with its
+    # channels zero-padded to an octet.
+    assert _capi.plan_names(lib, *c1, torch.bfloat16) == ("direct", "mfma", "mfma")
+    # fp32 runs as split precision on the bf16 MFMA: 6 x 2 channels padded to 16.
+    assert _capi.plan_names(lib, *c1, torch.float32) == ("mfma", "mfma", "mfma")
     assert _capi.plan_names(lib, *BASELINE["C2"], torch.float64) == ("direct",) * 3
+    # fp32 with more than 64 channels per group in the GEMM-input role stays direct.
+    wide = ((1, 72, 4, 4, 4, 8), (8, 72, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1)
+    assert _capi.plan_names(lib, *wide, torch.float32)[0] == "direct"
     big = ((1, 8, 3, 2, 2, 2), (8, 8, 1, 1, 1, 1), (2**35, 1, 1, 1), (2**34, 0, 0, 0), (1,) * 4, 1)
     assert _capi.plan_names(lib, *big, torch.bfloat16) == ("direct",) * 3
 

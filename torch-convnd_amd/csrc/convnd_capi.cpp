@@ -392,13 +392,26 @@ const PlanFilter& plan_filter(int mode) {
 }
 
 // mode 0: forward over x; mode 1: input gradient over grad_output.
+// fp32 runs as split precision on the bf16 MFMA (kSplit copies of the GEMM-input channels,
+// see convnd_types.h), when the real channel count per group is small enough to stage.
+constexpr int kSplit = 6;
+constexpr int kSplitMaxChannels = 64;
+
 IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
   IgemmPlan plan;
-  if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g)) return plan;
+  const bool split = dt == CONVND_HIP_FLOAT32;
+  if ((!is_half(dt) && !split) || g.rank > kFastRank || !fits_int32(g)) return plan;
   const int R = g.rank;
-  const int gemm_cin = static_cast<int>(mode == 0 ? g.cin_g : g.cout_g);
+  const int real_cin = static_cast<int>(mode == 0 ? g.cin_g : g.cout_g);
+  if (split && real_cin > kSplitMaxChannels) return plan;
+  const int gemm_cin = split ? (kSplit * real_cin + 7) / 8 * 8 : real_cin;
   const int gemm_cout = static_cast<int>(mode == 0 ? g.cout_g : g.cin_g);
   if (gemm_cin % 8 != 0) return plan;
+  // The split copies multiply the staged input; keep it int32-addressable.
+  if (split && (int64_t)gemm_cin * g.groups * g.batch *
+                       (mode == 0 ? g.in_vol : g.out_vol) > kI32Safe / 2)
+    return plan;
+  const int out_es = split ? 4 : 2;
   int nphase = 1;
   if (mode == 1) {
     for (int a = 0; a < R; ++a) nphase *= static_cast<int>(g.s[a]);
@@ -503,8 +516,8 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         conflict = hit->second.conflict;
         const int64_t plane_pos = hit->second.plane_pos;
         const int64_t plane_bytes = align_up(plane_pos * 16);
-        // The epilogue reuses the LDS as a [channels][box positions] tile of 16-bit values.
-        const int64_t tile_bytes = (int64_t)wm * mb * 16 * (box_vol + 8) * 2;
+        // The epilogue reuses the LDS as a [channels][box positions] tile of output values.
+        const int64_t tile_bytes = (int64_t)wm * mb * 16 * (box_vol + 8) * out_es;
         const int64_t lds =
             std::max(noct * plane_bytes + table_bytes + align_up(rows * 8), align_up(tile_bytes));
         if (rows > (int64_t{1} << 20)) return;
@@ -515,7 +528,7 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
           const int out_last = static_cast<int>(mode == 0 ? g.out[R - 1] : g.in[R - 1]);
           const bool unit_step = mode == 0 || g.s[R - 1] == 1;
           if (unit_step)
-            for (int v = 8; v > 1; v /= 2)
+            for (int v = 16 / out_es; v > 1; v /= 2)
               if (b[R - 1] % v == 0 && out_last % v == 0) {
                 out_vec = v;
                 break;
@@ -539,8 +552,8 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         const double stage = double(nchunk) * (noct * hvol * 16.0 / 64.0 + 1500.0);
         // Epilogue: output bytes of the box at 16 bytes per lane-store when out_vec == 8,
         // proportionally fewer useful bytes per store for shorter runs.
-        const double out_bytes = double(wm) * mb * 16 * box_vol * 2;
-        const double epilogue = out_bytes / (4.0 * out_vec) + 800.0;
+        const double out_bytes = double(wm) * mb * 16 * box_vol * out_es;
+        const double epilogue = out_bytes / (2.0 * out_es * out_vec) + 800.0;
         const double per_wg = core + (occ >= 2 ? 0.25 : 1.0) * stage + epilogue;
         const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
         const int64_t slots = 256 * occ;
@@ -604,6 +617,7 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.boxes = static_cast<int>(boxes);
         A.k_vol = static_cast<int>(g.k_vol);
         A.out_vec = out_vec;
+        A.split_c = split ? real_cin : 0;
         plan.lds = static_cast<size_t>(lds);
       });
     }
@@ -646,16 +660,20 @@ struct WgradPlan {
 
 WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
   WgradPlan plan;
-  if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g) || g.cin_g % 8 != 0 ||
-      g.batch == 0)
+  // Split-precision fp32: kSplit images of bf16 parts per image (see convnd_types.h).
+  const bool split = dt == CONVND_HIP_FLOAT32;
+  if ((!is_half(dt) && !split) || g.rank > kFastRank || !fits_int32(g) || g.batch == 0)
     return plan;
+  const int64_t batch = split ? g.batch * kSplit : g.batch;
   const int R = g.rank;
   const int cin_g = static_cast<int>(g.cin_g), cout_g = static_cast<int>(g.cout_g);
   const int k_vol = static_cast<int>(g.k_vol);
   const int mtiles = (cout_g + 15) / 16;
   const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
   const int mgroups = (mtiles + mb - 1) / mb;
-  const int octs = cin_g / 8;
+  // Input channels per group rounded up to whole octets (zero channels in the staged copy).
+  const int cin_gp = (cin_g + 7) / 8 * 8;
+  const int octs = cin_gp / 8;
   const int npairs = octs * k_vol;
   const int ncq = (npairs + 63) / 64;
   if (ncq > 65535 || g.groups * mgroups > 65535) return plan;
@@ -698,7 +716,8 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
         if (pvol > kI32Safe) return;
       }
       // The padded copy must stay int32-addressable and not dwarf the input.
-      if (pvol * g.batch * g.channels > kI32Safe / 2 || pvol > 8 * g.in_vol + (1 << 20)) return;
+      if (pvol * batch * g.groups * cin_gp > kI32Safe / 2 || pvol > 8 * g.in_vol + (1 << 20))
+        return;
       hpitch[R - 1] = 1;
       for (int a = R - 2; a >= 0; --a) hpitch[a] = hpitch[a + 1] * hext[a + 1];
       const int64_t plane_pos = (int64_t)hpitch[0] * hext[0];
@@ -714,7 +733,7 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       // do not tile the output exactly it is read from a copy padded to whole boxes.
       int64_t dvol = 1;
       for (int a = 0; a < R; ++a) dvol *= ((g.out[a] + b[a] - 1) / b[a]) * b[a];
-      if (dvol * g.batch * g.out_channels > kI32Safe / 2) return;
+      if (dvol * batch * g.out_channels > kI32Safe / 2) return;
       // Staging slots per thread (16-byte registers), the next item's held across the MFMAs;
       // an item needing more than the register budget stages the rest in batches of 8.
       const int64_t entries = max_oct * plane_pos + (int64_t)mb * 16 * (box_vol / 8);
@@ -724,16 +743,19 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       const bool multi = stg > stg_max;
       if (multi) stg = 8;
       const int64_t batches = (entries + stg * kThreads - 1) / (stg * kThreads);
-      const int64_t items = boxes * g.batch;
+      const int64_t items = boxes * batch;
       const int64_t per_chunk_wgs = (int64_t)ncq * g.groups * mgroups;
-      int64_t npc = std::max<int64_t>(1, 256 / per_chunk_wgs);
-      npc = std::min<int64_t>(npc, items);
-      const int64_t ipc = (items + npc - 1) / npc;
-      npc = (items + ipc - 1) / ipc;
-      if (npc * per_chunk_wgs > INT32_MAX) return;
-      // Item table: 8 bytes per item of a workgroup's range.
-      const int64_t lds = lds_items + align_up(ipc * 8);
-      if (lds > kLdsBudget) return;
+      // Position chunks: enough for one workgroup per CU; more (several rounds) only when a
+      // workgroup's item table (8 bytes per item) would not fit in LDS.
+      int64_t npc = 0, ipc = 0, lds = 0;
+      for (int64_t target = 256; target <= 256 * 16; target *= 2) {
+        npc = std::min<int64_t>(std::max<int64_t>(1, target / per_chunk_wgs), items);
+        ipc = (items + npc - 1) / npc;
+        npc = (items + ipc - 1) / ipc;
+        lds = lds_items + align_up(ipc * 8);
+        if (lds <= kLdsBudget) break;
+      }
+      if (lds > kLdsBudget || npc * per_chunk_wgs > INT32_MAX) return;
       // Per item: MFMA issue of one wave (8 fragments x MB tiles per K32 step) against the
       // staging of the next item (~64 B/clock/CU of L2 traffic), which overlap only in part,
       // plus ~1500 clocks of per-item work (barriers, LDS stores); unprefetched batches add
@@ -762,14 +784,19 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       PadArgs& P = plan.pad;
       std::memset(&P, 0, sizeof(P));
       A.rank = R;
-      A.batch = static_cast<int>(g.batch);
+      A.batch = static_cast<int>(batch);
       A.groups = static_cast<int>(g.groups);
       A.cin_g = cin_g;
+      A.cin_gp = cin_gp;
       A.cout_g = cout_g;
       A.cin_total = static_cast<int>(g.channels);
       A.cout_total = static_cast<int>(g.out_channels);
       P.rank = R;
-      P.channels = A.cin_total;
+      P.channels = static_cast<int>(g.groups * cin_gp);
+      P.src_channels = A.cin_total;
+      P.src_cg = cin_g;
+      P.dst_cg = cin_gp;
+      P.split_batch = split ? static_cast<int>(g.batch) : 0;
       int ovol = 1, pstride = 1;
       for (int a = R - 1; a >= 0; --a) {
         A.pstride[a] = pstride;
@@ -806,7 +833,7 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       A.dyrow = dyrow;
       A.dvol = static_cast<int>(dvol);
       plan.stg = stg;
-      plan.exact = dvol == g.out_vol;
+      plan.exact = dvol == g.out_vol && !split;
       A.mtiles = mtiles;
       A.mgroups = mgroups;
       A.npairs = npairs;
@@ -822,8 +849,8 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
     });
   }
   if (plan.ok) {
-    plan.staged_elems = (size_t)g.batch * plan.args.pvol * g.channels;
-    plan.dy_pad_elems = (size_t)g.batch * plan.args.dvol * g.out_channels;
+    plan.staged_elems = (size_t)batch * plan.args.pvol * g.groups * cin_gp;
+    plan.dy_pad_elems = (size_t)batch * plan.args.dvol * g.out_channels;
     plan.partial_elems =
         (size_t)plan.args.npc * wgrad_partial_slots(plan.mb, plan.args) * 4;
   }
@@ -884,9 +911,9 @@ ForwardSetup make_forward(const Geom& g, convnd_hip_dtype dt) {
   f.ig = plan_igemm(g, dt, 0);
   Layout L;
   if (f.ig.ok) {
-    const int64_t es = element_size(dt);
-    f.off_stage = L.take(f.ig.staged_elems * es);
-    f.off_wpk = L.take(f.ig.wpk_elems * es);
+    // Staged operands and packed weights are 16-bit (bf16 parts for split-precision fp32).
+    f.off_stage = L.take(f.ig.staged_elems * 2);
+    f.off_wpk = L.take(f.ig.wpk_elems * 2);
   }
   f.bytes = L.total;
   return f;
@@ -912,24 +939,24 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
   if (gi && g.batch > 0) {
     b.dg = plan_igemm(g, dt, 1);
     if (b.dg.ok) {
-      b.off_dy_stage = L.take(b.dg.staged_elems * es);
-      b.off_wpk = L.take(b.dg.wpk_elems * es);
+      b.off_dy_stage = L.take(b.dg.staged_elems * 2);
+      b.off_wpk = L.take(b.dg.wpk_elems * 2);
     }
   }
   if (gw && g.batch > 0) {
     b.wg = plan_wgrad(g, dt);
     if (b.wg.ok) {
-      b.off_x_stage = L.take(b.wg.staged_elems * es);
+      b.off_x_stage = L.take(b.wg.staged_elems * 2);
       b.off_partial = L.take(b.wg.partial_elems * sizeof(float));
-      b.off_dy_pad = L.take(b.wg.dy_pad_elems * es);
+      b.off_dy_pad = L.take(b.wg.dy_pad_elems * 2);
     }
   }
   if (gb) {
     // Partial sums of the bias gradient: per channel, kBiasChunks doubles on the standalone
     // path or one float per 64-position tile when they come with the channels-last copy.
-    const size_t fused = (gi && b.dg.ok) ? (size_t)channel_last_sum_blocks(g.batch, g.out_vol) *
-                                               sizeof(float)
-                                         : 0;
+    const size_t fused = (gi && b.dg.ok && is_half(dt))
+                             ? (size_t)channel_last_sum_blocks(g.batch, g.out_vol) * sizeof(float)
+                             : 0;
     b.off_bias = L.take((size_t)g.out_channels * std::max(fused, kBiasChunks * sizeof(double)));
   }
   b.bytes = L.total;
@@ -1071,9 +1098,16 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   IgemmArgs A = f.ig.args;
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
-  st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels, g.in_vol,
-                                         nullptr, stream),
-                 "channels-last staging");
+  if (A.split_c > 0) {
+    st = hip_check(launch_split_channels_last(static_cast<const float*>(input), staged, g.batch,
+                                              static_cast<int>(g.groups), A.split_c, A.cin_g,
+                                              g.in_vol, stream),
+                   "split-precision channels-last staging");
+  } else {
+    st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels, g.in_vol,
+                                           nullptr, stream),
+                   "channels-last staging");
+  }
   if (st != CONVND_HIP_SUCCESS) return st;
   st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream), "weight packing");
   if (st != CONVND_HIP_SUCCESS) return st;
@@ -1121,7 +1155,7 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   }
   // The bias gradient rides on the channels-last copy of grad_output when the input
   // gradient makes one; otherwise it reads grad_output on its own.
-  const bool fused_bias = gb && gi && b.dg.ok;
+  const bool fused_bias = gb && gi && b.dg.ok && is_half(dtype);
   if (gb && !fused_bias) {
     st = hip_check(launch_grad_bias(dtype, g.batch, g.out_channels, g.out_vol, grad_output,
                                     grad_bias, reinterpret_cast<float*>(ws + b.off_bias),
@@ -1135,9 +1169,16 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       void* staged = ws + b.off_dy_stage;
       void* wpk = ws + b.off_wpk;
       float* sums = fused_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
-      st = hip_check(launch_to_channels_last(dtype, grad_output, staged, g.batch,
-                                             g.out_channels, g.out_vol, sums, stream),
-                     "channels-last staging of grad_output");
+      if (A.split_c > 0) {
+        st = hip_check(launch_split_channels_last(static_cast<const float*>(grad_output), staged,
+                                                  g.batch, static_cast<int>(g.groups),
+                                                  A.split_c, A.cin_g, g.out_vol, stream),
+                       "split-precision channels-last staging of grad_output");
+      } else {
+        st = hip_check(launch_to_channels_last(dtype, grad_output, staged, g.batch,
+                                               g.out_channels, g.out_vol, sums, stream),
+                       "channels-last staging of grad_output");
+      }
       if (st != CONVND_HIP_SUCCESS) return st;
       if (fused_bias) {
         st = hip_check(launch_grad_bias_from_sums(dtype, sums,
@@ -1169,20 +1210,20 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       WgradArgs A = b.wg.args;
       void* staged = ws + b.off_x_stage;
       float* partial = reinterpret_cast<float*>(ws + b.off_partial);
-      st = hip_check(launch_to_octets_padded(dtype, input, staged, g.batch, b.wg.pad, stream),
+      st = hip_check(launch_to_octets_padded(dtype, input, staged, A.batch, b.wg.pad, stream),
                      "padded octet-major staging of input");
       if (st != CONVND_HIP_SUCCESS) return st;
       A.x = staged;
       A.dy = grad_output;
       A.partial = partial;
-      const int64_t es = element_size(dtype);
-      A.x_bytes = static_cast<int>(b.wg.staged_elems * es);
-      A.dy_bytes = static_cast<int>(b.wg.dy_pad_elems * es);
+      A.x_bytes = static_cast<int>(b.wg.staged_elems * 2);
+      A.dy_bytes = static_cast<int>(b.wg.dy_pad_elems * 2);
       // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the
       // boxes tile it exactly and its base is 16-byte aligned.
       if (!b.wg.exact || reinterpret_cast<uintptr_t>(grad_output) % 16 != 0) {
         void* padded = ws + b.off_dy_pad;
-        st = hip_check(launch_pad_grad_output(grad_output, padded, A, stream),
+        st = hip_check(launch_pad_grad_output(grad_output, padded, A,
+                                              b.wg.pad.split_batch, stream),
                        "padded copy of grad_output");
         if (st != CONVND_HIP_SUCCESS) return st;
         A.dy = padded;

@@ -114,8 +114,10 @@ __device__ __forceinline__ int phase_axes(const IgemmArgs& A, int phase, AxisTap
 // Packed weights: unit u = ((((phase*G + g)*nchunk + chunk)*kc_max + kc)*mtiles_padded
 // + mt)*64 + lane holds the 8 A-fragment elements W'[m][k], m = mt*16 + lane%16,
 // k = kc*32 + (lane/16)*8 + i (i < 8), zero where m or k is padding.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const T* w, T* wpk,
+// S = float (split precision): GEMM channel ci is part split_other_part(ci / split_c) of
+// channel ci % split_c of the fp32 weight (zero past kSplitProducts copies).
+template <typename T, typename S>
+__global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const S* w, T* wpk,
                                                               int64_t units) {
   const int R = A.rank;
   {
@@ -154,11 +156,21 @@ __global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int ci = ci0 + i;
+          int ci = ci0 + i, part = 0;
+          if constexpr (sizeof(S) == 4) {
+            const int sp = ci / A.split_c;
+            if (sp >= kSplitProducts) continue;
+            ci -= sp * A.split_c;
+            part = split_other_part(sp);
+          }
           const int64_t widx =
               A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
                           : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
-          vals[i] = w[widx];
+          if constexpr (sizeof(S) == 4) {
+            vals[i] = __builtin_bit_cast(T, bf16_part_bits(w[widx], part));
+          } else {
+            vals[i] = w[widx];
+          }
         }
       }
       T* dst = wpk + u * 8;
@@ -176,7 +188,8 @@ __global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const
 template <int MB, int NB>
 constexpr int igemm_waves = MB * NB >= 32 ? 1 : 2;
 
-template <typename T, int MB, int NB, int WM>
+// T: GEMM operand type; O: output and bias type (T, or float for split-precision fp32).
+template <typename T, typename O, int MB, int NB, int WM>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(igemm_waves<MB, NB>, igemm_waves<MB, NB>)))
 void igemm_kernel(IgemmArgs A) {
@@ -316,7 +329,7 @@ void igemm_kernel(IgemmArgs A) {
   const int lg = lane >> 4;
   float bias_v[MB][4];
   {
-    const T* bias = static_cast<const T*>(A.bias);
+    const O* bias = static_cast<const O*>(A.bias);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -493,11 +506,11 @@ void igemm_kernel(IgemmArgs A) {
   }
 
   // Epilogue. D[m][n] sits in lane (n + 16*(m/4)), register m%4. The tile (bias added,
-  // rounded to T) goes through LDS as [channel][box position] so that global stores write
+  // rounded to O) goes through LDS as [channel][box position] so that global stores write
   // A.out_vec consecutive positions (up to 16 bytes) of one channel per lane; box position
   // q maps to output offset origin + sum_a q_a * ofac[a] and lies inside the output when
   // q_a < J - J0 on every axis.
-  T* out = static_cast<T*>(A.out);
+  O* out = static_cast<O*>(A.out);
   int origin = 0;
   bool interior = true;
   int lim[kFastRank], ofac[kFastRank];
@@ -515,8 +528,9 @@ void igemm_kernel(IgemmArgs A) {
     }
   }
   constexpr int kRowsWG = WM * MB * 16;  // output channels of the workgroup
-  const int tstride = A.box_vol + 8;     // elements per tile row (16-byte skew per row)
-  T* tile = reinterpret_cast<T*>(lds);
+  // Elements per tile row: 16 bytes of skew per row for 16-bit O, 32 for float.
+  const int tstride = A.box_vol + 8;
+  O* tile = reinterpret_cast<O*>(lds);
   __syncthreads();  // every wave is done with the halo planes and tables
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -526,7 +540,7 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const int q = (wn * NB + nb) * 16 + (lane & 15);
-        tile[ml * tstride + q] = static_cast<T>(acc[mb][nb][i] + bias_v[mb][i]);
+        tile[ml * tstride + q] = static_cast<O>(acc[mb][nb][i] + bias_v[mb][i]);
       }
     }
   }
@@ -554,14 +568,15 @@ void igemm_kernel(IgemmArgs A) {
         }
       }
     }
-    T* dst = out + ((size_t)n * A.cout_total + g * A.cout_g + mg * kRowsWG + ml) * A.out_vol + oo;
-    const T* src = tile + ml * tstride + q;
+    O* dst = out + ((size_t)n * A.cout_total + g * A.cout_g + mg * kRowsWG + ml) * A.out_vol + oo;
+    const O* src = tile + ml * tstride + q;
     if (interior) {
-      if (vec == 8) {
+      const int bytes = vec * static_cast<int>(sizeof(O));
+      if (bytes == 16) {
         *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
-      } else if (vec == 4) {
+      } else if (bytes == 8) {
         *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
-      } else if (vec == 2) {
+      } else if (bytes == 4) {
         *reinterpret_cast<unsigned*>(dst) = *reinterpret_cast<const unsigned*>(src);
       } else {
         dst[0] = src[0];
@@ -578,12 +593,12 @@ void igemm_kernel(IgemmArgs A) {
   X(1, 2, 1) X(1, 4, 1) X(1, 8, 1) X(2, 2, 1) X(2, 4, 1) X(2, 8, 1) X(4, 2, 1) X(4, 4, 1) \
   X(4, 8, 1) X(1, 4, 2) X(1, 8, 2) X(2, 4, 2) X(2, 8, 2) X(1, 4, 4) X(1, 8, 4)
 
-template <typename T>
+template <typename T, typename O>
 hipError_t igemm_dispatch(int mb, int nb, const IgemmArgs& a, size_t lds, hipStream_t s) {
   const dim3 grid(a.boxes, a.groups * a.mgroups, a.batch * a.nphase);
 #define CONVND_IGEMM_CASE(MBV, NBV, WMV)                                                 \
   if (mb == MBV && nb == NBV && a.wm == WMV) {                                           \
-    auto fn = igemm_kernel<T, MBV, NBV, WMV>;                                            \
+    auto fn = igemm_kernel<T, O, MBV, NBV, WMV>;                                         \
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),              \
                                          hipFuncAttributeMaxDynamicSharedMemorySize,     \
                                          static_cast<int>(lds));                         \
@@ -613,11 +628,14 @@ hipError_t launch_igemm_prep(convnd_hip_dtype dtype, const IgemmArgs& a, const v
   const int64_t blocks64 = (units + kThreads - 1) / kThreads;
   const dim3 grid(static_cast<unsigned>(blocks64 < 4096 ? blocks64 : 4096));
   if (dtype == CONVND_HIP_BFLOAT16) {
-    hipLaunchKernelGGL((igemm_pack_kernel<__bf16>), grid, dim3(kThreads), 0, stream, a,
+    hipLaunchKernelGGL((igemm_pack_kernel<__bf16, __bf16>), grid, dim3(kThreads), 0, stream, a,
                        static_cast<const __bf16*>(w), static_cast<__bf16*>(wpk), units);
   } else if (dtype == CONVND_HIP_FLOAT16) {
-    hipLaunchKernelGGL((igemm_pack_kernel<_Float16>), grid, dim3(kThreads), 0, stream, a,
-                       static_cast<const _Float16*>(w), static_cast<_Float16*>(wpk), units);
+    hipLaunchKernelGGL((igemm_pack_kernel<_Float16, _Float16>), grid, dim3(kThreads), 0, stream,
+                       a, static_cast<const _Float16*>(w), static_cast<_Float16*>(wpk), units);
+  } else if (dtype == CONVND_HIP_FLOAT32 && a.split_c > 0) {
+    hipLaunchKernelGGL((igemm_pack_kernel<__bf16, float>), grid, dim3(kThreads), 0, stream, a,
+                       static_cast<const float*>(w), static_cast<__bf16*>(wpk), units);
   } else {
     return hipErrorInvalidValue;
   }
@@ -627,8 +645,12 @@ hipError_t launch_igemm_prep(convnd_hip_dtype dtype, const IgemmArgs& a, const v
 hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,
                         size_t lds_bytes, hipStream_t stream) {
   if (a.boxes == 0 || a.batch == 0) return hipSuccess;
-  if (dtype == CONVND_HIP_BFLOAT16) return igemm_dispatch<__bf16>(mb, nb, a, lds_bytes, stream);
-  if (dtype == CONVND_HIP_FLOAT16) return igemm_dispatch<_Float16>(mb, nb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_BFLOAT16)
+    return igemm_dispatch<__bf16, __bf16>(mb, nb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_FLOAT16)
+    return igemm_dispatch<_Float16, _Float16>(mb, nb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_FLOAT32 && a.split_c > 0)
+    return igemm_dispatch<__bf16, float>(mb, nb, a, lds_bytes, stream);
   return hipErrorInvalidValue;
 }
 

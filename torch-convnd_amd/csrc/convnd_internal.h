@@ -61,7 +61,8 @@ struct IgemmArgs {
   int box_vol, boxes;
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int k_vol;
-  int out_vec;                // output elements per epilogue store (consecutive positions)
+  int out_vec;     // output elements per epilogue store (consecutive positions, <= 16 bytes)
+  int split_c;     // split-precision fp32: real channels per group in the GEMM-input role
 };
 
 // Arguments of the MFMA weight-gradient kernel. Columns are (octet of 8 input channels,
@@ -69,12 +70,13 @@ struct IgemmArgs {
 // LDS: [max_oct octet planes | grad_output tile | box position offsets | halo row tables
 // (5 * rows ints) | box row offsets (box_vol / box[rank-1] ints)].
 struct WgradArgs {
-  const void* x;      // zero-padded octet-major input [N][cin_total/8][pe...][8] (PadArgs)
+  const void* x;      // zero-padded octet-major input [N][groups*cin_gp/8][pe...][8] (PadArgs)
   const void* dy;     // grad_output [N][cout_total][out_vol]
   float* partial;     // per-lane accumulator vectors, see wgrad_partial_slots
   int x_bytes, dy_bytes;  // sizes of the two buffers (loads past them read zero)
   int rank;
   int batch, groups, cin_g, cout_g, cin_total, cout_total;
+  int cin_gp;                // input channels per group rounded up to octets (staged copy)
   int out_size[kFastRank];
   int out_vol, k_vol;
   int dext[kFastRank];       // extents of the grad_output buffer read (output, or padded to
@@ -105,13 +107,22 @@ hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void
                                    float* chan_sums, hipStream_t stream);
 int64_t channel_last_sum_blocks(int64_t batch, int64_t volume);
 
-// Zero-padded octet-major copy: dst[n][c/8][u_0]..[u_{R-1}][c%8] = src[n][c][u - pad] (zero
-// when u - pad lies outside the input), u_a < pe[a]. 16-bit element types, channels % 8 == 0.
+// Zero-padded octet-major copy: dst[n][c/8][u_0]..[u_{R-1}][c%8] = src[n][c'][u - pad] (zero
+// when u - pad lies outside the input), u_a < pe[a], where destination channel c is channel
+// c % dst_cg of group c / dst_cg (zero past the group's src_cg source channels).
 struct PadArgs {
-  int rank, channels;
+  int rank, channels;       // destination channels (groups x dst_cg)
+  int src_channels;         // source channels (groups x src_cg)
+  int src_cg, dst_cg;       // channels per group: source, destination (multiple of 8, zero-filled)
+  int split_batch;  // fp32 source: images per split part (destination batch = 6x), else 0
   int in[kFastRank], pe[kFastRank], pad[kFastRank];
   int in_vol, pvol;
 };
+// fp32 [N][G*cin_g][V] -> bf16 channels-last [N][V][G*cg_split] with six split parts per
+// channel (split-precision GEMM input); cin_g <= 64, cg_split % 8 == 0.
+hipError_t launch_split_channels_last(const float* src, void* dst, int64_t batch, int groups,
+                                      int cin_g, int cg_split, int64_t volume,
+                                      hipStream_t stream);
 hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void* dst,
                                           int64_t batch, const PadArgs& args,
                                           hipStream_t stream);
@@ -141,9 +152,10 @@ bool igemm_tile_supported(int mb, int nb, int wm);
 // several batches of 8 slots (only the first is prefetched).
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
                              const WgradArgs& a, size_t lds_bytes, hipStream_t stream);
-// grad_output zero-padded to whole boxes (extents a.dext) for the weight gradient.
+// grad_output zero-padded to whole boxes (extents a.dext) for the weight gradient; with
+// split_batch > 0 the source is fp32 and a.batch = 6 x split_batch images of bf16 parts.
 hipError_t launch_pad_grad_output(const void* dy, void* dst, const WgradArgs& a,
-                                  hipStream_t stream);
+                                  int split_batch, hipStream_t stream);
 // Float slots (x4) of one position chunk's partial sums, and the pass that adds the npc
 // chunks in order and writes dW in the weight layout.
 int64_t wgrad_partial_slots(int mb, const WgradArgs& a);

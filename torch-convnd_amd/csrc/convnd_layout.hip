@@ -100,7 +100,11 @@ __global__ __launch_bounds__(kThreads) void to_channels_last16_kernel(
 // decoded once into LDS; loads are 2-byte with lanes along positions (coalesced within a
 // row, any alignment); stores are 16 bytes (one octet) with lanes along positions, so every
 // octet plane of the destination is written contiguously.
-__global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const unsigned short* src,
+// Src = float: the fp32 input split into bf16 parts; destination image n (of split_batch
+// x kSplitProducts) holds part split_data_part(n / split_batch) of source image
+// n % split_batch.
+template <typename Src>
+__global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const Src* src,
                                                                      unsigned short* dst,
                                                                      PadArgs P) {
   __shared__ __align__(16) unsigned short tile[kTileC * kTileStride];
@@ -135,14 +139,29 @@ __global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const unsi
     srcoff[tid] = off;
   }
   __syncthreads();
-  const unsigned short* s = src + ((size_t)n * P.channels + c0) * P.in_vol;
+  int nsrc = n, part = 0;
+  if constexpr (sizeof(Src) == 4) {
+    nsrc = n % P.split_batch;
+    part = split_data_part(n / P.split_batch);
+  }
+  // Destination channel c0 + c is channel cc of group gi (dst_cg per group, the source's
+  // src_cg channels first, zero after).
+  const Src* s = src + (size_t)nsrc * P.src_channels * P.in_vol;
   unsigned short e[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int i = tid + j * kThreads;
     const int c = i >> 6, v = i & 63;
     const int so = srcoff[v];
-    e[j] = (c < ct && so >= 0) ? s[(size_t)c * P.in_vol + so] : 0;
+    const int gi = (c0 + c) / P.dst_cg;
+    const int cc = c0 + c - gi * P.dst_cg;
+    const bool ok = c < ct && so >= 0 && cc < P.src_cg;
+    const size_t sidx = ((size_t)gi * P.src_cg + cc) * P.in_vol + so;
+    if constexpr (sizeof(Src) == 4) {
+      e[j] = ok ? bf16_part_bits(s[sidx], part) : 0;
+    } else {
+      e[j] = ok ? s[sidx] : 0;
+    }
   }
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -162,6 +181,49 @@ __global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const unsi
              ((unsigned)tile[(cg * 8 + 2 * k + 1) * kTileStride + v] << 16);
     const size_t plane = (size_t)n * octs + (c0 >> 3) + cg;
     *reinterpret_cast<u32x4*>(dst + (plane * P.pvol + p0 + v) * 8) = w;
+  }
+}
+
+// fp32 [N][G*cin_g][V] -> bf16 [N][V][G*cg_split] for the split-precision GEMM: destination
+// channel s*cin_g + c of group g (s < kSplitProducts) holds part split_data_part(s) of
+// source channel g*cin_g + c; channels past kSplitProducts*cin_g are zero. Block (position
+// tile, group, n): the group's channels (at most 64) x 64 positions through LDS, then
+// 16-byte stores of 8 destination channels, consecutive lanes along the channels.
+__global__ __launch_bounds__(kThreads) void split_channels_last_kernel(const float* src,
+                                                                      unsigned short* dst,
+                                                                      int cin_g, int cg_split,
+                                                                      int volume) {
+  __shared__ float tile[kTileC * (kTileV + 1)];
+  const int tid = threadIdx.x;
+  const int v0 = blockIdx.x * kTileV;
+  const int g = blockIdx.y;
+  const int n = blockIdx.z;
+  const int groups = gridDim.y;
+  const int vt = volume - v0 < kTileV ? volume - v0 : kTileV;
+  const float* s = src + ((size_t)n * groups * cin_g + (size_t)g * cin_g) * volume + v0;
+  for (int i = tid; i < cin_g * kTileV; i += kThreads) {
+    const int c = i >> 6, v = i & 63;
+    tile[c * (kTileV + 1) + v] = v < vt ? s[(size_t)c * volume + v] : 0.f;
+  }
+  __syncthreads();
+  const int chunks = cg_split >> 3;
+  const size_t row = (size_t)groups * cg_split;
+  unsigned short* d = dst + ((size_t)n * volume + v0) * row + (size_t)g * cg_split;
+  for (int i = tid; i < vt * chunks; i += kThreads) {
+    const int v = i / chunks;
+    const int q = i - v * chunks;
+    unsigned h[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int c6 = q * 8 + k;
+      const int sp = c6 / cin_g;
+      const int c = c6 - sp * cin_g;
+      h[k] = sp < kSplitProducts
+                 ? bf16_part_bits(tile[c * (kTileV + 1) + v], split_data_part(sp))
+                 : 0u;
+    }
+    *reinterpret_cast<u32x4*>(d + (size_t)v * row + q * 8) =
+        u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
   }
 }
 
@@ -282,7 +344,10 @@ hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void
                                           int64_t batch, const PadArgs& args,
                                           hipStream_t stream) {
   if (batch == 0 || args.channels == 0 || args.pvol == 0) return hipSuccess;
-  if (dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16) return hipErrorInvalidValue;
+  if (dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16 &&
+      !(dtype == CONVND_HIP_FLOAT32 && args.split_batch > 0 &&
+        batch == (int64_t)args.split_batch * kSplitProducts))
+    return hipErrorInvalidValue;
   if (args.channels % 8 != 0 || args.rank < 1 || args.rank > kFastRank || batch > 65535)
     return hipErrorInvalidValue;
   const int64_t blocks = ((int64_t)args.pvol + kTileV - 1) / kTileV;
@@ -290,9 +355,29 @@ hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void
   if (blocks > 0x7fffffff || ctiles > 65535) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ctiles),
                   static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(to_octets_padded16_kernel, grid, dim3(kThreads), 0, stream,
-                     static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst),
-                     args);
+  if (dtype == CONVND_HIP_FLOAT32) {
+    hipLaunchKernelGGL(to_octets_padded16_kernel<float>, grid, dim3(kThreads), 0, stream,
+                       static_cast<const float*>(src), static_cast<unsigned short*>(dst), args);
+  } else {
+    hipLaunchKernelGGL(to_octets_padded16_kernel<unsigned short>, grid, dim3(kThreads), 0,
+                       stream, static_cast<const unsigned short*>(src),
+                       static_cast<unsigned short*>(dst), args);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_split_channels_last(const float* src, void* dst, int64_t batch, int groups,
+                                      int cin_g, int cg_split, int64_t volume,
+                                      hipStream_t stream) {
+  if (batch == 0 || volume == 0) return hipSuccess;
+  if (cin_g > kTileC || cg_split % 8 != 0 || cg_split < kSplitProducts * cin_g ||
+      groups > 65535 || batch > 65535 || volume > 0x7fffffff)
+    return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((volume + kTileV - 1) / kTileV),
+                  static_cast<unsigned>(groups), static_cast<unsigned>(batch));
+  hipLaunchKernelGGL(split_channels_last_kernel, grid, dim3(kThreads), 0, stream, src,
+                     static_cast<unsigned short*>(dst), cin_g, cg_split,
+                     static_cast<int>(volume));
   return hipGetLastError();
 }
 

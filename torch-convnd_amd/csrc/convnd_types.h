@@ -32,6 +32,31 @@ __device__ __forceinline__ T narrow(A v) {
   return static_cast<T>(v);
 }
 
+// fp32 operands on the bf16 MFMA: each value v splits into three bf16 parts (each the
+// nearest bf16 of what the previous parts leave; every subtraction is exact), so
+// v = p0 + p1 + p2 + r with |r| <= 2^-24 |v|. A product x*w keeps the six part products of
+// order >= 2^-16 relative -- (0,0) (0,1) (1,0) (0,2) (2,0) (1,1) -- accumulated in fp32:
+// the GEMM runs over six copies of the channel (or batch) dimension, the data operand
+// contributing parts kSplitData[s] and the other operand parts kSplitOther[s].
+constexpr int kSplitProducts = 6;
+__device__ __forceinline__ int split_data_part(int s) {
+  return s == 2 || s == 5 ? 1 : (s == 4 ? 2 : 0);
+}
+__device__ __forceinline__ int split_other_part(int s) {
+  return s == 1 || s == 5 ? 1 : (s == 3 ? 2 : 0);
+}
+__device__ __forceinline__ unsigned short bf16_part_bits(float v, int part) {
+  const __bf16 h0 = static_cast<__bf16>(v);
+  float r = v;
+  __bf16 h = h0;
+  if (part >= 1) {
+    r = v - static_cast<float>(h0);
+    h = static_cast<__bf16>(r);
+    if (part >= 2) h = static_cast<__bf16>(r - static_cast<float>(h));
+  }
+  return __builtin_bit_cast(unsigned short, h);
+}
+
 // 16x16x32 MFMA with fp32 accumulation for the two 16-bit element types.
 template <typename T>
 struct Mfma16;

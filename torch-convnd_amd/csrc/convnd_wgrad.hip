@@ -92,7 +92,7 @@ void wgrad_kernel(WgradArgs A) {
   const int oct = pair_ok ? pair / A.k_vol : oct_lo;
   const int tap = pair_ok ? pair - oct * A.k_vol : 0;
   const int co0 = mg * MB * 16;
-  const int oct0 = (g * A.cin_g >> 3) + oct_lo;  // first octet plane of this workgroup
+  const int oct0 = (g * A.cin_gp >> 3) + oct_lo;  // first octet plane of this workgroup
   const int it0 = pc * A.items_per_pc;
   const int nitems = (it0 + A.items_per_pc < A.items ? it0 + A.items_per_pc : A.items) - it0;
 
@@ -152,7 +152,7 @@ void wgrad_kernel(WgradArgs A) {
         ostr *= A.dext[a];
       }
     }
-    itab[2 * k] = ((n * (A.cin_total >> 3) + oct0) * A.pvol + base) * 16;
+    itab[2 * k] = ((n * (A.groups * A.cin_gp >> 3) + oct0) * A.pvol + base) * 16;
     itab[2 * k + 1] = ((n * A.cout_total + g * A.cout_g + co0) * A.dvol + obase) * 2;
   }
   __syncthreads();
@@ -366,6 +366,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
   for (; i < A.npc; ++i) acc += part[(int64_t)i * nslots + s];
   const int oct = pair / A.k_vol;
   const int tap = pair - oct * A.k_vol;
+  if (oct * 8 + u >= A.cin_g) return;  // channel padding of the staged input
   const int co_base = mg * mbv * 16 + mb * 16 + 4 * (lane >> 4);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -378,9 +379,12 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
 
 // Zero-padded copy of grad_output: dst[nc][u...] = src[nc][u...] for u inside the output
 // extents, else zero; each thread writes 8 consecutive elements of the last axis (whose
-// padded extent is a multiple of 8).
-__global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const unsigned short* src,
-                                                            unsigned short* dst, WgradArgs A,
+// padded extent is a multiple of 8). Src = float (split precision): destination image n of
+// A.batch = kSplitProducts x split_batch holds part split_other_part(n / split_batch) of
+// source image n % split_batch.
+template <typename Src>
+__global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const Src* src, unsigned short* dst,
+                                                            WgradArgs A, int split_batch,
                                                             int64_t total_runs) {
   const int R = A.rank;
   int dlast = 8, olast = 1;
@@ -399,6 +403,13 @@ __global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const unsigned short
     const int u0 = static_cast<int>(t - rowd * runs) * 8;
     const int64_t nc = rowd / drows;
     int rem = static_cast<int>(rowd - nc * drows);
+    int64_t snc = nc;
+    int part = 0;
+    if constexpr (sizeof(Src) == 4) {
+      const int64_t n = nc / A.cout_total, c = nc - n * A.cout_total;
+      snc = (n % split_batch) * A.cout_total + c;
+      part = split_other_part(static_cast<int>(n / split_batch));
+    }
     int srow = 0, istr = olast;
     bool ok = true;
 #pragma unroll
@@ -411,15 +422,18 @@ __global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const unsigned short
         istr *= A.out_size[a];
       }
     }
-    const unsigned short* s = src + nc * A.out_vol + srow;
+    const Src* s = src + snc * A.out_vol + srow;
+    auto bits = [&](int e) -> unsigned {
+      if (!ok || e >= olast) return 0u;
+      if constexpr (sizeof(Src) == 4) {
+        return bf16_part_bits(s[e], part);
+      } else {
+        return s[e];
+      }
+    };
     unsigned w[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int e0 = u0 + 2 * k, e1 = e0 + 1;
-      const unsigned lo = ok && e0 < olast ? s[e0] : 0u;
-      const unsigned hi = ok && e1 < olast ? s[e1] : 0u;
-      w[k] = lo | (hi << 16);
-    }
+    for (int k = 0; k < 4; ++k) w[k] = bits(u0 + 2 * k) | (bits(u0 + 2 * k + 1) << 16);
     *reinterpret_cast<u32x4*>(dst + rowd * dlast + u0) = u32x4{w[0], w[1], w[2], w[3]};
   }
 }
@@ -459,7 +473,8 @@ hipError_t wgrad_dispatch(int mb, int stg, bool multi, const WgradArgs& a, size_
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
                              const WgradArgs& a, size_t lds_bytes, hipStream_t stream) {
   if (a.items == 0) return hipSuccess;
-  if (dtype == CONVND_HIP_BFLOAT16)
+  // Split-precision fp32 runs on bf16 parts.
+  if (dtype == CONVND_HIP_BFLOAT16 || dtype == CONVND_HIP_FLOAT32)
     return wgrad_dispatch<__bf16>(mb, stg, multi, a, lds_bytes, stream);
   if (dtype == CONVND_HIP_FLOAT16)
     return wgrad_dispatch<_Float16>(mb, stg, multi, a, lds_bytes, stream);
@@ -467,16 +482,23 @@ hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi
 }
 
 hipError_t launch_pad_grad_output(const void* dy, void* dst, const WgradArgs& a,
-                                  hipStream_t stream) {
+                                  int split_batch, hipStream_t stream) {
   int dlast = 8;
   for (int i = 0; i < a.rank; ++i)
     if (i == a.rank - 1) dlast = a.dext[i];
   const int64_t total = (int64_t)a.batch * a.cout_total * (a.dvol / dlast) * (dlast / 8);
   if (total == 0) return hipSuccess;
   const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, 8192);
-  hipLaunchKernelGGL(pad_dy16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                     stream, static_cast<const unsigned short*>(dy),
-                     static_cast<unsigned short*>(dst), a, total);
+  if (split_batch > 0) {
+    if (a.batch != split_batch * kSplitProducts) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pad_dy16_kernel<float>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kThreads), 0, stream, static_cast<const float*>(dy),
+                       static_cast<unsigned short*>(dst), a, split_batch, total);
+  } else {
+    hipLaunchKernelGGL(pad_dy16_kernel<unsigned short>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kThreads), 0, stream, static_cast<const unsigned short*>(dy),
+                       static_cast<unsigned short*>(dst), a, 0, total);
+  }
   return hipGetLastError();
 }
 
@@ -496,6 +518,9 @@ hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& 
   } else if (dtype == CONVND_HIP_FLOAT16) {
     hipLaunchKernelGGL(wgrad_reduce_kernel<_Float16>, grid, dim3(kThreads), 0, stream, part,
                        static_cast<_Float16*>(dw), a, mb, nslots);
+  } else if (dtype == CONVND_HIP_FLOAT32) {
+    hipLaunchKernelGGL(wgrad_reduce_kernel<float>, grid, dim3(kThreads), 0, stream, part,
+                       static_cast<float*>(dw), a, mb, nslots);
   } else {
     return hipErrorInvalidValue;
   }
