@@ -516,24 +516,12 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         conflict = hit->second.conflict;
         const int64_t plane_pos = hit->second.plane_pos;
         const int64_t plane_bytes = align_up(plane_pos * 16);
-        // The epilogue reuses the LDS as a [channels][box positions] tile of output values.
-        const int64_t tile_bytes = (int64_t)wm * mb * 16 * (box_vol + 8) * out_es;
-        const int64_t lds =
-            std::max(noct * plane_bytes + table_bytes + align_up(rows * 8), align_up(tile_bytes));
+        const int64_t lds = noct * plane_bytes + table_bytes + align_up(rows * 8);
         if (rows > (int64_t{1} << 20)) return;
-        // Output positions written per store: consecutive along the last axis (stride 1 in
-        // the output unless an input-gradient phase steps by the stride).
-        int out_vec = 1;
-        {
-          const int out_last = static_cast<int>(mode == 0 ? g.out[R - 1] : g.in[R - 1]);
-          const bool unit_step = mode == 0 || g.s[R - 1] == 1;
-          if (unit_step)
-            for (int v = 16 / out_es; v > 1; v /= 2)
-              if (b[R - 1] % v == 0 && out_last % v == 0) {
-                out_vec = v;
-                break;
-              }
-        }
+        // Epilogue stores: a lane writes 4 consecutive positions at once when they are
+        // adjacent in the output (box rows of at least 4, unit output step on the last axis).
+        const bool unit_step = mode == 0 || g.s[R - 1] == 1;
+        const int run = unit_step && b[R - 1] >= 4 ? 4 : 1;
         const bool grid_ok = boxes <= (int64_t{1} << 30) && g.groups * mgroups <= 65535 &&
                              g.batch * nphase <= 65535;
         if (lds > kLdsBudget || !grid_ok) return;
@@ -550,10 +538,9 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         const double eff = occ >= 2 ? 0.75 : 0.55;
         const double core = double(nchunk) * kc * step / eff;
         const double stage = double(nchunk) * (noct * hvol * 16.0 / 64.0 + 1500.0);
-        // Epilogue: output bytes of the box at 16 bytes per lane-store when out_vec == 8,
-        // proportionally fewer useful bytes per store for shorter runs.
+        // Epilogue: one store per lane of `run` output values.
         const double out_bytes = double(wm) * mb * 16 * box_vol * out_es;
-        const double epilogue = out_bytes / (2.0 * out_es * out_vec) + 800.0;
+        const double epilogue = out_bytes / (4.0 * out_es * run) + 400.0;
         const double per_wg = core + (occ >= 2 ? 0.25 : 1.0) * stage + epilogue;
         const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
         const int64_t slots = 256 * occ;
@@ -616,7 +603,6 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.box_vol = box_vol;
         A.boxes = static_cast<int>(boxes);
         A.k_vol = static_cast<int>(g.k_vol);
-        A.out_vec = out_vec;
         A.split_c = split ? real_cin : 0;
         plan.lds = static_cast<size_t>(lds);
       });
@@ -1098,18 +1084,21 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   IgemmArgs A = f.ig.args;
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
-  if (A.split_c > 0) {
-    st = hip_check(launch_split_channels_last(static_cast<const float*>(input), staged, g.batch,
-                                              static_cast<int>(g.groups), A.split_c, A.cin_g,
-                                              g.in_vol, stream),
-                   "split-precision channels-last staging");
-  } else {
-    st = hip_check(launch_to_channels_last(dtype, input, staged, g.batch, g.channels, g.in_vol,
-                                           nullptr, stream),
-                   "channels-last staging");
-  }
-  if (st != CONVND_HIP_SUCCESS) return st;
-  st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream), "weight packing");
+  // Input staging and weight packing in one launch.
+  PrologueParts pp;
+  pp.src = input;
+  pp.staged = staged;
+  pp.batch = g.batch;
+  pp.volume = g.in_vol;
+  pp.channels = g.channels;
+  pp.split = A.split_c > 0;
+  pp.groups = static_cast<int>(g.groups);
+  pp.cin_g = A.split_c;
+  pp.cg_split = A.cin_g;
+  pp.ig = &A;
+  pp.w = weight;
+  pp.wpk = wpk;
+  st = hip_check(launch_prologue(dtype, pp, stream), "input staging and weight packing");
   if (st != CONVND_HIP_SUCCESS) return st;
   A.in = staged;
   A.wpk = wpk;
@@ -1163,39 +1152,70 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                    "bias gradient");
     if (st != CONVND_HIP_SUCCESS) return st;
   }
+  // Staging passes of both MFMA gradients (grad_output channels-last copy with the bias
+  // sums, input-gradient weight packing, octet-major input, padded grad_output) in one
+  // launch.
+  const bool mfma_dx = gi && b.dg.ok, mfma_dw = gw && b.wg.ok;
+  IgemmArgs DA{};
+  WgradArgs WA{};
+  float* sums = fused_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
+  PrologueParts pp;
+  if (mfma_dx) {
+    DA = b.dg.args;
+    DA.in = ws + b.off_dy_stage;
+    DA.wpk = ws + b.off_wpk;
+    DA.bias = nullptr;
+    DA.out = grad_input;
+    pp.src = grad_output;
+    pp.staged = ws + b.off_dy_stage;
+    pp.sums = sums;
+    pp.batch = g.batch;
+    pp.volume = g.out_vol;
+    pp.channels = g.out_channels;
+    pp.split = DA.split_c > 0;
+    pp.groups = static_cast<int>(g.groups);
+    pp.cin_g = DA.split_c;
+    pp.cg_split = DA.cin_g;
+    pp.ig = &DA;
+    pp.w = weight;
+    pp.wpk = ws + b.off_wpk;
+  }
+  if (mfma_dw) {
+    WA = b.wg.args;
+    WA.x = ws + b.off_x_stage;
+    WA.dy = grad_output;
+    WA.partial = reinterpret_cast<float*>(ws + b.off_partial);
+    WA.x_bytes = static_cast<int>(b.wg.staged_elems * 2);
+    WA.dy_bytes = static_cast<int>(b.wg.dy_pad_elems * 2);
+    pp.pad = &b.wg.pad;
+    pp.x = input;
+    pp.x_oct = ws + b.off_x_stage;
+    pp.oct_batch = WA.batch;
+    // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the
+    // boxes tile it exactly and its base is 16-byte aligned.
+    if (!b.wg.exact || reinterpret_cast<uintptr_t>(grad_output) % 16 != 0) {
+      pp.wg = &WA;
+      pp.dy = grad_output;
+      pp.dy_pad = ws + b.off_dy_pad;
+      pp.split_batch = b.wg.pad.split_batch;
+      WA.dy = ws + b.off_dy_pad;
+    }
+  }
+  if (mfma_dx || mfma_dw) {
+    st = hip_check(launch_prologue(dtype, pp, stream), "gradient staging");
+    if (st != CONVND_HIP_SUCCESS) return st;
+  }
+  if (fused_bias) {
+    st = hip_check(launch_grad_bias_from_sums(dtype, sums,
+                                              channel_last_sum_blocks(g.batch, g.out_vol),
+                                              g.out_channels, grad_bias, stream),
+                   "bias gradient");
+    if (st != CONVND_HIP_SUCCESS) return st;
+  }
   if (gi) {
-    if (b.dg.ok) {
-      IgemmArgs A = b.dg.args;
-      void* staged = ws + b.off_dy_stage;
-      void* wpk = ws + b.off_wpk;
-      float* sums = fused_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
-      if (A.split_c > 0) {
-        st = hip_check(launch_split_channels_last(static_cast<const float*>(grad_output), staged,
-                                                  g.batch, static_cast<int>(g.groups),
-                                                  A.split_c, A.cin_g, g.out_vol, stream),
-                       "split-precision channels-last staging of grad_output");
-      } else {
-        st = hip_check(launch_to_channels_last(dtype, grad_output, staged, g.batch,
-                                               g.out_channels, g.out_vol, sums, stream),
-                       "channels-last staging of grad_output");
-      }
-      if (st != CONVND_HIP_SUCCESS) return st;
-      if (fused_bias) {
-        st = hip_check(launch_grad_bias_from_sums(dtype, sums,
-                                                  channel_last_sum_blocks(g.batch, g.out_vol),
-                                                  g.out_channels, grad_bias, stream),
-                       "bias gradient");
-        if (st != CONVND_HIP_SUCCESS) return st;
-      }
-      st = hip_check(launch_igemm_prep(dtype, A, weight, wpk, stream),
-                     "input-gradient weight packing");
-      if (st != CONVND_HIP_SUCCESS) return st;
-      A.in = staged;
-      A.wpk = wpk;
-      A.bias = nullptr;
-      A.out = grad_input;
+    if (mfma_dx) {
       const auto ev = timing_begin(1, stream);
-      st = hip_check(launch_igemm(dtype, b.dg.mb, b.dg.nb, A, b.dg.lds, stream),
+      st = hip_check(launch_igemm(dtype, b.dg.mb, b.dg.nb, DA, b.dg.lds, stream),
                      "implicit GEMM input gradient");
       timing_end(ev, stream);
     } else {
@@ -1206,35 +1226,14 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     if (st != CONVND_HIP_SUCCESS) return st;
   }
   if (gw) {
-    if (b.wg.ok) {
-      WgradArgs A = b.wg.args;
-      void* staged = ws + b.off_x_stage;
-      float* partial = reinterpret_cast<float*>(ws + b.off_partial);
-      st = hip_check(launch_to_octets_padded(dtype, input, staged, A.batch, b.wg.pad, stream),
-                     "padded octet-major staging of input");
-      if (st != CONVND_HIP_SUCCESS) return st;
-      A.x = staged;
-      A.dy = grad_output;
-      A.partial = partial;
-      A.x_bytes = static_cast<int>(b.wg.staged_elems * 2);
-      A.dy_bytes = static_cast<int>(b.wg.dy_pad_elems * 2);
-      // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the
-      // boxes tile it exactly and its base is 16-byte aligned.
-      if (!b.wg.exact || reinterpret_cast<uintptr_t>(grad_output) % 16 != 0) {
-        void* padded = ws + b.off_dy_pad;
-        st = hip_check(launch_pad_grad_output(grad_output, padded, A,
-                                              b.wg.pad.split_batch, stream),
-                       "padded copy of grad_output");
-        if (st != CONVND_HIP_SUCCESS) return st;
-        A.dy = padded;
-      }
+    if (mfma_dw) {
       const auto ev = timing_begin(2, stream);
       st = hip_check(
-          launch_wgrad_mfma(dtype, b.wg.mb, b.wg.stg, b.wg.multi, A, b.wg.lds, stream),
+          launch_wgrad_mfma(dtype, b.wg.mb, b.wg.stg, b.wg.multi, WA, b.wg.lds, stream),
           "MFMA weight gradient");
       timing_end(ev, stream);
       if (st != CONVND_HIP_SUCCESS) return st;
-      st = hip_check(launch_wgrad_reduce(dtype, b.wg.mb, A, grad_weight, stream),
+      st = hip_check(launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream),
                      "weight-gradient reduction");
     } else {
       st = hip_check(launch_direct_grad_weight(dtype, to_direct(g), grad_output, input,

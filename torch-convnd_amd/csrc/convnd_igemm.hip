@@ -21,164 +21,24 @@
 // kernel runs (blockIdx.z covers batch x phase).
 
 #include "convnd_internal.h"
+#include "convnd_stage.h"
 #include "convnd_types.h"
 
 namespace convnd {
 namespace {
 
-struct AxisTaps {
-  int ntap, first, step;  // taps t = first + i*step for i < ntap
-  int emin, emax;         // range of the input shift e(t)
-  int sigma, cshift;      // input coordinate = j*sigma + cshift + e(t)
-  int J, r, os;           // j extent; output coordinate = r + os*j
-};
+using stage::AxisTaps;
+using stage::axis_e;
+using stage::phase_axes;
 
-__device__ __forceinline__ int gcd_i(int a, int b) {
-  while (b != 0) {
-    const int t = a % b;
-    a = b;
-    b = t;
-  }
-  return a;
-}
-
-__device__ __forceinline__ int mod_pos(int a, int b) {
-  const int m = a % b;
-  return m < 0 ? m + b : m;
-}
-
-__device__ __forceinline__ AxisTaps axis_taps(const IgemmArgs& A, int a, int r) {
-  AxisTaps t;
-  if (A.mode == 0) {
-    t.ntap = A.k[a];
-    t.first = 0;
-    t.step = 1;
-    t.emin = 0;
-    t.emax = (A.k[a] - 1) * A.d[a];
-    t.sigma = A.s[a];
-    t.cshift = -A.p[a];
-    t.J = A.out_size[a];
-    t.r = 0;
-    t.os = 1;
-    return t;
-  }
-  const int s = A.s[a], d = A.d[a], k = A.k[a];
-  const int st = s / gcd_i(s, d);
-  int first = -1;
-  for (int c = 0; c < k && c < st; ++c) {
-    if (mod_pos(r + A.p[a] - c * d, s) == 0) {
-      first = c;
-      break;
-    }
-  }
-  t.first = first < 0 ? 0 : first;
-  t.step = st;
-  t.ntap = first < 0 ? 0 : (k - 1 - first) / st + 1;
-  if (t.ntap > 0) {
-    t.emax = (r + A.p[a] - t.first * d) / s;
-    t.emin = (r + A.p[a] - (t.first + (t.ntap - 1) * st) * d) / s;
-  } else {
-    t.emax = 0;
-    t.emin = 0;
-  }
-  t.sigma = 1;
-  t.cshift = 0;
-  t.J = (A.out_size[a] - r + s - 1) / s;
-  t.r = r;
-  t.os = s;
-  return t;
-}
-
-__device__ __forceinline__ int axis_e(const IgemmArgs& A, int a, const AxisTaps& t, int i) {
-  const int tap = t.first + i * t.step;
-  return A.mode == 0 ? tap * A.d[a] : (t.r + A.p[a] - tap * A.d[a]) / A.s[a];
-}
-
-// Axis information of every axis for one phase; returns the phase's tap count.
-__device__ __forceinline__ int phase_axes(const IgemmArgs& A, int phase, AxisTaps* ax) {
-  int rr = phase, ntaps = 1;
-#pragma unroll
-  for (int a = kFastRank - 1; a >= 0; --a) {
-    if (a < A.rank) {
-      const int radix = A.mode ? A.s[a] : 1;
-      ax[a] = axis_taps(A, a, rr % radix);
-      rr /= radix;
-      ntaps *= ax[a].ntap;
-    }
-  }
-  return ntaps;
-}
-
-// ---- weight packing --------------------------------------------------------------------
-
-// Packed weights: unit u = ((((phase*G + g)*nchunk + chunk)*kc_max + kc)*mtiles_padded
-// + mt)*64 + lane holds the 8 A-fragment elements W'[m][k], m = mt*16 + lane%16,
-// k = kc*32 + (lane/16)*8 + i (i < 8), zero where m or k is padding.
-// S = float (split precision): GEMM channel ci is part split_other_part(ci / split_c) of
-// channel ci % split_c of the fp32 weight (zero past kSplitProducts copies).
 template <typename T, typename S>
 __global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const S* w, T* wpk,
                                                               int64_t units) {
-  const int R = A.rank;
-  {
-    for (int64_t u = blockIdx.x * (int64_t)kThreads + threadIdx.x; u < units;
-         u += (int64_t)gridDim.x * kThreads) {
-      int64_t r = u;
-      const int lane = r & 63;
-      r >>= 6;
-      const int mt = r % A.mtiles_padded;
-      r /= A.mtiles_padded;
-      const int kc = r % A.kc_max;
-      r /= A.kc_max;
-      const int ck = r % A.nchunk;
-      r /= A.nchunk;
-      const int g = r % A.groups;
-      const int phase = (int)(r / A.groups);
-      AxisTaps ax[kFastRank];
-      const int ntaps = phase_axes(A, phase, ax);
-      const int m = mt * 16 + (lane & 15);
-      const int kk = kc * 32 + (lane >> 4) * 8;
-      const int tau = kk / A.cc;
-      const int ci0 = ck * A.cc + (kk - tau * A.cc);
-      T vals[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vals[i] = static_cast<T>(0.f);
-      if (m < A.cout_g && tau < ntaps) {
-        int rem = tau, tflat = 0, kstr = 1;
-#pragma unroll
-        for (int a = kFastRank - 1; a >= 0; --a) {
-          if (a < R) {
-            const int idx = rem % ax[a].ntap;
-            rem /= ax[a].ntap;
-            tflat += (ax[a].first + idx * ax[a].step) * kstr;
-            kstr *= A.k[a];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          int ci = ci0 + i, part = 0;
-          if constexpr (sizeof(S) == 4) {
-            const int sp = ci / A.split_c;
-            if (sp >= kSplitProducts) continue;
-            ci -= sp * A.split_c;
-            part = split_other_part(sp);
-          }
-          const int64_t widx =
-              A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
-                          : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
-          if constexpr (sizeof(S) == 4) {
-            vals[i] = __builtin_bit_cast(T, bf16_part_bits(w[widx], part));
-          } else {
-            vals[i] = w[widx];
-          }
-        }
-      }
-      T* dst = wpk + u * 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dst[i] = vals[i];
-    }
-  }
+  stage::igemm_pack_blocks<T, S>(A, w, wpk, units, blockIdx.x, gridDim.x);
 }
+
+
+// ---- weight packing --------------------------------------------------------------------
 
 // ---- main kernel ---------------------------------------------------------------------
 
@@ -327,17 +187,17 @@ void igemm_kernel(IgemmArgs A) {
   // Bias of this wave's output channels, loaded now so its latency hides behind the loop.
   const int mt0 = (mg * WM + wm) * MB;  // first m-tile of this wave
   const int lg = lane >> 4;
-  float bias_v[MB][4];
+  // The MFMAs run with the positions as the A operand, so D = (W X)^T: lane l holds output
+  // channel (l % 16) of its m-tile at four consecutive box positions 4*(l/16) .. +3.
+  float bias_v[MB];
   {
     const O* bias = static_cast<const O*>(A.bias);
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = (mt0 + mb) * 16 + 4 * lg + i;
-        bias_v[mb][i] =
-            (bias != nullptr && m < A.cout_g) ? static_cast<float>(bias[g * A.cout_g + m]) : 0.f;
-      }
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = (mt0 + mb) * 16 + (lane & 15);
+      bias_v[mb] =
+          (bias != nullptr && m < A.cout_g) ? static_cast<float>(bias[g * A.cout_g + m]) : 0.f;
+    }
   }
 
   // Staging walk: item = ((row * noct) + octet) * hlast + column, 256 items apart per
@@ -462,7 +322,7 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a0[mb], b0[nb], acc[mb][nb]);
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b0[nb], a0[mb], acc[mb][nb]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[(size_t)n2 * wstep + mb * 64];
 #pragma unroll
@@ -472,7 +332,7 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a1[mb], b1[nb], acc[mb][nb]);
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b1[nb], a1[mb], acc[mb][nb]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[(size_t)n3 * wstep + mb * 64];
       }
@@ -480,7 +340,7 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(a0[mb], b0[nb], acc[mb][nb]);
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b0[nb], a0[mb], acc[mb][nb]);
       }
     }
     if (tail) {
@@ -500,16 +360,16 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(at[mb], bt[nb], acc[mb][nb]);
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(bt[nb], at[mb], acc[mb][nb]);
     }
     if (ck + 1 < A.nchunk) __syncthreads();  // every wave is done reading this chunk's halo
   }
 
-  // Epilogue. D[m][n] sits in lane (n + 16*(m/4)), register m%4. The tile (bias added,
-  // rounded to O) goes through LDS as [channel][box position] so that global stores write
-  // A.out_vec consecutive positions (up to 16 bytes) of one channel per lane; box position
-  // q maps to output offset origin + sum_a q_a * ofac[a] and lies inside the output when
-  // q_a < J - J0 on every axis.
+  // Epilogue: straight from the accumulators. A lane's four values are consecutive box
+  // positions on the box's last axis (its extent is a power of two; when it is at least 4
+  // and the output steps by 1 along that axis they are adjacent in memory: one 8-byte
+  // store for 16-bit O, 16 bytes for float). Box position q maps to output offset
+  // origin + sum_a q_a * ofac[a] and lies inside the output when q_a < J - J0 on every axis.
   O* out = static_cast<O*>(A.out);
   int origin = 0;
   bool interior = true;
@@ -527,63 +387,77 @@ void igemm_kernel(IgemmArgs A) {
       }
     }
   }
-  constexpr int kRowsWG = WM * MB * 16;  // output channels of the workgroup
-  // Elements per tile row: 16 bytes of skew per row for 16-bit O, 32 for float.
-  const int tstride = A.box_vol + 8;
-  O* tile = reinterpret_cast<O*>(lds);
-  __syncthreads();  // every wave is done with the halo planes and tables
+  int last_fac = 1, last_shift = 0;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ml = (wm * MB + mb) * 16 + 4 * lg + i;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int q = (wn * NB + nb) * 16 + (lane & 15);
-        tile[ml * tstride + q] = static_cast<O>(acc[mb][nb][i] + bias_v[mb][i]);
-      }
+  for (int a = 0; a < kFastRank; ++a) {
+    if (a == R - 1) {
+      last_fac = ofac[a];
+      last_shift = A.box_shift[a];
     }
   }
-  __syncthreads();
-  const int vec = A.out_vec;
-  const int per_row = A.box_vol / vec;
-  const int m_valid = A.cout_g - mg * kRowsWG;
-  for (int it = tid; it < kRowsWG * per_row; it += kThreads) {
-    const int ml = it / per_row;
-    const int q = (it - ml * per_row) * vec;
-    if (ml >= m_valid) continue;
-    // Output offset of box position q and, off the interior, whether its row is inside.
-    int qq = q, oo = origin, last_lim = vec;
-    bool ok = true;
+  const bool packed = interior && last_fac == 1 && last_shift >= 2;
 #pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        const int qa = qq & (A.box[a] - 1);
-        qq >>= A.box_shift[a];
-        oo += qa * ofac[a];
-        if (a == R - 1) {
-          last_lim = lim[a] - qa;
-        } else {
-          ok = ok && qa < lim[a];
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = (mt0 + mb) * 16 + (lane & 15);
+    if (m >= A.cout_g) continue;
+    O* orow = out + ((size_t)n * A.cout_total + g * A.cout_g + m) * A.out_vol + origin;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int q0 = (wn * NB + nb) * 16 + 4 * lg;
+      // Offset of box position q0 and, off the interior, how many of its 4 positions lie
+      // inside the output.
+      int qq = q0, oo = 0, nvalid = 4;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < R) {
+          const int qa = qq & (A.box[a] - 1);
+          qq >>= A.box_shift[a];
+          oo += qa * ofac[a];
+          if (!interior) {
+            if (a == R - 1) {
+              const int left = lim[a] - qa;
+              nvalid = left < nvalid ? left : nvalid;
+            } else if (qa >= lim[a]) {
+              nvalid = 0;
+            }
+          }
         }
       }
-    }
-    O* dst = out + ((size_t)n * A.cout_total + g * A.cout_g + mg * kRowsWG + ml) * A.out_vol + oo;
-    const O* src = tile + ml * tstride + q;
-    if (interior) {
-      const int bytes = vec * static_cast<int>(sizeof(O));
-      if (bytes == 16) {
-        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
-      } else if (bytes == 8) {
-        *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
-      } else if (bytes == 4) {
-        *reinterpret_cast<unsigned*>(dst) = *reinterpret_cast<const unsigned*>(src);
+      O v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(acc[mb][nb][i] + bias_v[mb]);
+      O* dst = orow + oo;
+      if (packed) {
+        if constexpr (sizeof(O) == 2) {
+          uint2 w;
+          w.x = __builtin_bit_cast(unsigned short, v[0]) |
+                ((unsigned)__builtin_bit_cast(unsigned short, v[1]) << 16);
+          w.y = __builtin_bit_cast(unsigned short, v[2]) |
+                ((unsigned)__builtin_bit_cast(unsigned short, v[3]) << 16);
+          *reinterpret_cast<uint2*>(dst) = w;
+        } else {
+          *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+        }
+      } else if (last_shift >= 2) {
+        // The four positions share every coordinate but the last.
+        for (int i = 0; i < nvalid; ++i) dst[i * last_fac] = v[i];
       } else {
-        dst[0] = src[0];
+        // Box rows shorter than 4: each position decodes on its own.
+        for (int i = 0; i < 4; ++i) {
+          int q = q0 + i, o2 = 0;
+          bool ok = true;
+#pragma unroll
+          for (int a = kFastRank - 1; a >= 0; --a) {
+            if (a < R) {
+              const int qa = q & (A.box[a] - 1);
+              q >>= A.box_shift[a];
+              o2 += qa * ofac[a];
+              ok = ok && (interior || qa < lim[a]);
+            }
+          }
+          if (ok) orow[o2] = v[i];
+        }
       }
-    } else if (ok) {
-      // Boundary box: the vector's positions share every coordinate but the last.
-      for (int v = 0; v < vec && v < last_lim; ++v) dst[v * ofac[R - 1]] = src[v];
     }
   }
 }

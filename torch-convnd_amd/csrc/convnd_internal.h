@@ -61,7 +61,6 @@ struct IgemmArgs {
   int box_vol, boxes;
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int k_vol;
-  int out_vec;     // output elements per epilogue store (consecutive positions, <= 16 bytes)
   int split_c;     // split-precision fp32: real channels per group in the GEMM-input role
 };
 
@@ -106,6 +105,37 @@ hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void
                                    int64_t batch, int64_t channels, int64_t volume,
                                    float* chan_sums, hipStream_t stream);
 int64_t channel_last_sum_blocks(int64_t batch, int64_t volume);
+
+// One launch for the staging passes that precede the MFMA kernels; each part is optional
+// (null pointers skip it) and runs on its own range of workgroups:
+//   GEMM input: channels-last copy (16-bit, with optional channel sums) or split-precision
+//               channels-last copy (split == true, fp32 source);
+//   weights:    packing for the implicit GEMM (ig);
+//   octets:     zero-padded octet-major input for the weight gradient (pad);
+//   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg).
+struct IgemmArgs;
+struct WgradArgs;
+struct PadArgs;
+struct PrologueParts {
+  const void* src = nullptr;
+  void* staged = nullptr;
+  float* sums = nullptr;
+  int64_t batch = 0, channels = 0, volume = 0;
+  bool split = false;
+  int groups = 1, cin_g = 0, cg_split = 0;
+  const IgemmArgs* ig = nullptr;
+  const void* w = nullptr;
+  void* wpk = nullptr;
+  const PadArgs* pad = nullptr;
+  const void* x = nullptr;
+  void* x_oct = nullptr;
+  int64_t oct_batch = 0;
+  const WgradArgs* wg = nullptr;
+  const void* dy = nullptr;
+  void* dy_pad = nullptr;
+  int split_batch = 0;
+};
+hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream);
 
 // Zero-padded octet-major copy: dst[n][c/8][u_0]..[u_{R-1}][c%8] = src[n][c'][u - pad] (zero
 // when u - pad lies outside the input), u_a < pe[a], where destination channel c is channel

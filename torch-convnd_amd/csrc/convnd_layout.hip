@@ -17,214 +17,118 @@
 // Every reduction has a fixed summation order, so results are bitwise repeatable.
 
 #include "convnd_internal.h"
+#include <cstring>
+#include <type_traits>
+
+#include "convnd_stage.h"
 #include "convnd_types.h"
 
 namespace convnd {
 namespace {
 
-constexpr int kTileV = 64;   // positions per transpose tile
-constexpr int kTileC = 64;   // channels per transpose tile
-constexpr int kTileStride = kTileV + 8;  // u16 per LDS tile row (16-byte skew)
+using stage::kTileC;
+using stage::kTileStride;
+using stage::kTileV;
 
-// Block (vt, ct, n): positions [vt*64, +64), channels [ct*64, +64) of image n.
 __global__ __launch_bounds__(kThreads) void to_channels_last16_kernel(
     const unsigned short* src, unsigned short* dst, int channels, int volume, float* sums,
     int sum_stride, bool is_bf16) {
   __shared__ __align__(16) unsigned short tile[kTileC * kTileStride];
   __shared__ float csum[kTileC];
-  const int tid = threadIdx.x;
-  const int v0 = blockIdx.x * kTileV;
-  const int c0 = blockIdx.y * kTileC;
-  const int n = blockIdx.z;
-  const int ct = channels - c0 < kTileC ? channels - c0 : kTileC;
-  const int vt = volume - v0 < kTileV ? volume - v0 : kTileV;
-  const bool full_v = vt == kTileV && (volume & 7) == 0;
-  const unsigned short* s = src + ((size_t)n * channels + c0) * volume + v0;
-  if (tid < kTileC) csum[tid] = 0.f;
-  // Load: item i -> channel i/8, positions 8*(i%8) .. +8.
-  for (int i = tid; i < ct * 8; i += kThreads) {
-    const int c = i >> 3;
-    const int p = (i & 7) * 8;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (full_v) {
-      v = *reinterpret_cast<const u32x4*>(s + (size_t)c * volume + p);
-    } else {
-      unsigned short e[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) e[k] = p + k < vt ? s[(size_t)c * volume + p + k] : 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) v[k] = e[2 * k] | ((unsigned)e[2 * k + 1] << 16);
-    }
-    *reinterpret_cast<u32x4*>(tile + c * kTileStride + p) = v;
-    if (sums != nullptr) {
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const unsigned lo = v[k] & 0xffffu, hi = v[k] >> 16;
-        if (is_bf16) {
-          acc += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
-        } else {
-          acc += static_cast<float>(__builtin_bit_cast(_Float16, (unsigned short)lo)) +
-                 static_cast<float>(__builtin_bit_cast(_Float16, (unsigned short)hi));
-        }
-      }
-      // The eight items of a channel are consecutive lanes: fixed-order butterfly.
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      acc += __shfl_xor(acc, 4);
-      if ((i & 7) == 0) csum[c] = acc;
-    }
-  }
-  __syncthreads();
-  if (sums != nullptr && tid < ct) {
-    const int blk = n * gridDim.x + blockIdx.x;
-    sums[(size_t)(c0 + tid) * sum_stride + blk] = csum[tid];
-  }
-  // Store: item i -> position i/8, channels 8*(i%8) .. +8.
-  const int cgroups = ct >> 3;
-  unsigned short* d = dst + ((size_t)n * volume + v0) * channels + c0;
-  for (int i = tid; i < vt * cgroups; i += kThreads) {
-    const int p = i / cgroups;
-    const int cg = (i - p * cgroups) * 8;
-    u32x4 v;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      v[k] = tile[(cg + 2 * k) * kTileStride + p] |
-             ((unsigned)tile[(cg + 2 * k + 1) * kTileStride + p] << 16);
-    *reinterpret_cast<u32x4*>(d + (size_t)p * channels + cg) = v;
-  }
+  stage::channels_last16_block(src, dst, channels, volume, sums, sum_stride, is_bf16,
+                               blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, tile, csum);
 }
 
-// Block (position tile, channel tile, n): 64 consecutive padded positions (flattened,
-// crossing rows) times 64 channels, through an LDS tile. Each position's source offset is
-// decoded once into LDS; loads are 2-byte with lanes along positions (coalesced within a
-// row, any alignment); stores are 16 bytes (one octet) with lanes along positions, so every
-// octet plane of the destination is written contiguously.
-// Src = float: the fp32 input split into bf16 parts; destination image n (of split_batch
-// x kSplitProducts) holds part split_data_part(n / split_batch) of source image
-// n % split_batch.
 template <typename Src>
 __global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const Src* src,
                                                                      unsigned short* dst,
                                                                      PadArgs P) {
   __shared__ __align__(16) unsigned short tile[kTileC * kTileStride];
   __shared__ int srcoff[kTileV];
-  const int tid = threadIdx.x;
-  const int R = P.rank;
-  const int p0 = blockIdx.x * kTileV;
-  const int c0 = blockIdx.y * kTileC;
-  const int n = blockIdx.z;
-  const int ct = P.channels - c0 < kTileC ? P.channels - c0 : kTileC;
-  const int vt = P.pvol - p0 < kTileV ? P.pvol - p0 : kTileV;
-  if (tid < kTileV) {
-    int off = -1;
-    if (tid < vt) {
-      int rem = p0 + tid, istr = 1;
-      off = 0;
-#pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int u = rem % P.pe[a];
-          rem /= P.pe[a];
-          const int i = u - P.pad[a];
-          if (off >= 0 && i >= 0 && i < P.in[a]) {
-            off += i * istr;
-          } else {
-            off = -1;
-          }
-          istr *= P.in[a];
-        }
-      }
-    }
-    srcoff[tid] = off;
-  }
-  __syncthreads();
-  int nsrc = n, part = 0;
-  if constexpr (sizeof(Src) == 4) {
-    nsrc = n % P.split_batch;
-    part = split_data_part(n / P.split_batch);
-  }
-  // Destination channel c0 + c is channel cc of group gi (dst_cg per group, the source's
-  // src_cg channels first, zero after).
-  const Src* s = src + (size_t)nsrc * P.src_channels * P.in_vol;
-  unsigned short e[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int i = tid + j * kThreads;
-    const int c = i >> 6, v = i & 63;
-    const int so = srcoff[v];
-    const int gi = (c0 + c) / P.dst_cg;
-    const int cc = c0 + c - gi * P.dst_cg;
-    const bool ok = c < ct && so >= 0 && cc < P.src_cg;
-    const size_t sidx = ((size_t)gi * P.src_cg + cc) * P.in_vol + so;
-    if constexpr (sizeof(Src) == 4) {
-      e[j] = ok ? bf16_part_bits(s[sidx], part) : 0;
-    } else {
-      e[j] = ok ? s[sidx] : 0;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int i = tid + j * kThreads;
-    tile[(i >> 6) * kTileStride + (i & 63)] = e[j];
-  }
-  __syncthreads();
-  const int octs = P.channels >> 3;
-  const int cgroups = ct >> 3;
-  for (int i = tid; i < cgroups * kTileV; i += kThreads) {
-    const int cg = i >> 6, v = i & 63;
-    if (v >= vt) continue;
-    u32x4 w;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      w[k] = tile[(cg * 8 + 2 * k) * kTileStride + v] |
-             ((unsigned)tile[(cg * 8 + 2 * k + 1) * kTileStride + v] << 16);
-    const size_t plane = (size_t)n * octs + (c0 >> 3) + cg;
-    *reinterpret_cast<u32x4*>(dst + (plane * P.pvol + p0 + v) * 8) = w;
-  }
+  stage::octets_padded16_block<Src>(src, dst, P, blockIdx.x, blockIdx.y, blockIdx.z, tile,
+                                    srcoff);
 }
 
-// fp32 [N][G*cin_g][V] -> bf16 [N][V][G*cg_split] for the split-precision GEMM: destination
-// channel s*cin_g + c of group g (s < kSplitProducts) holds part split_data_part(s) of
-// source channel g*cin_g + c; channels past kSplitProducts*cin_g are zero. Block (position
-// tile, group, n): the group's channels (at most 64) x 64 positions through LDS, then
-// 16-byte stores of 8 destination channels, consecutive lanes along the channels.
 __global__ __launch_bounds__(kThreads) void split_channels_last_kernel(const float* src,
                                                                       unsigned short* dst,
                                                                       int cin_g, int cg_split,
                                                                       int volume) {
   __shared__ float tile[kTileC * (kTileV + 1)];
-  const int tid = threadIdx.x;
-  const int v0 = blockIdx.x * kTileV;
-  const int g = blockIdx.y;
-  const int n = blockIdx.z;
-  const int groups = gridDim.y;
-  const int vt = volume - v0 < kTileV ? volume - v0 : kTileV;
-  const float* s = src + ((size_t)n * groups * cin_g + (size_t)g * cin_g) * volume + v0;
-  for (int i = tid; i < cin_g * kTileV; i += kThreads) {
-    const int c = i >> 6, v = i & 63;
-    tile[c * (kTileV + 1) + v] = v < vt ? s[(size_t)c * volume + v] : 0.f;
-  }
-  __syncthreads();
-  const int chunks = cg_split >> 3;
-  const size_t row = (size_t)groups * cg_split;
-  unsigned short* d = dst + ((size_t)n * volume + v0) * row + (size_t)g * cg_split;
-  for (int i = tid; i < vt * chunks; i += kThreads) {
-    const int v = i / chunks;
-    const int q = i - v * chunks;
-    unsigned h[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int c6 = q * 8 + k;
-      const int sp = c6 / cin_g;
-      const int c = c6 - sp * cin_g;
-      h[k] = sp < kSplitProducts
-                 ? bf16_part_bits(tile[c * (kTileV + 1) + v], split_data_part(sp))
-                 : 0u;
+  stage::split_channels_last_block(src, dst, cin_g, cg_split, volume, gridDim.y, blockIdx.x,
+                                   blockIdx.y, blockIdx.z, tile);
+}
+
+// ---- fused prologue ----------------------------------------------------------------------
+
+struct DevPrologue {
+  // GEMM input staging: grid (gx, gy, batch) flattened; channels-last or split.
+  const void* src;
+  void* staged;
+  float* sums;
+  int channels, volume, sum_stride, cin_g, cg_split, groups;
+  int gx, gy, a_blocks;
+  bool is_bf16;
+  // weight packing
+  IgemmArgs ig;
+  const void* w;
+  void* wpk;
+  int64_t units;
+  int b_blocks;
+  // octet-major padded input
+  PadArgs pad;
+  const void* x;
+  void* x_oct;
+  int cgx, cgy, c_blocks;
+  // padded grad_output
+  WgradArgs wg;
+  const void* dy;
+  void* dy_pad;
+  int split_batch;
+  int64_t runs;
+  int d_blocks;
+};
+
+// SPLIT: fp32 sources (split-precision staging, packing and weight-gradient copies).
+template <typename T, bool SPLIT>
+__global__ __launch_bounds__(kThreads) void prologue_kernel(DevPrologue P) {
+  __shared__ __align__(16) unsigned char smem[stage::kSmemBytes];
+  using S = typename std::conditional<SPLIT, float, unsigned short>::type;
+  using W = typename std::conditional<SPLIT, float, T>::type;
+  int b = blockIdx.x;
+  if (b < P.a_blocks) {
+    const int bx = b % P.gx, r = b / P.gx, by = r % P.gy, bz = r / P.gy;
+    if constexpr (SPLIT) {
+      stage::split_channels_last_block(static_cast<const float*>(P.src),
+                                       static_cast<unsigned short*>(P.staged), P.cin_g,
+                                       P.cg_split, P.volume, P.groups, bx, by, bz,
+                                       reinterpret_cast<float*>(smem));
+    } else {
+      stage::channels_last16_block(
+          static_cast<const unsigned short*>(P.src), static_cast<unsigned short*>(P.staged),
+          P.channels, P.volume, P.sums, P.sum_stride, P.is_bf16, bx, by, bz, P.gx,
+          reinterpret_cast<unsigned short*>(smem),
+          reinterpret_cast<float*>(smem + kTileC * kTileStride * 2));
     }
-    *reinterpret_cast<u32x4*>(d + (size_t)v * row + q * 8) =
-        u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    return;
   }
+  b -= P.a_blocks;
+  if (b < P.b_blocks) {
+    stage::igemm_pack_blocks<T, W>(P.ig, static_cast<const W*>(P.w), static_cast<T*>(P.wpk),
+                                   P.units, b, P.b_blocks);
+    return;
+  }
+  b -= P.b_blocks;
+  if (b < P.c_blocks) {
+    const int bx = b % P.cgx, r = b / P.cgx, by = r % P.cgy, bz = r / P.cgy;
+    stage::octets_padded16_block<S>(static_cast<const S*>(P.x),
+                                    static_cast<unsigned short*>(P.x_oct), P.pad, bx, by, bz,
+                                    reinterpret_cast<unsigned short*>(smem),
+                                    reinterpret_cast<int*>(smem + kTileC * kTileStride * 2));
+    return;
+  }
+  b -= P.c_blocks;
+  stage::pad_dy16_blocks<S>(static_cast<const S*>(P.dy), static_cast<unsigned short*>(P.dy_pad),
+                            P.wg, P.split_batch, P.runs, b, P.d_blocks);
 }
 
 // Partial sums of channel c over [N][C][V] (any element type): block (chunk, c) sums a
@@ -378,6 +282,83 @@ hipError_t launch_split_channels_last(const float* src, void* dst, int64_t batch
   hipLaunchKernelGGL(split_channels_last_kernel, grid, dim3(kThreads), 0, stream, src,
                      static_cast<unsigned short*>(dst), cin_g, cg_split,
                      static_cast<int>(volume));
+  return hipGetLastError();
+}
+
+hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream) {
+  DevPrologue P;
+  std::memset(&P, 0, sizeof(P));
+  const bool split = dtype == CONVND_HIP_FLOAT32;
+  if (!split && dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16)
+    return hipErrorInvalidValue;
+  int64_t total = 0;
+  if (p.staged != nullptr && p.batch > 0 && p.volume > 0) {
+    if (p.split != split || p.batch > 65535 || p.volume > 0x7fffffff) return hipErrorInvalidValue;
+    P.src = p.src;
+    P.staged = p.staged;
+    P.volume = static_cast<int>(p.volume);
+    P.gx = static_cast<int>((p.volume + kTileV - 1) / kTileV);
+    if (split) {
+      if (p.cin_g > kTileC || p.cg_split % 8 != 0 || p.cg_split < kSplitProducts * p.cin_g)
+        return hipErrorInvalidValue;
+      P.cin_g = p.cin_g;
+      P.cg_split = p.cg_split;
+      P.groups = p.groups;
+      P.gy = p.groups;
+    } else {
+      if (p.channels % 8 != 0) return hipErrorInvalidValue;
+      P.channels = static_cast<int>(p.channels);
+      P.gy = static_cast<int>((p.channels + kTileC - 1) / kTileC);
+      P.sums = p.sums;
+      P.sum_stride = static_cast<int>(P.gx * p.batch);
+      P.is_bf16 = dtype == CONVND_HIP_BFLOAT16;
+    }
+    total = (int64_t)P.gx * P.gy * p.batch;
+    P.a_blocks = static_cast<int>(total);
+  }
+  if (p.wpk != nullptr && p.ig != nullptr) {
+    const IgemmArgs& a = *p.ig;
+    P.ig = a;
+    P.w = p.w;
+    P.wpk = p.wpk;
+    P.units = (int64_t)a.nphase * a.groups * a.nchunk * a.kc_max * a.mtiles_padded * 64;
+    const int64_t blocks = (P.units + kThreads - 1) / kThreads;
+    P.b_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
+    total += P.b_blocks;
+  }
+  if (p.x_oct != nullptr && p.pad != nullptr && p.oct_batch > 0) {
+    P.pad = *p.pad;
+    P.x = p.x;
+    P.x_oct = p.x_oct;
+    P.cgx = static_cast<int>(((int64_t)P.pad.pvol + kTileV - 1) / kTileV);
+    P.cgy = (P.pad.channels + kTileC - 1) / kTileC;
+    P.c_blocks = static_cast<int>((int64_t)P.cgx * P.cgy * p.oct_batch);
+    total += P.c_blocks;
+  }
+  if (p.dy_pad != nullptr && p.wg != nullptr) {
+    const WgradArgs& a = *p.wg;
+    P.wg = a;
+    P.dy = p.dy;
+    P.dy_pad = p.dy_pad;
+    P.split_batch = p.split_batch;
+    int dlast = 8;
+    for (int i = 0; i < a.rank; ++i)
+      if (i == a.rank - 1) dlast = a.dext[i];
+    P.runs = (int64_t)a.batch * a.cout_total * (a.dvol / dlast) * (dlast / 8);
+    const int64_t blocks = (P.runs + kThreads - 1) / kThreads;
+    P.d_blocks = static_cast<int>(blocks < 2048 ? blocks : 2048);
+    total += P.d_blocks;
+  }
+  if (total == 0) return hipSuccess;
+  if (total > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(total));
+  if (split) {
+    hipLaunchKernelGGL((prologue_kernel<__bf16, true>), grid, dim3(kThreads), 0, stream, P);
+  } else if (dtype == CONVND_HIP_BFLOAT16) {
+    hipLaunchKernelGGL((prologue_kernel<__bf16, false>), grid, dim3(kThreads), 0, stream, P);
+  } else {
+    hipLaunchKernelGGL((prologue_kernel<_Float16, false>), grid, dim3(kThreads), 0, stream, P);
+  }
   return hipGetLastError();
 }
 

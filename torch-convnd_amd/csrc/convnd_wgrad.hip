@@ -27,6 +27,7 @@
 //     fixed order and scatters them into the weight layout (deterministic, no atomics).
 
 #include "convnd_internal.h"
+#include "convnd_stage.h"
 #include "convnd_types.h"
 
 namespace convnd {
@@ -377,65 +378,11 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
   }
 }
 
-// Zero-padded copy of grad_output: dst[nc][u...] = src[nc][u...] for u inside the output
-// extents, else zero; each thread writes 8 consecutive elements of the last axis (whose
-// padded extent is a multiple of 8). Src = float (split precision): destination image n of
-// A.batch = kSplitProducts x split_batch holds part split_other_part(n / split_batch) of
-// source image n % split_batch.
 template <typename Src>
 __global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const Src* src, unsigned short* dst,
                                                             WgradArgs A, int split_batch,
                                                             int64_t total_runs) {
-  const int R = A.rank;
-  int dlast = 8, olast = 1;
-#pragma unroll
-  for (int a = 0; a < kFastRank; ++a) {
-    if (a == R - 1) {
-      dlast = A.dext[a];
-      olast = A.out_size[a];
-    }
-  }
-  const int runs = dlast >> 3;
-  const int drows = A.dvol / dlast;
-  for (int64_t t = blockIdx.x * (int64_t)kThreads + threadIdx.x; t < total_runs;
-       t += (int64_t)gridDim.x * kThreads) {
-    const int64_t rowd = t / runs;  // (nc, padded row) index
-    const int u0 = static_cast<int>(t - rowd * runs) * 8;
-    const int64_t nc = rowd / drows;
-    int rem = static_cast<int>(rowd - nc * drows);
-    int64_t snc = nc;
-    int part = 0;
-    if constexpr (sizeof(Src) == 4) {
-      const int64_t n = nc / A.cout_total, c = nc - n * A.cout_total;
-      snc = (n % split_batch) * A.cout_total + c;
-      part = split_other_part(static_cast<int>(n / split_batch));
-    }
-    int srow = 0, istr = olast;
-    bool ok = true;
-#pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        const int u = rem % A.dext[a];
-        rem /= A.dext[a];
-        ok = ok && u < A.out_size[a];
-        srow += u * istr;
-        istr *= A.out_size[a];
-      }
-    }
-    const Src* s = src + snc * A.out_vol + srow;
-    auto bits = [&](int e) -> unsigned {
-      if (!ok || e >= olast) return 0u;
-      if constexpr (sizeof(Src) == 4) {
-        return bf16_part_bits(s[e], part);
-      } else {
-        return s[e];
-      }
-    };
-    unsigned w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w[k] = bits(u0 + 2 * k) | (bits(u0 + 2 * k + 1) << 16);
-    *reinterpret_cast<u32x4*>(dst + rowd * dlast + u0) = u32x4{w[0], w[1], w[2], w[3]};
-  }
+  stage::pad_dy16_blocks<Src>(src, dst, A, split_batch, total_runs, blockIdx.x, gridDim.x);
 }
 
 template <typename T, int MB, int STG, bool MULTI>
