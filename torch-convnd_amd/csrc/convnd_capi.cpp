@@ -229,6 +229,7 @@ struct IgemmPlan {
   size_t lds = 0;
   size_t wpk_elems = 0;
   size_t staged_elems = 0;  // channels-last copy of the GEMM's input operand
+  size_t table_bytes = 0;   // geometry tables (IgemmArgs::tables)
   int conflict = 1;         // lanes per 16-byte bank slot in a B-fragment read (1 = none)
   double cost = 0.0;
 };
@@ -475,12 +476,13 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
       if (filter.cc && filter.cc != cc) continue;
       const int noct = cc / 8;
       const int64_t kc = (ntaps_max * cc + 31) / 32;
-      const int64_t table_bytes = align_up(kc * 4 * 4);
       const int64_t nchunk = gemm_cin / cc;
+      // Box coordinates are packed in 16-bit fields up to rank 4 and in 8-bit fields above
+      // (extents at most 64 there).
       int limit[kFastRank];
       for (int a = 0; a < R; ++a) {
         int l = 1;
-        while (l < J[a] && l < box_vol) l *= 2;
+        while (l < J[a] && l < box_vol && (R <= 4 || l < 64)) l *= 2;
         limit[a] = l;
       }
       for_each_box(R, limit, box_vol, [&](const int* b) {
@@ -498,7 +500,7 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
           boxes *= (J[a] + b[a] - 1) / b[a];
           useful *= J[a];
         }
-        if (noct * hvol * 16 + table_bytes > kLdsBudget) return;
+        if (noct * hvol * 16 > kLdsBudget) return;
         // Row validity masks hold 64 halo coordinates per axis; coordinates are packed in
         // bytes in the row table.
         for (int a = 0; a < R; ++a)
@@ -516,7 +518,9 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         conflict = hit->second.conflict;
         const int64_t plane_pos = hit->second.plane_pos;
         const int64_t plane_bytes = align_up(plane_pos * 16);
-        const int64_t lds = noct * plane_bytes + table_bytes + align_up(rows * 8);
+        const int tap_row = static_cast<int>((kc + kTapPad + 3) / 4 * 4);
+        const int64_t lds = noct * plane_bytes + align_up(rows * 8) + align_up(box_vol * 4) +
+                            align_up(16 * tap_row);
         if (rows > (int64_t{1} << 20)) return;
         // Epilogue stores: a lane writes 4 consecutive positions at once when they are
         // adjacent in the output (box rows of at least 4, unit output step on the last axis).
@@ -604,14 +608,36 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.boxes = static_cast<int>(boxes);
         A.k_vol = static_cast<int>(g.k_vol);
         A.split_c = split ? real_cin : 0;
+        A.last_size = A.in_size[R - 1];
+        A.packed_ok = run == 4 ? 1 : 0;
+        A.coord_bits = R <= 4 ? 16 : 8;
+        A.tap_row = tap_row;
         plan.lds = static_cast<size_t>(lds);
       });
     }
   }
   if (plan.ok) {
-    const IgemmArgs& A = plan.args;
+    IgemmArgs& A = plan.args;
     plan.wpk_elems = (size_t)A.nphase * A.groups * A.nchunk * A.kc_max * A.mtiles_padded * 64 * 8;
     plan.staged_elems = (size_t)A.batch * A.in_vol * A.cin_total;
+    // Geometry tables: taps, tail, positions, rows, boxes (each 256-byte aligned).
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+      const size_t o = at;
+      at += align_up(bytes);
+      return static_cast<int>(o);
+    };
+    A.tab_taps = take((size_t)A.nphase * 4 * A.tap_row * 4);
+    A.tab_tail = take((size_t)A.nphase * 4 * 4);
+    A.tab_pos = take((size_t)A.box_vol * 16);
+    A.tab_rows = take((size_t)A.rows * 16);
+    A.tab_box = take((size_t)A.nphase * A.boxes * sizeof(IgemmBox));
+    if (at > (size_t)kI32Safe) {
+      plan.ok = false;
+      return plan;
+    }
+    A.tab_bytes = static_cast<int>(at);
+    plan.table_bytes = at;
   }
   return plan;
 }
@@ -857,7 +883,7 @@ struct Layout {
 
 struct ForwardSetup {
   IgemmPlan ig;
-  size_t off_stage = 0, off_wpk = 0;
+  size_t off_stage = 0, off_wpk = 0, off_tables = 0;
   size_t bytes = 0;
 };
 
@@ -900,6 +926,7 @@ ForwardSetup make_forward(const Geom& g, convnd_hip_dtype dt) {
     // Staged operands and packed weights are 16-bit (bf16 parts for split-precision fp32).
     f.off_stage = L.take(f.ig.staged_elems * 2);
     f.off_wpk = L.take(f.ig.wpk_elems * 2);
+    f.off_tables = L.take(f.ig.table_bytes);
   }
   f.bytes = L.total;
   return f;
@@ -909,7 +936,7 @@ struct BackwardSetup {
   IgemmPlan dg;
   WgradPlan wg;
   size_t off_dy_stage = 0, off_wpk = 0, off_x_stage = 0, off_partial = 0, off_bias = 0;
-  size_t off_dy_pad = 0;
+  size_t off_dy_pad = 0, off_tables = 0;
   size_t bytes = 0;
 };
 
@@ -927,6 +954,7 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
     if (b.dg.ok) {
       b.off_dy_stage = L.take(b.dg.staged_elems * 2);
       b.off_wpk = L.take(b.dg.wpk_elems * 2);
+      b.off_tables = L.take(b.dg.table_bytes);
     }
   }
   if (gw && g.batch > 0) {
@@ -1084,7 +1112,8 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   IgemmArgs A = f.ig.args;
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
-  // Input staging and weight packing in one launch.
+  A.tables = ws + f.off_tables;
+  // Input staging, weight packing and the geometry tables in one launch.
   PrologueParts pp;
   pp.src = input;
   pp.staged = staged;
@@ -1162,6 +1191,7 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   PrologueParts pp;
   if (mfma_dx) {
     DA = b.dg.args;
+    DA.tables = ws + b.off_tables;
     DA.in = ws + b.off_dy_stage;
     DA.wpk = ws + b.off_wpk;
     DA.bias = nullptr;

@@ -11,9 +11,10 @@
 //   * K is ordered (channel chunk, tap, channel). A B fragment is one 16-byte LDS read at
 //     pos[q] + tap[k]; A fragments (weights) are packed per call in MFMA lane order and read
 //     from global memory (L2 resident, 16 bytes per lane).
-//   * Per-workgroup index tables (tap offsets, halo rows) are computed into LDS with plain
-//     arithmetic before the first halo load, so no global-memory round trip precedes the
-//     staging; box positions decode with shifts (power-of-two box extents).
+//   * The geometry (tap offsets, halo rows, box positions and per-box origins and bounds)
+//     comes from small tables that the prologue launch writes once per call, so the kernel
+//     has no per-axis code: its setup is a few table reads and its epilogue one store per
+//     fragment for boxes inside the output.
 // The input gradient of a strided convolution is split into stride phases: output
 // coordinate x = r + s*j (r the phase residue); the taps that reach phase r are those with
 // (r + pad - t*d) divisible by s, each at the shifted input e(t) = (r + pad - t*d) / s.
@@ -27,19 +28,6 @@
 namespace convnd {
 namespace {
 
-using stage::AxisTaps;
-using stage::axis_e;
-using stage::phase_axes;
-
-template <typename T, typename S>
-__global__ __launch_bounds__(kThreads) void igemm_pack_kernel(IgemmArgs A, const S* w, T* wpk,
-                                                              int64_t units) {
-  stage::igemm_pack_blocks<T, S>(A, w, wpk, units, blockIdx.x, gridDim.x);
-}
-
-
-// ---- weight packing --------------------------------------------------------------------
-
 // ---- main kernel ---------------------------------------------------------------------
 
 // Register budget: two waves per SIMD (256 VGPR+AGPR per wave) for tiles up to 16
@@ -49,6 +37,8 @@ template <int MB, int NB>
 constexpr int igemm_waves = MB * NB >= 32 ? 1 : 2;
 
 // T: GEMM operand type; O: output and bias type (T, or float for split-precision fp32).
+// Every per-axis quantity comes from the geometry tables (IgemmArgs::tables), so the
+// kernel body is the same for every rank.
 template <typename T, typename O, int MB, int NB, int WM>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(igemm_waves<MB, NB>, igemm_waves<MB, NB>)))
@@ -61,7 +51,7 @@ void igemm_kernel(IgemmArgs A) {
   const int wave = tid >> 6;
   const int wm = wave % WM;
   const int wn = wave / WM;
-  const int R = A.rank;
+  const int lg = lane >> 4;
   const int n = blockIdx.z / A.nphase;
   const int phase = blockIdx.z % A.nphase;
   const int g = blockIdx.y / A.mgroups;
@@ -77,116 +67,49 @@ void igemm_kernel(IgemmArgs A) {
       bx = x * q + (x < rem ? x : rem) + idx;
     }
   }
+  const char* tab = static_cast<const char*>(A.tables);
+  const IgemmBox& box = reinterpret_cast<const IgemmBox*>(tab + A.tab_box)[phase * A.boxes + bx];
+  const int flags = box.flags;
+  if (flags & 1) return;  // uniform over the workgroup (phase with a shorter j extent)
+  const int KC = box.kc;
+  const int KF = box.kf;
 
-  AxisTaps ax[kFastRank];
-  const int ntaps = phase_axes(A, phase, ax);
-  int J0[kFastRank], horg[kFastRank];
-  bool outside = false;
-  {
-    int bb = bx;
-#pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        J0[a] = (bb % A.nbox[a]) * A.box[a];
-        bb /= A.nbox[a];
-        outside |= J0[a] >= ax[a].J;
-        horg[a] = J0[a] * ax[a].sigma + ax[a].cshift + ax[a].emin;
-      }
-    }
-  }
-  if (outside) return;  // uniform over the workgroup (phase with a shorter j extent)
-  const int KC = (ntaps * A.cc + 31) / 32;
-  const int KF = (ntaps * A.cc) / 32;
-
-  // Per axis (all but the last): bit h of valid[a] says halo coordinate h is inside the
-  // tensor. The input position of the halo origin over those axes (may lie outside the
-  // tensor; only rows whose coordinates are all valid use it).
-  unsigned long long valid[kFastRank];
-  int in_base = n * A.in_vol;
-  int istride[kFastRank];
-  {
-    int istr = A.in_size[R - 1];
-#pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        const int lo = horg[a] < 0 ? -horg[a] : 0;
-        int hi = A.in_size[a] - horg[a];
-        hi = hi < A.hext[a] ? hi : A.hext[a];
-        unsigned long long m = 0;
-        if (hi > lo) {
-          const unsigned long long upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1);
-          m = upto & ~((1ull << lo) - 1);
-        }
-        valid[a] = m;
-        istride[a] = istr;
-        in_base += horg[a] * istr;
-        istr *= A.in_size[a];
-      }
-    }
-  }
-  const int hlast = A.hlast;
-  const int corg = horg[R - 1];
-  const int last_size = A.in_size[R - 1];
-
-  // LDS: [octet planes | tap table (kc_max*4 ints) | rows: input offset (-1 outside), LDS
-  // position offset]. Both tables are computed here, before the first halo load.
-  int* tbl = reinterpret_cast<int*>(lds + A.halo_bytes);
-  int* rowin = tbl + A.kc_max * 4;
+  // LDS: [octet planes | rows: input offset (-1 outside the input), LDS position offset |
+  // output offset of every box position (read by the epilogue; kept out of registers
+  // during the main loop) | the phase's tap offsets, 4 lane groups x tap_row].
+  int* rowin = reinterpret_cast<int*>(lds + A.halo_bytes);
   int* rowlds = rowin + A.rows;
-  for (int idx = tid; idx < KC * 4; idx += kThreads) {
-    // K-group idx: 8 channels of one tap; -1 past the phase's last tap.
-    const int kk = idx * 8;
-    const int tau = kk / A.cc;
-    const int ci = kk - tau * A.cc;
-    int off = -1;
-    if (tau < ntaps) {
-      int rem = tau, t = 0;
-#pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int i = rem % ax[a].ntap;
-          rem /= ax[a].ntap;
-          t += (axis_e(A, a, ax[a], i) - ax[a].emin) * A.hpitch[a];
-        }
-      }
-      off = t * 16 + (ci >> 3) * A.plane_bytes;
-    }
-    tbl[idx] = off;
+  int* posout = rowlds + A.rows;
+  int* ltaps = posout + ((A.box_vol + 3) & ~3);
+  const int4* pt = reinterpret_cast<const int4*>(tab + A.tab_pos);
+  for (int q = tid; q < A.box_vol; q += kThreads) posout[q] = pt[q].y;
+  {
+    const int* gt = reinterpret_cast<const int*>(tab + A.tab_taps) + phase * 4 * A.tap_row;
+    for (int i = tid; i < 4 * A.tap_row; i += kThreads) ltaps[i] = gt[i];
   }
-  for (int r = tid; r < A.rows; r += kThreads) {
-    int rem = r, lds_pos = 0, in_off = 0;
-    bool ok = true;
-#pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        const int h = rem % A.hext[a];
-        rem /= A.hext[a];
-        lds_pos += h * A.hpitch[a];
-        in_off += h * istride[a];
-        ok = ok && ((valid[a] >> h) & 1ull);
-      }
+  {
+    const int4* rt = reinterpret_cast<const int4*>(tab + A.tab_rows);
+    const unsigned long long lo = box.lo, hi = box.hi;
+    const int in_base = n * A.in_vol + box.in_base;
+    for (int r = tid; r < A.rows; r += kThreads) {
+      const int4 e = rt[r];
+      const unsigned long long h =
+          static_cast<unsigned>(e.z) | (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
+      const bool ok = swar_all_ge(h, lo, kGuard8) && swar_all_less(h, hi, kGuard8, kOnes8);
+      rowin[r] = ok ? in_base + e.y : -1;
+      rowlds[r] = e.x;
     }
-    rowin[r] = ok ? in_base + in_off : -1;
-    rowlds[r] = lds_pos;
   }
-  // Per-lane LDS byte offsets of this wave's NB position blocks (box extents are powers of
-  // two, so positions decode with shifts).
+  // Per lane and position block: LDS byte offset of the lane's B-fragment position.
   int pbase[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    int q = (wn * NB + nb) * 16 + (lane & 15), off = 0;
-#pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        off += (q & (A.box[a] - 1)) * ax[a].sigma * A.hpitch[a];
-        q >>= A.box_shift[a];
-      }
-    }
-    pbase[nb] = off * 16;
-  }
+  for (int nb = 0; nb < NB; ++nb) pbase[nb] = pt[(wn * NB + nb) * 16 + (lane & 15)].x;
+  // Tap offsets of this lane group (LDS, read in pairs of steps ahead of use); the partial
+  // last step separately.
+  const int* tp = ltaps + lg * A.tap_row;
+  const int tail_tap = reinterpret_cast<const int*>(tab + A.tab_tail)[phase * 4 + lg];
   // Bias of this wave's output channels, loaded now so its latency hides behind the loop.
   const int mt0 = (mg * WM + wm) * MB;  // first m-tile of this wave
-  const int lg = lane >> 4;
   // The MFMAs run with the positions as the A operand, so D = (W X)^T: lane l holds output
   // channel (l % 16) of its m-tile at four consecutive box positions 4*(l/16) .. +3.
   float bias_v[MB];
@@ -202,6 +125,9 @@ void igemm_kernel(IgemmArgs A) {
 
   // Staging walk: item = ((row * noct) + octet) * hlast + column, 256 items apart per
   // thread; the division happens once and every later item updates incrementally.
+  const int hlast = A.hlast;
+  const int corg = box.corg;
+  const int last_size = A.last_size;
   const int items = A.rows * A.noct * hlast;
   const int rp0 = tid / hlast, c0 = tid - (tid / hlast) * hlast;
   const int drp = kThreads / hlast, dc = kThreads - drp * hlast;
@@ -216,12 +142,11 @@ void igemm_kernel(IgemmArgs A) {
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const size_t wstep = (size_t)A.mtiles_padded * 64;  // fragments per K32 step
-  const bool tail = KF < KC;
   // Halo staging in batches of kStageBatch items per thread: the loads of a batch are all
   // in flight before the first LDS store. The first batch of the next chunk is loaded into
   // registers before the current chunk's MFMA loop and stored after it, so its latency
   // hides behind the MFMAs.
-  constexpr int kStageBatch = 8;
+  constexpr int kStageBatch = 4;
   const T* chunk_base = in + g * A.cin_g;
   u32x4 pre[kStageBatch];
   auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v) {
@@ -295,66 +220,93 @@ void igemm_kernel(IgemmArgs A) {
                       ((size_t)((phase * A.groups + g) * A.nchunk + ck) * A.kc_max) * wstep +
                       (size_t)mt0 * 64 + lane;
     if (KF > 0) {
-      // Software pipeline over the full steps: weights two K32 steps ahead (global,
-      // L2-resident), B fragments one step ahead and tap offsets two steps ahead (LDS).
-      // Every prefetch is unconditional (indices clamp to the last full step), so the
-      // compiler's wait counts cover exactly the loads each MFMA group needs.
+      // Software pipeline over the whole steps, four steps per iteration: weights three
+      // K32 steps ahead (global, L2-resident; four fragment sets in flight), B fragments
+      // one step ahead (LDS), tap offsets four at a time a full iteration ahead (LDS; the
+      // table repeats the last whole step past the end, so every prefetch is unconditional
+      // and stays inside the halo). The scheduling fences keep each step's loads ahead of
+      // the MFMAs they overlap (left alone, the scheduler sinks every load next to its
+      // first use and the prefetch distance collapses).
       const int last = KF - 1;
-      frag a0[MB], a1[MB], b0[NB], b1[NB];
-      const int s1 = last < 1 ? last : 1;
+      auto wstep_at = [&](int k) { return (size_t)(k < last ? k : last) * wstep; };
+      frag a0[MB], a1[MB], a2[MB], a3[MB], b0[NB], b1[NB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[mb * 64];
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[(size_t)s1 * wstep + mb * 64];
-      const int t0 = tbl[lg];
-      int t1 = tbl[s1 * 4 + lg];
+      for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[wstep_at(1) + mb * 64];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) a2[mb] = wck[wstep_at(2) + mb * 64];
+      int4 t = *reinterpret_cast<const int4*>(tp);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
-        b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t0);
-      int kc = 0;
-      for (; kc + 1 < KF; kc += 2) {
-        const int n2 = kc + 2 < last ? kc + 2 : last;
-        const int n3 = kc + 3 < last ? kc + 3 : last;
+        b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t.x);
+      // One step: B fragments of the next step into bn (tap offset tn), weights of step
+      // ks into al, MFMAs of the current step (bc, ac).
+      auto step = [&](frag* bn, int tn, frag* al, int ks, const frag* bc, const frag* ac) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          b1[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t1);
-        const int t2 = tbl[n2 * 4 + lg];
+          bn[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + tn);
+        const size_t ws = wstep_at(ks);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) al[mb] = wck[ws + mb * 64];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(bc[nb], ac[mb], acc[mb][nb]);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      int kc = 0;
+      for (; kc + 3 < KF; kc += 4) {
+        const int4 tn = *reinterpret_cast<const int4*>(tp + kc + 4);
+        step(b1, t.y, a3, kc + 3, b0, a0);
+        step(b0, t.z, a0, kc + 4, b1, a1);
+        step(b1, t.w, a1, kc + 5, b0, a2);
+        step(b0, tn.x, a2, kc + 6, b1, a3);
+        t = tn;
+      }
+      // 0 to 3 whole steps remain: B of step kc is in b0, weights of kc .. kc+2 in a0..a2.
+      const int left = KF - kc;
+      if (left >= 1) {
+        if (left >= 2) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            b1[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t.y);
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b0[nb], a0[mb], acc[mb][nb]);
+      }
+      if (left >= 2) {
+        if (left >= 3) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) a0[mb] = wck[(size_t)n2 * wstep + mb * 64];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t2);
-        t1 = tbl[n3 * 4 + lg];
+          for (int nb = 0; nb < NB; ++nb)
+            b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t.z);
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b1[nb], a1[mb], acc[mb][nb]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) a1[mb] = wck[(size_t)n3 * wstep + mb * 64];
       }
-      if (kc < KF) {  // odd number of full steps: the last one is already in (a0, b0)
+      if (left >= 3) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b0[nb], a0[mb], acc[mb][nb]);
+          for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b0[nb], a2[mb], acc[mb][nb]);
       }
     }
-    if (tail) {
-      // The last K32 step holds k-groups past the phase's last tap (table entry -1): their
+    if (KC > KF) {
+      // The partial last step holds k-groups past the phase's last tap (offset -1): their
       // B fragments are zero, so padding never multiplies a zero weight by a non-finite
       // input.
-      const int tt = tbl[KF * 4 + lg];
       frag at[MB], bt[NB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) at[mb] = wck[(size_t)KF * wstep + mb * 64];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(lds + pbase[nb] + (tt < 0 ? 0 : tt));
-        if (tt < 0) v = u32x4{0u, 0u, 0u, 0u};
+        u32x4 v = *reinterpret_cast<const u32x4*>(lds + pbase[nb] + (tail_tap < 0 ? 0 : tail_tap));
+        if (tail_tap < 0) v = u32x4{0u, 0u, 0u, 0u};
         bt[nb] = __builtin_bit_cast(frag, v);
       }
 #pragma unroll
@@ -365,69 +317,25 @@ void igemm_kernel(IgemmArgs A) {
     if (ck + 1 < A.nchunk) __syncthreads();  // every wave is done reading this chunk's halo
   }
 
-  // Epilogue: straight from the accumulators. A lane's four values are consecutive box
-  // positions on the box's last axis (its extent is a power of two; when it is at least 4
-  // and the output steps by 1 along that axis they are adjacent in memory: one 8-byte
-  // store for 16-bit O, 16 bytes for float). Box position q maps to output offset
-  // origin + sum_a q_a * ofac[a] and lies inside the output when q_a < J - J0 on every axis.
+  // Epilogue: straight from the accumulators. A lane's four values are box positions
+  // 4*lg .. 4*lg+3 of its position block. In a box inside the output whose rows have at
+  // least 4 positions on a unit output step they are adjacent: one 8-byte store for 16-bit
+  // O, 16 bytes for float. Otherwise every position has its own offset and bounds check.
   O* out = static_cast<O*>(A.out);
-  int origin = 0;
-  bool interior = true;
-  int lim[kFastRank], ofac[kFastRank];
-  {
-    int ostr = 1;
+  const size_t chan0 = (size_t)n * A.cout_total + (size_t)g * A.cout_g;
+  O* obox = out + box.out_origin;
+  if (A.packed_ok && (flags & 2)) {
 #pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        origin += (ax[a].r + ax[a].os * J0[a]) * ostr;
-        ofac[a] = ax[a].os * ostr;
-        ostr *= A.out_size[a];
-        lim[a] = ax[a].J - J0[a];
-        interior = interior && lim[a] >= A.box[a];
-      }
-    }
-  }
-  int last_fac = 1, last_shift = 0;
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = (mt0 + mb) * 16 + (lane & 15);
+      if (m >= A.cout_g) continue;
+      O* orow = obox + (chan0 + m) * A.out_vol;
 #pragma unroll
-  for (int a = 0; a < kFastRank; ++a) {
-    if (a == R - 1) {
-      last_fac = ofac[a];
-      last_shift = A.box_shift[a];
-    }
-  }
-  const bool packed = interior && last_fac == 1 && last_shift >= 2;
+      for (int nb = 0; nb < NB; ++nb) {
+        O v[4];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int m = (mt0 + mb) * 16 + (lane & 15);
-    if (m >= A.cout_g) continue;
-    O* orow = out + ((size_t)n * A.cout_total + g * A.cout_g + m) * A.out_vol + origin;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int q0 = (wn * NB + nb) * 16 + 4 * lg;
-      // Offset of box position q0 and, off the interior, how many of its 4 positions lie
-      // inside the output.
-      int qq = q0, oo = 0, nvalid = 4;
-#pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int qa = qq & (A.box[a] - 1);
-          qq >>= A.box_shift[a];
-          oo += qa * ofac[a];
-          if (!interior) {
-            if (a == R - 1) {
-              const int left = lim[a] - qa;
-              nvalid = left < nvalid ? left : nvalid;
-            } else if (qa >= lim[a]) {
-              nvalid = 0;
-            }
-          }
-        }
-      }
-      O v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(acc[mb][nb][i] + bias_v[mb]);
-      O* dst = orow + oo;
-      if (packed) {
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(acc[mb][nb][i] + bias_v[mb]);
+        O* dst = orow + posout[(wn * NB + nb) * 16 + 4 * lg];
         if constexpr (sizeof(O) == 2) {
           uint2 w;
           w.x = __builtin_bit_cast(unsigned short, v[0]) |
@@ -438,25 +346,33 @@ void igemm_kernel(IgemmArgs A) {
         } else {
           *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
         }
-      } else if (last_shift >= 2) {
-        // The four positions share every coordinate but the last.
-        for (int i = 0; i < nvalid; ++i) dst[i * last_fac] = v[i];
-      } else {
-        // Box rows shorter than 4: each position decodes on its own.
-        for (int i = 0; i < 4; ++i) {
-          int q = q0 + i, o2 = 0;
-          bool ok = true;
+      }
+    }
+  } else {
+    const unsigned long long lim = box.lim;
+    const unsigned long long guard = A.coord_bits == 16 ? kGuard16 : kGuard8;
+    const unsigned long long ones = A.coord_bits == 16 ? kOnes16 : kOnes8;
+    int off[NB][4];
 #pragma unroll
-          for (int a = kFastRank - 1; a >= 0; --a) {
-            if (a < R) {
-              const int qa = q & (A.box[a] - 1);
-              q >>= A.box_shift[a];
-              o2 += qa * ofac[a];
-              ok = ok && (interior || qa < lim[a]);
-            }
-          }
-          if (ok) orow[o2] = v[i];
-        }
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int4 e = pt[(wn * NB + nb) * 16 + 4 * lg + i];
+        const unsigned long long c =
+            static_cast<unsigned>(e.z) | (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
+        off[nb][i] = swar_all_less(c, lim, guard, ones) ? e.y : -1;
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = (mt0 + mb) * 16 + (lane & 15);
+      if (m >= A.cout_g) continue;
+      O* orow = obox + (chan0 + m) * A.out_vol;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (off[nb][i] >= 0) orow[off[nb][i]] = static_cast<O>(acc[mb][nb][i] + bias_v[mb]);
       }
     }
   }
@@ -493,27 +409,6 @@ bool igemm_tile_supported(int mb, int nb, int wm) {
   CONVND_IGEMM_TILES(CONVND_IGEMM_HAS)
 #undef CONVND_IGEMM_HAS
   return false;
-}
-
-hipError_t launch_igemm_prep(convnd_hip_dtype dtype, const IgemmArgs& a, const void* w,
-                             void* wpk, hipStream_t stream) {
-  const int64_t units = (int64_t)a.nphase * a.groups * a.nchunk * a.kc_max * a.mtiles_padded * 64;
-  if (units == 0) return hipSuccess;
-  const int64_t blocks64 = (units + kThreads - 1) / kThreads;
-  const dim3 grid(static_cast<unsigned>(blocks64 < 4096 ? blocks64 : 4096));
-  if (dtype == CONVND_HIP_BFLOAT16) {
-    hipLaunchKernelGGL((igemm_pack_kernel<__bf16, __bf16>), grid, dim3(kThreads), 0, stream, a,
-                       static_cast<const __bf16*>(w), static_cast<__bf16*>(wpk), units);
-  } else if (dtype == CONVND_HIP_FLOAT16) {
-    hipLaunchKernelGGL((igemm_pack_kernel<_Float16, _Float16>), grid, dim3(kThreads), 0, stream,
-                       a, static_cast<const _Float16*>(w), static_cast<_Float16*>(wpk), units);
-  } else if (dtype == CONVND_HIP_FLOAT32 && a.split_c > 0) {
-    hipLaunchKernelGGL((igemm_pack_kernel<__bf16, float>), grid, dim3(kThreads), 0, stream, a,
-                       static_cast<const float*>(w), static_cast<__bf16*>(wpk), units);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
 }
 
 hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,

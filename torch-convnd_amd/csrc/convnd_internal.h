@@ -62,7 +62,57 @@ struct IgemmArgs {
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int k_vol;
   int split_c;     // split-precision fp32: real channels per group in the GEMM-input role
+  // Geometry tables in device memory, written by the prologue launch (igemm_tables) and
+  // read by the GEMM kernel, which then needs no per-axis code:
+  //   taps  int  [nphase][4 lane groups][tap_row]: LDS byte offset of the k-group (tap,
+  //              octet) of K32 step k; entries from the phase's last whole step on repeat
+  //              that step (prefetches past the end stay inside the halo);
+  //   tail  int  [nphase][4]: the same for the partial last step, -1 past the last tap;
+  //   pos   int4 [box_vol]: {halo byte offset, output offset, box coordinates (2 x 32 bit)};
+  //   rows  int4 [rows]: {halo position offset, input position offset, halo coordinates};
+  //   boxes IgemmBox [nphase][boxes].
+  // Coordinates are packed one field per axis (axis a in field a) so that one subtraction
+  // compares every axis against packed bounds (see swar_all_less / swar_all_ge).
+  void* tables;
+  int tab_taps, tab_tail, tab_pos, tab_rows, tab_box;  // byte offsets in `tables`
+  int tab_bytes;
+  int tap_row;       // entries per (phase, lane group): kc_max + kTapPad, rounded to 4
+  int last_size;     // input extent of the last axis
+  int packed_ok;     // interior boxes store 4 adjacent outputs per lane
+  int coord_bits;    // field width of box coordinates (16 when rank <= 4, else 8)
 };
+
+constexpr int kTapPad = 8;
+
+// Per (phase, box) state of the implicit GEMM (64 bytes).
+struct IgemmBox {
+  int in_base;     // input position offset of the halo origin over all axes but the last
+  int corg;        // halo origin on the last axis (may be negative)
+  int out_origin;  // output offset of the box origin
+  int flags;       // bit 0: the box lies past the phase's output; bit 1: fully inside it
+  int kc, kf;      // K32 steps of the phase: all, and whole ones
+  int unused0, unused1;
+  unsigned long long lo, hi;  // halo rows inside the input: lo <= h < hi per axis (8 bits)
+  unsigned long long lim;     // box positions inside the output: q < lim per axis
+  unsigned long long unused2;
+};
+static_assert(sizeof(IgemmBox) == 64, "IgemmBox is one 64-byte record");
+
+// Packed-field comparisons (every value below the guard bit of its field, so no borrow
+// crosses a field boundary): all fields of c below lim / at least lo.
+__host__ __device__ inline bool swar_all_less(unsigned long long c, unsigned long long lim,
+                                              unsigned long long guard,
+                                              unsigned long long ones) {
+  return (((lim | guard) - (c + ones)) & guard) == guard;
+}
+__host__ __device__ inline bool swar_all_ge(unsigned long long c, unsigned long long lo,
+                                            unsigned long long guard) {
+  return (((c | guard) - lo) & guard) == guard;
+}
+constexpr unsigned long long kGuard8 = 0x8080808080808080ull;
+constexpr unsigned long long kOnes8 = 0x0101010101010101ull;
+constexpr unsigned long long kGuard16 = 0x8000800080008000ull;
+constexpr unsigned long long kOnes16 = 0x0001000100010001ull;
 
 // Arguments of the MFMA weight-gradient kernel. Columns are (octet of 8 input channels,
 // tap) pairs, octet slowest; a workgroup owns 64 consecutive pairs (max_oct octets at most).
@@ -110,7 +160,8 @@ int64_t channel_last_sum_blocks(int64_t batch, int64_t volume);
 // (null pointers skip it) and runs on its own range of workgroups:
 //   GEMM input: channels-last copy (16-bit, with optional channel sums) or split-precision
 //               channels-last copy (split == true, fp32 source);
-//   weights:    packing for the implicit GEMM (ig);
+//   weights:    packing for the implicit GEMM (ig), and its geometry tables when
+//               ig->tables is set;
 //   octets:     zero-padded octet-major input for the weight gradient (pad);
 //   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg).
 struct IgemmArgs;
@@ -170,9 +221,6 @@ hipError_t launch_direct_grad_weight(convnd_hip_dtype dtype, const DirectGeom& g
 hipError_t launch_grad_bias(convnd_hip_dtype dtype, int64_t batch, int64_t channels,
                             int64_t volume, const void* dy, void* db, float* scratch,
                             int64_t chunks, hipStream_t stream);
-// Packs the weights into the implicit GEMM's A-fragment order.
-hipError_t launch_igemm_prep(convnd_hip_dtype dtype, const IgemmArgs& a, const void* w,
-                             void* wpk, hipStream_t stream);
 hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,
                         size_t lds_bytes, hipStream_t stream);
 // Whether launch_igemm has a compiled kernel for this wave tile (mb x nb fragments) and

@@ -74,6 +74,8 @@ struct DevPrologue {
   void* wpk;
   int64_t units;
   int b_blocks;
+  // implicit-GEMM geometry tables (of ig)
+  int t_blocks;
   // octet-major padded input
   PadArgs pad;
   const void* x;
@@ -118,6 +120,11 @@ __global__ __launch_bounds__(kThreads) void prologue_kernel(DevPrologue P) {
     return;
   }
   b -= P.b_blocks;
+  if (b < P.t_blocks) {
+    stage::igemm_table_blocks(P.ig, b, P.t_blocks);
+    return;
+  }
+  b -= P.t_blocks;
   if (b < P.c_blocks) {
     const int bx = b % P.cgx, r = b / P.cgx, by = r % P.cgy, bz = r / P.cgy;
     stage::octets_padded16_block<S>(static_cast<const S*>(P.x),
@@ -325,6 +332,12 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     const int64_t blocks = (P.units + kThreads - 1) / kThreads;
     P.b_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
     total += P.b_blocks;
+    if (a.tables != nullptr) {
+      const int64_t tunits = stage::igemm_table_units(a);
+      const int64_t tb = (tunits + kThreads - 1) / kThreads;
+      P.t_blocks = static_cast<int>(tb < 1024 ? tb : 1024);
+      total += P.t_blocks;
+    }
   }
   if (p.x_oct != nullptr && p.pad != nullptr && p.oct_batch > 0) {
     P.pad = *p.pad;

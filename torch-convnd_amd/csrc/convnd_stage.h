@@ -172,6 +172,158 @@ __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w
   }
 }
 
+// ---- implicit-GEMM geometry tables ------------------------------------------------------
+
+// Entries of the geometry tables (IgemmArgs::tables): taps, tail, positions, rows, boxes.
+__host__ __device__ inline int64_t igemm_table_units(const IgemmArgs& A) {
+  return (int64_t)A.nphase * 4 * A.tap_row + (int64_t)A.nphase * 4 + A.box_vol + A.rows +
+         (int64_t)A.nphase * A.boxes;
+}
+
+// LDS byte offset of k-group (K32 step `step`, lane group lg) of a phase: tap part plus
+// octet plane, or -1 past the phase's last tap.
+__device__ __forceinline__ int igemm_tap_offset(const IgemmArgs& A, const AxisTaps* ax,
+                                                int ntaps, int step, int lg) {
+  const int kk = (step * 4 + lg) * 8;
+  const int tau = kk / A.cc;
+  const int ci = kk - tau * A.cc;
+  if (tau >= ntaps) return -1;
+  int rem = tau, t = 0;
+#pragma unroll
+  for (int a = kFastRank - 1; a >= 0; --a) {
+    if (a < A.rank) {
+      const int i = rem % ax[a].ntap;
+      rem /= ax[a].ntap;
+      t += (axis_e(A, a, ax[a], i) - ax[a].emin) * A.hpitch[a];
+    }
+  }
+  return t * 16 + (ci >> 3) * A.plane_bytes;
+}
+
+// Writes the geometry tables that the GEMM kernel reads (one entry per thread).
+__device__ __forceinline__ void igemm_table_blocks(const IgemmArgs& A, int block, int nblocks) {
+  const int R = A.rank;
+  char* tab = static_cast<char*>(A.tables);
+  const int64_t n_taps = (int64_t)A.nphase * 4 * A.tap_row;
+  const int64_t n_tail = (int64_t)A.nphase * 4;
+  const int64_t units = igemm_table_units(A);
+  const int cb = A.coord_bits;
+  for (int64_t u = block * (int64_t)kThreads + threadIdx.x; u < units;
+       u += (int64_t)nblocks * kThreads) {
+    int64_t e = u;
+    if (e < n_taps + n_tail) {
+      const bool tail = e >= n_taps;
+      if (tail) e -= n_taps;
+      const int k = tail ? 0 : static_cast<int>(e % A.tap_row);
+      const int pl = static_cast<int>(tail ? e : e / A.tap_row);
+      const int phase = pl >> 2, lg = pl & 3;
+      AxisTaps ax[kFastRank];
+      const int ntaps = phase_axes(A, phase, ax);
+      const int kf = ntaps * A.cc / 32, kcn = (ntaps * A.cc + 31) / 32;
+      int v;
+      if (tail) {
+        v = kcn > kf ? igemm_tap_offset(A, ax, ntaps, kf, lg) : -1;
+        reinterpret_cast<int*>(tab + A.tab_tail)[e] = v;
+      } else {
+        v = kf > 0 ? igemm_tap_offset(A, ax, ntaps, k < kf ? k : kf - 1, lg) : 0;
+        reinterpret_cast<int*>(tab + A.tab_taps)[e] = v;
+      }
+      continue;
+    }
+    e -= n_taps + n_tail;
+    if (e < A.box_vol) {
+      int qq = static_cast<int>(e), halo = 0, orel = 0, ostr = 1;
+      unsigned long long c = 0;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < R) {
+          const int qa = qq & (A.box[a] - 1);
+          qq >>= A.box_shift[a];
+          halo += qa * (A.mode == 0 ? A.s[a] : 1) * A.hpitch[a];
+          orel += qa * (A.mode == 0 ? 1 : A.s[a]) * ostr;
+          ostr *= A.out_size[a];
+          c |= static_cast<unsigned long long>(qa) << (a * cb);
+        }
+      }
+      reinterpret_cast<int4*>(tab + A.tab_pos)[e] =
+          int4{halo * 16, orel, static_cast<int>(c & 0xffffffffu), static_cast<int>(c >> 32)};
+      continue;
+    }
+    e -= A.box_vol;
+    if (e < A.rows) {
+      int rem = static_cast<int>(e), lpos = 0, irel = 0, istr = A.last_size;
+      unsigned long long h = 0;
+#pragma unroll
+      for (int a = kFastRank - 2; a >= 0; --a) {
+        if (a < R - 1) {
+          const int ha = rem % A.hext[a];
+          rem /= A.hext[a];
+          lpos += ha * A.hpitch[a];
+          irel += ha * istr;
+          istr *= A.in_size[a];
+          h |= static_cast<unsigned long long>(ha) << (a * 8);
+        }
+      }
+      reinterpret_cast<int4*>(tab + A.tab_rows)[e] =
+          int4{lpos, irel, static_cast<int>(h & 0xffffffffu), static_cast<int>(h >> 32)};
+      continue;
+    }
+    e -= A.rows;
+    {
+      const int phase = static_cast<int>(e / A.boxes);
+      int bb = static_cast<int>(e - (int64_t)phase * A.boxes);
+      AxisTaps ax[kFastRank];
+      const int ntaps = phase_axes(A, phase, ax);
+      IgemmBox B;
+      B.in_base = 0;
+      B.corg = 0;
+      B.out_origin = 0;
+      B.kc = (ntaps * A.cc + 31) / 32;
+      B.kf = ntaps * A.cc / 32;
+      B.unused0 = B.unused1 = 0;
+      B.unused2 = 0;
+      bool outside = false, interior = true;
+      unsigned long long lo = 0, hi = 0, lim = 0;
+      int istr = 1, ostr = 1;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < R) {
+          const int j0 = (bb % A.nbox[a]) * A.box[a];
+          bb /= A.nbox[a];
+          outside = outside || j0 >= ax[a].J;
+          const int horg = j0 * ax[a].sigma + ax[a].cshift + ax[a].emin;
+          int l = ax[a].J - j0;
+          interior = interior && l >= A.box[a];
+          l = l < 0 ? 0 : (l > A.box[a] ? A.box[a] : l);
+          lim |= static_cast<unsigned long long>(l) << (a * cb);
+          B.out_origin += (ax[a].r + ax[a].os * j0) * ostr;
+          ostr *= A.out_size[a];
+          if (a == R - 1) {
+            B.corg = horg;
+          } else {
+            B.in_base += horg * istr;
+            int lo_a = -horg, hi_a = A.in_size[a] - horg;
+            lo_a = lo_a < 0 ? 0 : (lo_a > A.hext[a] ? A.hext[a] : lo_a);
+            hi_a = hi_a < 0 ? 0 : (hi_a > A.hext[a] ? A.hext[a] : hi_a);
+            lo |= static_cast<unsigned long long>(lo_a) << (a * 8);
+            hi |= static_cast<unsigned long long>(hi_a) << (a * 8);
+          }
+          istr *= A.in_size[a];
+        } else {
+          // Axes past the rank: coordinate 0 always passes.
+          if (a * cb < 64) lim |= 1ull << (a * cb);
+        }
+        if (a >= R - 1) hi |= 1ull << (a * 8);
+      }
+      B.flags = (outside ? 1 : 0) | (interior ? 2 : 0);
+      B.lo = lo;
+      B.hi = hi;
+      B.lim = lim;
+      reinterpret_cast<IgemmBox*>(tab + A.tab_box)[e] = B;
+    }
+  }
+}
+
 
 // ---- layout passes ----------------------------------------------------------------------
 
