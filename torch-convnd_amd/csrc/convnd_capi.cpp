@@ -19,6 +19,7 @@
 #include <utility>
 #include <vector>
 
+#include "convnd_geometry.h"
 #include "convnd_internal.h"
 
 namespace convnd {
@@ -230,6 +231,7 @@ struct IgemmPlan {
   size_t wpk_elems = 0;
   size_t staged_elems = 0;  // channels-last copy of the GEMM's input operand
   size_t table_bytes = 0;   // geometry tables (IgemmArgs::tables)
+  PadArgs stage{};          // octet-major copy of the GEMM input (no padding)
   int conflict = 1;         // lanes per 16-byte bank slot in a B-fragment read (1 = none)
   double cost = 0.0;
 };
@@ -620,24 +622,29 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
     IgemmArgs& A = plan.args;
     plan.wpk_elems = (size_t)A.nphase * A.groups * A.nchunk * A.kc_max * A.mtiles_padded * 64 * 8;
     plan.staged_elems = (size_t)A.batch * A.in_vol * A.cin_total;
-    // Geometry tables: taps, tail, positions, rows, boxes (each 256-byte aligned).
-    size_t at = 0;
-    auto take = [&](size_t bytes) {
-      const size_t o = at;
-      at += align_up(bytes);
-      return static_cast<int>(o);
-    };
-    A.tab_taps = take((size_t)A.nphase * 4 * A.tap_row * 4);
-    A.tab_tail = take((size_t)A.nphase * 4 * 4);
-    A.tab_pos = take((size_t)A.box_vol * 16);
-    A.tab_rows = take((size_t)A.rows * 16);
-    A.tab_box = take((size_t)A.nphase * A.boxes * sizeof(IgemmBox));
+    // Geometry tables (built and copied to the device once per plan and device).
+    const size_t at = igemm_table_layout(A);
     if (at > (size_t)kI32Safe) {
       plan.ok = false;
       return plan;
     }
-    A.tab_bytes = static_cast<int>(at);
     plan.table_bytes = at;
+    PadArgs& S = plan.stage;
+    std::memset(&S, 0, sizeof(S));
+    S.rank = R;
+    S.channels = A.cin_total;
+    S.src_channels = static_cast<int>(real_cin * g.groups);
+    S.src_cg = real_cin;
+    S.dst_cg = A.cin_g;
+    S.split_c = split ? real_cin : 0;
+    S.split_batch = 0;
+    for (int a = 0; a < R; ++a) {
+      S.in[a] = A.in_size[a];
+      S.pe[a] = A.in_size[a];
+      S.pad[a] = 0;
+    }
+    S.in_vol = A.in_vol;
+    S.pvol = A.in_vol;
   }
   return plan;
 }
@@ -883,7 +890,7 @@ struct Layout {
 
 struct ForwardSetup {
   IgemmPlan ig;
-  size_t off_stage = 0, off_wpk = 0, off_tables = 0;
+  size_t off_stage = 0, off_wpk = 0;
   size_t bytes = 0;
 };
 
@@ -926,7 +933,6 @@ ForwardSetup make_forward(const Geom& g, convnd_hip_dtype dt) {
     // Staged operands and packed weights are 16-bit (bf16 parts for split-precision fp32).
     f.off_stage = L.take(f.ig.staged_elems * 2);
     f.off_wpk = L.take(f.ig.wpk_elems * 2);
-    f.off_tables = L.take(f.ig.table_bytes);
   }
   f.bytes = L.total;
   return f;
@@ -936,7 +942,7 @@ struct BackwardSetup {
   IgemmPlan dg;
   WgradPlan wg;
   size_t off_dy_stage = 0, off_wpk = 0, off_x_stage = 0, off_partial = 0, off_bias = 0;
-  size_t off_dy_pad = 0, off_tables = 0;
+  size_t off_dy_pad = 0;
   size_t bytes = 0;
 };
 
@@ -954,7 +960,6 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
     if (b.dg.ok) {
       b.off_dy_stage = L.take(b.dg.staged_elems * 2);
       b.off_wpk = L.take(b.dg.wpk_elems * 2);
-      b.off_tables = L.take(b.dg.table_bytes);
     }
   }
   if (gw && g.batch > 0) {
@@ -969,7 +974,7 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
     // Partial sums of the bias gradient: per channel, kBiasChunks doubles on the standalone
     // path or one float per 64-position tile when they come with the channels-last copy.
     const size_t fused = (gi && b.dg.ok && is_half(dt))
-                             ? (size_t)channel_last_sum_blocks(g.batch, g.out_vol) * sizeof(float)
+                             ? (size_t)octet_sum_blocks(g.batch, g.out_vol) * sizeof(float)
                              : 0;
     b.off_bias = L.take((size_t)g.out_channels * std::max(fused, kBiasChunks * sizeof(double)));
   }
@@ -981,6 +986,32 @@ BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool g
   static PlanCache<BackwardSetup> cache;
   const int kind = 1 + (gi ? 1 : 0) + (gw ? 2 : 0) + (gb ? 4 : 0);
   return cached_plan(cache, plan_key(g, dt, kind), [&] { return make_backward(g, dt, gi, gw, gb); });
+}
+
+// Geometry tables of an implicit-GEMM plan in device memory: built on the host and copied
+// once per (plan, device) on first use, then shared by every call with that plan (they are
+// never written again, so concurrent calls on any stream may read them). The copy is
+// synchronous, so the first call of a geometry must not be under stream capture. The
+// memory lives as long as the process.
+const void* igemm_device_tables(const std::string& key, const IgemmArgs& A) {
+  static std::mutex lock;
+  static std::unordered_map<std::string, const void*> map;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const std::string k = key + std::string(reinterpret_cast<const char*>(&dev), sizeof(dev));
+  std::lock_guard<std::mutex> guard(lock);
+  auto it = map.find(k);
+  if (it != map.end()) return it->second;
+  std::vector<unsigned char> host(static_cast<size_t>(A.tab_bytes), 0);
+  igemm_build_tables(A, host.data());
+  void* d = nullptr;
+  if (hipMalloc(&d, host.size()) != hipSuccess) return nullptr;
+  if (hipMemcpy(d, host.data(), host.size(), hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(d);
+    return nullptr;
+  }
+  map.emplace(k, d);
+  return d;
 }
 
 // Diagnostic kernel timing (convnd_hip_timing_enable/read): event pairs recorded around
@@ -1112,18 +1143,15 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   IgemmArgs A = f.ig.args;
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
-  A.tables = ws + f.off_tables;
+  A.tables = igemm_device_tables(plan_key(g, dtype, 0), A);
+  if (A.tables == nullptr)
+    return fail(CONVND_HIP_LAUNCH_FAILED, "implicit GEMM geometry tables: device allocation failed");
   // Input staging, weight packing and the geometry tables in one launch.
   PrologueParts pp;
+  pp.sa = &f.ig.stage;
   pp.src = input;
   pp.staged = staged;
   pp.batch = g.batch;
-  pp.volume = g.in_vol;
-  pp.channels = g.channels;
-  pp.split = A.split_c > 0;
-  pp.groups = static_cast<int>(g.groups);
-  pp.cin_g = A.split_c;
-  pp.cg_split = A.cin_g;
   pp.ig = &A;
   pp.w = weight;
   pp.wpk = wpk;
@@ -1191,21 +1219,19 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   PrologueParts pp;
   if (mfma_dx) {
     DA = b.dg.args;
-    DA.tables = ws + b.off_tables;
+    DA.tables = igemm_device_tables(plan_key(g, dtype, 64), DA);
+    if (DA.tables == nullptr)
+      return fail(CONVND_HIP_LAUNCH_FAILED,
+                  "implicit GEMM geometry tables: device allocation failed");
     DA.in = ws + b.off_dy_stage;
     DA.wpk = ws + b.off_wpk;
     DA.bias = nullptr;
     DA.out = grad_input;
+    pp.sa = &b.dg.stage;
     pp.src = grad_output;
     pp.staged = ws + b.off_dy_stage;
     pp.sums = sums;
     pp.batch = g.batch;
-    pp.volume = g.out_vol;
-    pp.channels = g.out_channels;
-    pp.split = DA.split_c > 0;
-    pp.groups = static_cast<int>(g.groups);
-    pp.cin_g = DA.split_c;
-    pp.cg_split = DA.cin_g;
     pp.ig = &DA;
     pp.w = weight;
     pp.wpk = ws + b.off_wpk;
@@ -1237,7 +1263,7 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   }
   if (fused_bias) {
     st = hip_check(launch_grad_bias_from_sums(dtype, sums,
-                                              channel_last_sum_blocks(g.batch, g.out_vol),
+                                              octet_sum_blocks(g.batch, g.out_vol),
                                               g.out_channels, grad_bias, stream),
                    "bias gradient");
     if (st != CONVND_HIP_SUCCESS) return st;

@@ -1,0 +1,265 @@
+// Tap geometry of the implicit GEMM, shared by the host planner and the kernels.
+//
+// The planner builds the geometry tables (IgemmArgs::tables) once per plan with the
+// functions below and copies them to device memory owned by the plan; the kernels only
+// read them. Everything here is plain integer arithmetic, compiled for host and device.
+#pragma once
+
+#include "convnd_internal.h"
+
+namespace convnd {
+
+struct AxisTaps {
+  int ntap, first, step;  // taps t = first + i*step for i < ntap
+  int emin, emax;         // range of the input shift e(t)
+  int sigma, cshift;      // input coordinate = j*sigma + cshift + e(t)
+  int J, r, os;           // j extent; output coordinate = r + os*j
+};
+
+__host__ __device__ inline int gcd_i(int a, int b) {
+  while (b != 0) {
+    const int t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+__host__ __device__ inline int mod_pos(int a, int b) {
+  const int m = a % b;
+  return m < 0 ? m + b : m;
+}
+
+// Axis a of the forward convolution (mode 0), or of stride phase r of the input gradient
+// (mode 1): output coordinate x = r + s*j; the taps reaching phase r are those with
+// (r + pad - t*d) divisible by s, each at the shifted input e(t) = (r + pad - t*d) / s.
+__host__ __device__ inline AxisTaps axis_taps(const IgemmArgs& A, int a, int r) {
+  AxisTaps t;
+  if (A.mode == 0) {
+    t.ntap = A.k[a];
+    t.first = 0;
+    t.step = 1;
+    t.emin = 0;
+    t.emax = (A.k[a] - 1) * A.d[a];
+    t.sigma = A.s[a];
+    t.cshift = -A.p[a];
+    t.J = A.out_size[a];
+    t.r = 0;
+    t.os = 1;
+    return t;
+  }
+  const int s = A.s[a], d = A.d[a], k = A.k[a];
+  const int st = s / gcd_i(s, d);
+  int first = -1;
+  for (int c = 0; c < k && c < st; ++c) {
+    if (mod_pos(r + A.p[a] - c * d, s) == 0) {
+      first = c;
+      break;
+    }
+  }
+  t.first = first < 0 ? 0 : first;
+  t.step = st;
+  t.ntap = first < 0 ? 0 : (k - 1 - first) / st + 1;
+  if (t.ntap > 0) {
+    t.emax = (r + A.p[a] - t.first * d) / s;
+    t.emin = (r + A.p[a] - (t.first + (t.ntap - 1) * st) * d) / s;
+  } else {
+    t.emax = 0;
+    t.emin = 0;
+  }
+  t.sigma = 1;
+  t.cshift = 0;
+  t.J = (A.out_size[a] - r + s - 1) / s;
+  t.r = r;
+  t.os = s;
+  return t;
+}
+
+__host__ __device__ inline int axis_e(const IgemmArgs& A, int a, const AxisTaps& t, int i) {
+  const int tap = t.first + i * t.step;
+  return A.mode == 0 ? tap * A.d[a] : (t.r + A.p[a] - tap * A.d[a]) / A.s[a];
+}
+
+// Axis information of every axis for one phase; returns the phase's tap count.
+__host__ __device__ inline int phase_axes(const IgemmArgs& A, int phase, AxisTaps* ax) {
+  int rr = phase, ntaps = 1;
+  for (int a = A.rank - 1; a >= 0; --a) {
+    const int radix = A.mode ? A.s[a] : 1;
+    ax[a] = axis_taps(A, a, rr % radix);
+    rr /= radix;
+    ntaps *= ax[a].ntap;
+  }
+  return ntaps;
+}
+
+// LDS byte offset of k-group (K32 step `step`, lane group lg) of a phase: tap part plus
+// octet plane, or -1 past the phase's last tap.
+__host__ __device__ inline int igemm_tap_offset(const IgemmArgs& A, const AxisTaps* ax,
+                                                int ntaps, int step, int lg) {
+  const int kk = (step * 4 + lg) * 8;
+  const int tau = kk / A.cc;
+  const int ci = kk - tau * A.cc;
+  if (tau >= ntaps) return -1;
+  int rem = tau, t = 0;
+  for (int a = A.rank - 1; a >= 0; --a) {
+    const int i = rem % ax[a].ntap;
+    rem /= ax[a].ntap;
+    t += (axis_e(A, a, ax[a], i) - ax[a].emin) * A.hpitch[a];
+  }
+  return t * 16 + (ci >> 3) * A.plane_bytes;
+}
+
+// Flat weight tap index (row-major over the kernel extents) of tap tau of a phase, and the
+// channel of k-group (step, lg) within its chunk: the weight-packing map {tflat, channel},
+// tflat = -1 past the phase's last tap.
+__host__ __device__ inline void igemm_pack_entry(const IgemmArgs& A, const AxisTaps* ax,
+                                                 int ntaps, int step, int lg, int* tflat,
+                                                 int* chan) {
+  const int kk = step * 32 + lg * 8;
+  const int tau = kk / A.cc;
+  *chan = kk - tau * A.cc;
+  if (tau >= ntaps) {
+    *tflat = -1;
+    return;
+  }
+  int rem = tau, tf = 0, kstr = 1;
+  for (int a = A.rank - 1; a >= 0; --a) {
+    const int idx = rem % ax[a].ntap;
+    rem /= ax[a].ntap;
+    tf += (ax[a].first + idx * ax[a].step) * kstr;
+    kstr *= A.k[a];
+  }
+  *tflat = tf;
+}
+
+// Per (phase, box) record of the box table.
+__host__ __device__ inline IgemmBox igemm_box_entry(const IgemmArgs& A, int phase, int bx) {
+  const int R = A.rank;
+  const int cb = A.coord_bits;
+  AxisTaps ax[kFastRank];
+  const int ntaps = phase_axes(A, phase, ax);
+  IgemmBox B;
+  B.in_base = 0;
+  B.corg = 0;
+  B.out_origin = 0;
+  B.kc = (ntaps * A.cc + 31) / 32;
+  B.kf = ntaps * A.cc / 32;
+  B.unused0 = B.unused1 = 0;
+  B.unused2 = 0;
+  bool outside = false, interior = true;
+  unsigned long long lo = 0, hi = 0, lim = 0;
+  int istr = 1, ostr = 1, bb = bx;
+  for (int a = kFastRank - 1; a >= 0; --a) {
+    if (a < R) {
+      const int j0 = (bb % A.nbox[a]) * A.box[a];
+      bb /= A.nbox[a];
+      outside = outside || j0 >= ax[a].J;
+      const int horg = j0 * ax[a].sigma + ax[a].cshift + ax[a].emin;
+      int l = ax[a].J - j0;
+      interior = interior && l >= A.box[a];
+      l = l < 0 ? 0 : (l > A.box[a] ? A.box[a] : l);
+      lim |= static_cast<unsigned long long>(l) << (a * cb);
+      B.out_origin += (ax[a].r + ax[a].os * j0) * ostr;
+      ostr *= A.out_size[a];
+      if (a == R - 1) {
+        B.corg = horg;
+      } else {
+        B.in_base += horg * istr;
+        int lo_a = -horg, hi_a = A.in_size[a] - horg;
+        lo_a = lo_a < 0 ? 0 : (lo_a > A.hext[a] ? A.hext[a] : lo_a);
+        hi_a = hi_a < 0 ? 0 : (hi_a > A.hext[a] ? A.hext[a] : hi_a);
+        lo |= static_cast<unsigned long long>(lo_a) << (a * 8);
+        hi |= static_cast<unsigned long long>(hi_a) << (a * 8);
+      }
+      istr *= A.in_size[a];
+    } else if (a * cb < 64) {
+      // Axes past the rank: coordinate 0 always passes.
+      lim |= 1ull << (a * cb);
+    }
+    if (a >= R - 1) hi |= 1ull << (a * 8);
+  }
+  B.flags = (outside ? 1 : 0) | (interior ? 2 : 0);
+  B.lo = lo;
+  B.hi = hi;
+  B.lim = lim;
+  return B;
+}
+
+// Byte layout of the geometry tables (offsets into IgemmArgs::tables); returns the size.
+inline size_t igemm_table_layout(IgemmArgs& A) {
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = at;
+    at += (bytes + 255) & ~size_t{255};
+    return static_cast<int>(o);
+  };
+  A.tab_taps = take((size_t)A.nphase * 4 * A.tap_row * 4);
+  A.tab_tail = take((size_t)A.nphase * 4 * 4);
+  A.tab_pos = take((size_t)A.box_vol * 16);
+  A.tab_rows = take((size_t)A.rows * 16);
+  A.tab_box = take((size_t)A.nphase * A.boxes * sizeof(IgemmBox));
+  A.tab_pack = take((size_t)A.nphase * A.kc_max * 4 * 8);
+  A.tab_bytes = static_cast<int>(at);
+  return at;
+}
+
+// Fills the geometry tables (host memory of igemm_table_layout(A) bytes).
+inline void igemm_build_tables(const IgemmArgs& A, unsigned char* tab) {
+  const int R = A.rank;
+  const int cb = A.coord_bits;
+  for (int phase = 0; phase < A.nphase; ++phase) {
+    AxisTaps ax[kFastRank];
+    const int ntaps = phase_axes(A, phase, ax);
+    const int kf = ntaps * A.cc / 32, kcn = (ntaps * A.cc + 31) / 32;
+    for (int lg = 0; lg < 4; ++lg) {
+      int* row = reinterpret_cast<int*>(tab + A.tab_taps) + (phase * 4 + lg) * A.tap_row;
+      for (int k = 0; k < A.tap_row; ++k)
+        row[k] = kf > 0 ? igemm_tap_offset(A, ax, ntaps, k < kf ? k : kf - 1, lg) : 0;
+      reinterpret_cast<int*>(tab + A.tab_tail)[phase * 4 + lg] =
+          kcn > kf ? igemm_tap_offset(A, ax, ntaps, kf, lg) : -1;
+      for (int k = 0; k < A.kc_max; ++k) {
+        int* e = reinterpret_cast<int*>(tab + A.tab_pack) + ((phase * A.kc_max + k) * 4 + lg) * 2;
+        igemm_pack_entry(A, ax, ntaps, k, lg, &e[0], &e[1]);
+      }
+    }
+    for (int bx = 0; bx < A.boxes; ++bx)
+      reinterpret_cast<IgemmBox*>(tab + A.tab_box)[phase * A.boxes + bx] =
+          igemm_box_entry(A, phase, bx);
+  }
+  for (int q = 0; q < A.box_vol; ++q) {
+    int qq = q, halo = 0, orel = 0, ostr = 1;
+    unsigned long long c = 0;
+    for (int a = R - 1; a >= 0; --a) {
+      const int qa = qq & (A.box[a] - 1);
+      qq >>= A.box_shift[a];
+      halo += qa * (A.mode == 0 ? A.s[a] : 1) * A.hpitch[a];
+      orel += qa * (A.mode == 0 ? 1 : A.s[a]) * ostr;
+      ostr *= A.out_size[a];
+      c |= static_cast<unsigned long long>(qa) << (a * cb);
+    }
+    int* e = reinterpret_cast<int*>(tab + A.tab_pos) + q * 4;
+    e[0] = halo * 16;
+    e[1] = orel;
+    e[2] = static_cast<int>(c & 0xffffffffu);
+    e[3] = static_cast<int>(c >> 32);
+  }
+  for (int r = 0; r < A.rows; ++r) {
+    int rem = r, lpos = 0, irel = 0, istr = A.last_size;
+    unsigned long long h = 0;
+    for (int a = R - 2; a >= 0; --a) {
+      const int ha = rem % A.hext[a];
+      rem /= A.hext[a];
+      lpos += ha * A.hpitch[a];
+      irel += ha * istr;
+      istr *= A.in_size[a];
+      h |= static_cast<unsigned long long>(ha) << (a * 8);
+    }
+    int* e = reinterpret_cast<int*>(tab + A.tab_rows) + r * 4;
+    e[0] = lpos;
+    e[1] = irel;
+    e[2] = static_cast<int>(h & 0xffffffffu);
+    e[3] = static_cast<int>(h >> 32);
+  }
+}
+
+}  // namespace convnd

@@ -4,7 +4,8 @@
 //   * A workgroup owns a box of output positions (a power-of-two extent per axis) and a
 //     group of output channels. Its four waves are arranged WM along the channels and 4/WM
 //     along the positions; each wave accumulates MB x NB fragments of 16 x 16.
-//   * The input region the box reads through every tap (the halo) is staged once per
+//   * The GEMM input is staged per call into octet-major planes (8 channels = 16 bytes per
+//     position). The region the box reads through every tap (the halo) is copied once per
 //     channel chunk into LDS: one plane per octet of 8 channels, 16 bytes per position,
 //     zero outside the tensor, with host-chosen pitches that keep every 16-lane B-fragment
 //     read on distinct bank slots. Every tap then reuses the same LDS bytes.
@@ -21,8 +22,8 @@
 // Every phase is then a stride-1 convolution with per-tap offsets e(t), which the same
 // kernel runs (blockIdx.z covers batch x phase).
 
+#include "convnd_geometry.h"
 #include "convnd_internal.h"
-#include "convnd_stage.h"
 #include "convnd_types.h"
 
 namespace convnd {
@@ -90,7 +91,7 @@ void igemm_kernel(IgemmArgs A) {
   {
     const int4* rt = reinterpret_cast<const int4*>(tab + A.tab_rows);
     const unsigned long long lo = box.lo, hi = box.hi;
-    const int in_base = n * A.in_vol + box.in_base;
+    const int in_base = box.in_base;
     for (int r = tid; r < A.rows; r += kThreads) {
       const int4 e = rt[r];
       const unsigned long long h =
@@ -147,10 +148,12 @@ void igemm_kernel(IgemmArgs A) {
   // registers before the current chunk's MFMA loop and stored after it, so its latency
   // hides behind the MFMAs.
   constexpr int kStageBatch = 4;
-  const T* chunk_base = in + g * A.cin_g;
+  // Octet planes of this image and group: [cin_total/8][in_vol][8].
+  const T* chunk_base =
+      in + ((size_t)n * (A.cin_total >> 3) + (size_t)(g * (A.cin_g >> 3))) * A.in_vol * 8;
   u32x4 pre[kStageBatch];
   auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v) {
-    const T* base = chunk_base + ck * A.cc;
+    const T* base = chunk_base + (size_t)ck * A.noct * A.in_vol * 8;
 #pragma unroll
     for (int u = 0; u < kStageBatch; ++u) {
       const int it = it0 + u * kThreads;
@@ -160,7 +163,7 @@ void igemm_kernel(IgemmArgs A) {
       const int cl = corg + c;
       v[u] = u32x4{0u, 0u, 0u, 0u};
       if (ro >= 0 && cl >= 0 && cl < last_size)
-        v[u] = *reinterpret_cast<const u32x4*>(base + (size_t)(ro + cl) * A.cin_total + o * 8);
+        v[u] = *reinterpret_cast<const u32x4*>(base + ((size_t)o * A.in_vol + ro + cl) * 8);
       c += dc;
       rp += drp;
       if (c >= hlast) {

@@ -36,7 +36,7 @@ struct DirectGeom {
 // lanes of every B-fragment read fall on distinct 16-byte bank slots. The halo covers the
 // widest phase (hext is the maximum over the phases).
 struct IgemmArgs {
-  const void* in;    // channels-last staged operand [N][in_vol][cin_total]
+  const void* in;    // octet-major staged operand [N][cin_total/8][in_vol][8]
   const void* wpk;   // packed A fragments [phase][group][chunk][kc][mtile][64 lanes][8]
   const void* bias;  // [cout_total] or null (forward only)
   void* out;         // [N][cout_total][out_vol], channels-first
@@ -62,19 +62,21 @@ struct IgemmArgs {
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int k_vol;
   int split_c;     // split-precision fp32: real channels per group in the GEMM-input role
-  // Geometry tables in device memory, written by the prologue launch (igemm_tables) and
-  // read by the GEMM kernel, which then needs no per-axis code:
+  // Geometry tables in device memory, built once per plan by the host (convnd_geometry.h)
+  // and read by the packing pass and the GEMM kernel, which then needs no per-axis code:
   //   taps  int  [nphase][4 lane groups][tap_row]: LDS byte offset of the k-group (tap,
   //              octet) of K32 step k; entries from the phase's last whole step on repeat
   //              that step (prefetches past the end stay inside the halo);
   //   tail  int  [nphase][4]: the same for the partial last step, -1 past the last tap;
   //   pos   int4 [box_vol]: {halo byte offset, output offset, box coordinates (2 x 32 bit)};
   //   rows  int4 [rows]: {halo position offset, input position offset, halo coordinates};
-  //   boxes IgemmBox [nphase][boxes].
+  //   boxes IgemmBox [nphase][boxes];
+  //   pack  int2 [nphase][kc_max][4 lane groups]: weight tap index (-1 past the last tap)
+  //              and channel within the chunk of each k-group.
   // Coordinates are packed one field per axis (axis a in field a) so that one subtraction
   // compares every axis against packed bounds (see swar_all_less / swar_all_ge).
-  void* tables;
-  int tab_taps, tab_tail, tab_pos, tab_rows, tab_box;  // byte offsets in `tables`
+  const void* tables;
+  int tab_taps, tab_tail, tab_pos, tab_rows, tab_box, tab_pack;  // byte offsets in `tables`
   int tab_bytes;
   int tap_row;       // entries per (phase, lane group): kc_max + kTapPad, rounded to 4
   int last_size;     // input extent of the last axis
@@ -148,35 +150,46 @@ struct WgradArgs {
 };
 
 // ---- kernel launchers (defined in the .hip files) -------------------------------------
-// [N][C][V] -> [N][V][C] for 16-bit types (C % 8 == 0). With chan_sums non-null it also
-// writes fp32 partial sums per channel and 64-position tile:
-// chan_sums[c * channel_last_sum_blocks(N, V) + block].
-hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void* dst,
-                                   int64_t batch, int64_t channels, int64_t volume,
-                                   float* chan_sums, hipStream_t stream);
-int64_t channel_last_sum_blocks(int64_t batch, int64_t volume);
+
+// Octet-major copy of a channels-first tensor, optionally zero-padded:
+// dst[n][c/8][u_0]..[u_{R-1}][c%8] = src[n][c'][u - pad] (zero when u - pad lies outside the
+// input), u_a < pe[a], where destination channel c is channel cc = c % dst_cg of group
+// gi = c / dst_cg: source channel gi*src_cg + cc (zero past src_cg), or with split_c > 0 part
+// split_data_part(s) of source channel gi*split_c + c for cc = s*split_c + c (fp32 source,
+// split-precision GEMM input). With split_batch > 0 (fp32 source) destination image n holds
+// part split_data_part(n / split_batch) of source image n % split_batch.
+struct PadArgs {
+  int rank, channels;       // destination channels (groups x dst_cg)
+  int src_channels;         // source channels per image
+  int src_cg, dst_cg;       // channels per group: source, destination (multiple of 8, zero-filled)
+  int split_c;              // split-precision channel copies (fp32 source), else 0
+  int split_batch;  // fp32 source: images per split part (destination batch = 6x), else 0
+  int in[kFastRank], pe[kFastRank], pad[kFastRank];
+  int in_vol, pvol;
+};
+
+// Channel partial sums written by the GEMM-input copy: sums[c * octet_sum_blocks(N, V) +
+// block], one per channel and run of positions.
+int64_t octet_sum_blocks(int64_t batch, int64_t volume);
 
 // One launch for the staging passes that precede the MFMA kernels; each part is optional
 // (null pointers skip it) and runs on its own range of workgroups:
-//   GEMM input: channels-last copy (16-bit, with optional channel sums) or split-precision
-//               channels-last copy (split == true, fp32 source);
-//   weights:    packing for the implicit GEMM (ig), and its geometry tables when
-//               ig->tables is set;
+//   weights:    packing for the implicit GEMM (reads ig->tables);
+//   GEMM input: octet-major copy of src with geometry and channel map sa (no padding),
+//               with optional channel sums (16-bit source);
 //   octets:     zero-padded octet-major input for the weight gradient (pad);
 //   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg).
 struct IgemmArgs;
 struct WgradArgs;
-struct PadArgs;
 struct PrologueParts {
-  const void* src = nullptr;
-  void* staged = nullptr;
-  float* sums = nullptr;
-  int64_t batch = 0, channels = 0, volume = 0;
-  bool split = false;
-  int groups = 1, cin_g = 0, cg_split = 0;
   const IgemmArgs* ig = nullptr;
   const void* w = nullptr;
   void* wpk = nullptr;
+  const PadArgs* sa = nullptr;
+  const void* src = nullptr;
+  void* staged = nullptr;
+  float* sums = nullptr;
+  int64_t batch = 0;
   const PadArgs* pad = nullptr;
   const void* x = nullptr;
   void* x_oct = nullptr;
@@ -188,25 +201,6 @@ struct PrologueParts {
 };
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream);
 
-// Zero-padded octet-major copy: dst[n][c/8][u_0]..[u_{R-1}][c%8] = src[n][c'][u - pad] (zero
-// when u - pad lies outside the input), u_a < pe[a], where destination channel c is channel
-// c % dst_cg of group c / dst_cg (zero past the group's src_cg source channels).
-struct PadArgs {
-  int rank, channels;       // destination channels (groups x dst_cg)
-  int src_channels;         // source channels (groups x src_cg)
-  int src_cg, dst_cg;       // channels per group: source, destination (multiple of 8, zero-filled)
-  int split_batch;  // fp32 source: images per split part (destination batch = 6x), else 0
-  int in[kFastRank], pe[kFastRank], pad[kFastRank];
-  int in_vol, pvol;
-};
-// fp32 [N][G*cin_g][V] -> bf16 channels-last [N][V][G*cg_split] with six split parts per
-// channel (split-precision GEMM input); cin_g <= 64, cg_split % 8 == 0.
-hipError_t launch_split_channels_last(const float* src, void* dst, int64_t batch, int groups,
-                                      int cin_g, int cg_split, int64_t volume,
-                                      hipStream_t stream);
-hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void* dst,
-                                          int64_t batch, const PadArgs& args,
-                                          hipStream_t stream);
 // db[c] = sum of the nsum partial sums of channel c (fixed order).
 hipError_t launch_grad_bias_from_sums(convnd_hip_dtype dtype, const float* sums, int64_t nsum,
                                       int64_t channels, void* db, hipStream_t stream);

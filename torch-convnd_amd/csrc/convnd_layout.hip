@@ -1,15 +1,12 @@
 // Layout transforms and deterministic reductions around the MFMA kernels (gfx950).
 //
-//   * to_channels_last16: [N][C][V] -> [N][V][C] for 16-bit element types, 16-byte global
-//     loads and stores through a 64 x 64 LDS tile. Optionally the same pass writes fp32
-//     partial sums of every channel over its 64-position tile, which the bias gradient
-//     (the reference's flat_grad.sum({0, 3}), src/torch_convnd/csrc/convnd.cpp:388-390)
-//     then reduces without reading grad_output again.
-//   * to_octets_padded16: [N][C][in...] -> [N][C/8][pe...][8], octet-major (8 channels = 16
-//     bytes per position, one contiguous plane per octet), where padded coordinate u holds
-//     input coordinate u - pad (zero outside the input): every halo a convolution box reads
-//     is then in bounds and each octet's rows are contiguous, so the consumer stages it with
-//     coalesced loads and no validity tests.
+//   * The fused prologue: one launch for the staging passes that precede the MFMA kernels
+//     (weight packing of the implicit GEMM, octet-major copies of its
+//     input and of the weight gradient's padded input, grad_output padded to whole boxes).
+//     The octet-major copy (stage::octets16_block) optionally writes fp32 partial sums of
+//     every channel over its position run, which the bias gradient (the reference's
+//     flat_grad.sum({0, 3}), src/torch_convnd/csrc/convnd.cpp:388-390) then reduces without
+//     reading grad_output again.
 //   * channel_sums: the same partial sums straight from [N][C][V] (bias gradient when no
 //     transposed copy of grad_output is made).
 //   * reduce_channel_sums: db[c] = sum over the partials of channel c in a fixed order.
@@ -26,62 +23,30 @@
 namespace convnd {
 namespace {
 
-using stage::kTileC;
-using stage::kTileStride;
-using stage::kTileV;
-
-__global__ __launch_bounds__(kThreads) void to_channels_last16_kernel(
-    const unsigned short* src, unsigned short* dst, int channels, int volume, float* sums,
-    int sum_stride, bool is_bf16) {
-  __shared__ __align__(16) unsigned short tile[kTileC * kTileStride];
-  __shared__ float csum[kTileC];
-  stage::channels_last16_block(src, dst, channels, volume, sums, sum_stride, is_bf16,
-                               blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, tile, csum);
-}
-
-template <typename Src>
-__global__ __launch_bounds__(kThreads) void to_octets_padded16_kernel(const Src* src,
-                                                                     unsigned short* dst,
-                                                                     PadArgs P) {
-  __shared__ __align__(16) unsigned short tile[kTileC * kTileStride];
-  __shared__ int srcoff[kTileV];
-  stage::octets_padded16_block<Src>(src, dst, P, blockIdx.x, blockIdx.y, blockIdx.z, tile,
-                                    srcoff);
-}
-
-__global__ __launch_bounds__(kThreads) void split_channels_last_kernel(const float* src,
-                                                                      unsigned short* dst,
-                                                                      int cin_g, int cg_split,
-                                                                      int volume) {
-  __shared__ float tile[kTileC * (kTileV + 1)];
-  stage::split_channels_last_block(src, dst, cin_g, cg_split, volume, gridDim.y, blockIdx.x,
-                                   blockIdx.y, blockIdx.z, tile);
-}
-
 // ---- fused prologue ----------------------------------------------------------------------
 
 struct DevPrologue {
-  // GEMM input staging: grid (gx, gy, batch) flattened; channels-last or split.
-  const void* src;
-  void* staged;
-  float* sums;
-  int channels, volume, sum_stride, cin_g, cg_split, groups;
-  int gx, gy, a_blocks;
-  bool is_bf16;
-  // weight packing
+  // Weight packing of the implicit GEMM (reads the plan's geometry tables): first in block
+  // order (the longest-running blocks), so they overlap the copies.
   IgemmArgs ig;
   const void* w;
   void* wpk;
   int64_t units;
   int b_blocks;
-  // implicit-GEMM geometry tables (of ig)
-  int t_blocks;
-  // octet-major padded input
+  // Octet-major copy of the GEMM input (sa), with optional channel sums.
+  PadArgs sa;
+  const void* src;
+  void* staged;
+  float* sums;
+  int a_nbx, a_octs, a_blocks;
+  bool a_vec, c_vec;  // 16-byte load path of the octet copies
+  bool is_bf16;
+  // Octet-major zero-padded copy of the input for the weight gradient.
   PadArgs pad;
   const void* x;
   void* x_oct;
-  int cgx, cgy, c_blocks;
-  // padded grad_output
+  int c_nbx, c_octs, c_blocks;
+  // grad_output padded to whole boxes.
   WgradArgs wg;
   const void* dy;
   void* dy_pad;
@@ -90,47 +55,32 @@ struct DevPrologue {
   int d_blocks;
 };
 
-// SPLIT: fp32 sources (split-precision staging, packing and weight-gradient copies).
+// SPLIT: fp32 sources (split-precision copies and packing).
 template <typename T, bool SPLIT>
-__global__ __launch_bounds__(kThreads) void prologue_kernel(DevPrologue P) {
-  __shared__ __align__(16) unsigned char smem[stage::kSmemBytes];
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void prologue_kernel(DevPrologue P) {
+  __shared__ stage::OctetSmem smem;
   using S = typename std::conditional<SPLIT, float, unsigned short>::type;
   using W = typename std::conditional<SPLIT, float, T>::type;
   int b = blockIdx.x;
-  if (b < P.a_blocks) {
-    const int bx = b % P.gx, r = b / P.gx, by = r % P.gy, bz = r / P.gy;
-    if constexpr (SPLIT) {
-      stage::split_channels_last_block(static_cast<const float*>(P.src),
-                                       static_cast<unsigned short*>(P.staged), P.cin_g,
-                                       P.cg_split, P.volume, P.groups, bx, by, bz,
-                                       reinterpret_cast<float*>(smem));
-    } else {
-      stage::channels_last16_block(
-          static_cast<const unsigned short*>(P.src), static_cast<unsigned short*>(P.staged),
-          P.channels, P.volume, P.sums, P.sum_stride, P.is_bf16, bx, by, bz, P.gx,
-          reinterpret_cast<unsigned short*>(smem),
-          reinterpret_cast<float*>(smem + kTileC * kTileStride * 2));
-    }
-    return;
-  }
-  b -= P.a_blocks;
   if (b < P.b_blocks) {
     stage::igemm_pack_blocks<T, W>(P.ig, static_cast<const W*>(P.w), static_cast<T*>(P.wpk),
                                    P.units, b, P.b_blocks);
     return;
   }
   b -= P.b_blocks;
-  if (b < P.t_blocks) {
-    stage::igemm_table_blocks(P.ig, b, P.t_blocks);
+  if (b < P.a_blocks) {
+    const int bx = b % P.a_nbx, r = b / P.a_nbx, o = r % P.a_octs, n = r / P.a_octs;
+    stage::octets16_block<S>(static_cast<const S*>(P.src), static_cast<unsigned short*>(P.staged),
+                             P.sa, P.a_vec, bx, o, n, P.a_nbx, P.sums,
+                             P.a_nbx * (P.a_blocks / (P.a_nbx * P.a_octs)), P.is_bf16, &smem);
     return;
   }
-  b -= P.t_blocks;
+  b -= P.a_blocks;
   if (b < P.c_blocks) {
-    const int bx = b % P.cgx, r = b / P.cgx, by = r % P.cgy, bz = r / P.cgy;
-    stage::octets_padded16_block<S>(static_cast<const S*>(P.x),
-                                    static_cast<unsigned short*>(P.x_oct), P.pad, bx, by, bz,
-                                    reinterpret_cast<unsigned short*>(smem),
-                                    reinterpret_cast<int*>(smem + kTileC * kTileStride * 2));
+    const int bx = b % P.c_nbx, r = b / P.c_nbx, o = r % P.c_octs, n = r / P.c_octs;
+    stage::octets16_block<S>(static_cast<const S*>(P.x), static_cast<unsigned short*>(P.x_oct),
+                             P.pad, P.c_vec, bx, o, n, P.c_nbx, nullptr, 0, P.is_bf16, &smem);
     return;
   }
   b -= P.c_blocks;
@@ -235,95 +185,36 @@ __global__ __launch_bounds__(kThreads) void reduce_partials4_kernel(const float*
 
 }  // namespace
 
-hipError_t launch_to_channels_last(convnd_hip_dtype dtype, const void* src, void* dst,
-                                   int64_t batch, int64_t channels, int64_t volume,
-                                   float* chan_sums, hipStream_t stream) {
-  if (batch == 0 || channels == 0 || volume == 0) return hipSuccess;
-  if (dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16) return hipErrorInvalidValue;
-  if (channels % 8 != 0 || channels > 65535 * kTileC || volume > 0x7fffffff ||
-      batch > 65535)
-    return hipErrorInvalidValue;
-  const dim3 grid((volume + kTileV - 1) / kTileV, (channels + kTileC - 1) / kTileC, batch);
-  hipLaunchKernelGGL(to_channels_last16_kernel, grid, dim3(kThreads), 0, stream,
-                     static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst),
-                     static_cast<int>(channels), static_cast<int>(volume), chan_sums,
-                     static_cast<int>(grid.x * batch), dtype == CONVND_HIP_BFLOAT16);
-  return hipGetLastError();
-}
-
-hipError_t launch_to_octets_padded(convnd_hip_dtype dtype, const void* src, void* dst,
-                                          int64_t batch, const PadArgs& args,
-                                          hipStream_t stream) {
-  if (batch == 0 || args.channels == 0 || args.pvol == 0) return hipSuccess;
-  if (dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16 &&
-      !(dtype == CONVND_HIP_FLOAT32 && args.split_batch > 0 &&
-        batch == (int64_t)args.split_batch * kSplitProducts))
-    return hipErrorInvalidValue;
-  if (args.channels % 8 != 0 || args.rank < 1 || args.rank > kFastRank || batch > 65535)
-    return hipErrorInvalidValue;
-  const int64_t blocks = ((int64_t)args.pvol + kTileV - 1) / kTileV;
-  const int64_t ctiles = (args.channels + kTileC - 1) / kTileC;
-  if (blocks > 0x7fffffff || ctiles > 65535) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ctiles),
-                  static_cast<unsigned>(batch));
-  if (dtype == CONVND_HIP_FLOAT32) {
-    hipLaunchKernelGGL(to_octets_padded16_kernel<float>, grid, dim3(kThreads), 0, stream,
-                       static_cast<const float*>(src), static_cast<unsigned short*>(dst), args);
-  } else {
-    hipLaunchKernelGGL(to_octets_padded16_kernel<unsigned short>, grid, dim3(kThreads), 0,
-                       stream, static_cast<const unsigned short*>(src),
-                       static_cast<unsigned short*>(dst), args);
-  }
-  return hipGetLastError();
-}
-
-hipError_t launch_split_channels_last(const float* src, void* dst, int64_t batch, int groups,
-                                      int cin_g, int cg_split, int64_t volume,
-                                      hipStream_t stream) {
-  if (batch == 0 || volume == 0) return hipSuccess;
-  if (cin_g > kTileC || cg_split % 8 != 0 || cg_split < kSplitProducts * cin_g ||
-      groups > 65535 || batch > 65535 || volume > 0x7fffffff)
-    return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>((volume + kTileV - 1) / kTileV),
-                  static_cast<unsigned>(groups), static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(split_channels_last_kernel, grid, dim3(kThreads), 0, stream, src,
-                     static_cast<unsigned short*>(dst), cin_g, cg_split,
-                     static_cast<int>(volume));
-  return hipGetLastError();
-}
-
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream) {
   DevPrologue P;
   std::memset(&P, 0, sizeof(P));
   const bool split = dtype == CONVND_HIP_FLOAT32;
   if (!split && dtype != CONVND_HIP_BFLOAT16 && dtype != CONVND_HIP_FLOAT16)
     return hipErrorInvalidValue;
+  P.is_bf16 = dtype == CONVND_HIP_BFLOAT16;
   int64_t total = 0;
-  if (p.staged != nullptr && p.batch > 0 && p.volume > 0) {
-    if (p.split != split || p.batch > 65535 || p.volume > 0x7fffffff) return hipErrorInvalidValue;
-    P.src = p.src;
-    P.staged = p.staged;
-    P.volume = static_cast<int>(p.volume);
-    P.gx = static_cast<int>((p.volume + kTileV - 1) / kTileV);
-    if (split) {
-      if (p.cin_g > kTileC || p.cg_split % 8 != 0 || p.cg_split < kSplitProducts * p.cin_g)
-        return hipErrorInvalidValue;
-      P.cin_g = p.cin_g;
-      P.cg_split = p.cg_split;
-      P.groups = p.groups;
-      P.gy = p.groups;
-    } else {
-      if (p.channels % 8 != 0) return hipErrorInvalidValue;
-      P.channels = static_cast<int>(p.channels);
-      P.gy = static_cast<int>((p.channels + kTileC - 1) / kTileC);
-      P.sums = p.sums;
-      P.sum_stride = static_cast<int>(P.gx * p.batch);
-      P.is_bf16 = dtype == CONVND_HIP_BFLOAT16;
-    }
-    total = (int64_t)P.gx * P.gy * p.batch;
-    P.a_blocks = static_cast<int>(total);
-  }
-  if (p.wpk != nullptr && p.ig != nullptr) {
+  auto octet_grid = [](const PadArgs& a, int64_t batch, int* nbx, int* octs) {
+    *nbx = static_cast<int>(((int64_t)a.pvol + stage::kOctRun - 1) / stage::kOctRun);
+    *octs = a.channels >> 3;
+    return (int64_t)*nbx * *octs * batch;
+  };
+  // The 16-byte path: 16-bit source without padding, whole runs of 8 positions, aligned.
+  auto octet_vec = [&](const PadArgs& a, const void* src) {
+    if (split || a.split_c > 0 || a.split_batch > 0 || a.pvol != a.in_vol || a.in_vol % 8 != 0)
+      return false;
+    for (int i = 0; i < a.rank; ++i)
+      if (a.pad[i] != 0 || a.pe[i] != a.in[i]) return false;
+    return reinterpret_cast<uintptr_t>(src) % 16 == 0;
+  };
+  auto octet_ok = [&](const PadArgs& a, int64_t batch) {
+    if (a.channels % 8 != 0 || a.rank < 1 || a.rank > kFastRank || a.dst_cg <= 0) return false;
+    // fp32 sources only as split-precision copies; 16-bit sources never split.
+    const bool fp32_src = a.split_c > 0 || a.split_batch > 0;
+    if (fp32_src != split) return false;
+    if (a.split_batch > 0 && batch != (int64_t)a.split_batch * kSplitProducts) return false;
+    return true;
+  };
+  if (p.ig != nullptr && p.wpk != nullptr) {
     const IgemmArgs& a = *p.ig;
     P.ig = a;
     P.w = p.w;
@@ -332,20 +223,25 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     const int64_t blocks = (P.units + kThreads - 1) / kThreads;
     P.b_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
     total += P.b_blocks;
-    if (a.tables != nullptr) {
-      const int64_t tunits = stage::igemm_table_units(a);
-      const int64_t tb = (tunits + kThreads - 1) / kThreads;
-      P.t_blocks = static_cast<int>(tb < 1024 ? tb : 1024);
-      total += P.t_blocks;
-    }
   }
-  if (p.x_oct != nullptr && p.pad != nullptr && p.oct_batch > 0) {
+  if (p.staged != nullptr && p.sa != nullptr && p.batch > 0 && p.sa->pvol > 0) {
+    if (!octet_ok(*p.sa, p.batch)) return hipErrorInvalidValue;
+    if (p.sums != nullptr && (split || p.sa->pvol != p.sa->in_vol)) return hipErrorInvalidValue;
+    P.sa = *p.sa;
+    P.src = p.src;
+    P.staged = p.staged;
+    P.sums = p.sums;
+    P.a_vec = octet_vec(P.sa, p.src);
+    P.a_blocks = static_cast<int>(octet_grid(P.sa, p.batch, &P.a_nbx, &P.a_octs));
+    total += P.a_blocks;
+  }
+  if (p.x_oct != nullptr && p.pad != nullptr && p.oct_batch > 0 && p.pad->pvol > 0) {
+    if (!octet_ok(*p.pad, p.oct_batch)) return hipErrorInvalidValue;
     P.pad = *p.pad;
     P.x = p.x;
     P.x_oct = p.x_oct;
-    P.cgx = static_cast<int>(((int64_t)P.pad.pvol + kTileV - 1) / kTileV);
-    P.cgy = (P.pad.channels + kTileC - 1) / kTileC;
-    P.c_blocks = static_cast<int>((int64_t)P.cgx * P.cgy * p.oct_batch);
+    P.c_vec = octet_vec(P.pad, p.x);
+    P.c_blocks = static_cast<int>(octet_grid(P.pad, p.oct_batch, &P.c_nbx, &P.c_octs));
     total += P.c_blocks;
   }
   if (p.dy_pad != nullptr && p.wg != nullptr) {
@@ -375,8 +271,8 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
   return hipGetLastError();
 }
 
-int64_t channel_last_sum_blocks(int64_t batch, int64_t volume) {
-  return batch * ((volume + kTileV - 1) / kTileV);
+int64_t octet_sum_blocks(int64_t batch, int64_t volume) {
+  return batch * ((volume + stage::kOctRun - 1) / stage::kOctRun);
 }
 
 hipError_t launch_grad_bias_from_sums(convnd_hip_dtype dtype, const float* sums, int64_t nsum,

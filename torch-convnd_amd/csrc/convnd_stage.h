@@ -3,102 +3,12 @@
 // launch (each pass on its own range of workgroups).
 #pragma once
 
+#include "convnd_geometry.h"
 #include "convnd_internal.h"
 #include "convnd_types.h"
 
 namespace convnd {
 namespace stage {
-
-constexpr int kTileV = 64;   // positions per transpose tile
-constexpr int kTileC = 64;   // channels per transpose tile
-constexpr int kTileStride = kTileV + 8;  // u16 per LDS tile row (16-byte skew)
-// Shared memory of the largest pass (the split-precision tile of 64 x 65 floats).
-constexpr int kSmemBytes = kTileC * (kTileV + 1) * 4 + 256;
-
-// ---- implicit-GEMM tap geometry (also used by the GEMM kernel) -------------------------
-
-struct AxisTaps {
-  int ntap, first, step;  // taps t = first + i*step for i < ntap
-  int emin, emax;         // range of the input shift e(t)
-  int sigma, cshift;      // input coordinate = j*sigma + cshift + e(t)
-  int J, r, os;           // j extent; output coordinate = r + os*j
-};
-
-__device__ __forceinline__ int gcd_i(int a, int b) {
-  while (b != 0) {
-    const int t = a % b;
-    a = b;
-    b = t;
-  }
-  return a;
-}
-
-__device__ __forceinline__ int mod_pos(int a, int b) {
-  const int m = a % b;
-  return m < 0 ? m + b : m;
-}
-
-__device__ __forceinline__ AxisTaps axis_taps(const IgemmArgs& A, int a, int r) {
-  AxisTaps t;
-  if (A.mode == 0) {
-    t.ntap = A.k[a];
-    t.first = 0;
-    t.step = 1;
-    t.emin = 0;
-    t.emax = (A.k[a] - 1) * A.d[a];
-    t.sigma = A.s[a];
-    t.cshift = -A.p[a];
-    t.J = A.out_size[a];
-    t.r = 0;
-    t.os = 1;
-    return t;
-  }
-  const int s = A.s[a], d = A.d[a], k = A.k[a];
-  const int st = s / gcd_i(s, d);
-  int first = -1;
-  for (int c = 0; c < k && c < st; ++c) {
-    if (mod_pos(r + A.p[a] - c * d, s) == 0) {
-      first = c;
-      break;
-    }
-  }
-  t.first = first < 0 ? 0 : first;
-  t.step = st;
-  t.ntap = first < 0 ? 0 : (k - 1 - first) / st + 1;
-  if (t.ntap > 0) {
-    t.emax = (r + A.p[a] - t.first * d) / s;
-    t.emin = (r + A.p[a] - (t.first + (t.ntap - 1) * st) * d) / s;
-  } else {
-    t.emax = 0;
-    t.emin = 0;
-  }
-  t.sigma = 1;
-  t.cshift = 0;
-  t.J = (A.out_size[a] - r + s - 1) / s;
-  t.r = r;
-  t.os = s;
-  return t;
-}
-
-__device__ __forceinline__ int axis_e(const IgemmArgs& A, int a, const AxisTaps& t, int i) {
-  const int tap = t.first + i * t.step;
-  return A.mode == 0 ? tap * A.d[a] : (t.r + A.p[a] - tap * A.d[a]) / A.s[a];
-}
-
-// Axis information of every axis for one phase; returns the phase's tap count.
-__device__ __forceinline__ int phase_axes(const IgemmArgs& A, int phase, AxisTaps* ax) {
-  int rr = phase, ntaps = 1;
-#pragma unroll
-  for (int a = kFastRank - 1; a >= 0; --a) {
-    if (a < A.rank) {
-      const int radix = A.mode ? A.s[a] : 1;
-      ax[a] = axis_taps(A, a, rr % radix);
-      rr /= radix;
-      ntaps *= ax[a].ntap;
-    }
-  }
-  return ntaps;
-}
 
 
 // ---- weight packing --------------------------------------------------------------------
@@ -111,413 +21,274 @@ __device__ __forceinline__ int phase_axes(const IgemmArgs& A, int phase, AxisTap
 template <typename T, typename S>
 __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w, T* wpk,
                                                   int64_t units, int block, int nblocks) {
-  const int R = A.rank;
-  {
-    for (int64_t u = block * (int64_t)kThreads + threadIdx.x; u < units;
-         u += (int64_t)nblocks * kThreads) {
-      int64_t r = u;
-      const int lane = r & 63;
-      r >>= 6;
-      const int mt = r % A.mtiles_padded;
-      r /= A.mtiles_padded;
-      const int kc = r % A.kc_max;
-      r /= A.kc_max;
-      const int ck = r % A.nchunk;
-      r /= A.nchunk;
-      const int g = r % A.groups;
-      const int phase = (int)(r / A.groups);
-      AxisTaps ax[kFastRank];
-      const int ntaps = phase_axes(A, phase, ax);
-      const int m = mt * 16 + (lane & 15);
-      const int kk = kc * 32 + (lane >> 4) * 8;
-      const int tau = kk / A.cc;
-      const int ci0 = ck * A.cc + (kk - tau * A.cc);
-      T vals[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vals[i] = static_cast<T>(0.f);
-      if (m < A.cout_g && tau < ntaps) {
-        int rem = tau, tflat = 0, kstr = 1;
-#pragma unroll
-        for (int a = kFastRank - 1; a >= 0; --a) {
-          if (a < R) {
-            const int idx = rem % ax[a].ntap;
-            rem /= ax[a].ntap;
-            tflat += (ax[a].first + idx * ax[a].step) * kstr;
-            kstr *= A.k[a];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          int ci = ci0 + i, part = 0;
-          if constexpr (sizeof(S) == 4) {
-            const int sp = ci / A.split_c;
-            if (sp >= kSplitProducts) continue;
-            ci -= sp * A.split_c;
-            part = split_other_part(sp);
-          }
-          const int64_t widx =
-              A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
-                          : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
-          if constexpr (sizeof(S) == 4) {
-            vals[i] = __builtin_bit_cast(T, bf16_part_bits(w[widx], part));
-          } else {
-            vals[i] = w[widx];
-          }
-        }
-      }
-      T* dst = wpk + u * 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dst[i] = vals[i];
-    }
-  }
-}
-
-// ---- implicit-GEMM geometry tables ------------------------------------------------------
-
-// Entries of the geometry tables (IgemmArgs::tables): taps, tail, positions, rows, boxes.
-__host__ __device__ inline int64_t igemm_table_units(const IgemmArgs& A) {
-  return (int64_t)A.nphase * 4 * A.tap_row + (int64_t)A.nphase * 4 + A.box_vol + A.rows +
-         (int64_t)A.nphase * A.boxes;
-}
-
-// LDS byte offset of k-group (K32 step `step`, lane group lg) of a phase: tap part plus
-// octet plane, or -1 past the phase's last tap.
-__device__ __forceinline__ int igemm_tap_offset(const IgemmArgs& A, const AxisTaps* ax,
-                                                int ntaps, int step, int lg) {
-  const int kk = (step * 4 + lg) * 8;
-  const int tau = kk / A.cc;
-  const int ci = kk - tau * A.cc;
-  if (tau >= ntaps) return -1;
-  int rem = tau, t = 0;
-#pragma unroll
-  for (int a = kFastRank - 1; a >= 0; --a) {
-    if (a < A.rank) {
-      const int i = rem % ax[a].ntap;
-      rem /= ax[a].ntap;
-      t += (axis_e(A, a, ax[a], i) - ax[a].emin) * A.hpitch[a];
-    }
-  }
-  return t * 16 + (ci >> 3) * A.plane_bytes;
-}
-
-// Writes the geometry tables that the GEMM kernel reads (one entry per thread).
-__device__ __forceinline__ void igemm_table_blocks(const IgemmArgs& A, int block, int nblocks) {
-  const int R = A.rank;
-  char* tab = static_cast<char*>(A.tables);
-  const int64_t n_taps = (int64_t)A.nphase * 4 * A.tap_row;
-  const int64_t n_tail = (int64_t)A.nphase * 4;
-  const int64_t units = igemm_table_units(A);
-  const int cb = A.coord_bits;
+  const int* pmap = reinterpret_cast<const int*>(static_cast<const char*>(A.tables) + A.tab_pack);
   for (int64_t u = block * (int64_t)kThreads + threadIdx.x; u < units;
        u += (int64_t)nblocks * kThreads) {
-    int64_t e = u;
-    if (e < n_taps + n_tail) {
-      const bool tail = e >= n_taps;
-      if (tail) e -= n_taps;
-      const int k = tail ? 0 : static_cast<int>(e % A.tap_row);
-      const int pl = static_cast<int>(tail ? e : e / A.tap_row);
-      const int phase = pl >> 2, lg = pl & 3;
-      AxisTaps ax[kFastRank];
-      const int ntaps = phase_axes(A, phase, ax);
-      const int kf = ntaps * A.cc / 32, kcn = (ntaps * A.cc + 31) / 32;
-      int v;
-      if (tail) {
-        v = kcn > kf ? igemm_tap_offset(A, ax, ntaps, kf, lg) : -1;
-        reinterpret_cast<int*>(tab + A.tab_tail)[e] = v;
-      } else {
-        v = kf > 0 ? igemm_tap_offset(A, ax, ntaps, k < kf ? k : kf - 1, lg) : 0;
-        reinterpret_cast<int*>(tab + A.tab_taps)[e] = v;
-      }
-      continue;
-    }
-    e -= n_taps + n_tail;
-    if (e < A.box_vol) {
-      int qq = static_cast<int>(e), halo = 0, orel = 0, ostr = 1;
-      unsigned long long c = 0;
+    int64_t r = u;
+    const int lane = r & 63;
+    r >>= 6;
+    const int mt = r % A.mtiles_padded;
+    r /= A.mtiles_padded;
+    const int kc = r % A.kc_max;
+    r /= A.kc_max;
+    const int ck = r % A.nchunk;
+    r /= A.nchunk;
+    const int g = r % A.groups;
+    const int phase = (int)(r / A.groups);
+    const int m = mt * 16 + (lane & 15);
+    const int* pe = pmap + ((phase * A.kc_max + kc) * 4 + (lane >> 4)) * 2;
+    const int tflat = pe[0];
+    const int ci0 = ck * A.cc + pe[1];
+    T vals[8];
 #pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int qa = qq & (A.box[a] - 1);
-          qq >>= A.box_shift[a];
-          halo += qa * (A.mode == 0 ? A.s[a] : 1) * A.hpitch[a];
-          orel += qa * (A.mode == 0 ? 1 : A.s[a]) * ostr;
-          ostr *= A.out_size[a];
-          c |= static_cast<unsigned long long>(qa) << (a * cb);
+    for (int i = 0; i < 8; ++i) vals[i] = static_cast<T>(0.f);
+    if (m < A.cout_g && tflat >= 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int ci = ci0 + i, part = 0;
+        if constexpr (sizeof(S) == 4) {
+          const int sp = ci / A.split_c;
+          if (sp >= kSplitProducts) continue;
+          ci -= sp * A.split_c;
+          part = split_other_part(sp);
         }
-      }
-      reinterpret_cast<int4*>(tab + A.tab_pos)[e] =
-          int4{halo * 16, orel, static_cast<int>(c & 0xffffffffu), static_cast<int>(c >> 32)};
-      continue;
-    }
-    e -= A.box_vol;
-    if (e < A.rows) {
-      int rem = static_cast<int>(e), lpos = 0, irel = 0, istr = A.last_size;
-      unsigned long long h = 0;
-#pragma unroll
-      for (int a = kFastRank - 2; a >= 0; --a) {
-        if (a < R - 1) {
-          const int ha = rem % A.hext[a];
-          rem /= A.hext[a];
-          lpos += ha * A.hpitch[a];
-          irel += ha * istr;
-          istr *= A.in_size[a];
-          h |= static_cast<unsigned long long>(ha) << (a * 8);
-        }
-      }
-      reinterpret_cast<int4*>(tab + A.tab_rows)[e] =
-          int4{lpos, irel, static_cast<int>(h & 0xffffffffu), static_cast<int>(h >> 32)};
-      continue;
-    }
-    e -= A.rows;
-    {
-      const int phase = static_cast<int>(e / A.boxes);
-      int bb = static_cast<int>(e - (int64_t)phase * A.boxes);
-      AxisTaps ax[kFastRank];
-      const int ntaps = phase_axes(A, phase, ax);
-      IgemmBox B;
-      B.in_base = 0;
-      B.corg = 0;
-      B.out_origin = 0;
-      B.kc = (ntaps * A.cc + 31) / 32;
-      B.kf = ntaps * A.cc / 32;
-      B.unused0 = B.unused1 = 0;
-      B.unused2 = 0;
-      bool outside = false, interior = true;
-      unsigned long long lo = 0, hi = 0, lim = 0;
-      int istr = 1, ostr = 1;
-#pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
-          const int j0 = (bb % A.nbox[a]) * A.box[a];
-          bb /= A.nbox[a];
-          outside = outside || j0 >= ax[a].J;
-          const int horg = j0 * ax[a].sigma + ax[a].cshift + ax[a].emin;
-          int l = ax[a].J - j0;
-          interior = interior && l >= A.box[a];
-          l = l < 0 ? 0 : (l > A.box[a] ? A.box[a] : l);
-          lim |= static_cast<unsigned long long>(l) << (a * cb);
-          B.out_origin += (ax[a].r + ax[a].os * j0) * ostr;
-          ostr *= A.out_size[a];
-          if (a == R - 1) {
-            B.corg = horg;
-          } else {
-            B.in_base += horg * istr;
-            int lo_a = -horg, hi_a = A.in_size[a] - horg;
-            lo_a = lo_a < 0 ? 0 : (lo_a > A.hext[a] ? A.hext[a] : lo_a);
-            hi_a = hi_a < 0 ? 0 : (hi_a > A.hext[a] ? A.hext[a] : hi_a);
-            lo |= static_cast<unsigned long long>(lo_a) << (a * 8);
-            hi |= static_cast<unsigned long long>(hi_a) << (a * 8);
-          }
-          istr *= A.in_size[a];
+        const int64_t widx =
+            A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
+                        : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
+        if constexpr (sizeof(S) == 4) {
+          vals[i] = __builtin_bit_cast(T, bf16_part_bits(w[widx], part));
         } else {
-          // Axes past the rank: coordinate 0 always passes.
-          if (a * cb < 64) lim |= 1ull << (a * cb);
+          vals[i] = w[widx];
         }
-        if (a >= R - 1) hi |= 1ull << (a * 8);
       }
-      B.flags = (outside ? 1 : 0) | (interior ? 2 : 0);
-      B.lo = lo;
-      B.hi = hi;
-      B.lim = lim;
-      reinterpret_cast<IgemmBox*>(tab + A.tab_box)[e] = B;
     }
+    T* dst = wpk + u * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = vals[i];
   }
 }
-
 
 // ---- layout passes ----------------------------------------------------------------------
 
-// Block (vt, ct, n): positions [vt*64, +64), channels [ct*64, +64) of image n.
-__device__ __forceinline__ void channels_last16_block(
-    const unsigned short* src, unsigned short* dst, int channels, int volume, float* sums,
-    int sum_stride, bool is_bf16, int bx, int by, int bz, int gx, unsigned short* tile,
-    float* csum) {
-  const int tid = threadIdx.x;
-  const int v0 = bx * kTileV;
-  const int c0 = by * kTileC;
-  const int n = bz;
-  const int ct = channels - c0 < kTileC ? channels - c0 : kTileC;
-  const int vt = volume - v0 < kTileV ? volume - v0 : kTileV;
-  const bool full_v = vt == kTileV && (volume & 7) == 0;
-  const unsigned short* s = src + ((size_t)n * channels + c0) * volume + v0;
-  if (tid < kTileC) csum[tid] = 0.f;
-  // Load: item i -> channel i/8, positions 8*(i%8) .. +8.
-  for (int i = tid; i < ct * 8; i += kThreads) {
-    const int c = i >> 3;
-    const int p = (i & 7) * 8;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (full_v) {
-      v = *reinterpret_cast<const u32x4*>(s + (size_t)c * volume + p);
-    } else {
-      unsigned short e[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) e[k] = p + k < vt ? s[(size_t)c * volume + p + k] : 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) v[k] = e[2 * k] | ((unsigned)e[2 * k + 1] << 16);
-    }
-    *reinterpret_cast<u32x4*>(tile + c * kTileStride + p) = v;
-    if (sums != nullptr) {
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const unsigned lo = v[k] & 0xffffu, hi = v[k] >> 16;
-        if (is_bf16) {
-          acc += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
-        } else {
-          acc += static_cast<float>(__builtin_bit_cast(_Float16, (unsigned short)lo)) +
-                 static_cast<float>(__builtin_bit_cast(_Float16, (unsigned short)hi));
-        }
-      }
-      // The eight items of a channel are consecutive lanes: fixed-order butterfly.
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      acc += __shfl_xor(acc, 4);
-      if ((i & 7) == 0) csum[c] = acc;
-    }
-  }
-  __syncthreads();
-  if (sums != nullptr && tid < ct) {
-    const int blk = n * gx + bx;
-    sums[(size_t)(c0 + tid) * sum_stride + blk] = csum[tid];
-  }
-  // Store: item i -> position i/8, channels 8*(i%8) .. +8.
-  const int cgroups = ct >> 3;
-  unsigned short* d = dst + ((size_t)n * volume + v0) * channels + c0;
-  for (int i = tid; i < vt * cgroups; i += kThreads) {
-    const int p = i / cgroups;
-    const int cg = (i - p * cgroups) * 8;
-    u32x4 v;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      v[k] = tile[(cg + 2 * k) * kTileStride + p] |
-             ((unsigned)tile[(cg + 2 * k + 1) * kTileStride + p] << 16);
-    *reinterpret_cast<u32x4*>(d + (size_t)p * channels + cg) = v;
-  }
-}
+constexpr int kOctRun = 2048;  // destination positions per octet-copy block
+constexpr int kOctSub = 512;   // positions per pass of the element-wise path
 
-// Block (position tile, channel tile, n): 64 consecutive padded positions (flattened,
-// crossing rows) times 64 channels, through an LDS tile. Each position's source offset is
-// decoded once into LDS; loads are 2-byte with lanes along positions (coalesced within a
-// row, any alignment); stores are 16 bytes (one octet) with lanes along positions, so every
-// octet plane of the destination is written contiguously.
-// Src = float: the fp32 input split into bf16 parts; destination image n (of split_batch
-// x kSplitProducts) holds part split_data_part(n / split_batch) of source image
-// n % split_batch.
+// Shared memory of one octet-copy block: padded-row source offsets and the channel-sum
+// reduction.
+struct OctetSmem {
+  int rowoff[kOctRun + 2];
+  float red[4][8];
+};
+
+// Octet-major 16-bit copy of a channels-first tensor [N][C][in...], optionally zero-padded:
+// dst[n][o][p][k] (16 bytes per position and octet, one contiguous plane per octet) holds
+// destination channel c = 8*o + k at position p of the geometry P.pe, where padded
+// coordinate u is input coordinate u - P.pad (zero outside the input). Channels, per group
+// of P.dst_cg destination channels:
+//   split_c == 0: channel cc < P.src_cg is source channel g*P.src_cg + cc, zero past it;
+//   split_c > 0 (fp32 source): cc = s*split_c + c holds part split_data_part(s) of source
+//                 channel g*split_c + c (zero past kSplitProducts copies);
+//   split_batch > 0 (fp32 source): destination image n holds part
+//                 split_data_part(n / split_batch) of source image n % split_batch.
+// Block (position run bx of kOctRun, octet o, image n). Two paths:
+//   vec (16-bit source, no padding, volume a multiple of 8, 16-byte aligned source): each
+//       thread loads 8 consecutive positions of each of the 8 channels (16-byte loads),
+//       transposes the 8 x 8 block in registers (v_perm) and stores 8 whole positions
+//       (128 contiguous bytes);
+//   element-wise: every thread builds 16-byte units from eight 2-byte (4-byte for fp32)
+//       loads whose lanes run along the positions (coalesced within a row).
+// Loads go through a buffer resource over the source image: an offset past its end reads
+// zero, so padding and missing channels need no branch between the loads.
+// With sums non-null (16-bit source, no padding) the block also writes the fp32 sum of
+// each of its 8 channels over its positions: sums[c * sum_stride + n * nbx + bx], in a fixed
+// order (the bias gradient, the reference's flat_grad.sum({0, 3}),
+// src/torch_convnd/csrc/convnd.cpp:388-390, then reduces them).
 template <typename Src>
-__device__ __forceinline__ void octets_padded16_block(const Src* src, unsigned short* dst,
-                                                      const PadArgs& P, int bx, int by, int bz,
-                                                      unsigned short* tile, int* srcoff) {
+__device__ __forceinline__ void octets16_block(const Src* src, unsigned short* dst,
+                                               const PadArgs& P, bool vec, int bx, int o, int n,
+                                               int nbx, float* sums, int sum_stride,
+                                               bool is_bf16, OctetSmem* sm) {
   const int tid = threadIdx.x;
   const int R = P.rank;
-  const int p0 = bx * kTileV;
-  const int c0 = by * kTileC;
-  const int n = bz;
-  const int ct = P.channels - c0 < kTileC ? P.channels - c0 : kTileC;
-  const int vt = P.pvol - p0 < kTileV ? P.pvol - p0 : kTileV;
-  if (tid < kTileV) {
-    int off = -1;
-    if (tid < vt) {
-      int rem = p0 + tid, istr = 1;
-      off = 0;
+  const int p0 = bx * kOctRun;
+  const int pend = P.pvol - p0 < kOctRun ? P.pvol : p0 + kOctRun;
+  // Channel sources of this block's octet (uniform over the block).
+  int nsrc = n, ipart = -1;
+  if constexpr (sizeof(Src) == 4) {
+    if (P.split_batch > 0) {
+      nsrc = n % P.split_batch;
+      ipart = split_data_part(n / P.split_batch);
+    }
+  }
+  const Src* simg = src + (size_t)nsrc * P.src_channels * P.in_vol;
+  const uint64_t img_bytes = (uint64_t)P.src_channels * P.in_vol * sizeof(Src);
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<Src*>(simg), 0,
+      static_cast<int>(img_bytes < 0xfffffff0ull ? img_bytes : 0xfffffff0ull), 0x00020000);
+  constexpr unsigned kPast = 0xfffffff0u;
+  int choff[8], cpart[8];
 #pragma unroll
-      for (int a = kFastRank - 1; a >= 0; --a) {
-        if (a < R) {
+  for (int k = 0; k < 8; ++k) {
+    const int c = o * 8 + k;
+    const int gi = c / P.dst_cg;
+    const int cc = c - gi * P.dst_cg;
+    int sc = -1, part = ipart < 0 ? 0 : ipart;
+    if (P.split_c > 0) {
+      const int sp = cc / P.split_c;
+      if (sp < kSplitProducts) {
+        sc = gi * P.split_c + (cc - sp * P.split_c);
+        part = split_data_part(sp);
+      }
+    } else if (cc < P.src_cg) {
+      sc = gi * P.src_cg + cc;
+    }
+    choff[k] = sc < 0 ? -1 : sc * P.in_vol;
+    cpart[k] = part;
+  }
+  float csum[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) csum[k] = 0.f;
+  unsigned short* dimg = dst + ((size_t)n * (P.channels >> 3) + o) * P.pvol * 8;
+  auto add_sum = [&](int k, unsigned pair) {
+    csum[k] += is_bf16 ? __uint_as_float(pair << 16) + __uint_as_float(pair & 0xffff0000u)
+                       : static_cast<float>(__builtin_bit_cast(_Float16, (unsigned short)(pair & 0xffffu))) +
+                             static_cast<float>(__builtin_bit_cast(_Float16, (unsigned short)(pair >> 16)));
+  };
+  if constexpr (sizeof(Src) == 2) {
+    if (vec) {
+      const int pb = p0 + tid * 8;
+      if (pb < pend) {
+        u32x4 r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const unsigned off =
+              choff[k] >= 0 ? static_cast<unsigned>(choff[k] + pb) * 2u : kPast;
+          r[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+        }
+        if (sums != nullptr) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) add_sum(k, r[k][i]);
+        }
+        // Position 2i + h of the run: channel pairs (2j, 2j+1) from half h of word i.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              w[j] = __builtin_amdgcn_perm(r[2 * j + 1][i], r[2 * j][i],
+                                           h ? 0x07060302u : 0x05040100u);
+            *reinterpret_cast<u32x4*>(dimg + (size_t)(pb + 2 * i + h) * 8) = w;
+          }
+        }
+      }
+    }
+  }
+  if (!vec) {
+    int pe_last = 1, pad_last = 0, in_last = 1;
+#pragma unroll
+    for (int a = 0; a < kFastRank; ++a) {
+      if (a == R - 1) {
+        pe_last = P.pe[a];
+        pad_last = P.pad[a];
+        in_last = P.in[a];
+      }
+    }
+    const int r0 = p0 / pe_last;
+    const int nrows = (pend - 1) / pe_last - r0 + 1;
+    // Source position offset of every padded row the block touches (-1: padding row).
+    for (int i = tid; i < nrows; i += kThreads) {
+      int rem = r0 + i, off = 0, istr = in_last;
+      bool ok = true;
+#pragma unroll
+      for (int a = kFastRank - 2; a >= 0; --a) {
+        if (a < R - 1) {
           const int u = rem % P.pe[a];
           rem /= P.pe[a];
-          const int i = u - P.pad[a];
-          if (off >= 0 && i >= 0 && i < P.in[a]) {
-            off += i * istr;
-          } else {
-            off = -1;
-          }
+          const int ia = u - P.pad[a];
+          ok = ok && ia >= 0 && ia < P.in[a];
+          off += ia * istr;
           istr *= P.in[a];
         }
       }
+      sm->rowoff[i] = ok ? off : -1;
     }
-    srcoff[tid] = off;
-  }
-  __syncthreads();
-  int nsrc = n, part = 0;
-  if constexpr (sizeof(Src) == 4) {
-    nsrc = n % P.split_batch;
-    part = split_data_part(n / P.split_batch);
-  }
-  // Destination channel c0 + c is channel cc of group gi (dst_cg per group, the source's
-  // src_cg channels first, zero after).
-  const Src* s = src + (size_t)nsrc * P.src_channels * P.in_vol;
-  unsigned short e[16];
+    __syncthreads();
+    // Passes of kOctSub positions; all loads of a pass are issued before the first use.
+    constexpr int kPer = kOctSub / kThreads;
+    for (int q0 = p0; q0 < pend; q0 += kOctSub) {
+      unsigned short e[kPer][8];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int i = tid + j * kThreads;
-    const int c = i >> 6, v = i & 63;
-    const int so = srcoff[v];
-    const int gi = (c0 + c) / P.dst_cg;
-    const int cc = c0 + c - gi * P.dst_cg;
-    const bool ok = c < ct && so >= 0 && cc < P.src_cg;
-    const size_t sidx = ((size_t)gi * P.src_cg + cc) * P.in_vol + so;
-    if constexpr (sizeof(Src) == 4) {
-      e[j] = ok ? bf16_part_bits(s[sidx], part) : 0;
-    } else {
-      e[j] = ok ? s[sidx] : 0;
+      for (int j = 0; j < kPer; ++j) {
+        const int p = q0 + tid + j * kThreads;
+        int soff = -1;
+        if (p < pend) {
+          const int row = p / pe_last;
+          const int col = p - row * pe_last - pad_last;
+          const int ro = sm->rowoff[row - r0];
+          soff = (ro >= 0 && col >= 0 && col < in_last) ? ro + col : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const unsigned off = (soff >= 0 && choff[k] >= 0)
+                                   ? static_cast<unsigned>(choff[k] + soff) * (unsigned)sizeof(Src)
+                                   : kPast;
+          if constexpr (sizeof(Src) == 4) {
+            const float v =
+                __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+            e[j][k] = bf16_part_bits(v, cpart[k]);
+          } else {
+            e[j][k] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int p = q0 + tid + j * kThreads;
+        if (p >= pend) break;
+        u32x4 w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = e[j][2 * k] | ((unsigned)e[j][2 * k + 1] << 16);
+        if (sums != nullptr) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            add_sum(2 * k, e[j][2 * k]);
+            add_sum(2 * k + 1, e[j][2 * k + 1]);
+          }
+        }
+        *reinterpret_cast<u32x4*>(dimg + (size_t)p * 8) = w;
+      }
     }
   }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int i = tid + j * kThreads;
-    tile[(i >> 6) * kTileStride + (i & 63)] = e[j];
-  }
-  __syncthreads();
-  const int octs = P.channels >> 3;
-  const int cgroups = ct >> 3;
-  for (int i = tid; i < cgroups * kTileV; i += kThreads) {
-    const int cg = i >> 6, v = i & 63;
-    if (v >= vt) continue;
-    u32x4 w;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      w[k] = tile[(cg * 8 + 2 * k) * kTileStride + v] |
-             ((unsigned)tile[(cg * 8 + 2 * k + 1) * kTileStride + v] << 16);
-    const size_t plane = (size_t)n * octs + (c0 >> 3) + cg;
-    *reinterpret_cast<u32x4*>(dst + (plane * P.pvol + p0 + v) * 8) = w;
-  }
-}
-
-// fp32 [N][G*cin_g][V] -> bf16 [N][V][G*cg_split] for the split-precision GEMM: destination
-// channel s*cin_g + c of group g (s < kSplitProducts) holds part split_data_part(s) of
-// source channel g*cin_g + c; channels past kSplitProducts*cin_g are zero. Block (position
-// tile, group, n): the group's channels (at most 64) x 64 positions through LDS, then
-// 16-byte stores of 8 destination channels, consecutive lanes along the channels.
-__device__ __forceinline__ void split_channels_last_block(const float* src, unsigned short* dst,
-                                                          int cin_g, int cg_split, int volume,
-                                                          int groups, int bx, int g, int n,
-                                                          float* tile) {
-  const int tid = threadIdx.x;
-  const int v0 = bx * kTileV;
-  const int vt = volume - v0 < kTileV ? volume - v0 : kTileV;
-  const float* s = src + ((size_t)n * groups * cin_g + (size_t)g * cin_g) * volume + v0;
-  for (int i = tid; i < cin_g * kTileV; i += kThreads) {
-    const int c = i >> 6, v = i & 63;
-    tile[c * (kTileV + 1) + v] = v < vt ? s[(size_t)c * volume + v] : 0.f;
-  }
-  __syncthreads();
-  const int chunks = cg_split >> 3;
-  const size_t row = (size_t)groups * cg_split;
-  unsigned short* d = dst + ((size_t)n * volume + v0) * row + (size_t)g * cg_split;
-  for (int i = tid; i < vt * chunks; i += kThreads) {
-    const int v = i / chunks;
-    const int q = i - v * chunks;
-    unsigned h[8];
+  if (sums != nullptr) {
+    // Fixed-order butterfly within each wave, then the four waves in order.
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int c6 = q * 8 + k;
-      const int sp = c6 / cin_g;
-      const int c = c6 - sp * cin_g;
-      h[k] = sp < kSplitProducts
-                 ? bf16_part_bits(tile[c * (kTileV + 1) + v], split_data_part(sp))
-                 : 0u;
+      float v = csum[k];
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      csum[k] = v;
     }
-    *reinterpret_cast<u32x4*>(d + (size_t)v * row + q * 8) =
-        u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    const int lane = tid & 63, wave = tid >> 6;
+    if (lane < 8) {
+      float v = csum[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k)
+        if (lane == k) v = csum[k];
+      sm->red[wave][lane] = v;
+    }
+    __syncthreads();
+    if (tid < 8) {
+      const float v = ((sm->red[0][tid] + sm->red[1][tid]) + sm->red[2][tid]) + sm->red[3][tid];
+      sums[(size_t)(o * 8 + tid) * sum_stride + (size_t)n * nbx + bx] = v;
+    }
   }
 }
 
