@@ -745,8 +745,7 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       const int dyrow = box_vol * 2 + 32;
       const int64_t lds_dy = max_oct * plane_bytes;
       const int64_t lds_pos = lds_dy + align_up((int64_t)mb * 16 * dyrow);
-      const int64_t lds_rel = lds_pos + align_up((int64_t)box_vol * 4);
-      const int64_t lds_items = lds_rel + align_up(plane_pos * 4);
+      const int64_t lds_items = lds_pos + align_up((int64_t)box_vol * 4);
       if (lds_items > kLdsBudget) return;
       // grad_output is read in runs of 8 positions along the box's last axis; when the boxes
       // do not tile the output exactly it is read from a copy padded to whole boxes.
@@ -755,9 +754,11 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       if (dvol * batch * g.out_channels > kI32Safe / 2) return;
       // Staging slots per thread (16-byte registers), the next item's held across the MFMAs;
       // an item needing more than the register budget stages the rest in batches of 8.
-      const int64_t entries = max_oct * plane_pos + (int64_t)mb * 16 * (box_vol / 8);
+      const int64_t halo_slots = (max_oct * plane_pos + kThreads - 1) / kThreads;
+      const int64_t dy_slots = ((int64_t)mb * 16 * (box_vol / 8) + kThreads - 1) / kThreads;
+      const int64_t entries = (halo_slots + dy_slots) * kThreads;
       const int stg_max = 24;
-      int stg = static_cast<int>((entries + kThreads - 1) / kThreads);
+      int stg = static_cast<int>(halo_slots + dy_slots);
       stg = (stg + 7) / 8 * 8;
       const bool multi = stg > stg_max;
       if (multi) stg = 8;
@@ -862,12 +863,15 @@ WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
       A.items_per_pc = static_cast<int>(ipc);
       A.lds_dy = static_cast<int>(lds_dy);
       A.lds_pos = static_cast<int>(lds_pos);
-      A.lds_rel = static_cast<int>(lds_rel);
       A.lds_items = static_cast<int>(lds_items);
       plan.lds = static_cast<size_t>(lds);
     });
   }
   if (plan.ok) {
+    if (wgrad_table_layout(plan.args, plan.mb) > (size_t)kI32Safe) {
+      plan.ok = false;
+      return plan;
+    }
     plan.staged_elems = (size_t)batch * plan.args.pvol * g.groups * cin_gp;
     plan.dy_pad_elems = (size_t)batch * plan.args.dvol * g.out_channels;
     plan.partial_elems =
@@ -993,7 +997,8 @@ BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool g
 // never written again, so concurrent calls on any stream may read them). The copy is
 // synchronous, so the first call of a geometry must not be under stream capture. The
 // memory lives as long as the process.
-const void* igemm_device_tables(const std::string& key, const IgemmArgs& A) {
+template <typename Build>
+const void* device_tables(const std::string& key, size_t bytes, Build&& build) {
   static std::mutex lock;
   static std::unordered_map<std::string, const void*> map;
   int dev = 0;
@@ -1002,8 +1007,8 @@ const void* igemm_device_tables(const std::string& key, const IgemmArgs& A) {
   std::lock_guard<std::mutex> guard(lock);
   auto it = map.find(k);
   if (it != map.end()) return it->second;
-  std::vector<unsigned char> host(static_cast<size_t>(A.tab_bytes), 0);
-  igemm_build_tables(A, host.data());
+  std::vector<unsigned char> host(bytes, 0);
+  build(host.data());
   void* d = nullptr;
   if (hipMalloc(&d, host.size()) != hipSuccess) return nullptr;
   if (hipMemcpy(d, host.data(), host.size(), hipMemcpyHostToDevice) != hipSuccess) {
@@ -1012,6 +1017,16 @@ const void* igemm_device_tables(const std::string& key, const IgemmArgs& A) {
   }
   map.emplace(k, d);
   return d;
+}
+
+const void* igemm_device_tables(const std::string& key, const IgemmArgs& A) {
+  return device_tables(key, static_cast<size_t>(A.tab_bytes),
+                       [&](unsigned char* h) { igemm_build_tables(A, h); });
+}
+
+const void* wgrad_device_tables(const std::string& key, const WgradArgs& A) {
+  return device_tables(key, static_cast<size_t>(A.tab_bytes),
+                       [&](unsigned char* h) { wgrad_build_tables(A, h); });
 }
 
 // Diagnostic kernel timing (convnd_hip_timing_enable/read): event pairs recorded around
@@ -1238,6 +1253,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   }
   if (mfma_dw) {
     WA = b.wg.args;
+    WA.tables = wgrad_device_tables(plan_key(g, dtype, 65), WA);
+    if (WA.tables == nullptr)
+      return fail(CONVND_HIP_LAUNCH_FAILED,
+                  "weight-gradient geometry tables: device allocation failed");
     WA.x = ws + b.off_x_stage;
     WA.dy = grad_output;
     WA.partial = reinterpret_cast<float*>(ws + b.off_partial);

@@ -263,3 +263,178 @@ inline void igemm_build_tables(const IgemmArgs& A, unsigned char* tab) {
 }
 
 }  // namespace convnd
+
+namespace convnd {
+
+// ---- weight-gradient geometry ------------------------------------------------------------
+
+// Tap offset (positions in the halo) of flat tap index tap (row-major over the kernel).
+inline int wgrad_tap_offset(const WgradArgs& A, int tap) {
+  int rem = tap, off = 0;
+  for (int a = A.rank - 1; a >= 0; --a) {
+    const int ta = rem % A.k[a];
+    rem /= A.k[a];
+    off += ta * A.d[a] * A.hpitch[a];
+  }
+  return off;
+}
+
+// Byte layout of the weight-gradient tables for `mb` output-channel tiles; returns the size.
+inline size_t wgrad_table_layout(WgradArgs& A, int mb) {
+  int shift_last = A.box_shift[A.rank - 1], rows_shift = 0;
+  for (int a = 0; a < A.rank - 1; ++a) rows_shift += A.box_shift[a];
+  const int per_ch_shift = rows_shift + shift_last - 3;
+  const int64_t dy_items = (int64_t)(mb * 16) << per_ch_shift;
+  A.nh = static_cast<int>(((int64_t)A.max_oct * A.plane_pos + 255) / 256);
+  // Rounded up to whole batches of 8 slots (the kernel loads records in batches).
+  A.nslot_rows = (A.nh + static_cast<int>((dy_items + 255) / 256) + 7) / 8 * 8;
+  A.slot_mb = mb;
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = at;
+    at += (bytes + 255) & ~size_t{255};
+    return static_cast<int>(o);
+  };
+  A.tab_pairs = take((size_t)A.ncq * 64 * 4);
+  A.tab_col = take((size_t)A.ncq * 64 * 4);
+  A.tab_pos = take((size_t)A.box_vol * 4);
+  A.tab_item = take((size_t)A.items * 8);
+  A.tab_slot = take((size_t)A.nslot_rows * 256 * 8);
+  A.tab_bytes = static_cast<int>(at);
+  return at;
+}
+
+inline void wgrad_build_tables(const WgradArgs& A, unsigned char* tab) {
+  const int R = A.rank;
+  int* pairs = reinterpret_cast<int*>(tab + A.tab_pairs);
+  int* cols = reinterpret_cast<int*>(tab + A.tab_col);
+  // Pair chunks: an LDS read of 16 bytes per lane is served eight lanes at a time, and the
+  // eight lanes (a half of a lane group: lane % 16 in 0-7 or 8-15) conflict when two of them
+  // fall on the same 16-byte slot of a 256-byte bank row. The lanes of a lane group read
+  // their pairs' columns at one common position offset, so the chunk's pairs are placed in
+  // eight groups of eight (wave, half) with distinct column slots wherever the slot counts
+  // allow: most frequent slots first, each pair in the group with fewest of its slot (then
+  // most free lanes).
+  for (int cq = 0; cq < A.ncq; ++cq) {
+    const int p0 = cq * 64;
+    const int p1 = p0 + 64 < A.npairs ? p0 + 64 : A.npairs;
+    const int oct_lo = p0 / A.k_vol;
+    int freq[16] = {0};
+    struct P {
+      int pair, col, slot;
+    };
+    P list[64];
+    int np = 0;
+    for (int p = p0; p < p1; ++p) {
+      const int oct = p / A.k_vol, tap = p - oct * A.k_vol;
+      const int col = (oct - oct_lo) * A.plane_bytes + wgrad_tap_offset(A, tap) * 16;
+      list[np++] = {p, col, (col >> 4) & 15};
+      ++freq[(col >> 4) & 15];
+    }
+    // Stable order by decreasing slot frequency.
+    for (int i = 1; i < np; ++i) {
+      const P v = list[i];
+      int j = i - 1;
+      while (j >= 0 && freq[list[j].slot] < freq[v.slot]) {
+        list[j + 1] = list[j];
+        --j;
+      }
+      list[j + 1] = v;
+    }
+    int count[8][16] = {{0}}, fill[8] = {0};
+    for (int s = 0; s < 64; ++s) {
+      pairs[cq * 64 + s] = -1;
+      cols[cq * 64 + s] = 0;
+    }
+    for (int i = 0; i < np; ++i) {
+      const int sl = list[i].slot;
+      int best = -1;
+      for (int grp = 0; grp < 8; ++grp) {
+        if (fill[grp] >= 8) continue;
+        if (best < 0 || count[grp][sl] < count[best][sl] ||
+            (count[grp][sl] == count[best][sl] && fill[grp] < fill[best]))
+          best = grp;
+      }
+      // Group grp = wave * 2 + half: lanes wave*16 + half*8 .. +7.
+      const int s = (best >> 1) * 16 + (best & 1) * 8 + fill[best]++;
+      ++count[best][sl];
+      pairs[cq * 64 + s] = list[i].pair;
+      cols[cq * 64 + s] = list[i].col;
+    }
+  }
+  int* pos = reinterpret_cast<int*>(tab + A.tab_pos);
+  for (int q = 0; q < A.box_vol; ++q) {
+    int qq = q, off = 0;
+    for (int a = R - 1; a >= 0; --a) {
+      off += (qq & (A.box[a] - 1)) * A.s[a] * A.hpitch[a];
+      qq >>= A.box_shift[a];
+    }
+    pos[q] = off * 16;
+  }
+  int* item = reinterpret_cast<int*>(tab + A.tab_item);
+  const int64_t octs_total = (int64_t)A.groups * A.cin_gp / 8;
+  for (int it = 0; it < A.items; ++it) {
+    const int n = it / A.boxes;
+    int bb = it - n * A.boxes;
+    int64_t base = 0, obase = 0, ostr = 1;
+    for (int a = R - 1; a >= 0; --a) {
+      const int j0 = (bb % A.nbox[a]) * A.box[a];
+      bb /= A.nbox[a];
+      base += (int64_t)j0 * A.s[a] * A.pstride[a];
+      obase += (int64_t)j0 * ostr;
+      ostr *= A.dext[a];
+    }
+    item[2 * it] = static_cast<int>((n * octs_total * A.pvol + base) * 16);
+    item[2 * it + 1] = static_cast<int>(((int64_t)n * A.cout_total * A.dvol + obase) * 2);
+  }
+  // Staging slots: J < nh halo entry e = J*256 + t (plane wo, halo position pp); the rest
+  // grad_output runs of 8 positions d = (J - nh)*256 + t: (channel row, box row, run).
+  int shift_last = A.box_shift[R - 1], rows_shift = 0;
+  for (int a = 0; a < R - 1; ++a) rows_shift += A.box_shift[a];
+  const int runs_shift = shift_last - 3;
+  const int per_ch_shift = rows_shift + runs_shift;
+  const int64_t dy_items = (int64_t)(A.slot_mb * 16) << per_ch_shift;
+  const int blast = A.box[R - 1], dlast = A.dext[R - 1];
+  int* slot = reinterpret_cast<int*>(tab + A.tab_slot);
+  for (int J = 0; J < A.nslot_rows; ++J) {
+    for (int t = 0; t < 256; ++t) {
+      unsigned off = kWgradOob;
+      int dst = -1;
+      if (J < A.nh) {
+        const int e = J * 256 + t;
+        if (e < A.max_oct * A.plane_pos) {
+          const int wo = e / A.plane_pos, pp = e - wo * A.plane_pos;
+          int rem = pp, rel = 0;
+          for (int a = R - 1; a >= 0; --a) {
+            const int h = rem % A.hext[a];
+            rem /= A.hext[a];
+            rel += h * A.pstride[a];
+          }
+          off = static_cast<unsigned>(((int64_t)wo * A.pvol + rel) * 16);
+          dst = wo * A.plane_bytes + pp * 16;
+        }
+      } else {
+        const int d = (J - A.nh) * 256 + t;
+        if (d < dy_items) {
+          const int row = d >> per_ch_shift;
+          const int c = d & ((1 << per_ch_shift) - 1);
+          const int br = c >> runs_shift;
+          const int run = c & ((1 << runs_shift) - 1);
+          int64_t qoff = run * 8, ostr = dlast;
+          int rem = br;
+          for (int a = R - 2; a >= 0; --a) {
+            qoff += (rem & (A.box[a] - 1)) * ostr;
+            rem >>= A.box_shift[a];
+            ostr *= A.dext[a];
+          }
+          off = static_cast<unsigned>(((int64_t)row * A.dvol + qoff) * 2);
+          dst = A.lds_dy + row * A.dyrow + (br * blast + run * 8) * 2;
+        }
+      }
+      slot[(J * 256 + t) * 2] = static_cast<int>(off);
+      slot[(J * 256 + t) * 2 + 1] = dst;
+    }
+  }
+}
+
+}  // namespace convnd

@@ -146,8 +146,26 @@ struct WgradArgs {
   int mtiles, mgroups;
   int npairs, ncq;
   int npc, items, items_per_pc;
-  int lds_dy, lds_pos, lds_rel, lds_items;  // LDS byte offsets of the regions after the planes
+  int lds_dy, lds_pos, lds_items;  // LDS byte offsets of the regions after the planes
+  // Geometry tables in device memory, built once per plan by the host (convnd_geometry.h):
+  //   pairs int  [ncq][64]: pair held by lane slot wave*16 + lane%16 (-1: none); the pairs
+  //              of a chunk are spread over the waves so that the sixteen lanes of a wave
+  //              read distinct 16-byte LDS bank slots wherever the tap offsets allow;
+  //   col   int  [ncq][64]: that pair's LDS column offset (octet plane + tap, bytes);
+  //   pos   int  [box_vol]: LDS byte offset of each box position's halo base;
+  //   item  int2 [items]: byte bases of the item's halo (padded input) and grad_output
+  //              tile, without the workgroup's octet and channel offsets;
+  //   slot  int2 [nslot_rows][256]: staging slot J of thread t: {source byte offset from the
+  //              item's base (kWgradOob: none), LDS byte destination (-1: none)}.
+  const void* tables;
+  int tab_pairs, tab_col, tab_pos, tab_item, tab_slot, tab_bytes;
+  int nslot_rows;  // staging slots per thread: halo (max_oct planes) then grad_output rows
+  int nh;          // halo slots per thread
+  int slot_mb;     // output-channel tiles of the grad_output rows in the slot table
 };
+
+// Byte offset past every buffer the weight-gradient kernel reads: such a load returns zero.
+constexpr unsigned kWgradOob = 0x80000000u;
 
 // ---- kernel launchers (defined in the .hip files) -------------------------------------
 
@@ -224,10 +242,6 @@ bool igemm_tile_supported(int mb, int nb, int wm);
 // several batches of 8 slots (only the first is prefetched).
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
                              const WgradArgs& a, size_t lds_bytes, hipStream_t stream);
-// grad_output zero-padded to whole boxes (extents a.dext) for the weight gradient; with
-// split_batch > 0 the source is fp32 and a.batch = 6 x split_batch images of bf16 parts.
-hipError_t launch_pad_grad_output(const void* dy, void* dst, const WgradArgs& a,
-                                  int split_batch, hipStream_t stream);
 // Float slots (x4) of one position chunk's partial sums, and the pass that adds the npc
 // chunks in order and writes dW in the weight layout.
 int64_t wgrad_partial_slots(int mb, const WgradArgs& a);

@@ -35,8 +35,7 @@ namespace {
 
 // Buffer resource word 3 for raw (unstructured) loads: 32-bit data format, no swizzle.
 constexpr int kRsrcWord3 = 0x00020000;
-// Byte offset past every buffer this kernel reads: such a load returns zero.
-constexpr unsigned kOob = 0x80000000u;
+constexpr unsigned kOob = kWgradOob;
 
 // Low halves of a and b as one dword (a's in the low half): v_perm_b32 byte selection.
 __device__ __forceinline__ unsigned lo_pair(unsigned a, unsigned b) {
@@ -57,8 +56,8 @@ void wgrad_kernel(WgradArgs A) {
   extern __shared__ __align__(16) unsigned char lds[];
   const unsigned char* dyt = lds + A.lds_dy;
   int* posoff = reinterpret_cast<int*>(lds + A.lds_pos);
-  int* halo_rel = reinterpret_cast<int*>(lds + A.lds_rel);
   int* itab = reinterpret_cast<int*>(lds + A.lds_items);
+  const char* tab = static_cast<const char*>(A.tables);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -88,73 +87,26 @@ void wgrad_kernel(WgradArgs A) {
   const int p1 = p0 + 64 < A.npairs ? p0 + 64 : A.npairs;
   const int oct_lo = p0 / A.k_vol;
   const int noct = (p1 - 1) / A.k_vol - oct_lo + 1;
-  const int pair = p0 + wave * 16 + nl;
-  const bool pair_ok = pair < p1;
-  const int oct = pair_ok ? pair / A.k_vol : oct_lo;
-  const int tap = pair_ok ? pair - oct * A.k_vol : 0;
   const int co0 = mg * MB * 16;
   const int oct0 = (g * A.cin_gp >> 3) + oct_lo;  // first octet plane of this workgroup
   const int it0 = pc * A.items_per_pc;
   const int nitems = (it0 + A.items_per_pc < A.items ? it0 + A.items_per_pc : A.items) - it0;
 
-  // This lane's column offset in the halo: plane of its octet + its tap's position offset.
-  int coloff;
+  // This lane's column offset in the halo (plane of its pair's octet + its tap's position
+  // offset), from the plan's tables; the same for every item.
+  const int coloff = reinterpret_cast<const int*>(tab + A.tab_col)[cq * 64 + wave * 16 + nl];
+  // Box-relative LDS offsets of every box position's halo base, and the item table (the
+  // workgroup's byte bases of each item's halo and grad_output tile).
   {
-    int rem = tap, off = 0;
-#pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        const int ta = rem % A.k[a];
-        rem /= A.k[a];
-        off += ta * A.d[a] * A.hpitch[a];
-      }
+    const int* pt = reinterpret_cast<const int*>(tab + A.tab_pos);
+    for (int q = tid; q < A.box_vol; q += kThreads) posoff[q] = pt[q];
+    const int* gi = reinterpret_cast<const int*>(tab + A.tab_item);
+    const int hoff = oct0 * A.pvol * 16;
+    const int doff = (g * A.cout_g + co0) * A.dvol * 2;
+    for (int k = tid; k < nitems; k += kThreads) {
+      itab[2 * k] = gi[2 * (it0 + k)] + hoff;
+      itab[2 * k + 1] = gi[2 * (it0 + k) + 1] + doff;
     }
-    coloff = (oct - oct_lo) * A.plane_bytes + off * 16;
-  }
-  // Box-relative tables, the same for every box: LDS offset of each box position's halo
-  // base, and the padded-input offset (in positions) of each halo position.
-  for (int q = tid; q < A.box_vol; q += kThreads) {
-    int qq = q, off = 0;
-#pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        off += (qq & (A.box[a] - 1)) * A.s[a] * A.hpitch[a];
-        qq >>= A.box_shift[a];
-      }
-    }
-    posoff[q] = off * 16;
-  }
-  for (int pp = tid; pp < A.plane_pos; pp += kThreads) {
-    int rem = pp, rel = 0;
-#pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        const int h = rem % A.hext[a];
-        rem /= A.hext[a];
-        rel += h * A.pstride[a];
-      }
-    }
-    halo_rel[pp] = rel;
-  }
-  // Item table: byte bases of each item's halo (in the octet-major input) and grad_output
-  // tile (in the buffer read, extents dext).
-  for (int k = tid; k < nitems; k += kThreads) {
-    const int it = it0 + k;
-    const int n = it / A.boxes;
-    int bb = it - n * A.boxes;
-    int base = 0, obase = 0, ostr = 1;
-#pragma unroll
-    for (int a = kFastRank - 1; a >= 0; --a) {
-      if (a < R) {
-        const int j0 = (bb % A.nbox[a]) * A.box[a];
-        bb /= A.nbox[a];
-        base += j0 * A.s[a] * A.pstride[a];
-        obase += j0 * ostr;
-        ostr *= A.dext[a];
-      }
-    }
-    itab[2 * k] = ((n * (A.groups * A.cin_gp >> 3) + oct0) * A.pvol + base) * 16;
-    itab[2 * k + 1] = ((n * A.cout_total + g * A.cout_g + co0) * A.dvol + obase) * 2;
   }
   __syncthreads();
 
@@ -178,47 +130,26 @@ void wgrad_kernel(WgradArgs A) {
   for (int a = 0; a < kFastRank - 1; ++a)
     if (a < R - 1) rows_shift += A.box_shift[a];
   const int per_ch_shift = rows_shift + runs_shift;
-  const int dy_items = (MB * 16) << per_ch_shift;
   const int halo_items = noct * A.plane_pos;
-  const int nh = (A.max_oct * A.plane_pos + kThreads - 1) / kThreads;
-  const int nslots = nh + (dy_items + kThreads - 1) / kThreads;
+  const int nh = A.nh;
+  const int nslots = A.nslot_rows;  // multiple of 8
   const int co_valid = A.cout_g - co0;
+  const int2* slot_tab = reinterpret_cast<const int2*>(tab + A.tab_slot);
 
   // Staging slots J = 0, 1, ...: the first nh hold halo entries e = J*256 + tid, the rest
-  // grad_output copies d = (J - nh)*256 + tid. Offsets are relative to the item's bases.
+  // grad_output runs d = (J - nh)*256 + tid; offsets (relative to the item's bases) and LDS
+  // destinations come from the plan's slot table. Entries past this workgroup's octets or
+  // output channels read zero.
+  // The table has at least STG rows (the ones past nslots read nothing), so every record
+  // load is unconditional and the loads of a batch are all in flight together.
   auto slot_offsets = [&](int J, unsigned& off, int& dst) {
-    off = kOob;
-    dst = -1;
-    if (J < nh) {
-      const int e = J * kThreads + tid;
-      if (e < halo_items) {
-        int wo = static_cast<int>(static_cast<float>(e) * A.inv_plane_pos);
-        if (wo * A.plane_pos > e) --wo;
-        if ((wo + 1) * A.plane_pos <= e) ++wo;
-        const int pp = e - wo * A.plane_pos;
-        off = static_cast<unsigned>((wo * A.pvol + halo_rel[pp]) * 16);
-        dst = wo * A.plane_bytes + pp * 16;
-      }
-    } else if (J < nslots) {
-      const int d = (J - nh) * kThreads + tid;
-      if (d < dy_items) {
-        const int row = d >> per_ch_shift;
-        const int c = d & ((1 << per_ch_shift) - 1);
-        const int br = c >> runs_shift;
-        const int run = c & ((1 << runs_shift) - 1);
-        int qoff = run * 8, ostr = dlast, rem = br;
-#pragma unroll
-        for (int a = kFastRank - 2; a >= 0; --a) {
-          if (a < R - 1) {
-            qoff += (rem & (A.box[a] - 1)) * ostr;
-            rem >>= A.box_shift[a];
-            ostr *= A.dext[a];
-          }
-        }
-        if (row < co_valid) off = static_cast<unsigned>((row * A.dvol + qoff) * 2);
-        dst = A.lds_dy + row * A.dyrow + (br * blast + run * 8) * 2;
-      }
-    }
+    const int2 e = slot_tab[J * kThreads + tid];
+    const bool halo = J < nh;
+    const int hi = J * kThreads + tid;
+    const int di = (J - nh) * kThreads + tid;
+    const bool valid = halo ? hi < halo_items : (di >> per_ch_shift) < co_valid;
+    off = valid ? static_cast<unsigned>(e.x) : kOob;
+    dst = e.y;
   };
 
   const T* x = static_cast<const T*>(A.x);
@@ -260,32 +191,43 @@ void wgrad_kernel(WgradArgs A) {
   const int step = s_last * 16;
   // LDS fragments of K step kc: A from the grad_output tile, B raw (8 positions x 8
   // channels of this lane's pair) for the in-register transpose.
-  auto read_frags = [&](int kc, frag* a, u32x4* v) {
+  // LDS reads of K step kc: A fragments (grad_output rows) and the B data raw (8 positions x
+  // 8 channels of this lane's pair) for the in-register transpose. b0 is the lane's halo byte
+  // offset of the step's first position (posoff + coloff).
+  auto read_a = [&](int kc, frag* a) {
     const int q0 = kc * 32 + lg * 8;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
       a[mb] = *reinterpret_cast<const frag*>(dyt + (mb * 16 + nl) * A.dyrow + q0 * 2);
+  };
+  auto read_b = [&](int b0, u32x4* v) {
     // Positions q0 .. q0+7 lie on one row of the box's last axis (its extent is a multiple
     // of 8), so their halo offsets step by stride * 16 bytes.
-    const int b0 = posoff[q0] + coloff;
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4*>(lds + b0 + i * step);
   };
-  auto mfmas = [&](const frag* a, const u32x4* v) {
+  auto base_of = [&](int kc) {
+    return posoff[(kc < ksteps ? kc : ksteps - 1) * 32 + lg * 8] + coloff;
+  };
+  // Fragment u: channel u of the octet at the 8 positions (two per dword).
+  auto transpose = [&](const u32x4* v, frag* t) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      // Fragment u: channel u of the octet at the 8 positions (two per dword).
-      u32x4 t;
+      u32x4 w;
 #pragma unroll
       for (int w2 = 0; w2 < 4; ++w2) {
         const unsigned lo = v[2 * w2][u >> 1];
         const unsigned hi = v[2 * w2 + 1][u >> 1];
-        t[w2] = (u & 1) ? hi_pair(lo, hi) : lo_pair(lo, hi);
+        w[w2] = (u & 1) ? hi_pair(lo, hi) : lo_pair(lo, hi);
       }
-      const frag b = __builtin_bit_cast(frag, t);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb][u] = M::run(a[mb], b, acc[mb][u]);
+      t[u] = __builtin_bit_cast(frag, w);
     }
+  };
+  auto mfmas = [&](const frag* a, const frag* t) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb][u] = M::run(a[mb], t[u], acc[mb][u]);
   };
 
   // The first batch starts at slot 0, passed through an opaque register so the compiler
@@ -312,14 +254,30 @@ void wgrad_kernel(WgradArgs A) {
     }
     __syncthreads();
     if (k + 1 < nitems) load_slots(k + 1, opaque_zero(), soff);  // in flight during the MFMAs
-    frag a0[MB], a1[MB];
+    // Pipeline over K steps (two per iteration): the B data of a step is read two steps
+    // ahead and transposed one step ahead (its v_perm work overlaps the previous step's
+    // MFMAs), A fragments are read one step ahead; steps past the end repeat the last one.
+    frag a0[MB], a1[MB], t0[8], t1[8];
     u32x4 v0[8], v1[8];
-    read_frags(0, a0, v0);
+    read_a(0, a0);
+    read_b(base_of(0), v0);
+    read_a(1, a1);
+    read_b(base_of(1), v1);
+    // Halo bases of the steps read next (kc+2, kc+3), themselves read a full iteration
+    // ahead so that no LDS wait for them falls among the fragment reads.
+    int pb2 = base_of(2), pb3 = base_of(3);
+    transpose(v0, t0);
     for (int kc = 0; kc < ksteps; kc += 2) {
-      read_frags(kc + 1, a1, v1);
-      mfmas(a0, v0);
-      read_frags(kc + 2 < ksteps ? kc + 2 : kc + 1, a0, v0);
-      mfmas(a1, v1);
+      read_b(pb2, v0);  // step kc+2
+      pb2 = base_of(kc + 4);
+      transpose(v1, t1);
+      mfmas(a0, t0);
+      read_a(kc + 2 < ksteps ? kc + 2 : ksteps - 1, a0);
+      read_b(pb3, v1);  // step kc+3
+      pb3 = base_of(kc + 5);
+      transpose(v0, t0);
+      mfmas(a1, t1);
+      read_a(kc + 3 < ksteps ? kc + 3 : ksteps - 1, a1);
     }
   }
 
@@ -353,8 +311,9 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
   const int zq = tile / A.ncq;
   const int g = zq / A.mgroups;
   const int mg = zq % A.mgroups;
-  const int pair = cq * 64 + wave * 16 + (lane & 15);
-  if (pair >= A.npairs) return;
+  const int pair = reinterpret_cast<const int*>(
+      static_cast<const char*>(A.tables) + A.tab_pairs)[cq * 64 + wave * 16 + (lane & 15)];
+  if (pair < 0) return;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   int i = 0;
   for (; i + 8 <= A.npc; i += 8) {
@@ -376,13 +335,6 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
       dw[(((int64_t)g * A.cout_g + co) * A.cin_g + oct * 8 + u) * A.k_vol + tap] =
           static_cast<T>(acc[k]);
   }
-}
-
-template <typename Src>
-__global__ __launch_bounds__(kThreads) void pad_dy16_kernel(const Src* src, unsigned short* dst,
-                                                            WgradArgs A, int split_batch,
-                                                            int64_t total_runs) {
-  stage::pad_dy16_blocks<Src>(src, dst, A, split_batch, total_runs, blockIdx.x, gridDim.x);
 }
 
 template <typename T, int MB, int STG, bool MULTI>
@@ -426,27 +378,6 @@ hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi
   if (dtype == CONVND_HIP_FLOAT16)
     return wgrad_dispatch<_Float16>(mb, stg, multi, a, lds_bytes, stream);
   return hipErrorInvalidValue;
-}
-
-hipError_t launch_pad_grad_output(const void* dy, void* dst, const WgradArgs& a,
-                                  int split_batch, hipStream_t stream) {
-  int dlast = 8;
-  for (int i = 0; i < a.rank; ++i)
-    if (i == a.rank - 1) dlast = a.dext[i];
-  const int64_t total = (int64_t)a.batch * a.cout_total * (a.dvol / dlast) * (dlast / 8);
-  if (total == 0) return hipSuccess;
-  const int64_t blocks = std::min<int64_t>((total + kThreads - 1) / kThreads, 8192);
-  if (split_batch > 0) {
-    if (a.batch != split_batch * kSplitProducts) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pad_dy16_kernel<float>, dim3(static_cast<unsigned>(blocks)),
-                       dim3(kThreads), 0, stream, static_cast<const float*>(dy),
-                       static_cast<unsigned short*>(dst), a, split_batch, total);
-  } else {
-    hipLaunchKernelGGL(pad_dy16_kernel<unsigned short>, dim3(static_cast<unsigned>(blocks)),
-                       dim3(kThreads), 0, stream, static_cast<const unsigned short*>(dy),
-                       static_cast<unsigned short*>(dst), a, 0, total);
-  }
-  return hipGetLastError();
 }
 
 int64_t wgrad_partial_slots(int mb, const WgradArgs& a) {
