@@ -162,6 +162,40 @@ def _cpu_model():
     return "unknown CPU"
 
 
+def measure_peaks(torch, device):
+    """Achieved bf16 GEMM rate (torch.matmul, square n^3) and device copy bandwidth."""
+    res = {}
+    for n, it in ((8192, 20), (16384, 5)):
+        a = torch.randn(n, n, device=device, dtype=torch.bfloat16)
+        b = torch.randn(n, n, device=device, dtype=torch.bfloat16)
+        for _ in range(3):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(it):
+            torch.matmul(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / it
+        res[f"bf16_matmul_{n}"] = {"ms": round(ms, 3), "tflops": round(2 * n**3 / (ms * 1e-3) / 1e12, 1)}
+        del a, b
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    res["copy_1GiB"] = {"ms": round(ms, 3), "tb_s_read_plus_write": round(2 * (1 << 30) / (ms * 1e-3) / 1e12, 2)}
+    return res
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -172,6 +206,10 @@ def main():
         "--calibration-copy-mib", type=int, default=0,
         help="first run a plain elementwise copy of this many MiB three times (the known-size "
         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    parser.add_argument(
+        "--peaks", action="store_true",
+        help="only measure the on-box achieved peaks (a large bf16 GEMM through torch.matmul, "
+        "i.e. hipBLASLt, and a 1 GiB device copy) and print them as one JSON line")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -193,6 +231,9 @@ def main():
     torch_convnd.load_native()
     lib = _build.hip_library()
     device = torch.device("cuda", 0)
+    if args.peaks:
+        print(json.dumps(measure_peaks(torch, device)), flush=True)
+        return
     if args.calibration_copy_mib > 0:
         src = torch.ones(args.calibration_copy_mib << 18, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)

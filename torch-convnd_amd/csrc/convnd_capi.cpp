@@ -1280,7 +1280,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     st = hip_check(launch_prologue(dtype, pp, stream), "gradient staging");
     if (st != CONVND_HIP_SUCCESS) return st;
   }
-  if (fused_bias) {
+  // The bias gradient from the staging sums rides in the weight-gradient reduction's launch
+  // when there is one.
+  const bool bias_in_reduce = fused_bias && mfma_dw;
+  if (fused_bias && !bias_in_reduce) {
     st = hip_check(launch_grad_bias_from_sums(dtype, sums,
                                               octet_sum_blocks(g.batch, g.out_vol),
                                               g.out_channels, grad_bias, stream),
@@ -1308,7 +1311,11 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
           "MFMA weight gradient");
       timing_end(ev, stream);
       if (st != CONVND_HIP_SUCCESS) return st;
-      st = hip_check(launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream),
+      st = hip_check(bias_in_reduce
+                         ? launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream, sums,
+                                               octet_sum_blocks(g.batch, g.out_vol),
+                                               g.out_channels, grad_bias)
+                         : launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream),
                      "weight-gradient reduction");
     } else {
       st = hip_check(launch_direct_grad_weight(dtype, to_direct(g), grad_output, input,

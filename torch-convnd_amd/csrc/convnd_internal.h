@@ -245,8 +245,11 @@ hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi
 // Float slots (x4) of one position chunk's partial sums, and the pass that adds the npc
 // chunks in order and writes dW in the weight layout.
 int64_t wgrad_partial_slots(int mb, const WgradArgs& a);
+// With bias_sums non-null (16-bit dtypes) the same launch also reduces the channel sums of the
+// grad_output staging (nsum per channel) into db.
 hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& a, void* dw,
-                               hipStream_t stream);
+                               hipStream_t stream, const float* bias_sums = nullptr,
+                               int64_t nsum = 0, int64_t channels = 0, void* db = nullptr);
 hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream);
 hipError_t launch_reduce_partials(convnd_hip_dtype dtype, const float* partial, void* out,
                                   int64_t count, int64_t parts, hipStream_t stream);

@@ -70,7 +70,7 @@ __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w
 
 // ---- layout passes ----------------------------------------------------------------------
 
-constexpr int kOctRun = 2048;  // destination positions per octet-copy block
+constexpr int kOctRun = 1024;  // destination positions per octet-copy block
 constexpr int kOctSub = 512;   // positions per pass of the element-wise path
 
 // Shared memory of one octet-copy block: padded-row source offsets and the channel-sum
@@ -92,9 +92,9 @@ struct OctetSmem {
 //                 split_data_part(n / split_batch) of source image n % split_batch.
 // Block (position run bx of kOctRun, octet o, image n). Two paths:
 //   vec (16-bit source, no padding, volume a multiple of 8, 16-byte aligned source): each
-//       thread loads 8 consecutive positions of each of the 8 channels (16-byte loads),
-//       transposes the 8 x 8 block in registers (v_perm) and stores 8 whole positions
-//       (128 contiguous bytes);
+//       thread loads 4 consecutive positions of each of the 8 channels (8-byte loads),
+//       transposes the 4 x 8 block in registers (v_perm) and stores 4 whole positions
+//       (64 contiguous bytes);
 //   element-wise: every thread builds 16-byte units from eight 2-byte (4-byte for fp32)
 //       loads whose lanes run along the positions (coalesced within a row).
 // Loads go through a buffer resource over the source image: an offset past its end reads
@@ -156,31 +156,34 @@ __device__ __forceinline__ void octets16_block(const Src* src, unsigned short* d
   };
   if constexpr (sizeof(Src) == 2) {
     if (vec) {
-      const int pb = p0 + tid * 8;
+      const int pb = p0 + tid * 4;
       if (pb < pend) {
-        u32x4 r[8];
+        uint2 r[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const unsigned off =
               choff[k] >= 0 ? static_cast<unsigned>(choff[k] + pb) * 2u : kPast;
-          r[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+          r[k] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, 0));
         }
         if (sums != nullptr) {
 #pragma unroll
-          for (int k = 0; k < 8; ++k)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) add_sum(k, r[k][i]);
+          for (int k = 0; k < 8; ++k) {
+            add_sum(k, r[k].x);
+            add_sum(k, r[k].y);
+          }
         }
         // Position 2i + h of the run: channel pairs (2j, 2j+1) from half h of word i.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             u32x4 w;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              w[j] = __builtin_amdgcn_perm(r[2 * j + 1][i], r[2 * j][i],
-                                           h ? 0x07060302u : 0x05040100u);
+            for (int j = 0; j < 4; ++j) {
+              const unsigned lo = i ? r[2 * j].y : r[2 * j].x;
+              const unsigned hi = i ? r[2 * j + 1].y : r[2 * j + 1].x;
+              w[j] = __builtin_amdgcn_perm(hi, lo, h ? 0x07060302u : 0x05040100u);
+            }
             *reinterpret_cast<u32x4*>(dimg + (size_t)(pb + 2 * i + h) * 8) = w;
           }
         }

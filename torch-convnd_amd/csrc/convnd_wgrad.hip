@@ -293,10 +293,33 @@ void wgrad_kernel(WgradArgs A) {
 // dW from the partial sums: slot s = ((tile*4 + wave)*MB + mb)*8 + u)*64 + lane holds four
 // output channels of one (pair, input channel); the npc partials are added in order, eight
 // loads in flight.
+// Optional second part (blocks past the reduction's): the bias gradient from the fp32
+// channel sums of the staging pass, one block per channel, fixed-order tree.
+struct BiasSums {
+  const float* sums;
+  void* db;
+  int nsum, channels;
+};
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* part, T* dw,
                                                                 WgradArgs A, int mbv,
-                                                                int64_t nslots) {
+                                                                int64_t nslots, int rblocks,
+                                                                BiasSums bs) {
+  if (static_cast<int>(blockIdx.x) >= rblocks) {
+    __shared__ float red[kThreads];
+    const int c = blockIdx.x - rblocks;
+    float acc = 0.f;
+    for (int b = threadIdx.x; b < bs.nsum; b += kThreads) acc += bs.sums[(size_t)c * bs.nsum + b];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = kThreads / 2; w > 0; w >>= 1) {
+      if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) static_cast<T*>(bs.db)[c] = static_cast<T>(red[0]);
+    return;
+  }
   const int64_t s = blockIdx.x * (int64_t)kThreads + threadIdx.x;
   if (s >= nslots) return;
   const int lane = static_cast<int>(s & 63);
@@ -385,20 +408,27 @@ int64_t wgrad_partial_slots(int mb, const WgradArgs& a) {
 }
 
 hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& a, void* dw,
-                               hipStream_t stream) {
+                               hipStream_t stream, const float* bias_sums, int64_t nsum,
+                               int64_t channels, void* db) {
   const int64_t nslots = wgrad_partial_slots(mb, a);
-  if (nslots == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((nslots + kThreads - 1) / kThreads));
+  const int64_t rblocks = (nslots + kThreads - 1) / kThreads;
+  BiasSums bs{bias_sums, db, static_cast<int>(nsum), static_cast<int>(channels)};
+  const int64_t bblocks = bias_sums != nullptr ? channels : 0;
+  if (bias_sums != nullptr && (dtype == CONVND_HIP_FLOAT32 || nsum > INT32_MAX)) return hipErrorInvalidValue;
+  if (rblocks + bblocks == 0) return hipSuccess;
+  if (rblocks + bblocks > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(rblocks + bblocks));
+  const int rb = static_cast<int>(rblocks);
   const f32x4* part = reinterpret_cast<const f32x4*>(a.partial);
   if (dtype == CONVND_HIP_BFLOAT16) {
     hipLaunchKernelGGL(wgrad_reduce_kernel<__bf16>, grid, dim3(kThreads), 0, stream, part,
-                       static_cast<__bf16*>(dw), a, mb, nslots);
+                       static_cast<__bf16*>(dw), a, mb, nslots, rb, bs);
   } else if (dtype == CONVND_HIP_FLOAT16) {
     hipLaunchKernelGGL(wgrad_reduce_kernel<_Float16>, grid, dim3(kThreads), 0, stream, part,
-                       static_cast<_Float16*>(dw), a, mb, nslots);
+                       static_cast<_Float16*>(dw), a, mb, nslots, rb, bs);
   } else if (dtype == CONVND_HIP_FLOAT32) {
     hipLaunchKernelGGL(wgrad_reduce_kernel<float>, grid, dim3(kThreads), 0, stream, part,
-                       static_cast<float*>(dw), a, mb, nslots);
+                       static_cast<float*>(dw), a, mb, nslots, rb, bs);
   } else {
     return hipErrorInvalidValue;
   }
