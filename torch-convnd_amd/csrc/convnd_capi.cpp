@@ -622,6 +622,13 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
     IgemmArgs& A = plan.args;
     plan.wpk_elems = (size_t)A.nphase * A.groups * A.nchunk * A.kc_max * A.mtiles_padded * 64 * 8;
     plan.staged_elems = (size_t)A.batch * A.in_vol * A.cin_total;
+    // Byte offsets into the staged operand are 32-bit (buffer loads, an offset of 0xffffffe0
+    // or more reads zero).
+    if (plan.staged_elems * 2 > 0xffffffe0ull) {
+      plan.ok = false;
+      return plan;
+    }
+    A.in_bytes = static_cast<int>(static_cast<uint32_t>(plan.staged_elems * 2));
     // Geometry tables (built and copied to the device once per plan and device).
     const size_t at = igemm_table_layout(A);
     if (at > (size_t)kI32Safe) {

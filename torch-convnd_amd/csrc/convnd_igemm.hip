@@ -22,6 +22,8 @@
 // Every phase is then a stride-1 convolution with per-tap offsets e(t), which the same
 // kernel runs (blockIdx.z covers batch x phase).
 
+#include <type_traits>
+
 #include "convnd_geometry.h"
 #include "convnd_internal.h"
 #include "convnd_types.h"
@@ -143,27 +145,35 @@ void igemm_kernel(IgemmArgs A) {
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const size_t wstep = (size_t)A.mtiles_padded * 64;  // fragments per K32 step
-  // Halo staging in batches of kStageBatch items per thread: the loads of a batch are all
-  // in flight before the first LDS store. The first batch of the next chunk is loaded into
-  // registers before the current chunk's MFMA loop and stored after it, so its latency
-  // hides behind the MFMAs.
-  constexpr int kStageBatch = 4;
-  // Octet planes of this image and group: [cin_total/8][in_vol][8].
-  const T* chunk_base =
-      in + ((size_t)n * (A.cin_total >> 3) + (size_t)(g * (A.cin_g >> 3))) * A.in_vol * 8;
-  u32x4 pre[kStageBatch];
-  auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v) {
-    const T* base = chunk_base + (size_t)ck * A.noct * A.in_vol * 8;
+  // Halo staging in batches of items per thread: the loads of a batch (branch-free buffer
+  // loads; entries outside the input read zero through an offset past the buffer) are all
+  // in flight before the first LDS store. The first kPreBatch items of the next chunk are
+  // loaded into registers before the current chunk's MFMA loop and stored after it, so
+  // their latency hides behind the MFMAs; the rest go in batches of kStageBatch.
+  constexpr int kPreBatch = 4;
+  constexpr int kStageBatch = 8;
+  constexpr unsigned kPast = 0xffffffe0u;  // past every staged tensor (planner: < kPast bytes)
+  // Octet planes of this image and group: [cin_total/8][in_vol][8], addressed in bytes from
+  // the staged tensor's base.
+  const __amdgpu_buffer_rsrc_t srsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(in), 0, A.in_bytes, 0x00020000);
+  const unsigned img_base =
+      static_cast<unsigned>(((size_t)n * (A.cin_total >> 3) + (size_t)(g * (A.cin_g >> 3))) *
+                            A.in_vol * 16);
+  u32x4 pre[kPreBatch];
+  auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v, auto nbatch) {
+    const unsigned cbase = img_base + static_cast<unsigned>(ck * A.noct) * A.in_vol * 16u;
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
+    for (int u = 0; u < decltype(nbatch)::value; ++u) {
       const int it = it0 + u * kThreads;
       const int r = rp >> A.log2_noct;
       const int o = rp & onoct;
       const int ro = it < items ? rowin[r < A.rows ? r : 0] : -1;
       const int cl = corg + c;
-      v[u] = u32x4{0u, 0u, 0u, 0u};
-      if (ro >= 0 && cl >= 0 && cl < last_size)
-        v[u] = *reinterpret_cast<const u32x4*>(base + ((size_t)o * A.in_vol + ro + cl) * 8);
+      const bool ok = ro >= 0 && cl >= 0 && cl < last_size;
+      const unsigned off =
+          ok ? cbase + static_cast<unsigned>(o * A.in_vol + ro + cl) * 16u : kPast;
+      v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
       c += dc;
       rp += drp;
       if (c >= hlast) {
@@ -172,9 +182,9 @@ void igemm_kernel(IgemmArgs A) {
       }
     }
   };
-  auto stage_store = [&](int it0, int rp, int c, const u32x4* v) {
+  auto stage_store = [&](int it0, int rp, int c, const u32x4* v, auto nbatch) {
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
+    for (int u = 0; u < decltype(nbatch)::value; ++u) {
       const int it = it0 + u * kThreads;
       if (it < items) {
         const int r = rp >> A.log2_noct;
@@ -189,10 +199,10 @@ void igemm_kernel(IgemmArgs A) {
       }
     }
   };
-  // Position of item it0 + kStageBatch * kThreads in the walk, from the position of it0.
-  auto advance = [&](int& rp, int& c) {
+  // Position of item it0 + n * kThreads in the walk, from the position of it0.
+  auto advance = [&](int& rp, int& c, auto nbatch) {
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
+    for (int u = 0; u < decltype(nbatch)::value; ++u) {
       c += dc;
       rp += drp;
       if (c >= hlast) {
@@ -201,23 +211,25 @@ void igemm_kernel(IgemmArgs A) {
       }
     }
   };
+  using PreN = std::integral_constant<int, kPreBatch>;
+  using StageN = std::integral_constant<int, kStageBatch>;
   __syncthreads();  // row tables in LDS
-  stage_load(0, tid, rp0, c0, pre);
+  stage_load(0, tid, rp0, c0, pre, PreN{});
   for (int ck = 0; ck < A.nchunk; ++ck) {
     {
-      // Chunk ck: the first batch is in `pre`; the rest is loaded and stored here.
-      stage_store(tid, rp0, c0, pre);
+      // Chunk ck: the first kPreBatch items are in `pre`; the rest is loaded and stored here.
+      stage_store(tid, rp0, c0, pre, PreN{});
       int rp = rp0, c = c0;
-      advance(rp, c);
-      for (int it0 = tid + kStageBatch * kThreads; it0 < items; it0 += kStageBatch * kThreads) {
+      advance(rp, c, PreN{});
+      for (int it0 = tid + kPreBatch * kThreads; it0 < items; it0 += kStageBatch * kThreads) {
         u32x4 v[kStageBatch];
-        stage_load(ck, it0, rp, c, v);
-        stage_store(it0, rp, c, v);
-        advance(rp, c);
+        stage_load(ck, it0, rp, c, v, StageN{});
+        stage_store(it0, rp, c, v, StageN{});
+        advance(rp, c, StageN{});
       }
     }
     __syncthreads();
-    if (ck + 1 < A.nchunk) stage_load(ck + 1, tid, rp0, c0, pre);
+    if (ck + 1 < A.nchunk) stage_load(ck + 1, tid, rp0, c0, pre, PreN{});
 
     const frag* wck = wp +
                       ((size_t)((phase * A.groups + g) * A.nchunk + ck) * A.kc_max) * wstep +

@@ -62,6 +62,7 @@ struct IgemmArgs {
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int k_vol;
   int split_c;     // split-precision fp32: real channels per group in the GEMM-input role
+  int in_bytes;    // bytes of the staged operand (unsigned bit pattern, below 0xffffffe0)
   // Geometry tables in device memory, built once per plan by the host (convnd_geometry.h)
   // and read by the packing pass and the GEMM kernel, which then needs no per-axis code:
   //   taps  int  [nphase][4 lane groups][tap_row]: LDS byte offset of the k-group (tap,
