@@ -32,6 +32,7 @@ HIP_SOURCES = (
     "convnd_layout.hip",
     "convnd_igemm.hip",
     "convnd_wgrad.hip",
+    "convnd_wgrad_cm.hip",
     "convnd_capi.cpp",
 )
 OFFLOAD_ARCH = os.environ.get("TORCH_CONVND_OFFLOAD_ARCH", "gfx950")

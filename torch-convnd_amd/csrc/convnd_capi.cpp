@@ -346,7 +346,7 @@ int64_t choose_pitches(int R, const int* box, const int* sigma, const int* hext,
 // Any subset of the keys may be given; the planner then searches only plans matching it and
 // ignores the override when none does.
 struct PlanFilter {
-  int mb = 0, nb = 0, wm = 0, cc = 0, occ = 0;
+  int mb = 0, nb = 0, wm = 0, cc = 0, occ = 0, cm = -1;
   std::vector<int> box;
   bool active = false;
 };
@@ -379,6 +379,7 @@ PlanFilter parse_filter(const char* text) {
         if (key == "wm") f.wm = v;
         if (key == "cc") f.cc = v;
         if (key == "occ") f.occ = v;
+        if (key == "cm") f.cm = v;
       }
     }
     pos = end + 1;
@@ -682,9 +683,223 @@ struct WgradPlan {
   size_t dy_pad_elems = 0;   // grad_output padded to whole boxes (used when needed)
   size_t partial_elems = 0;
   double cost = 0.0;
+  // Channel-major kernel (convnd_wgrad_cm.hip) in place of the octet-major one: reads the
+  // caller's input directly (no staged copy); `args` then only describes grad_output for
+  // the padded copy (rank, extents, batch, channels).
+  bool cm = false;
+  WgradCmArgs cm_args{};
+  PlanarPadArgs ppad{};  // the zero-padded channels-first input it reads (staged_elems)
 };
 
+// Channel-major weight-gradient plan: 16-bit data and a unit stride along the last axis
+// (the runs of a halo row are contiguous in the padded input).
+bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
+  if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g) || g.batch == 0) return false;
+  const int R = g.rank;
+  if (g.s[R - 1] != 1) return false;
+  const int cin_g = static_cast<int>(g.cin_g), cout_g = static_cast<int>(g.cout_g);
+  const int k_vol = static_cast<int>(g.k_vol);
+  const int kl = static_cast<int>(g.k[R - 1]), dl = static_cast<int>(g.d[R - 1]);
+  const int mtiles = (cout_g + 15) / 16;
+  const int mb = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
+  const int mgroups = (mtiles + mb - 1) / mb;
+  const int ncol = cin_g * k_vol;
+  const int ntiles = (ncol + 15) / 16;
+  const PlanFilter& filter = plan_filter(2);
+  // LDS past the two item buffers (static): run table and item records.
+  const int64_t dyn_budget = 160 * 1024 - 2 * kWgradCmBuffer;
+  double best = -1.0;
+  WgradPlan plan;
+  {
+    const int box_vol = kWgradCmBoxVol;
+    int limit[kFastRank];
+    for (int a = 0; a < R; ++a) {
+      int l = 1;
+      while (l < g.out[a] && l < box_vol) l *= 2;
+      limit[a] = l;
+    }
+    limit[R - 1] = std::max(limit[R - 1], 8);
+    for_each_box(R, limit, box_vol, [&](const int* b) {
+      const int bl = b[R - 1];
+      if (bl != 8 && bl != 16) return;
+      if (!filter.box.empty()) {
+        if (static_cast<int>(filter.box.size()) != R) return;
+        for (int a = 0; a < R; ++a)
+          if (filter.box[a] != b[a]) return;
+      }
+      int hext[kFastRank] = {}, pe[kFastRank] = {};
+      int64_t rows_h = 1, boxes = 1, dvol = 1, pvol = 1;
+      int dext[kFastRank], nbox[kFastRank];
+      for (int a = 0; a < R; ++a) {
+        nbox[a] = static_cast<int>((g.out[a] + b[a] - 1) / b[a]);
+        dext[a] = nbox[a] * b[a];
+        boxes *= nbox[a];
+        dvol *= dext[a];
+        int64_t e;
+        if (a < R - 1) {
+          const int64_t h = (b[a] - 1) * g.s[a] + (g.k[a] - 1) * g.d[a] + 1;
+          if (h > 4096) return;
+          hext[a] = static_cast<int>(h);
+          rows_h *= h;
+          e = (int64_t)(nbox[a] - 1) * b[a] * g.s[a] + h;
+        } else {
+          e = ((int64_t)nbox[a] * b[a] + (kl - 1) * dl + 7) / 8 * 8;
+        }
+        if (e > kI32Safe) return;
+        pe[a] = static_cast<int>(e);
+        pvol *= e;
+        if (pvol > kI32Safe) return;
+      }
+      // The padded copy must stay int32-addressable and not dwarf the input.
+      if (pvol * g.batch * g.channels * 2 > kI32Safe || pvol > 8 * g.in_vol + (1 << 20)) return;
+      const int bl8 = bl / 8;
+      const int nrho = kl * bl8;
+      const int runpitch = nrho * 16;
+      const int64_t chpitch = rows_h * runpitch;
+      if (dvol * g.batch * g.out_channels > kI32Safe / 2) return;
+      const int64_t items = boxes * g.batch;
+      if (items > (int64_t{1} << 22)) return;
+      const int64_t dyt_bytes = (int64_t)mb * 16 * box_vol * 2;
+      const int ksteps = box_vol / 32;
+      int prev_nt = -1;
+      for (int ncq = 1; ncq <= ntiles; ++ncq) {
+        const int tpc = (ntiles + ncq - 1) / ncq;
+        if ((ntiles + tpc - 1) / tpc != ncq) continue;  // same split as a smaller ncq
+        int nt = (tpc + 3) / 4;
+        while (nt <= 8 && !wgrad_cm_supported(mb, nt)) ++nt;
+        if (nt > 8) continue;
+        if (nt == prev_nt) continue;
+        prev_nt = nt;
+        if (filter.nb && filter.nb != nt) continue;
+        // Channels a chunk spans (its columns are consecutive in (channel, tap) order).
+        int nch = 1;
+        for (int cq = 0; cq < ncq; ++cq) {
+          const int c0 = cq * tpc * 16;
+          const int c1 = std::min((cq + 1) * tpc * 16, ncol);
+          if (c0 < c1) nch = std::max(nch, (c1 - 1) / k_vol - c0 / k_vol + 1);
+        }
+        // Input runs per item in 64-run load instructions (at most 16 per wave), landing
+        // after the grad_output tile in one item buffer.
+        const int64_t xi = (nch * chpitch / 16 + 63) / 64;
+        if (xi > 64 || dyt_bytes + xi * 1024 > kWgradCmBuffer) continue;
+        const int64_t per_chunk_wgs = (int64_t)ncq * g.groups * mgroups;
+        int64_t npc = std::min<int64_t>(std::max<int64_t>(1, 256 / per_chunk_wgs), items);
+        const int64_t ipc = (items + npc - 1) / npc;
+        npc = (items + ipc - 1) / ipc;
+        const int64_t lds_items = align_up((int64_t)(box_vol / 8) * 4);
+        const int64_t lds = lds_items + ipc * 8;
+        if (lds > dyn_budget) continue;
+        if (npc * per_chunk_wgs > INT32_MAX) continue;
+        // Per item, clocks of one CU: MFMA issue of one wave (MB x NT per K32 step) and the
+        // LDS fragment reads of four waves (128 B/clock) against the item's loads straight
+        // into LDS (~64 B/clock/CU of L2 traffic), which overlap, plus barriers.
+        const double mfma = double(ksteps) * mb * nt * 16.0 / 0.8;
+        const double ldsr = double(ksteps) * (mb + nt) * 32.0;
+        const double stage = (double(xi) * 1024 + double(dyt_bytes)) / 64.0;
+        const double per_item = std::max(std::max(mfma, ldsr), stage) + 800.0;
+        const double per_wg = double(ipc) * per_item + 4000.0;
+        const int64_t wgs = npc * per_chunk_wgs;
+        const double rounds = double((wgs + 255) / 256);
+        const double partial_clk = double(wgs) * 4 * mb * nt * 64 * 16 * 2 / 3000.0;
+        const double cost = rounds * per_wg + partial_clk;
+        if (best >= 0 && cost >= best) continue;
+        best = cost;
+        plan = WgradPlan{};
+        plan.ok = true;
+        plan.cm = true;
+        plan.mb = mb;
+        plan.cost = cost;
+        plan.lds = static_cast<size_t>(lds);
+        plan.exact = dvol == g.out_vol;
+        plan.staged_elems = (size_t)g.batch * g.channels * pvol;
+        WgradCmArgs& C = plan.cm_args;
+        std::memset(&C, 0, sizeof(C));
+        C.x_bytes = static_cast<unsigned>(plan.staged_elems * 2);
+        C.rank = R;
+        C.batch = static_cast<int>(g.batch);
+        C.groups = static_cast<int>(g.groups);
+        C.cin_g = cin_g;
+        C.cout_g = cout_g;
+        C.cin_total = static_cast<int>(g.channels);
+        C.cout_total = static_cast<int>(g.out_channels);
+        C.pvol = static_cast<int>(pvol);
+        C.k_vol = k_vol;
+        C.dvol = static_cast<int>(dvol);
+        C.box_vol = box_vol;
+        C.ksteps = ksteps;
+        C.rows_h = static_cast<int>(rows_h);
+        C.kl = kl;
+        C.bl8 = bl8;
+        C.runpitch = runpitch;
+        C.chpitch = static_cast<int>(chpitch);
+        C.dl = dl;
+        C.dyt_bytes = static_cast<int>(dyt_bytes);
+        C.xi = static_cast<int>(xi);
+        C.di = static_cast<int>(dyt_bytes / 1024);
+        C.mgroups = mgroups;
+        C.ncq = ncq;
+        C.nt = nt;
+        C.npc = static_cast<int>(npc);
+        C.items = static_cast<int>(items);
+        C.items_per_pc = static_cast<int>(ipc);
+        C.lds_items = static_cast<int>(lds_items);
+        PlanarPadArgs& P = plan.ppad;
+        std::memset(&P, 0, sizeof(P));
+        P.rank = R;
+        P.channels = static_cast<int>(g.channels);
+        P.in_vol = static_cast<int>(g.in_vol);
+        P.pvol = static_cast<int>(pvol);
+        P.src_bytes = static_cast<unsigned>(g.batch * g.channels * g.in_vol * 2);
+        for (int a = 0; a < R; ++a) {
+          C.box[a] = b[a];
+          C.nbox[a] = nbox[a];
+          C.dext[a] = dext[a];
+          C.hext[a] = hext[a];
+          C.pe[a] = pe[a];
+          C.k[a] = static_cast<int>(g.k[a]);
+          C.s[a] = static_cast<int>(g.s[a]);
+          C.d[a] = static_cast<int>(g.d[a]);
+          P.in[a] = static_cast<int>(g.in[a]);
+          P.pe[a] = pe[a];
+          P.pad[a] = static_cast<int>(g.p[a]);
+        }
+        // grad_output as the padded copy's source/destination sees it.
+        WgradArgs& D = plan.args;
+        std::memset(&D, 0, sizeof(D));
+        D.rank = R;
+        D.batch = C.batch;
+        D.cout_total = C.cout_total;
+        D.dvol = C.dvol;
+        int ovol = 1;
+        for (int a = 0; a < R; ++a) {
+          D.out_size[a] = static_cast<int>(g.out[a]);
+          D.dext[a] = dext[a];
+          ovol *= D.out_size[a];
+        }
+        D.out_vol = ovol;
+      }
+    });
+  }
+  if (!plan.ok) return false;
+  if (wgrad_cm_table_layout(plan.cm_args) > (size_t)kI32Safe) return false;
+  plan.dy_pad_elems = plan.exact ? 0 : (size_t)g.batch * plan.cm_args.dvol * g.out_channels;
+  plan.partial_elems = (size_t)plan.cm_args.npc * wgrad_cm_partial_slots(plan.mb, plan.cm_args) * 4;
+  *out = plan;
+  return true;
+}
+
+WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt);
+
+// The channel-major kernel where it applies (CONVND_HIP_WGRAD_PLAN=cm=0 forces the
+// octet-major one), else the octet-major kernel.
 WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
+  const PlanFilter& filter = plan_filter(2);
+  WgradPlan cm;
+  if (filter.cm != 0 && plan_wgrad_cm(g, dt, &cm)) return cm;
+  return plan_wgrad_octets(g, dt);
+}
+
+WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt) {
   WgradPlan plan;
   // Split-precision fp32: kSplit images of bf16 parts per image (see convnd_types.h).
   const bool split = dt == CONVND_HIP_FLOAT32;
@@ -1036,6 +1251,11 @@ const void* wgrad_device_tables(const std::string& key, const WgradArgs& A) {
                        [&](unsigned char* h) { wgrad_build_tables(A, h); });
 }
 
+const void* wgrad_cm_device_tables(const std::string& key, const WgradCmArgs& A) {
+  return device_tables(key, static_cast<size_t>(A.tab_bytes),
+                       [&](unsigned char* h) { wgrad_cm_build_tables(A, h); });
+}
+
 // Diagnostic kernel timing (convnd_hip_timing_enable/read): event pairs recorded around
 // the main kernels. Process-global on purpose — autograd runs backward on its own thread.
 constexpr int kTimedKernels = 3;
@@ -1237,6 +1457,7 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   const bool mfma_dx = gi && b.dg.ok, mfma_dw = gw && b.wg.ok;
   IgemmArgs DA{};
   WgradArgs WA{};
+  WgradCmArgs CA{};
   float* sums = fused_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
   PrologueParts pp;
   if (mfma_dx) {
@@ -1258,7 +1479,31 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     pp.w = weight;
     pp.wpk = ws + b.off_wpk;
   }
-  if (mfma_dw) {
+  if (mfma_dw && b.wg.cm) {
+    WA = b.wg.args;
+    CA = b.wg.cm_args;
+    CA.tables = wgrad_cm_device_tables(plan_key(g, dtype, 66), CA);
+    if (CA.tables == nullptr)
+      return fail(CONVND_HIP_LAUNCH_FAILED,
+                  "weight-gradient geometry tables: device allocation failed");
+    CA.x = ws + b.off_x_stage;
+    CA.dy = grad_output;
+    pp.pp = &b.wg.ppad;
+    pp.x = input;
+    pp.x_pp = ws + b.off_x_stage;
+    pp.pp_batch = g.batch;
+    CA.partial = reinterpret_cast<float*>(ws + b.off_partial);
+    CA.dy_bytes = static_cast<unsigned>(g.batch * g.out_channels * g.out_vol * 2);
+    // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the
+    // boxes tile it exactly and its base is 16-byte aligned.
+    if (!b.wg.exact || reinterpret_cast<uintptr_t>(grad_output) % 16 != 0) {
+      pp.wg = &WA;
+      pp.dy = grad_output;
+      pp.dy_pad = ws + b.off_dy_pad;
+      CA.dy = ws + b.off_dy_pad;
+      CA.dy_bytes = static_cast<unsigned>(b.wg.dy_pad_elems * 2);
+    }
+  } else if (mfma_dw) {
     WA = b.wg.args;
     WA.tables = wgrad_device_tables(plan_key(g, dtype, 65), WA);
     if (WA.tables == nullptr)
@@ -1313,17 +1558,27 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   if (gw) {
     if (mfma_dw) {
       const auto ev = timing_begin(2, stream);
-      st = hip_check(
-          launch_wgrad_mfma(dtype, b.wg.mb, b.wg.stg, b.wg.multi, WA, b.wg.lds, stream),
-          "MFMA weight gradient");
+      st = hip_check(b.wg.cm ? launch_wgrad_cm(dtype, b.wg.mb, CA, b.wg.lds, stream)
+                             : launch_wgrad_mfma(dtype, b.wg.mb, b.wg.stg, b.wg.multi, WA,
+                                                 b.wg.lds, stream),
+                     "MFMA weight gradient");
       timing_end(ev, stream);
       if (st != CONVND_HIP_SUCCESS) return st;
-      st = hip_check(bias_in_reduce
-                         ? launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream, sums,
-                                               octet_sum_blocks(g.batch, g.out_vol),
-                                               g.out_channels, grad_bias)
-                         : launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream),
-                     "weight-gradient reduction");
+      if (b.wg.cm) {
+        st = hip_check(bias_in_reduce
+                           ? launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream,
+                                                    sums, octet_sum_blocks(g.batch, g.out_vol),
+                                                    g.out_channels, grad_bias)
+                           : launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream),
+                       "weight-gradient reduction");
+      } else {
+        st = hip_check(bias_in_reduce
+                           ? launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream, sums,
+                                                 octet_sum_blocks(g.batch, g.out_vol),
+                                                 g.out_channels, grad_bias)
+                           : launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream),
+                       "weight-gradient reduction");
+      }
     } else {
       st = hip_check(launch_direct_grad_weight(dtype, to_direct(g), grad_output, input,
                                                grad_weight, stream),
@@ -1368,6 +1623,17 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
     const WgradPlan p = plan_wgrad(g, dtype);
     if (!p.ok) {
       text = "{\"kernel\":\"direct\"}";
+    } else if (p.cm) {
+      const WgradCmArgs& C = p.cm_args;
+      text = "{\"kernel\":\"mfma_wgrad_cm\",\"mb\":" + std::to_string(p.mb) +
+             ",\"nt\":" + std::to_string(C.nt) + ",\"box\":" + join(C.box, C.rank) +
+             ",\"items\":" + std::to_string(C.items) + ",\"npc\":" + std::to_string(C.npc) +
+             ",\"items_per_pc\":" + std::to_string(C.items_per_pc) +
+             ",\"ncq\":" + std::to_string(C.ncq) + ",\"mgroups\":" +
+             std::to_string(C.mgroups) + ",\"xi\":" + std::to_string(C.xi) +
+             ",\"di\":" + std::to_string(C.di) + ",\"lds\":" + std::to_string(p.lds) +
+             ",\"exact\":" + std::to_string(p.exact ? 1 : 0) + ",\"workgroups\":" +
+             std::to_string((int64_t)C.npc * C.ncq * C.groups * C.mgroups) + "}";
     } else {
       const WgradArgs& A = p.args;
       text = "{\"kernel\":\"mfma_wgrad\",\"mb\":" + std::to_string(p.mb) +

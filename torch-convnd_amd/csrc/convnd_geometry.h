@@ -5,6 +5,8 @@
 // read them. Everything here is plain integer arithmetic, compiled for host and device.
 #pragma once
 
+#include <vector>
+
 #include "convnd_internal.h"
 
 namespace convnd {
@@ -434,6 +436,217 @@ inline void wgrad_build_tables(const WgradArgs& A, unsigned char* tab) {
       slot[(J * 256 + t) * 2] = static_cast<int>(off);
       slot[(J * 256 + t) * 2 + 1] = dst;
     }
+  }
+}
+
+// ---- channel-major weight gradient ---------------------------------------------------
+
+// Byte layout of the channel-major weight-gradient tables (WgradCmArgs::tables).
+inline size_t wgrad_cm_table_layout(WgradCmArgs& A) {
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = at;
+    at += (bytes + 255) & ~size_t{255};
+    return static_cast<int>(o);
+  };
+  const size_t lanes = (size_t)A.ncq * 4 * A.nt * 16;
+  A.tab_chunk = take((size_t)A.ncq * 8);
+  A.tab_col = take(lanes * 4);
+  A.tab_cid = take(lanes * 4);
+  A.tab_run = take((size_t)(A.box_vol / 8) * 4);
+  A.tab_xsrc = take((size_t)A.ncq * A.xi * 64 * 4);
+  A.tab_dsrc = take((size_t)A.di * 64 * 4);
+  A.tab_item = take((size_t)A.items * 8);
+  A.tab_bytes = static_cast<int>(at);
+  return at;
+}
+
+// Column tiles: chunk cq holds tiles [cq * tpc, (cq + 1) * tpc); wave w of its workgroup the
+// chunk's tiles w * nt .. w * nt + nt - 1.
+inline int wgrad_cm_tiles_per_chunk(const WgradCmArgs& A) {
+  const int ntiles = (A.cin_g * A.k_vol + 15) / 16;
+  return (ntiles + A.ncq - 1) / A.ncq;
+}
+
+// Channels spanned by chunk cq: first (group-relative) and count.
+inline void wgrad_cm_chunk_channels(const WgradCmArgs& A, int cq, int* first, int* count) {
+  const int ncol = A.cin_g * A.k_vol;
+  const int ntiles = (ncol + 15) / 16;
+  const int tpc = wgrad_cm_tiles_per_chunk(A);
+  const int t0 = cq * tpc;
+  const int t1 = t0 + tpc < ntiles ? t0 + tpc : ntiles;
+  const int c_end = t1 * 16 < ncol ? t1 * 16 : ncol;
+  *first = t0 < t1 ? t0 * 16 / A.k_vol : 0;
+  *count = t0 < t1 ? (c_end - 1) / A.k_vol - *first + 1 : 0;
+}
+
+// Halo-row pitch (in rows) of each axis but the last.
+inline void wgrad_cm_row_pitch(const WgradCmArgs& A, int* hpitch) {
+  int hp = 1;
+  for (int a = A.rank - 2; a >= 0; --a) {
+    hpitch[a] = hp;
+    hp *= A.hext[a];
+  }
+}
+
+// LDS byte offset of tap t (flat over the kernel axes, last fastest) in a channel's runs:
+// its halo row shift times the row pitch, plus its last-axis run block.
+inline int wgrad_cm_tap_offset(const WgradCmArgs& A, int t) {
+  const int R = A.rank;
+  int hpitch[kFastRank];
+  wgrad_cm_row_pitch(A, hpitch);
+  int rem = t;
+  const int tl = rem % A.k[R - 1];
+  rem /= A.k[R - 1];
+  int rows = 0;
+  for (int a = R - 2; a >= 0; --a) {
+    const int ta = rem % A.k[a];
+    rem /= A.k[a];
+    rows += ta * A.d[a] * hpitch[a];
+  }
+  return rows * A.runpitch + tl * A.bl8 * 16;
+}
+
+// Fills the tables (host memory of wgrad_cm_table_layout(A) bytes).
+inline void wgrad_cm_build_tables(const WgradCmArgs& A, unsigned char* tab) {
+  const int R = A.rank;
+  const int ncol = A.cin_g * A.k_vol;
+  const int ntiles = (ncol + 15) / 16;
+  const int tpc = wgrad_cm_tiles_per_chunk(A);
+  int* chunk = reinterpret_cast<int*>(tab + A.tab_chunk);
+  int* col = reinterpret_cast<int*>(tab + A.tab_col);
+  int* cid = reinterpret_cast<int*>(tab + A.tab_cid);
+  for (int cq = 0; cq < A.ncq; ++cq) {
+    const int t0 = cq * tpc;
+    const int t1 = t0 + tpc < ntiles ? t0 + tpc : ntiles;
+    int ci_lo, nch;
+    wgrad_cm_chunk_channels(A, cq, &ci_lo, &nch);
+    chunk[2 * cq] = ci_lo;
+    chunk[2 * cq + 1] = nch;
+    for (int w = 0; w < 4; ++w) {
+      for (int j = 0; j < A.nt; ++j) {
+        const int lt = w * A.nt + j;
+        const int T = t0 + lt;
+        int cols[16], offs[16];
+        for (int i = 0; i < 16; ++i) {
+          const int c = T * 16 + i;
+          const bool ok = lt < tpc && T < t1 && c < ncol;
+          cols[i] = ok ? c : -1;
+          offs[i] = ok ? (c / A.k_vol - ci_lo) * A.chpitch + wgrad_cm_tap_offset(A, c % A.k_vol)
+                       : 0;
+        }
+        // Lanes 0-7 and 8-15 are read together (eight 16-byte reads per pass): give each
+        // half columns on distinct 16-byte bank slots (bits 4-7 of the offset) where possible.
+        int lane_of[16];
+        bool used[2][16] = {};
+        int fill[2] = {0, 0};
+        bool placed[16] = {};
+        for (int i = 0; i < 16; ++i) {
+          if (cols[i] < 0) continue;
+          const int sl = (offs[i] >> 4) & 15;
+          for (int h = 0; h < 2; ++h) {
+            if (fill[h] < 8 && !used[h][sl]) {
+              used[h][sl] = true;
+              lane_of[i] = h * 8 + fill[h]++;
+              placed[i] = true;
+              break;
+            }
+          }
+        }
+        for (int i = 0; i < 16; ++i) {
+          if (placed[i]) continue;
+          const int h = fill[0] < 8 ? 0 : 1;
+          lane_of[i] = h * 8 + fill[h]++;
+        }
+        int* cl = col + (((size_t)cq * 4 + w) * A.nt + j) * 16;
+        int* ci = cid + (((size_t)cq * 4 + w) * A.nt + j) * 16;
+        for (int i = 0; i < 16; ++i) {
+          cl[lane_of[i]] = offs[i];
+          ci[lane_of[i]] = cols[i];
+        }
+      }
+    }
+  }
+  // Strides: padded input (pe), grad_output buffer (dext); halo-row pitches.
+  int pstride[kFastRank], dstride[kFastRank], hpitch[kFastRank];
+  {
+    int ps = 1, ds = 1;
+    for (int a = R - 1; a >= 0; --a) {
+      pstride[a] = ps;
+      dstride[a] = ds;
+      ps *= A.pe[a];
+      ds *= A.dext[a];
+    }
+  }
+  wgrad_cm_row_pitch(A, hpitch);
+  // Runs of the box: run r = (box row br, run sr of the last extent); B fragments read the
+  // run of halo row (box row * stride) + tap shift.
+  const int nruns = A.box_vol / 8;
+  int* run = reinterpret_cast<int*>(tab + A.tab_run);
+  std::vector<int> dyrun(nruns);
+  for (int r = 0; r < nruns; ++r) {
+    const int sr = r % A.bl8;
+    int br = r / A.bl8;
+    int rows = 0, doff = sr * 8;
+    for (int a = R - 2; a >= 0; --a) {
+      const int bc = br % A.box[a];
+      br /= A.box[a];
+      rows += bc * A.s[a] * hpitch[a];
+      doff += bc * dstride[a];
+    }
+    run[r] = rows * A.runpitch + sr * 16;
+    dyrun[r] = doff;
+  }
+  // Input run slots: slot = (channel c, halo row hr, run rho = tl * bl8 + sr) in LDS order;
+  // its first element in the padded input: channel c, halo row hr (padded coordinates from
+  // the box origin), last-axis offset tl * dl + 8 * sr from the box origin.
+  const int nrho = A.kl * A.bl8;
+  int* xsrc = reinterpret_cast<int*>(tab + A.tab_xsrc);
+  for (int cq = 0; cq < A.ncq; ++cq) {
+    int ci_lo, nch;
+    wgrad_cm_chunk_channels(A, cq, &ci_lo, &nch);
+    const int nslots = nch * A.rows_h * nrho;
+    for (int sl = 0; sl < A.xi * 64; ++sl) {
+      int v = -1;
+      if (sl < nslots) {
+        const int rho = sl % nrho;
+        const int hr = (sl / nrho) % A.rows_h;
+        const int c = sl / (nrho * A.rows_h);
+        int rem = hr, roff = 0;
+        for (int a = R - 2; a >= 0; --a) {
+          roff += (rem % A.hext[a]) * pstride[a];
+          rem /= A.hext[a];
+        }
+        const int tl = rho / A.bl8, sr = rho % A.bl8;
+        v = c * A.pvol + roff + tl * A.dl + 8 * sr;
+      }
+      xsrc[(size_t)cq * A.xi * 64 + sl] = v;
+    }
+  }
+  // grad_output slots: co * nruns + (r ^ (co % 16)) holds run r of channel row co.
+  int* dsrc = reinterpret_cast<int*>(tab + A.tab_dsrc);
+  for (int sl = 0; sl < A.di * 64; ++sl) {
+    const int co = sl / nruns;
+    const int r = (sl % nruns) ^ (co % 16);
+    dsrc[sl] = co * A.dvol + dyrun[r];
+  }
+  // Items: (image, box) -> element bases of the box origin.
+  int boxes = 1;
+  for (int a = 0; a < R; ++a) boxes *= A.nbox[a];
+  int* item = reinterpret_cast<int*>(tab + A.tab_item);
+  for (int it = 0; it < A.items; ++it) {
+    const int n = it / boxes;
+    int bb = it - n * boxes;
+    long long xbase = (long long)n * A.cin_total * A.pvol;
+    long long dbase = (long long)n * A.cout_total * A.dvol;
+    for (int a = R - 1; a >= 0; --a) {
+      const int j0 = (bb % A.nbox[a]) * A.box[a];
+      bb /= A.nbox[a];
+      xbase += (long long)j0 * A.s[a] * pstride[a];
+      dbase += (long long)j0 * dstride[a];
+    }
+    item[2 * it] = static_cast<int>(xbase);
+    item[2 * it + 1] = static_cast<int>(dbase);
   }
 }
 

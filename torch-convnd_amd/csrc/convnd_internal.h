@@ -168,6 +168,67 @@ struct WgradArgs {
 // Byte offset past every buffer the weight-gradient kernel reads: such a load returns zero.
 constexpr unsigned kWgradOob = 0x80000000u;
 
+// Arguments of the channel-major MFMA weight gradient (convnd_wgrad_cm.hip): the GEMM
+// M = output channels, N = columns (input channel, tap) in the weight layout's order (16 per
+// MFMA tile), K = output positions. Per box of positions the workgroup keeps in LDS, for
+// each input channel of its column chunk and each halo row (all axes but the last), one
+// 16-byte run of 8 consecutive positions per (last-axis tap, run of the box's last extent),
+// read from a zero-padded channels-first copy of the input: every B fragment is one aligned
+// LDS read, the last-axis tap shift applied once when the run is loaded.
+struct WgradCmArgs {
+  const void* x;        // zero-padded input [N][cin_total][pe...] (pe: WgradCmArgs::pe)
+  const void* dy;       // grad_output [N][cout_total][dvol] (the output, or padded to boxes)
+  float* partial;       // per-lane accumulator vectors, see wgrad_cm_partial_slots
+  unsigned x_bytes, dy_bytes;  // buffer sizes (offsets at or past them read zero)
+  int rank, batch, groups, cin_g, cout_g, cin_total, cout_total;
+  int pvol, k_vol, dvol;  // per-channel volumes: padded input, grad_output buffer
+  int box_vol, ksteps;  // positions per item; K32 steps per item
+  int rows_h;           // halo rows per channel (product of the halo extents but the last)
+  int kl, bl8;          // last-axis taps; runs of 8 per box row
+  int runpitch;         // LDS bytes per halo row: kl * bl8 runs of 16 bytes
+  int chpitch;          // LDS bytes per staged channel (rows_h * runpitch)
+  int dl;               // last-axis tap step (dilation)
+  int dyt_bytes;        // LDS bytes of the grad_output tile (MB * 16 rows of box_vol * 2)
+  int xi, di;           // 64-run load instructions per item: input runs, grad_output runs
+  int mgroups, ncq, nt; // output-channel groups of 16 * MB, column chunks, tiles per wave
+  int npc, items, items_per_pc;
+  int lds_items;        // dynamic LDS byte offset of the item records (after the run table)
+  int box[kFastRank], nbox[kFastRank], dext[kFastRank], hext[kFastRank], pe[kFastRank];
+  int k[kFastRank], s[kFastRank], d[kFastRank];
+  // Geometry tables in device memory, built once per plan by the host (convnd_geometry.h):
+  //   chunk int2 [ncq]: first input channel (group-relative) and channels of the chunk;
+  //   col   int  [ncq][4][nt][16]: LDS byte offset of lane's column (channel, tap) in the
+  //              chunk's runs (0 for padding lanes);
+  //   cid   int  [ncq][4][nt][16]: the column, ci * k_vol + tap (-1: padding);
+  //   run   int  [box_vol / 8]: LDS byte offset of run r of the box in a channel's runs;
+  //   xsrc  int  [ncq][xi][64]: element offset (padded input, from the item's base and the
+  //              chunk's first channel) of the run that lane l of load instruction m stages
+  //              into LDS run slot m*64 + l (-1: past the chunk's runs);
+  //   dsrc  int  [di][64]: element offset (grad_output buffer, from the item's base and the
+  //              workgroup's first channel) of the run staged into grad_output slot
+  //              m*64 + l = co*(box_vol/8) + (r ^ (co % 16)) (channel row co, run r);
+  //   item  int2 [items]: element bases of the item's box in the padded input and in the
+  //              grad_output buffer (image and box origin; channel offsets added per
+  //              workgroup).
+  const void* tables;
+  int tab_chunk, tab_col, tab_cid, tab_run, tab_xsrc, tab_dsrc, tab_item, tab_bytes;
+};
+
+// LDS bytes of one item buffer of the channel-major weight gradient (two per workgroup).
+constexpr int kWgradCmBuffer = 78 * 1024;
+// Positions per item (box volume) of the channel-major weight gradient.
+constexpr int kWgradCmBoxVol = 256;
+
+// Zero-padded channels-first copy of the input for the channel-major weight gradient:
+// dst[n][c][u] = src[n][c][u - pad] (zero outside the input), u_a < pe[a] (pe[rank-1] a
+// multiple of 8).
+struct PlanarPadArgs {
+  int rank, channels;
+  int in[kFastRank], pe[kFastRank], pad[kFastRank];
+  int in_vol, pvol;
+  unsigned src_bytes;  // size of the source tensor (loads past it read zero)
+};
+
 // ---- kernel launchers (defined in the .hip files) -------------------------------------
 
 // Octet-major copy of a channels-first tensor, optionally zero-padded:
@@ -197,7 +258,9 @@ int64_t octet_sum_blocks(int64_t batch, int64_t volume);
 //   GEMM input: octet-major copy of src with geometry and channel map sa (no padding),
 //               with optional channel sums (16-bit source);
 //   octets:     zero-padded octet-major input for the weight gradient (pad);
-//   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg).
+//   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg);
+//   planar pad: zero-padded channels-first input for the channel-major weight gradient
+//               (pp, 16-bit data).
 struct IgemmArgs;
 struct WgradArgs;
 struct PrologueParts {
@@ -217,6 +280,9 @@ struct PrologueParts {
   const void* dy = nullptr;
   void* dy_pad = nullptr;
   int split_batch = 0;
+  const PlanarPadArgs* pp = nullptr;  // zero-padded channels-first input (x -> x_pp)
+  void* x_pp = nullptr;
+  int64_t pp_batch = 0;
 };
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream);
 
@@ -243,6 +309,15 @@ bool igemm_tile_supported(int mb, int nb, int wm);
 // several batches of 8 slots (only the first is prefetched).
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
                              const WgradArgs& a, size_t lds_bytes, hipStream_t stream);
+// Channel-major weight gradient: mb tiles of 16 output channels and nt column tiles per
+// wave (wgrad_cm_supported lists the compiled pairs).
+bool wgrad_cm_supported(int mb, int nt);
+hipError_t launch_wgrad_cm(convnd_hip_dtype dtype, int mb, const WgradCmArgs& a,
+                           size_t lds_bytes, hipStream_t stream);
+int64_t wgrad_cm_partial_slots(int mb, const WgradCmArgs& a);
+hipError_t launch_wgrad_cm_reduce(convnd_hip_dtype dtype, int mb, const WgradCmArgs& a,
+                                  void* dw, hipStream_t stream, const float* bias_sums = nullptr,
+                                  int64_t nsum = 0, int64_t channels = 0, void* db = nullptr);
 // Float slots (x4) of one position chunk's partial sums, and the pass that adds the npc
 // chunks in order and writes dW in the weight layout.
 int64_t wgrad_partial_slots(int mb, const WgradArgs& a);

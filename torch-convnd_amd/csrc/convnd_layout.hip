@@ -53,6 +53,12 @@ struct DevPrologue {
   int split_batch;
   int64_t runs;
   int d_blocks;
+  // Zero-padded channels-first input for the channel-major weight gradient.
+  PlanarPadArgs ppa;
+  const void* xpp_src;
+  void* x_pp;
+  int64_t e_total;
+  int e_blocks;
 };
 
 // SPLIT: fp32 sources (split-precision copies and packing).
@@ -84,8 +90,17 @@ void prologue_kernel(DevPrologue P) {
     return;
   }
   b -= P.c_blocks;
-  stage::pad_dy16_blocks<S>(static_cast<const S*>(P.dy), static_cast<unsigned short*>(P.dy_pad),
-                            P.wg, P.split_batch, P.runs, b, P.d_blocks);
+  if (b < P.d_blocks) {
+    stage::pad_dy16_blocks<S>(static_cast<const S*>(P.dy), static_cast<unsigned short*>(P.dy_pad),
+                              P.wg, P.split_batch, P.runs, b, P.d_blocks);
+    return;
+  }
+  b -= P.d_blocks;
+  if constexpr (!SPLIT) {
+    stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
+                               static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b,
+                               P.e_blocks);
+  }
 }
 
 // Partial sums of channel c over [N][C][V] (any element type): block (chunk, c) sums a
@@ -257,6 +272,16 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     const int64_t blocks = (P.runs + kThreads - 1) / kThreads;
     P.d_blocks = static_cast<int>(blocks < 2048 ? blocks : 2048);
     total += P.d_blocks;
+  }
+  if (p.x_pp != nullptr && p.pp != nullptr) {
+    if (split) return hipErrorInvalidValue;
+    P.ppa = *p.pp;
+    P.xpp_src = p.x;
+    P.x_pp = p.x_pp;
+    P.e_total = p.pp_batch * p.pp->channels * (p.pp->pvol / 8);
+    const int64_t blocks = (P.e_total + kThreads - 1) / kThreads;
+    P.e_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
+    total += P.e_blocks;
   }
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffff) return hipErrorInvalidValue;

@@ -356,5 +356,100 @@ __device__ __forceinline__ void pad_dy16_blocks(const Src* src, unsigned short* 
   }
 }
 
+// Zero-padded channels-first copy (PlanarPadArgs), 16-bit elements: each thread writes 8
+// consecutive elements of a destination row (pe[rank-1] is a multiple of 8) as one 16-byte
+// store.
+__device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
+                                                    unsigned short* dst,
+                                                    const PlanarPadArgs& P, int64_t total,
+                                                    int block, int nblocks) {
+  const int R = P.rank;
+  int pe_last = 8, in_last = 1, pad_last = 0;
+#pragma unroll
+  for (int a = 0; a < kFastRank; ++a) {
+    if (a == R - 1) {
+      pe_last = P.pe[a];
+      in_last = P.in[a];
+      pad_last = P.pad[a];
+    }
+  }
+  const int chunks = pe_last >> 3;
+  const int rows_per_img = P.pvol / pe_last;
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned short*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes),
+      0x00020000);
+  for (int64_t t = block * (int64_t)kThreads + threadIdx.x; t < total;
+       t += (int64_t)nblocks * kThreads) {
+    const int64_t row = t / chunks;  // (image, channel, padded row)
+    const int u0 = static_cast<int>(t - row * chunks) * 8 - pad_last;
+    const int64_t nc = row / rows_per_img;
+    int rem = static_cast<int>(row - nc * rows_per_img);
+    int srow = 0, istr = in_last;
+    bool ok = true;
+#pragma unroll
+    for (int a = kFastRank - 2; a >= 0; --a) {
+      if (a < R - 1) {
+        const int u = rem % P.pe[a] - P.pad[a];
+        rem /= P.pe[a];
+        ok = ok && u >= 0 && u < P.in[a];
+        srow += u * istr;
+        istr *= P.in[a];
+      }
+    }
+    const int64_t base = nc * P.in_vol + srow;
+    // One 16-byte load at the (2-byte-aligned) first element when it lies wholly inside the
+    // source; elements outside the row are masked to zero. At the source's two ends (a load
+    // there would start before it or end past it) the elements are read one by one.
+    const int64_t first = base + u0;
+    const int lo_i = -u0 < 0 ? 0 : (-u0 > 8 ? 8 : -u0);
+    const int hi_i = in_last - u0 < 0 ? 0 : (in_last - u0 > 8 ? 8 : in_last - u0);
+    u32x4 w = u32x4{0u, 0u, 0u, 0u};
+    if (ok && lo_i < hi_i) {
+      if (first >= 0 && (first + 8) * 2 <= static_cast<int64_t>(P.src_bytes)) {
+        w = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, static_cast<unsigned>(first * 2), 0, 0));
+        const unsigned bits = ((1u << hi_i) - 1u) & ~((1u << lo_i) - 1u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] &= ((bits >> (2 * j)) & 1u ? 0x0000ffffu : 0u) |
+                  ((bits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+      } else {
+        unsigned short v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bool in = i >= lo_i && i < hi_i;
+          const unsigned off = in ? static_cast<unsigned>((first + i) * 2) : 0xfffffff0u;
+          v[i] = __builtin_amdgcn_raw_buffer_load_b16(sr, off, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = v[2 * j] | (static_cast<unsigned>(v[2 * j + 1]) << 16);
+      }
+    }
+    *reinterpret_cast<u32x4*>(dst + t * 8) = w;
+  }
+}
+
+// Bias gradient from the fp32 channel sums of a staging pass: db[c] = sum of the nsum
+// partial sums of channel c, one workgroup per channel, fixed-order tree.
+struct BiasSums {
+  const float* sums;
+  void* db;
+  int nsum, channels;
+};
+
+template <typename T>
+__device__ __forceinline__ void bias_from_sums(const BiasSums& bs, int c) {
+  __shared__ float red[kThreads];
+  float acc = 0.f;
+  for (int b = threadIdx.x; b < bs.nsum; b += kThreads) acc += bs.sums[(size_t)c * bs.nsum + b];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = kThreads / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) static_cast<T*>(bs.db)[c] = static_cast<T>(red[0]);
+}
+
 }  // namespace stage
 }  // namespace convnd

@@ -294,12 +294,8 @@ void wgrad_kernel(WgradArgs A) {
 // output channels of one (pair, input channel); the npc partials are added in order, eight
 // loads in flight.
 // Optional second part (blocks past the reduction's): the bias gradient from the fp32
-// channel sums of the staging pass, one block per channel, fixed-order tree.
-struct BiasSums {
-  const float* sums;
-  void* db;
-  int nsum, channels;
-};
+// channel sums of the staging pass (stage::bias_from_sums).
+using stage::BiasSums;
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* part, T* dw,
@@ -307,17 +303,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
                                                                 int64_t nslots, int rblocks,
                                                                 BiasSums bs) {
   if (static_cast<int>(blockIdx.x) >= rblocks) {
-    __shared__ float red[kThreads];
-    const int c = blockIdx.x - rblocks;
-    float acc = 0.f;
-    for (int b = threadIdx.x; b < bs.nsum; b += kThreads) acc += bs.sums[(size_t)c * bs.nsum + b];
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int w = kThreads / 2; w > 0; w >>= 1) {
-      if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) static_cast<T*>(bs.db)[c] = static_cast<T>(red[0]);
+    stage::bias_from_sums<T>(bs, blockIdx.x - rblocks);
     return;
   }
   const int64_t s = blockIdx.x * (int64_t)kThreads + threadIdx.x;

@@ -1,0 +1,387 @@
+// Channel-major MFMA weight gradient (gfx950, 16x16x32 bf16/fp16 -> fp32) of the N-d
+// convolution, for a unit stride along the last axis.
+//
+// dW[co][ci][t] = sum over images n and output positions o of dY[n][co][o] * X[n][ci][o*s - p
+// + t*d]: a GEMM with M = output channels, N = columns (input channel, tap) in the weight
+// layout's order, K = output positions, reduced over a box of positions at a time.
+//
+//   * A workgroup owns a chunk of consecutive column tiles (16 columns each) and all output
+//     channels of one M group; wave w owns NT tiles of the chunk, so per K32 step its B
+//     fragments are NT aligned 16-byte LDS reads, each used by MB MFMAs. Columns are dealt
+//     out in the weight layout's order, so only the last tile of the last chunk is partial.
+//   * Per box of positions (an "item") the workgroup stages, for each input channel of its
+//     chunk and each halo row (all axes but the last), the 16-byte runs of 8 consecutive
+//     positions that the last-axis taps read, each one 16-byte load (at a 2-byte-aligned
+//     offset) from a zero-padded channels-first copy of the input. A lane's column (channel,
+//     tap) is then a fixed LDS offset and a K32 step (four runs of 8 positions) adds a
+//     per-run offset: no transposes.
+//   * grad_output runs [channel][box positions], from grad_output itself when the boxes tile
+//     it exactly, else from a copy padded to whole boxes; run r of channel row co sits in
+//     slot r ^ (co % 16) so the 16 rows of an A fragment read distinct bank slots.
+//   * Loads go straight to LDS (no registers, no stores): two item buffers in LDS alternate,
+//     the MFMAs of one item running while the next item's loads land in the other buffer.
+//     One workgroup per CU (one wave per SIMD). Each workgroup writes fp32 partial sums of
+//     its range of items; a second pass adds them in a fixed order into the weight layout
+//     (deterministic, no atomics).
+
+#include "convnd_internal.h"
+#include "convnd_stage.h"
+#include "convnd_types.h"
+
+namespace convnd {
+namespace {
+
+// Buffer resource word 3 for raw (unstructured) loads: 32-bit data format, no swizzle.
+constexpr int kCmRsrcWord3 = 0x00020000;
+// Offset past every buffer read (the planner keeps buffers below it): such a load reads zero.
+constexpr unsigned kCmPast = 0xffffffe0u;
+// LDS per item buffer (grad_output tile, then the input runs); two buffers alternate, one
+// read by the MFMAs while the loads of the next item land in the other.
+constexpr int kCmBuf = kWgradCmBuffer;
+// Load instructions per wave whose per-lane source offsets stay in registers.
+constexpr int kXi = 16;
+constexpr int kDi = 8;
+// Of which issued per pair of K steps (four pairs per item).
+constexpr int kXs = 4;
+constexpr int kDs = 2;
+// Positions per item (box volume) and K32 steps per item.
+constexpr int kBoxVol = kWgradCmBoxVol;
+constexpr int kSteps = kBoxVol / 32;
+
+__shared__ __align__(16) unsigned char cm_buf0[kCmBuf];
+__shared__ __align__(16) unsigned char cm_buf1[kCmBuf];
+
+// 16 bytes per lane from the buffer straight into LDS: lane l writes dst + 16 l (dst the
+// same for every lane). Outside a lambda: the builtin's address-space cast inside one
+// leaves the kernel's host stub undefined.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, unsigned char* dst,
+                                           unsigned voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)(dst), 16, voff, 0, 0, 0);
+}
+
+// Waits until every load this wave issued has landed (vmcnt 0; expcnt, lgkmcnt untouched).
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+template <typename T, int MB, int NT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void wgrad_cm_kernel(WgradCmArgs A) {
+  using M = Mfma16<T>;
+  using frag = typename M::frag;
+  extern __shared__ __align__(16) unsigned char lds[];
+  int* const runl = reinterpret_cast<int*>(lds);
+  int* const items = reinterpret_cast<int*>(lds + A.lds_items);
+  const char* tab = static_cast<const char*>(A.tables);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+  const int nl = lane & 15;
+  const int lg = lane >> 4;
+  // Consecutive workgroup ids go round-robin to the eight XCDs; give each XCD a contiguous
+  // run of logical ids, ordered (position chunk, group, column chunk) with the column chunk
+  // fastest, so the workgroups that stage the same grad_output tiles share one L2.
+  int wid = blockIdx.x;
+  {
+    const int nb = gridDim.x;
+    if (nb >= 8) {
+      const int q = nb >> 3, rem = nb & 7, x = wid & 7, idx = wid >> 3;
+      wid = x * q + (x < rem ? x : rem) + idx;
+    }
+  }
+  const int ntiles = A.groups * A.mgroups * A.ncq;
+  const int tile = wid % ntiles;
+  const int pc = wid / ntiles;
+  const int cq = tile % A.ncq;
+  const int zq = tile / A.ncq;
+  const int g = zq / A.mgroups;
+  const int mg = zq % A.mgroups;
+  const int co0 = mg * MB * 16;
+  const int it0 = pc * A.items_per_pc;
+  const int nitems = (it0 + A.items_per_pc < A.items ? it0 + A.items_per_pc : A.items) - it0;
+  const int2 chunk = reinterpret_cast<const int2*>(tab + A.tab_chunk)[cq];
+
+  // This lane's column offsets (LDS bytes within the input runs), the box's run offsets and
+  // the workgroup's item records (LDS).
+  int colb[NT];
+  {
+    const int* ct = reinterpret_cast<const int*>(tab + A.tab_col) + ((size_t)(cq * 4 + wave) * NT) * 16 + nl;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) colb[j] = ct[j * 16] + A.dyt_bytes;
+    const int* rt = reinterpret_cast<const int*>(tab + A.tab_run);
+    for (int q = tid; q < kBoxVol / 8; q += kThreads) runl[q] = rt[q];
+    const int* gi = reinterpret_cast<const int*>(tab + A.tab_item) + (size_t)it0 * 2;
+    for (int q = tid; q < nitems * 2; q += kThreads) items[q] = gi[q];
+  }
+  // Load instructions of this wave: m = wave + 4 i. Input runs: slot m*64 + lane of the
+  // chunk's runs; grad_output: slot m*64 + lane of the tile (rows past the group's output
+  // channels read zero).
+  const int* xs = reinterpret_cast<const int*>(tab + A.tab_xsrc) + (size_t)cq * A.xi * 64;
+  const int* ds = reinterpret_cast<const int*>(tab + A.tab_dsrc);
+  const int nruns = kBoxVol / 8;
+  const int co_valid = A.cout_g - co0;
+  int xoff[kXi], doff[kDi];
+#pragma unroll
+  for (int i = 0; i < kXi; ++i) {
+    const int m = wave + 4 * i;
+    xoff[i] = m < A.xi ? xs[m * 64 + lane] : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kDi; ++i) {
+    const int m = wave + 4 * i;
+    const int sl = m * 64 + lane;
+    doff[i] = m < A.di && sl / nruns < co_valid ? ds[sl] : -1;
+  }
+  const int xwave = (A.xi - wave + 3) / 4;  // this wave's input-run instructions
+  const int dwave = (A.di - wave + 3) / 4;
+
+  const T* x = static_cast<const T*>(A.x);
+  const T* dy = static_cast<const T*>(A.dy);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(x), static_cast<short>(0), static_cast<int>(A.x_bytes), kCmRsrcWord3);
+  const __amdgpu_buffer_rsrc_t dr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(dy), static_cast<short>(0), static_cast<int>(A.dy_bytes), kCmRsrcWord3);
+  const int x_chan = (g * A.cin_g + chunk.x) * A.pvol;
+  const int dy_chan = (g * A.cout_g + co0) * A.dvol;
+
+  // Loads of item k into buf, issued a few at a time between the MFMA steps of the current
+  // item (past the last item: loads that read zero). Per K-step pair, up to kXs input-run
+  // and kDs grad_output instructions of this wave (m = wave + 4 i, in order); the per-lane
+  // offsets of the next ones rotate into fixed registers so the loop stays rolled.
+  struct Bases {
+    int xb, db;
+    bool live;
+  };
+  auto bases = [&](int k) {
+    Bases b;
+    b.live = k < nitems;
+    b.xb = b.live ? items[2 * k] + x_chan : 0;
+    b.db = b.live ? items[2 * k + 1] + dy_chan : 0;
+    return b;
+  };
+
+  f32x4 acc[MB][NT];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int rowb = kBoxVol * 2;
+  // The MFMAs of one item from buf, with the loads of item kn into nbuf interleaved. A
+  // fragments: 8 positions of one grad_output row (run r of row co sits in slot r ^ (co %
+  // 16), so the 16 rows of a fragment read distinct bank slots); B fragments: 8 positions of
+  // the lane's column. The fragments of the next step are read during the current step's
+  // MFMAs.
+  auto compute = [&](const unsigned char* buf, unsigned char* nbuf, int kn) {
+    const Bases nb = bases(kn);
+    int xq[kXi], dq[kDi];
+#pragma unroll
+    for (int i = 0; i < kXi; ++i) xq[i] = xoff[i];
+#pragma unroll
+    for (int i = 0; i < kDi; ++i) dq[i] = doff[i];
+    int xm = wave, dm = wave, xleft = xwave, dleft = dwave;
+    auto read_ab = [&](int kc, frag* a, frag* b) {
+      const int r = kc * 4 + lg;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        a[mb] = *reinterpret_cast<const frag*>(buf + (mb * 16 + nl) * rowb + ((r ^ nl) << 4));
+      const int rb = runl[r];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) b[j] = *reinterpret_cast<const frag*>(buf + colb[j] + rb);
+    };
+    auto mfmas = [&](const frag* a, const frag* b) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb][j] = M::run(a[mb], b[j], acc[mb][j]);
+    };
+    frag a0[MB], a1[MB], b0[NT], b1[NT];
+    read_ab(0, a0, b0);
+    for (int kc = 0; kc < kSteps; kc += 2) {
+#pragma unroll
+      for (int u = 0; u < kXs; ++u) {
+        if (u < xleft) {
+          const unsigned o = xq[u] >= 0 && nb.live ? static_cast<unsigned>(nb.xb + xq[u]) * 2u : kCmPast;
+          load_lds16(xr, nbuf + A.dyt_bytes + (xm + 4 * u) * 1024, o);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kDs; ++u) {
+        if (u < dleft) {
+          const unsigned o = dq[u] >= 0 && nb.live ? static_cast<unsigned>(nb.db + dq[u]) * 2u : kCmPast;
+          load_lds16(dr, nbuf + (dm + 4 * u) * 1024, o);
+        }
+      }
+      xm += 4 * kXs;
+      dm += 4 * kDs;
+      xleft -= kXs;
+      dleft -= kDs;
+#pragma unroll
+      for (int i = 0; i + kXs < kXi; ++i) xq[i] = xq[i + kXs];
+#pragma unroll
+      for (int i = 0; i + kDs < kDi; ++i) dq[i] = dq[i + kDs];
+      read_ab(kc + 1, a1, b1);
+      mfmas(a0, b0);
+      read_ab(kc + 2 < kSteps ? kc + 2 : kSteps - 1, a0, b0);
+      mfmas(a1, b1);
+    }
+  };
+
+  __syncthreads();  // run table and item records in LDS
+  {
+    const Bases b0 = bases(0);
+#pragma unroll
+    for (int i = 0; i < kXi; ++i) {
+      if (i < xwave) {
+        const unsigned o = xoff[i] >= 0 && b0.live ? static_cast<unsigned>(b0.xb + xoff[i]) * 2u : kCmPast;
+        load_lds16(xr, cm_buf0 + A.dyt_bytes + (wave + 4 * i) * 1024, o);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kDi; ++i) {
+      if (i < dwave) {
+        const unsigned o = doff[i] >= 0 && b0.live ? static_cast<unsigned>(b0.db + doff[i]) * 2u : kCmPast;
+        load_lds16(dr, cm_buf0 + (wave + 4 * i) * 1024, o);
+      }
+    }
+  }
+  wait_loads();
+  __syncthreads();
+  // Items in pairs: even ones from buffer 0, odd ones from buffer 1; the next item's loads
+  // are waited for (by every wave, then a barrier) after the MFMAs.
+  for (int k = 0; k < nitems; k += 2) {
+    compute(cm_buf0, cm_buf1, k + 1);
+    wait_loads();
+    __syncthreads();
+    if (k + 1 >= nitems) break;
+    compute(cm_buf1, cm_buf0, k + 2);
+    wait_loads();
+    __syncthreads();
+  }
+
+  // Partial sums as each lane's accumulators: [pc][tile][wave][mb][j][lane] x 4 floats.
+  f32x4* part = reinterpret_cast<f32x4*>(A.partial) +
+                ((((size_t)pc * ntiles + tile) * 4 + wave) * MB * NT) * 64 + lane;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) part[(mb * NT + j) * 64] = acc[mb][j];
+}
+
+// dW from the partial sums: slot s = ((((tile*4 + wave)*MB + mb)*NT + j)*64 + lane) holds
+// four output channels of one column; the npc partials are added in order, eight loads in
+// flight. Blocks past the reduction's: the bias gradient from the staging pass's sums.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void wgrad_cm_reduce_kernel(const f32x4* part, T* dw,
+                                                                   WgradCmArgs A, int mbv,
+                                                                   int64_t nslots, int rblocks,
+                                                                   stage::BiasSums bs) {
+  if (static_cast<int>(blockIdx.x) >= rblocks) {
+    stage::bias_from_sums<T>(bs, blockIdx.x - rblocks);
+    return;
+  }
+  const int64_t s = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  if (s >= nslots) return;
+  const int lane = static_cast<int>(s & 63);
+  int64_t r = s >> 6;
+  const int j = static_cast<int>(r % A.nt);
+  r /= A.nt;
+  const int mb = static_cast<int>(r % mbv);
+  r /= mbv;
+  const int wave = static_cast<int>(r % 4);
+  const int tile = static_cast<int>(r / 4);
+  const int cq = tile % A.ncq;
+  const int zq = tile / A.ncq;
+  const int g = zq / A.mgroups;
+  const int mg = zq % A.mgroups;
+  const int col = reinterpret_cast<const int*>(static_cast<const char*>(A.tables) +
+                                               A.tab_cid)[((cq * 4 + wave) * A.nt + j) * 16 + (lane & 15)];
+  if (col < 0) return;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int i = 0;
+  for (; i + 8 <= A.npc; i += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = part[(int64_t)(i + k) * nslots + s];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc += v[k];
+  }
+  for (; i < A.npc; ++i) acc += part[(int64_t)i * nslots + s];
+  const int co_base = mg * mbv * 16 + mb * 16 + 4 * (lane >> 4);
+  const int64_t per_co = (int64_t)A.cin_g * A.k_vol;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int co = co_base + k;
+    if (co < A.cout_g) dw[((int64_t)g * A.cout_g + co) * per_co + col] = static_cast<T>(acc[k]);
+  }
+}
+
+// The compiled (MB, NT) pairs: accumulators MB * NT * 4 registers (at most 128).
+#define CONVND_WGRAD_CM_TILES(X) \
+  X(4, 4) X(4, 5) X(4, 6) X(4, 7) X(4, 8) X(2, 4) X(2, 6) X(2, 8) X(1, 4) X(1, 8)
+
+template <typename T>
+hipError_t wgrad_cm_dispatch(int mb, const WgradCmArgs& a, size_t lds, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.npc * a.ncq * a.groups * a.mgroups));
+#define CONVND_WGRAD_CM_CASE(MBV, NTV)                                               \
+  if (mb == MBV && a.nt == NTV) {                                                    \
+    auto fn = wgrad_cm_kernel<T, MBV, NTV>;                                          \
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),          \
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                         static_cast<int>(lds));                     \
+    if (err != hipSuccess) return err;                                               \
+    hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                         \
+    return hipGetLastError();                                                        \
+  }
+  CONVND_WGRAD_CM_TILES(CONVND_WGRAD_CM_CASE)
+#undef CONVND_WGRAD_CM_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool wgrad_cm_supported(int mb, int nt) {
+#define CONVND_WGRAD_CM_HAS(MBV, NTV) \
+  if (mb == MBV && nt == NTV) return true;
+  CONVND_WGRAD_CM_TILES(CONVND_WGRAD_CM_HAS)
+#undef CONVND_WGRAD_CM_HAS
+  return false;
+}
+
+hipError_t launch_wgrad_cm(convnd_hip_dtype dtype, int mb, const WgradCmArgs& a,
+                           size_t lds_bytes, hipStream_t stream) {
+  if (a.items == 0) return hipSuccess;
+  if (dtype == CONVND_HIP_BFLOAT16) return wgrad_cm_dispatch<__bf16>(mb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_FLOAT16) return wgrad_cm_dispatch<_Float16>(mb, a, lds_bytes, stream);
+  return hipErrorInvalidValue;
+}
+
+int64_t wgrad_cm_partial_slots(int mb, const WgradCmArgs& a) {
+  return (int64_t)a.groups * a.mgroups * a.ncq * 4 * mb * a.nt * 64;
+}
+
+hipError_t launch_wgrad_cm_reduce(convnd_hip_dtype dtype, int mb, const WgradCmArgs& a,
+                                  void* dw, hipStream_t stream, const float* bias_sums,
+                                  int64_t nsum, int64_t channels, void* db) {
+  const int64_t nslots = wgrad_cm_partial_slots(mb, a);
+  const int64_t rblocks = (nslots + kThreads - 1) / kThreads;
+  stage::BiasSums bs{bias_sums, db, static_cast<int>(nsum), static_cast<int>(channels)};
+  const int64_t bblocks = bias_sums != nullptr ? channels : 0;
+  if (bias_sums != nullptr && nsum > INT32_MAX) return hipErrorInvalidValue;
+  if (rblocks + bblocks == 0) return hipSuccess;
+  if (rblocks + bblocks > INT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(rblocks + bblocks));
+  const int rb = static_cast<int>(rblocks);
+  const f32x4* part = reinterpret_cast<const f32x4*>(a.partial);
+  if (dtype == CONVND_HIP_BFLOAT16) {
+    hipLaunchKernelGGL(wgrad_cm_reduce_kernel<__bf16>, grid, dim3(kThreads), 0, stream, part,
+                       static_cast<__bf16*>(dw), a, mb, nslots, rb, bs);
+  } else if (dtype == CONVND_HIP_FLOAT16) {
+    hipLaunchKernelGGL(wgrad_cm_reduce_kernel<_Float16>, grid, dim3(kThreads), 0, stream, part,
+                       static_cast<_Float16*>(dw), a, mb, nslots, rb, bs);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace convnd
