@@ -41,9 +41,9 @@ constexpr int kCmBuf = kWgradCmBuffer;
 // Load instructions per wave whose per-lane source offsets stay in registers.
 constexpr int kXi = 16;
 constexpr int kDi = 8;
-// Of which issued per pair of K steps (four pairs per item).
-constexpr int kXs = 4;
-constexpr int kDs = 2;
+// Of which issued per K step (eight steps per item).
+constexpr int kXs = 2;
+constexpr int kDs = 1;
 // Positions per item (box volume) and K32 steps per item.
 constexpr int kBoxVol = kWgradCmBoxVol;
 constexpr int kSteps = kBoxVol / 32;
@@ -144,9 +144,9 @@ void wgrad_cm_kernel(WgradCmArgs A) {
   const int dy_chan = (g * A.cout_g + co0) * A.dvol;
 
   // Loads of item k into buf, issued a few at a time between the MFMA steps of the current
-  // item (past the last item: loads that read zero). Per K-step pair, up to kXs input-run
-  // and kDs grad_output instructions of this wave (m = wave + 4 i, in order); the per-lane
-  // offsets of the next ones rotate into fixed registers so the loop stays rolled.
+  // item (past the last item: loads that read zero): per K step up to kXs input-run and kDs
+  // grad_output instructions of this wave (m = wave + 4 i, in order); the per-lane offsets
+  // of the next ones rotate into fixed registers so the loop stays rolled.
   struct Bases {
     int xb, db;
     bool live;
@@ -196,7 +196,9 @@ void wgrad_cm_kernel(WgradCmArgs A) {
     };
     frag a0[MB], a1[MB], b0[NT], b1[NT];
     read_ab(0, a0, b0);
-    for (int kc = 0; kc < kSteps; kc += 2) {
+    // Per K step: up to kXs input-run and kDs grad_output load instructions, then the
+    // offsets of the next ones rotate into the fixed registers.
+    auto issue = [&]() {
 #pragma unroll
       for (int u = 0; u < kXs; ++u) {
         if (u < xleft) {
@@ -219,8 +221,12 @@ void wgrad_cm_kernel(WgradCmArgs A) {
       for (int i = 0; i + kXs < kXi; ++i) xq[i] = xq[i + kXs];
 #pragma unroll
       for (int i = 0; i + kDs < kDi; ++i) dq[i] = dq[i + kDs];
+    };
+    for (int kc = 0; kc < kSteps; kc += 2) {
+      issue();
       read_ab(kc + 1, a1, b1);
       mfmas(a0, b0);
+      issue();
       read_ab(kc + 2 < kSteps ? kc + 2 : kSteps - 1, a0, b0);
       mfmas(a1, b1);
     }
