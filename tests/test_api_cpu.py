@@ -194,12 +194,11 @@ def test_portable_workspace_contract():
     conv_nd(x, w, backend="torch", workspace_bytes=8 * 4 * 32)
 
 
-def test_native_backend_refuses_cpu_tensors():
+def test_native_backend_runs_on_cpu_tensors():
     torch_convnd.load_native()
-    x = torch.randn(1, 2, 3, 3, 3, 3)
-    w = torch.randn(2, 2, 2, 2, 2, 2)
-    with pytest.raises(RuntimeError, match="run on ROCm GPUs"):
-        conv_nd(x, w, backend="native")
+    x = torch.randn(1, 2, 3, 3, 3, 3, dtype=torch.float64)
+    w = torch.randn(2, 2, 2, 2, 2, 2, dtype=torch.float64)
+    torch.testing.assert_close(conv_nd(x, w, backend="native"), conv_nd(x, w, backend="torch"))
     # Validation still comes first, with the reference's wording.
     with pytest.raises(RuntimeError, match="workspace_bytes is too small"):
         torch.ops.torch_convnd.conv_nd(x, w, None, [1] * 4, [0] * 4, [1] * 4, 1, 16)

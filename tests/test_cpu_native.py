@@ -1,0 +1,136 @@
+"""Native operators on CPU tensors (the tap-major CPU kernels) against the float64 oracle.
+
+The reference registers CPU kernels for both operators and routes ``backend="native"`` and
+``auto`` at rank 5+ on CPU to them (src/torch_convnd/_dispatch.py:97-103,
+src/torch_convnd/csrc/convnd.cpp:435-443); its CPU tests cover ranks 4-6 with stride,
+padding, dilation, groups and bias (tests/test_convnd.py). Same here, at sizes the oracle
+finishes in well under a second.
+"""
+
+import pytest
+import torch
+
+import helpers
+import torch_convnd
+from torch_convnd import conv_nd
+
+# name: x shape, w shape, stride, padding, dilation, groups, bias
+CASES = {
+    "r4_basic": ((2, 3, 5, 4, 6, 5), (4, 3, 3, 2, 3, 2), (1,) * 4, (1, 0, 1, 1), (1,) * 4, 1, True),
+    "r4_strided_dilated": ((1, 4, 7, 6, 5, 8), (6, 2, 2, 3, 2, 3), (2, 1, 2, 3), (1, 2, 0, 1), (2, 1, 1, 2), 2, True),
+    "r5_groups": ((2, 6, 4, 3, 4, 3, 5), (9, 2, 2, 2, 1, 2, 3), (1, 2, 1, 1, 2), (0, 1, 1, 0, 1), (1, 1, 2, 1, 1), 3, False),
+    "r6_depthwise": ((1, 3, 3, 3, 2, 3, 2, 4), (3, 1, 2, 1, 2, 2, 1, 3), (1,) * 6, (1, 0, 1, 1, 0, 1), (1,) * 6, 3, True),
+    "r4_pointwise": ((3, 5, 2, 3, 4, 3), (7, 5, 1, 1, 1, 1), (1,) * 4, (0,) * 4, (1,) * 4, 1, True),
+    "r4_kernel_covers_all": ((1, 2, 3, 2, 3, 2), (3, 2, 3, 2, 3, 2), (1,) * 4, (0,) * 4, (1,) * 4, 1, False),
+}
+DTYPES = [torch.float64, torch.float32, torch.bfloat16, torch.float16]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def native():
+    torch_convnd.load_native()
+
+
+def _op_forward(x, w, b, stride, padding, dilation, groups):
+    return torch.ops.torch_convnd.conv_nd(x, w, b, list(stride), list(padding), list(dilation), groups, 1 << 30)
+
+
+def _op_backward(dy, x, w, stride, padding, dilation, groups, mask):
+    return torch.ops.torch_convnd.conv_nd_backward(
+        dy, x, w, list(stride), list(padding), list(dilation), groups, 1 << 30, mask
+    )
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[1])
+@pytest.mark.parametrize("name", list(CASES))
+def test_forward_backward_match_oracle(name, dtype):
+    xs, ws, stride, padding, dilation, groups, bias = CASES[name]
+    x, w, b = helpers.seeded_problem(xs, ws, bias, dtype, seed=len(name))
+    y = _op_forward(x, w, b, stride, padding, dilation, groups)
+    assert y.dtype == dtype and y.is_contiguous()
+    helpers.assert_close(y, helpers.oracle_forward(x, w, b, stride, padding, dilation, groups), dtype, f"{name} y")
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(5)).to(dtype)
+    dx, dw, db = _op_backward(dy, x, w, stride, padding, dilation, groups, [True, True, True])
+    rx, rw, rb = helpers.oracle_backward(dy, x, w, stride, padding, dilation, groups)
+    for what, a, e in (("dx", dx, rx), ("dw", dw, rw), ("db", db, rb)):
+        assert a.dtype == dtype
+        helpers.assert_close(a, e, dtype, f"{name} {what}")
+
+
+def test_results_are_bitwise_repeatable():
+    xs, ws, stride, padding, dilation, groups, bias = CASES["r5_groups"]
+    x, w, b = helpers.seeded_problem(xs, ws, True, torch.float32, seed=2)
+    y1 = _op_forward(x, w, b, stride, padding, dilation, groups)
+    y2 = _op_forward(x, w, b, stride, padding, dilation, groups)
+    assert torch.equal(y1, y2)
+    dy = torch.randn_like(y1)
+    g1 = _op_backward(dy, x, w, stride, padding, dilation, groups, [True, True, True])
+    g2 = _op_backward(dy, x, w, stride, padding, dilation, groups, [True, True, True])
+    assert all(torch.equal(a, c) for a, c in zip(g1, g2))
+
+
+@pytest.mark.parametrize("mask", [[True, False, False], [False, True, False], [False, False, True], [False, True, True]])
+def test_backward_output_mask(mask):
+    xs, ws, stride, padding, dilation, groups, _ = CASES["r4_strided_dilated"]
+    x, w, _ = helpers.seeded_problem(xs, ws, False, torch.float64, seed=7)
+    y = _op_forward(x, w, None, stride, padding, dilation, groups)
+    dy = torch.randn_like(y)
+    got = _op_backward(dy, x, w, stride, padding, dilation, groups, mask)
+    want = helpers.oracle_backward(dy, x, w, stride, padding, dilation, groups)
+    for wanted, g, e in zip(mask, got, want):
+        if wanted:
+            helpers.assert_close(g, e, torch.float64)
+        else:
+            assert g is None
+
+
+def test_empty_batch_gives_zero_gradients():
+    x = torch.randn(0, 2, 3, 3, 3, 3, dtype=torch.float64)
+    w = torch.randn(4, 2, 2, 2, 2, 2, dtype=torch.float64)
+    y = _op_forward(x, w, None, (1,) * 4, (1,) * 4, (1,) * 4, 1)
+    assert y.shape == (0, 4, 4, 4, 4, 4)
+    dx, dw, db = _op_backward(torch.zeros_like(y), x, w, (1,) * 4, (1,) * 4, (1,) * 4, 1, [True] * 3)
+    assert dx.shape == x.shape and not dw.any() and not db.any() and db.shape == (4,)
+
+
+def test_native_backend_autograd_and_module():
+    # Through the public API: autograd over the CPU kernels, float64 gradcheck.
+    x = torch.randn(1, 2, 3, 2, 3, 2, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(2, 2, 2, 1, 2, 2, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(2, dtype=torch.float64, requires_grad=True)
+    f = lambda x, w, b: conv_nd(x, w, b, padding=(1, 0, 1, 0), backend="native")
+    assert torch.autograd.gradcheck(f, (x, w, b))
+    assert torch.autograd.gradgradcheck(f, (x, w, b))
+
+
+def test_auto_policy_on_cpu_matches_native_and_portable():
+    # auto: rank 4 -> portable slices, rank 5 -> native kernels; all agree with the oracle.
+    for xs, ws in (((1, 2, 4, 3, 4, 3), (3, 2, 2, 2, 2, 2)), ((1, 2, 3, 3, 2, 3, 2), (3, 2, 2, 1, 2, 2, 1))):
+        rank = len(xs) - 2
+        x, w, b = helpers.seeded_problem(xs, ws, True, torch.float32, seed=rank)
+        p = (1,) * rank
+        want = helpers.oracle_forward(x, w, b, (1,) * rank, p, (1,) * rank, 1)
+        for backend in ("auto", "native", "torch"):
+            helpers.assert_close(conv_nd(x, w, b, padding=p, backend=backend), want, torch.float32, backend)
+
+
+def test_autocast_cpu_runs_in_bfloat16():
+    x = torch.randn(1, 2, 3, 3, 2, 3, 2)
+    w = torch.randn(3, 2, 2, 1, 2, 2, 1)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        y = conv_nd(x, w, backend="native")
+    assert y.dtype == torch.bfloat16
+    want = helpers.oracle_forward(x.bfloat16(), w.bfloat16(), None, (1,) * 5, (0,) * 5, (1,) * 5, 1)
+    helpers.assert_close(y, want, torch.bfloat16)
+
+
+def test_validation_messages():
+    x = torch.randn(1, 2, 3, 3, 3, 3)
+    w = torch.randn(2, 2, 2, 2, 2, 2)
+    with pytest.raises(RuntimeError, match="workspace_bytes is too small"):
+        torch.ops.torch_convnd.conv_nd(x, w, None, [1] * 4, [0] * 4, [1] * 4, 1, 16)
+    y = _op_forward(x, w, None, (1,) * 4, (0,) * 4, (1,) * 4, 1)
+    with pytest.raises(RuntimeError, match="grad_output must match"):
+        _op_backward(y[:, :1], x, w, (1,) * 4, (0,) * 4, (1,) * 4, 1, [True] * 3)
+    with pytest.raises(RuntimeError, match="bias must match"):
+        _op_forward(x, w, torch.randn(3), (1,) * 4, (0,) * 4, (1,) * 4, 1)

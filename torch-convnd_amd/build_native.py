@@ -121,6 +121,8 @@ def build_ops_library(verbose: bool = False) -> Path:
         f"-I{rocm_home() / 'include'}",
         f"-I{INCLUDE}",
         str(CSRC / "torch_ops.cpp"),
+        str(CSRC / "convnd_cpu.cpp"),
+        "-fopenmp",
         "-o",
         str(temporary),
         f"-L{LIB_DIR}",

@@ -19,6 +19,7 @@
 #include <tuple>
 #include <vector>
 
+#include "convnd_cpu.h"
 #include "convnd_hip.h"
 
 namespace torch_convnd_hip {
@@ -181,8 +182,9 @@ Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& i
   return {grad_input, grad_weight, grad_bias};
 }
 
-// CPU tensors reach the native op only with backend="native": validate like the reference,
-// then refuse — this build's native kernels are the gfx950 ones.
+// CPU tensors: the same validation as the device path, then the tap-major CPU kernels
+// (convnd_cpu.cpp), as the reference registers its CPU implementation beside the CUDA one
+// (src/torch_convnd/csrc/convnd.cpp:179-415).
 at::Tensor conv_nd_cpu(const at::Tensor& input, const at::Tensor& weight,
                        const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
                        at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
@@ -195,10 +197,10 @@ at::Tensor conv_nd_cpu(const at::Tensor& input, const at::Tensor& weight,
                     bias->scalar_type() == input.scalar_type(),
                 "bias must match output channels, device and dtype");
   }
+  const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
-  TORCH_CHECK(false,
-              "native torch_convnd kernels in this build run on ROCm GPUs (gfx950); "
-              "use backend='torch' or backend='auto' for CPU tensors");
+  return torch_convnd_cpu::forward(input, weight, bias, shape, stride, padding, dilation,
+                                   groups);
 }
 
 Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& input,
@@ -206,27 +208,31 @@ Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& inpu
                            at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                            int64_t workspace_bytes, std::array<bool, 3> output_mask) {
   const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
-  (void)grad_output;
-  (void)output_mask;
+  const auto shape = output_shape(problem, input);
+  TORCH_CHECK(grad_output.sizes().vec() == shape && grad_output.device() == input.device() &&
+                  grad_output.scalar_type() == input.scalar_type() &&
+                  grad_output.layout() == at::kStrided,
+              "grad_output must match the convolution output shape, device and dtype");
   check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
-  TORCH_CHECK(false,
-              "native torch_convnd kernels in this build run on ROCm GPUs (gfx950); "
-              "use backend='torch' or backend='auto' for CPU tensors");
+  return torch_convnd_cpu::backward(grad_output, input, weight, stride, padding, dilation,
+                                    groups, output_mask);
 }
 
 // Autocast: cast the operands once to the autocast dtype and redispatch below autocast,
-// as the reference's autocast_conv_nd does (src/torch_convnd/csrc/convnd.cpp:417-431).
+// as the reference's autocast_conv_nd does (src/torch_convnd/csrc/convnd.cpp:417-431), for
+// the GPU (AutocastCUDA) and CPU (AutocastCPU) keys.
+template <c10::DeviceType kDevice, c10::DispatchKey kKey>
 at::Tensor conv_nd_autocast(const at::Tensor& input, const at::Tensor& weight,
                             const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
                             at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                             int64_t workspace_bytes) {
-  const c10::impl::ExcludeDispatchKeyGuard no_autocast(c10::DispatchKey::AutocastCUDA);
-  const auto dtype = at::autocast::get_autocast_dtype(at::kCUDA);
+  const c10::impl::ExcludeDispatchKeyGuard no_autocast(kKey);
+  const auto dtype = at::autocast::get_autocast_dtype(kDevice);
   static const auto op = c10::Dispatcher::singleton()
                              .findSchemaOrThrow("torch_convnd::conv_nd", "")
                              .typed<decltype(conv_nd_device)>();
   const auto cast = [&](const at::Tensor& t) {
-    return at::autocast::cached_cast(dtype, t, c10::DeviceType::CUDA);
+    return at::autocast::cached_cast(dtype, t, kDevice);
   };
   std::optional<at::Tensor> b;
   if (bias.has_value()) b = cast(*bias);
@@ -243,10 +249,16 @@ TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {
-  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autocast);
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autocast<c10::DeviceType::CUDA,
+                                                              c10::DispatchKey::AutocastCUDA>);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, CPU, library) {
   library.impl("conv_nd", &torch_convnd_hip::conv_nd_cpu);
   library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_cpu);
+}
+
+TORCH_LIBRARY_IMPL(torch_convnd, AutocastCPU, library) {
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autocast<c10::DeviceType::CPU,
+                                                              c10::DispatchKey::AutocastCPU>);
 }

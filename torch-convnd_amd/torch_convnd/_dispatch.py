@@ -3,8 +3,10 @@
 Reference counterpart: src/torch_convnd/_dispatch.py:24-181. Differences, on purpose:
 * the native device is a ROCm GPU (the reference refuses ROCm at :96-98 and :112-113);
 * ``backend="auto"`` on a ROCm GPU never falls back silently: if the gfx950 libraries
-  cannot be loaded it raises, naming the reason;
-* CPU tensors with ``auto`` use the portable path (this build has no native CPU kernels).
+  cannot be loaded it raises, naming the reason.
+CPU tensors follow the reference's measured policy (:97-103): ``auto`` sends rank 4 to the
+portable path (vendor conv3d slices) and ranks 5+ to the native CPU kernels when the
+libraries load, else to the portable path.
 """
 
 import threading
@@ -56,26 +58,31 @@ def real_conv(input, weight, bias, stride, padding, dilation, groups, workspace_
     """Dispatch one real-valued convolution.
 
     Ranks 1-3 use PyTorch's own convolutions unless ``native`` is forced. A ROCm GPU tensor
-    reaches the gfx950 kernels with ``native`` or ``auto``; transforms (vmap, forward AD),
-    ``torch`` and meta tensors use the portable differentiable path.
+    reaches the gfx950 kernels with ``native`` or ``auto``; a CPU tensor reaches the native
+    CPU kernels with ``native``, or with ``auto`` at rank 5 and above; transforms (vmap,
+    forward AD), ``torch`` and meta tensors use the portable differentiable path.
     """
     rank = weight.ndim - 2
     if backend != "native" and rank <= 3:
         return (F.conv1d, F.conv2d, F.conv3d)[rank - 1](input, weight, bias, stride, padding, dilation, groups)
-    native_device = is_rocm_device(input.device)
+    native_device = input.device.type == "cpu" or is_rocm_device(input.device)
+    prefer_vendor_4d = backend == "auto" and rank == 4 and input.device.type == "cpu"
     if (
         _transforms_active()
         or backend == "torch"
+        or prefer_vendor_4d
         or input.device.type == "meta"
         or (backend == "auto" and not native_device)
     ):
         return _portable_conv(input, weight, bias, stride, padding, dilation, groups, workspace_bytes)
-    if not native_device and input.device.type != "cpu":
-        raise RuntimeError("The native backend runs on ROCm GPUs; use backend='torch'")
+    if not native_device:
+        raise RuntimeError("The native backend runs on CPU and ROCm GPUs; use backend='torch'")
     if not _build._LOADED and not is_compiling():
-        reason = native_unavailable_reason(input.device.type) if native_device else None
+        reason = native_unavailable_reason(input.device.type)
         if reason is not None:
-            raise RuntimeError(f"Cannot load the gfx950 torch_convnd kernels: {reason}")
+            if input.device.type == "cpu" and backend == "auto":
+                return _portable_conv(input, weight, bias, stride, padding, dilation, groups, workspace_bytes)
+            raise RuntimeError(f"Cannot load the native torch_convnd kernels: {reason}")
         _build.load_native()
     return torch.ops.torch_convnd.conv_nd.default(
         input, weight, bias, stride, padding, dilation, groups, workspace_bytes

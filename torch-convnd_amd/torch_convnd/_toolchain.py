@@ -35,8 +35,8 @@ def native_unavailable_reason(device_type: str) -> str | None:
     """A missing prerequisite for native kernels on ``device_type``, or None."""
     if not HAS_NATIVE_AUTOGRAD:
         return "This PyTorch lacks the native custom-op/autocast APIs; use backend='torch'."
-    if device_type != "cuda":
-        return "Native kernels in this build run on ROCm GPUs; use backend='torch' or 'auto'."
+    if device_type not in {"cpu", "cuda"}:
+        return "Native kernels run on CPU and ROCm GPUs; use backend='torch' or 'auto'."
     if torch.version.hip is None:
         return "Native kernels require a ROCm (HIP) build of PyTorch."
     if prebuilt():
