@@ -196,6 +196,77 @@ def measure_peaks(torch, device):
     return res
 
 
+def _timed_ms(torch, fn, steps, warmup):
+    """Mean milliseconds of fn() over `steps` calls (HIP events on torch's current stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def measure_partial(torch, device, steps, warmup):
+    """Partial convolution on C2 (bf16, bias, single-channel mask with 30 % holes)."""
+    import torch_convnd
+
+    x, w, b = make_inputs(torch, torch.bfloat16, device)
+    g = torch.Generator().manual_seed(9)
+    mask = (torch.rand((X_SHAPE[0], 1, *X_SHAPE[2:]), generator=g) > 0.3).to(torch.bfloat16).to(device)
+
+    def partial():
+        return torch_convnd.partial_conv_nd(x, w, b, STRIDE, "same", DILATION, GROUPS, mask=mask, backend="native")
+
+    out, update = partial()
+    out_shape = tuple(out.shape)
+    n, co = out_shape[:2]
+    positions = math.prod(out_shape[2:])
+    # The rescale alone, on resident raw output and counts of the same shapes.
+    raw = torch.randn(out_shape, generator=g).to(torch.bfloat16).to(device)
+    counts = torch.randint(0, 82, (n, 1, *out_shape[2:]), generator=g).float().to(device)
+    window = float(math.prod(W_SHAPE[2:]))
+    op = torch.ops.torch_convnd.partial_rescale.default
+    fused_ms = _timed_ms(torch, lambda: op(raw, counts, b, window), steps, warmup)
+
+    def unfused():
+        # The same rescale as separate PyTorch elementwise launches (the reference's form).
+        upd = counts.clamp(0, 1)
+        ratio = (upd * window / counts.clamp_min(torch.finfo(torch.float32).tiny)).to(raw.dtype)
+        return torch.addcmul(b.reshape(1, -1, 1, 1, 1, 1), raw, ratio) * upd.to(raw.dtype)
+
+    unfused_ms = _timed_ms(torch, unfused, steps, warmup)
+    fwd_ms = _timed_ms(torch, partial, steps, warmup)
+    xs, ws, bs = (t.detach().requires_grad_() for t in (x, w, b))
+    cot = torch.randn(out_shape, generator=g).to(torch.bfloat16).to(device)
+
+    def step():
+        y, _ = torch_convnd.partial_conv_nd(xs, ws, bs, STRIDE, "same", DILATION, GROUPS, mask=mask, backend="native")
+        torch.autograd.grad(y, (xs, ws, bs), cot)
+
+    step_ms = _timed_ms(torch, step, steps, warmup)
+    # Algorithmic HBM bytes of one rescale launch: read raw, write out (2 B each per
+    # element), read the counts once (4 B per count position), read the bias.
+    rescale_bytes = 2 * 2 * n * co * positions + 4 * n * positions + 2 * co
+    achieved = rescale_bytes / (fused_ms * 1e-3) / 1e9
+    return {
+        "metric": "partial convolution on C2 (bf16, bias, 30% hole mask)",
+        "config": {"workload": "C2 partial_conv_nd x[2,32,16,16,16,16] w[64,32,3,3,3,3] same padding",
+                   "mask": "[2,1,16,16,16,16], 30% holes"},
+        "steps": steps, "warmup": warmup,
+        "rescale_fused_us": round(fused_ms * 1e3, 2),
+        "rescale_unfused_torch_us": round(unfused_ms * 1e3, 2),
+        "partial_fwd_us": round(fwd_ms * 1e3, 2),
+        "partial_fwd_bwd_us": round(step_ms * 1e3, 2),
+        "roofline": {"bound": "hbm", "kernel": "partial_rescale_runs", "achieved": round(achieved, 1),
+                     "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
+                     "bytes_per_launch": rescale_bytes},
+    }
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -210,6 +281,11 @@ def main():
         "--peaks", action="store_true",
         help="only measure the on-box achieved peaks (a large bf16 GEMM through torch.matmul, "
         "i.e. hipBLASLt, and a 1 GiB device copy) and print them as one JSON line")
+    parser.add_argument(
+        "--partial", action="store_true",
+        help="measure partial convolution on the C2 shape instead (bf16, bias, a 30%% hole "
+        "mask): the fused gfx950 rescale kernel against its HBM roofline, the same rescale as "
+        "PyTorch elementwise ops, and partial_conv_nd forward and forward+backward")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -233,6 +309,9 @@ def main():
     device = torch.device("cuda", 0)
     if args.peaks:
         print(json.dumps(measure_peaks(torch, device)), flush=True)
+        return
+    if args.partial:
+        print(json.dumps(measure_partial(torch, device, args.steps, args.warmup)), flush=True)
         return
     if args.calibration_copy_mib > 0:
         src = torch.ones(args.calibration_copy_mib << 18, dtype=torch.float32, device=device)

@@ -105,6 +105,24 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                         void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
                         size_t workspace_size, void* stream);
 
+/* Partial convolution's rescale epilogue, one pass over the raw convolution output
+ * (computed without bias). For element (n, c, p), with k = counts[n', c / (channels /
+ * count_channels), p] and n' = n when count_batch == batch, else 0:
+ *   u = clamp(k, 0, 1), r = u * window / max(k, smallest normal)
+ *   out = raw * r                   (bias NULL)
+ *   out = (raw * r + bias[c]) * u   (bias given)
+ * evaluated in the count type and rounded once to `dtype`.
+ * raw, out [batch, channels, positions] of `dtype` (out may equal raw); bias [channels] of
+ * `dtype`; counts [count_batch, count_channels, positions] float32 (float64 when dtype is
+ * CONVND_HIP_FLOAT64), count_batch 1 or batch, count_channels dividing channels.
+ * Replaces the elementwise rescale of partial convolution, _scale and the tail of
+ * _partial_conv_nd (src/torch_convnd/functional.py:312-321,592-616), which the reference
+ * runs as separate PyTorch launches. */
+int convnd_hip_partial_rescale(convnd_hip_dtype dtype, const void* raw, const void* counts,
+                               const void* bias, void* out, int64_t batch, int64_t channels,
+                               int64_t positions, int64_t count_batch, int64_t count_channels,
+                               double window, void* stream);
+
 /* Which kernel family convnd_hip_forward / convnd_hip_backward would use, as a short
  * string ("mfma", "direct", ...) for diagnostics and tests. `which`: 0 forward,
  * 1 input gradient, 2 weight gradient. No reference counterpart (diagnostic only). */

@@ -1659,6 +1659,32 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
   return CONVND_HIP_SUCCESS;
 }
 
+int convnd_hip_partial_rescale(convnd_hip_dtype dtype, const void* raw, const void* counts,
+                               const void* bias, void* out, int64_t batch, int64_t channels,
+                               int64_t positions, int64_t count_batch, int64_t count_channels,
+                               double window, void* stream) {
+  if (element_size(dtype) == 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT,
+                "native conv_nd supports float16, bfloat16, float32 and float64");
+  if (batch < 0 || channels <= 0 || positions < 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "partial rescale sizes must be nonnegative");
+  if (count_channels <= 0 || channels % count_channels != 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "count channels must divide the channels");
+  if (count_batch != 1 && count_batch != batch)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "count batch must be 1 or the batch");
+  if (!(window > 0.0)) return fail(CONVND_HIP_INVALID_ARGUMENT, "window must be positive");
+  int64_t total = 0;
+  if (!mul_ok(batch, channels, &total) || !mul_ok(total, positions, &total))
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "output volume overflows int64");
+  if (total == 0) return CONVND_HIP_SUCCESS;
+  if (raw == nullptr || counts == nullptr || out == nullptr)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "raw, counts and out must not be null");
+  PartialRescaleArgs a{batch, channels, positions, count_batch, count_channels, window};
+  return hip_check(launch_partial_rescale(dtype, a, raw, counts, bias, out,
+                                          static_cast<hipStream_t>(stream)),
+                   "partial rescale launch");
+}
+
 int convnd_hip_timing_enable(int enable) {
   TimingState& t = timing();
   std::lock_guard<std::mutex> guard(t.lock);

@@ -14,7 +14,9 @@
 
 #include <ATen/Parallel.h>
 
+#include <algorithm>
 #include <array>
+#include <limits>
 #include <vector>
 
 namespace torch_convnd_cpu {
@@ -204,6 +206,42 @@ Grads backward(const at::Tensor& grad_output, const at::Tensor& input,
   if (output_mask[0]) grad_input = dx.view(input.sizes()).to(type);
   if (output_mask[1]) grad_weight = dwt.permute({1, 2, 3, 0}).reshape(weight.sizes()).to(type).contiguous();
   return {grad_input, grad_weight, grad_bias};
+}
+
+at::Tensor partial_rescale(const at::Tensor& raw, const at::Tensor& counts,
+                           const std::optional<at::Tensor>& bias, double window) {
+  const auto ct = compute_type(raw.scalar_type());
+  const int64_t batch = raw.size(0), channels = raw.size(1);
+  const int64_t positions = raw.numel() / std::max<int64_t>(1, batch * channels);
+  const int64_t count_batch = counts.size(0), count_channels = counts.size(1);
+  const int64_t per_group = channels / count_channels;
+  const auto r = raw.contiguous().to(ct);
+  const auto k = counts.contiguous();
+  auto out = at::empty_like(r);
+  std::optional<at::Tensor> b;
+  if (bias.has_value()) b = bias->to(ct).contiguous();
+  AT_DISPATCH_FLOATING_TYPES(ct, "partial_rescale_cpu", [&] {
+    const scalar_t* src = r.const_data_ptr<scalar_t>();
+    const scalar_t* cnt = k.const_data_ptr<scalar_t>();
+    const scalar_t* bp = b.has_value() ? b->const_data_ptr<scalar_t>() : nullptr;
+    scalar_t* dst = out.mutable_data_ptr<scalar_t>();
+    const scalar_t w = static_cast<scalar_t>(window);
+    const scalar_t tiny = std::numeric_limits<scalar_t>::min();
+    at::parallel_for(0, batch * channels, 1, [&](int64_t begin, int64_t end) {
+      for (int64_t row = begin; row < end; ++row) {
+        const int64_t n = row / channels, c = row % channels;
+        const scalar_t* kr = cnt + ((count_batch > 1 ? n * count_channels : 0) + c / per_group) * positions;
+        for (int64_t p = 0; p < positions; ++p) {
+          const scalar_t kv = kr[p];
+          const scalar_t u = kv < 0 ? scalar_t(0) : (kv > 1 ? scalar_t(1) : kv);
+          const scalar_t ratio = u * w / (kv > tiny ? kv : tiny);
+          const scalar_t v = src[row * positions + p] * ratio;
+          dst[row * positions + p] = bp != nullptr ? (v + bp[c]) * u : v;
+        }
+      }
+    });
+  });
+  return out.to(raw.scalar_type());
 }
 
 }  // namespace torch_convnd_cpu

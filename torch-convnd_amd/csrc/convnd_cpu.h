@@ -25,4 +25,10 @@ Grads backward(const at::Tensor& grad_output, const at::Tensor& input,
                const at::Tensor& weight, at::IntArrayRef stride, at::IntArrayRef padding,
                at::IntArrayRef dilation, int64_t groups, std::array<bool, 3> output_mask);
 
+// Partial-convolution rescale of a raw output (shapes checked by the caller): per element
+// u = clamp(k, 0, 1), r = u * window / max(k, tiny), out = raw * r or (raw * r + b) * u,
+// in float32 (float64 for float64) and rounded once.
+at::Tensor partial_rescale(const at::Tensor& raw, const at::Tensor& counts,
+                           const std::optional<at::Tensor>& bias, double window);
+
 }  // namespace torch_convnd_cpu

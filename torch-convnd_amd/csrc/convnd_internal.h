@@ -219,6 +219,14 @@ constexpr int kWgradCmBuffer = 78 * 1024;
 // Positions per item (box volume) of the channel-major weight gradient.
 constexpr int kWgradCmBoxVol = 256;
 
+// Partial-convolution rescale: raw/out [batch][channels][positions], counts
+// [count_batch][count_channels][positions] (count_batch 1 or batch; count_channels divides
+// channels), window = valid samples of a full window.
+struct PartialRescaleArgs {
+  int64_t batch, channels, positions, count_batch, count_channels;
+  double window;
+};
+
 // Zero-padded channels-first copy of the input for the channel-major weight gradient:
 // dst[n][c][u] = src[n][c][u - pad] (zero outside the input), u_a < pe[a] (pe[rank-1] a
 // multiple of 8).
@@ -285,6 +293,10 @@ struct PrologueParts {
   int64_t pp_batch = 0;
 };
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream);
+// out = partial-convolution rescale of raw (see PartialRescaleArgs); out may alias raw.
+hipError_t launch_partial_rescale(convnd_hip_dtype dtype, const PartialRescaleArgs& a,
+                                  const void* raw, const void* counts, const void* bias,
+                                  void* out, hipStream_t stream);
 
 // db[c] = sum of the nsum partial sums of channel c (fixed order).
 hipError_t launch_grad_bias_from_sums(convnd_hip_dtype dtype, const float* sums, int64_t nsum,

@@ -218,6 +218,56 @@ Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& inpu
                                     groups, output_mask);
 }
 
+// torch_convnd::partial_rescale: shapes as convnd_hip_partial_rescale documents, raw
+// [N, C, *spatial], counts [1 or N, C or a divisor of C, *spatial] in float32 (float64 for
+// float64 raw), bias [C] or None.
+std::array<int64_t, 3> check_rescale(const at::Tensor& raw, const at::Tensor& counts,
+                                     const std::optional<at::Tensor>& bias, double window) {
+  const auto type = raw.scalar_type();
+  TORCH_CHECK(type == at::kFloat || type == at::kDouble || type == at::kHalf ||
+                  type == at::kBFloat16,
+              "partial_rescale supports float16, bfloat16, float32 and float64");
+  TORCH_CHECK(raw.dim() >= 3 && counts.dim() == raw.dim(),
+              "partial_rescale expects batched raw output and counts of the same rank");
+  TORCH_CHECK(counts.scalar_type() == (type == at::kDouble ? at::kDouble : at::kFloat),
+              "counts must be float32 (float64 for float64 outputs)");
+  TORCH_CHECK(counts.device() == raw.device(), "counts must be on the output's device");
+  TORCH_CHECK((counts.size(0) == 1 || counts.size(0) == raw.size(0)) && counts.size(1) > 0 &&
+                  raw.size(1) % counts.size(1) == 0,
+              "counts must have batch 1 or the output's, and channels dividing the output's");
+  for (int64_t a = 2; a < raw.dim(); ++a)
+    TORCH_CHECK(counts.size(a) == raw.size(a), "counts must have the output's spatial shape");
+  if (bias.has_value())
+    TORCH_CHECK(bias->dim() == 1 && bias->size(0) == raw.size(1) &&
+                    bias->device() == raw.device() && bias->scalar_type() == type,
+                "bias must match output channels, device and dtype");
+  TORCH_CHECK(window > 0, "window must be positive");
+  return {raw.size(0), raw.size(1), raw.numel() / std::max<int64_t>(1, raw.size(0) * raw.size(1))};
+}
+
+at::Tensor partial_rescale_device(const at::Tensor& raw, const at::Tensor& counts,
+                                  const std::optional<at::Tensor>& bias, double window) {
+  const auto sizes = check_rescale(raw, counts, bias, window);
+  const c10::OptionalDeviceGuard guard(raw.device());
+  const auto r = raw.contiguous();
+  const auto k = counts.contiguous();
+  std::optional<at::Tensor> b;
+  if (bias.has_value()) b = bias->contiguous();
+  auto out = at::empty(raw.sizes(), raw.options());
+  if (out.numel() == 0) return out;
+  raise_status(convnd_hip_partial_rescale(
+      to_dtype(raw.scalar_type()), r.const_data_ptr(), k.const_data_ptr(),
+      b.has_value() ? b->const_data_ptr() : nullptr, out.mutable_data_ptr(), sizes[0],
+      sizes[1], sizes[2], counts.size(0), counts.size(1), window, current_stream(raw)));
+  return out;
+}
+
+at::Tensor partial_rescale_cpu(const at::Tensor& raw, const at::Tensor& counts,
+                               const std::optional<at::Tensor>& bias, double window) {
+  check_rescale(raw, counts, bias, window);
+  return torch_convnd_cpu::partial_rescale(raw, counts, bias, window);
+}
+
 // Autocast: cast the operands once to the autocast dtype and redispatch below autocast,
 // as the reference's autocast_conv_nd does (src/torch_convnd/csrc/convnd.cpp:417-431), for
 // the GPU (AutocastCUDA) and CPU (AutocastCPU) keys.
@@ -246,6 +296,7 @@ at::Tensor conv_nd_autocast(const at::Tensor& input, const at::Tensor& weight,
 TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
   library.impl("conv_nd", &torch_convnd_hip::conv_nd_device);
   library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_device);
+  library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_device);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {
@@ -256,6 +307,7 @@ TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {
 TORCH_LIBRARY_IMPL(torch_convnd, CPU, library) {
   library.impl("conv_nd", &torch_convnd_hip::conv_nd_cpu);
   library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_cpu);
+  library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_cpu);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, AutocastCPU, library) {

@@ -10,7 +10,20 @@ from ._operators import ensure_native_definitions
 from ._version import __version__
 from .diagnostics import get_runtime_info
 from .functional import conv_nd
-from .modules import Conv1d, Conv2d, Conv3d, Conv4d, ConvNd
+from .modules import (
+    Conv1d,
+    Conv2d,
+    Conv3d,
+    Conv4d,
+    ConvNd,
+    PartialConv1d,
+    PartialConv2d,
+    PartialConv3d,
+    PartialConv4d,
+    PartialConvNd,
+    PartialSequential,
+)
+from .partial import PartialConvOutput, partial_conv_nd
 
 ensure_native_definitions()
 ensure_compatible_operator()
@@ -21,7 +34,15 @@ __all__ = [
     "Conv3d",
     "Conv4d",
     "ConvNd",
+    "PartialConv1d",
+    "PartialConv2d",
+    "PartialConv3d",
+    "PartialConv4d",
+    "PartialConvNd",
+    "PartialConvOutput",
+    "PartialSequential",
     "conv_nd",
+    "partial_conv_nd",
     "load_native",
     "get_runtime_info",
     "__version__",

@@ -120,9 +120,46 @@ def _vmap_forward(info, in_dims, input, weight, bias, stride, padding, dilation,
     return torch.stack(outputs), 0
 
 
+def _fake_rescale(raw, counts, bias, window):
+    return torch.empty_like(raw, memory_format=torch.contiguous_format)
+
+
+def _setup_rescale(ctx, inputs, output):
+    raw, counts, bias, window = inputs
+    ctx.save_for_backward(counts)
+    ctx.window = window
+    ctx.has_bias = bias is not None
+    ctx.bias_dtype = None if bias is None else bias.dtype
+
+
+def _rescale_backward(ctx, grad):
+    """out = raw * r or (raw * r + b) * u, with r and u fixed by the counts:
+    d raw = grad * r (* u with bias), the same op on grad with a zero bias; d b = sum(grad * u)."""
+    (counts,) = ctx.saved_tensors
+    grad_raw = grad_bias = None
+    channels = grad.shape[1]
+    if ctx.needs_input_grad[0]:
+        zero = grad.new_zeros(channels) if ctx.has_bias else None
+        grad_raw = torch.ops.torch_convnd.partial_rescale.default(grad.contiguous(), counts, zero, ctx.window)
+    if ctx.has_bias and ctx.needs_input_grad[2]:
+        # sum over images and positions of grad * update: one batched matrix-vector product
+        # per image and count channel (a plain reduction over the broadcast product is
+        # several times slower on the GPU).
+        batch, groups = grad.shape[0], counts.shape[1]
+        update = counts.clamp(0, 1).reshape(counts.shape[0], groups, -1, 1)
+        g = grad.to(counts.dtype).reshape(batch, groups, channels // groups, -1)
+        per_image = torch.matmul(g, update.expand(batch, -1, -1, -1))
+        grad_bias = per_image.sum(dim=0).reshape(channels).to(ctx.bias_dtype)
+    return grad_raw, None, grad_bias, None
+
+
 def register_training() -> None:
     torch.library.register_fake("torch_convnd::conv_nd")(_fake_forward)
     torch.library.register_fake("torch_convnd::conv_nd_backward")(_fake_backward)
+    torch.library.register_fake("torch_convnd::partial_rescale")(_fake_rescale)
+    torch.library.register_autograd(
+        "torch_convnd::partial_rescale", _rescale_backward, setup_context=_setup_rescale
+    )
     torch.library.register_autograd("torch_convnd::conv_nd", _backward, setup_context=_setup_context)
     torch.library.register_autograd(
         "torch_convnd::conv_nd_backward", _backward_backward, setup_context=_setup_backward_context

@@ -24,6 +24,7 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_plan_describe",
     "convnd_hip_timing_enable",
     "convnd_hip_timing_read",
+    "convnd_hip_partial_rescale",
 )
 
 
@@ -80,6 +81,10 @@ def bind(library: ctypes.CDLL) -> ctypes.CDLL:
     library.convnd_hip_timing_enable.argtypes = [ctypes.c_int]
     library.convnd_hip_timing_read.restype = ctypes.c_int
     library.convnd_hip_timing_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)]
+    library.convnd_hip_partial_rescale.restype = ctypes.c_int
+    library.convnd_hip_partial_rescale.argtypes = [
+        ctypes.c_int, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_double, vp
+    ]
     return library
 
 

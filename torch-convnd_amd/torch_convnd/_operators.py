@@ -46,6 +46,11 @@ def _lazy_backward(
     )
 
 
+def _lazy_rescale(raw, counts, bias, window):
+    _load_for(raw)
+    return torch.ops.torch_convnd.partial_rescale.default(raw, counts, bias, window)
+
+
 def ensure_native_definitions():
     """Define the schemas once per process (idempotent, thread-safe)."""
     global _LIBRARY
@@ -62,6 +67,12 @@ def ensure_native_definitions():
             "int[] padding, int[] dilation, int groups, int workspace_bytes, "
             "bool[3] output_mask) -> (Tensor?, Tensor?, Tensor?)"
         )
+        # Partial convolution's fused rescale epilogue; no reference counterpart (the
+        # reference runs it as PyTorch elementwise ops, functional.py:312-321,592-616).
+        library.define(
+            "partial_rescale(Tensor raw, Tensor counts, Tensor? bias, float window) -> Tensor"
+        )
+        library.impl("partial_rescale", _lazy_rescale, "CompositeExplicitAutograd")
         library.impl("conv_nd", _lazy_forward, "CompositeExplicitAutograd")
         library.impl("conv_nd_backward", _lazy_backward, "CompositeExplicitAutograd")
         if HAS_NATIVE_AUTOGRAD:

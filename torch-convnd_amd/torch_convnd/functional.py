@@ -98,9 +98,14 @@ def conv_nd(
         padding = _tuple(padding, rank, "padding")
     _check_options(padding_mode, workspace_bytes, backend)
     if padding_mode == "partial":
-        raise NotImplementedError(
-            "padding_mode='partial' (partial convolution) is not part of this build yet"
+        # Zero padding with partial-convolution rescaling: the mask-free partial convolution.
+        from .partial import partial_forward
+
+        output, _ = partial_forward(
+            input, weight, bias, stride, padding, dilation, groups, mask=None, multi_channel=False,
+            padding_mode="zeros", workspace_bytes=workspace_bytes, backend=backend, need_update=False,
         )
+        return output.squeeze(0) if unbatched else output
     amp = _check_arguments(input, weight, stride, padding, dilation, groups)
     _check_bias(input, weight, bias, amp)
     pairs = padding_pairs(padding, weight.shape[2:], stride, dilation)

@@ -10,6 +10,7 @@ from torch import Tensor, nn
 from ._geometry import DEFAULT_WORKSPACE_BYTES, _tuple, has_rank
 from ._padding import padding_pairs
 from .functional import _PADDING_MODES, conv_nd
+from .partial import PartialConvOutput, mask_free_is_full, partial_forward
 
 
 class ConvNd(nn.Module):
@@ -174,3 +175,197 @@ class Conv4d(_FixedConvNd):
     """Full 4D convolution; the axes may stand for x, y, z and time."""
 
     _spatial_dimensions = 4
+
+
+class PartialConvNd(ConvNd):
+    """Partial convolution layer at any spatial rank, with ConvNd's parameters and state.
+
+    ``forward(input, mask=None, mask_in=None, return_mask=None)``: ``mask_in`` is NVIDIA's
+    name for ``mask``; ``return_mask`` (None: the layer's setting) selects
+    ``PartialConvOutput(output, mask)`` or the output alone. ``multi_channel`` selects one
+    mask channel per input channel. Reference: src/torch_convnd/modules.py:219-345.
+    """
+
+    def __init__(
+        self,
+        in_channels,
+        out_channels,
+        kernel_size,
+        stride=1,
+        padding=0,
+        dilation=1,
+        groups=1,
+        bias=True,
+        padding_mode="zeros",
+        device=None,
+        dtype=None,
+        *,
+        dimensions: int,
+        workspace_bytes=DEFAULT_WORKSPACE_BYTES,
+        backend="auto",
+        multi_channel=False,
+        return_mask=False,
+    ):
+        super().__init__(
+            in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
+            padding_mode, device, dtype, dimensions=dimensions, workspace_bytes=workspace_bytes,
+            backend=backend,
+        )
+        if not isinstance(multi_channel, bool) or not isinstance(return_mask, bool):
+            raise TypeError("multi_channel and return_mask must be bools")
+        if padding_mode == "partial":
+            raise ValueError("PartialConvNd already rescales zero padding; use padding_mode='zeros'")
+        self.multi_channel = multi_channel
+        self.return_mask = return_mask
+
+    def forward(self, input, mask=None, mask_in=None, return_mask=None):
+        if mask_in is not None:
+            if mask is not None:
+                raise TypeError("pass mask or mask_in, not both")
+            mask = mask_in
+        if return_mask is None:
+            return_mask = self.return_mask
+        elif not isinstance(return_mask, bool):
+            raise TypeError("return_mask must be a bool or None")
+        output, update = partial_forward(
+            input, self.weight, self.bias, self.stride, self.padding, self.dilation, self.groups,
+            mask=mask, multi_channel=self.multi_channel, padding_mode=self.padding_mode,
+            workspace_bytes=self.workspace_bytes, backend=self.backend, need_update=return_mask,
+        )
+        return PartialConvOutput(output, update) if return_mask else output
+
+    def keeps_every_sample_valid(self, input) -> bool:
+        """Whether this layer, without a mask, leaves every output sample valid."""
+        return mask_free_is_full(
+            tuple(input.shape[-self.dimensions :]), self.kernel_size, self.stride, self.padding,
+            self.dilation, self.padding_mode,
+        )
+
+    def extra_repr(self) -> str:
+        return f"{super().extra_repr()}, multi_channel={self.multi_channel}, return_mask={self.return_mask}"
+
+
+class _FixedPartialConvNd(PartialConvNd):
+    _spatial_dimensions = 0
+
+    def __init__(
+        self,
+        in_channels,
+        out_channels,
+        kernel_size,
+        stride=1,
+        padding=0,
+        dilation=1,
+        groups=1,
+        bias=True,
+        padding_mode="zeros",
+        device=None,
+        dtype=None,
+        *,
+        workspace_bytes=DEFAULT_WORKSPACE_BYTES,
+        backend="auto",
+        multi_channel=False,
+        return_mask=False,
+    ):
+        super().__init__(
+            in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
+            padding_mode, device, dtype, dimensions=self._spatial_dimensions,
+            workspace_bytes=workspace_bytes, backend=backend, multi_channel=multi_channel,
+            return_mask=return_mask,
+        )
+
+
+class PartialConv1d(_FixedPartialConvNd):
+    """Partial 1D convolution with the torch.nn.Conv1d constructor."""
+
+    _spatial_dimensions = 1
+
+
+class PartialConv2d(_FixedPartialConvNd):
+    """Partial 2D convolution (NVIDIA's PartialConv2d) with the stock constructor."""
+
+    _spatial_dimensions = 2
+
+
+class PartialConv3d(_FixedPartialConvNd):
+    """Partial 3D convolution (NVIDIA's PartialConv3d) with the stock constructor."""
+
+    _spatial_dimensions = 3
+
+
+class PartialConv4d(_FixedPartialConvNd):
+    """Partial 4D convolution."""
+
+    _spatial_dimensions = 4
+
+
+def _partial_rank(container):
+    for module in container.modules():
+        if isinstance(module, PartialConvNd):
+            return module.dimensions
+    return None
+
+
+def _trailing(shape, rank):
+    return tuple(shape[max(len(shape) - rank, 0) :])
+
+
+class PartialSequential(nn.Sequential):
+    """Run modules in order, carrying the validity mask through the partial layers.
+
+    ``forward(input, mask=None)`` returns ``PartialConvOutput(output, mask)``. Partial
+    layers (also inside nested PartialSequential containers) consume the current mask and
+    replace it with their update mask; other modules see only the tensor and must keep the
+    spatial shape while a mask is carried. Without a mask, layers whose geometry keeps every
+    sample valid run mask-free and an all-valid result is reported as a broadcast view of
+    ones. Reference: src/torch_convnd/modules.py:442-506.
+    """
+
+    def forward(self, input, mask=None):
+        rank = _partial_rank(self)
+        layout = (max(input.ndim - 2, 0) if rank is None else rank, 1)
+        output, mask, layout = self._carry(input, mask, layout)
+        if mask is None:
+            mask = self._all_valid(output, *layout)
+        return PartialConvOutput(output, mask)
+
+    @staticmethod
+    def _all_valid(output, rank, channels):
+        if not has_rank(output.ndim, rank):
+            raise ValueError(
+                f"the {output.ndim}-dimensional output has lost the {rank} spatial axes "
+                "a validity mask describes"
+            )
+        level = {torch.complex64: torch.float32, torch.complex128: torch.float64}.get(output.dtype, output.dtype)
+        shape = (channels, *_trailing(output.shape, rank))
+        if output.ndim == rank + 2:
+            shape = (output.shape[0], *shape)
+        return torch.ones((), dtype=level, device=output.device).expand(shape)
+
+    def _carry(self, input, mask, layout):
+        for module in self:
+            if isinstance(module, PartialSequential):
+                input, mask, layout = module._carry(input, mask, layout)
+            elif isinstance(module, PartialConvNd):
+                layout = module.dimensions, module.out_channels if module.multi_channel else 1
+                if mask is None and module.keeps_every_sample_valid(input):
+                    input = module(input, return_mask=False)
+                else:
+                    input, mask = module(input, mask, return_mask=True)
+            elif _partial_rank(module) is not None:
+                raise TypeError(
+                    f"{type(module).__name__} holds partial layers the mask cannot reach; "
+                    "use PartialSequential"
+                )
+            elif mask is None:
+                input = module(input)
+            else:
+                shape, rank = input.shape, layout[0]
+                input = module(input)
+                if input.ndim != len(shape) or _trailing(input.shape, rank) != _trailing(shape, rank):
+                    raise ValueError(
+                        f"{type(module).__name__} changed the shape {tuple(shape)} to "
+                        f"{tuple(input.shape)} while a mask is carried; keep the spatial "
+                        "shape or resample the mask around it"
+                    )
+        return input, mask, layout
