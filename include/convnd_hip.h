@@ -105,6 +105,19 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                         void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
                         size_t workspace_size, void* stream);
 
+/* Partial convolution's counts: window sums of a validity map under the convolution's
+ * geometry (a depthwise all-ones convolution with symmetric zero padding). Reads
+ * problem->rank (1..8), batch, channels (the map's channels), groups (count channels,
+ * dividing channels), input, kernel, stride, padding and dilation; output_channels is
+ * ignored. mask [batch, channels, input...] of `mask_dtype`; counts [batch, groups, out...]
+ * float32 (float64 when mask_dtype is CONVND_HIP_FLOAT64); count channel q sums map
+ * channels [q*channels/groups, (q+1)*channels/groups) over each window's in-bounds taps.
+ * Replaces _count / _counting_kernel and the per-group channel sum of multi-channel masks
+ * (src/torch_convnd/functional.py:395-441,536-545), which run a convolution through the
+ * native operator. */
+int convnd_hip_partial_count(const convnd_hip_problem* problem, convnd_hip_dtype mask_dtype,
+                             const void* mask, void* counts, void* stream);
+
 /* Partial convolution's rescale epilogue, one pass over the raw convolution output
  * (computed without bias). For element (n, c, p), with k = counts[n', c / (channels /
  * count_channels), p] and n' = n when count_batch == batch, else 0:

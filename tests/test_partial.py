@@ -253,3 +253,33 @@ def test_partial_gpu_empty_batch_and_opcheck():
     bias = torch.randn(4, device="cuda", requires_grad=True)
     results = torch.library.opcheck(torch.ops.torch_convnd.partial_rescale.default, (raw, counts, bias, 9.0))
     assert all(v == "SUCCESS" for v in results.values()), results
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mask_dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64],
+                         ids=lambda d: str(d).split(".")[1])
+@pytest.mark.parametrize(
+    "geometry",
+    [
+        ((2, 4, 5, 6, 4, 7), (3, 2, 3, 2), (1, 2, 1, 3), (1, 0, 2, 1), (1, 1, 2, 1), 2),
+        ((1, 3, 4, 3, 5, 4, 3), (2, 3, 2, 2, 3), (2, 1, 1, 2, 1), (1, 1, 0, 1, 2), (1, 2, 1, 1, 1), 1),
+        ((3, 6, 7, 9), (3, 4), (2, 1), (3, 1), (2, 2), 3),
+    ],
+    ids=["rank4_groups2", "rank5", "rank2_wide_padding"],
+)
+def test_count_kernel_matches_ones_convolution(mask_dtype, geometry):
+    # Window sums of a fractional validity map against the float64 depthwise all-ones
+    # convolution of the group-summed map (the counting convolution it replaces).
+    print(f"[partial] count kernel {mask_dtype} {geometry[0]}", flush=True)
+    shape, kernel, stride, padding, dilation, count_channels = geometry
+    g = torch.Generator().manual_seed(len(shape))
+    mask = (torch.rand(shape, generator=g) * 2 - 0.25).to(mask_dtype)
+    got = torch.ops.torch_convnd.partial_count(mask.cuda(), list(kernel), list(stride), list(padding),
+                                               list(dilation), count_channels)
+    m = mask.double()
+    grouped = m.reshape(shape[0], count_channels, shape[1] // count_channels, *shape[2:]).sum(2)
+    ones = torch.ones((count_channels, 1, *kernel), dtype=torch.float64)
+    want = oracle.forward(grouped.numpy(), ones.numpy(), None, stride, padding, dilation, count_channels)
+    assert got.dtype == (torch.float64 if mask_dtype == torch.float64 else torch.float32)
+    tol = 1e-12 if mask_dtype == torch.float64 else 1e-5
+    torch.testing.assert_close(got.cpu().double(), torch.from_numpy(want), rtol=tol, atol=tol)

@@ -1659,6 +1659,60 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
   return CONVND_HIP_SUCCESS;
 }
 
+int convnd_hip_partial_count(const convnd_hip_problem* problem, convnd_hip_dtype mask_dtype,
+                             const void* mask, void* counts, void* stream) {
+  if (problem == nullptr) return fail(CONVND_HIP_INVALID_ARGUMENT, "problem must not be null");
+  if (element_size(mask_dtype) == 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT,
+                "native conv_nd supports float16, bfloat16, float32 and float64");
+  const convnd_hip_problem& pr = *problem;
+  if (pr.rank < 1 || pr.rank > kPartialMaxRank)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "partial counts support 1 to 8 spatial dimensions");
+  if (pr.batch < 0 || pr.channels <= 0 || pr.groups <= 0 || pr.channels % pr.groups != 0)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "count channels must divide the mask channels");
+  PartialCountArgs a{};
+  a.rank = static_cast<int>(pr.rank);
+  a.batch = pr.batch;
+  a.mask_channels = pr.channels;
+  a.count_channels = pr.groups;
+  a.in_vol = 1;
+  a.out_vol = 1;
+  for (int ax = 0; ax < a.rank; ++ax) {
+    const int64_t n = pr.input[ax], k = pr.kernel[ax], st = pr.stride[ax], p = pr.padding[ax],
+                  d = pr.dilation[ax];
+    if (n <= 0 || k <= 0 || st <= 0 || d <= 0 || p < 0 || n > kI32Safe || k > kI32Safe ||
+        st > kI32Safe || d > kI32Safe || p > kI32Safe)
+      return fail(CONVND_HIP_INVALID_ARGUMENT,
+                  "stride and dilation must be positive; padding must be nonnegative");
+    const int64_t span = d * (k - 1) + 1;
+    if (n + 2 * p < span) return fail(CONVND_HIP_INVALID_ARGUMENT, "kernel exceeds padded input");
+    a.in[ax] = n;
+    a.k[ax] = k;
+    a.s[ax] = st;
+    a.p[ax] = p;
+    a.d[ax] = d;
+    a.out[ax] = (n + 2 * p - span) / st + 1;
+    if (!mul_ok(a.in_vol, n, &a.in_vol) || !mul_ok(a.out_vol, a.out[ax], &a.out_vol))
+      return fail(CONVND_HIP_INVALID_ARGUMENT, "spatial volume overflows int64");
+  }
+  int64_t step = 1;
+  for (int ax = a.rank - 1; ax >= 0; --ax) {
+    a.istride[ax] = step;
+    step *= a.in[ax];
+  }
+  int64_t total = 0;
+  if (!mul_ok(pr.batch, pr.channels, &total) || !mul_ok(total, a.in_vol, &total) ||
+      !mul_ok(pr.batch * pr.groups, a.out_vol, &total))
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "mask volume overflows int64");
+  if (total == 0) return CONVND_HIP_SUCCESS;
+  if (total > kI32Safe / kCountLanesMax || pr.batch * pr.channels * a.in_vol > kI32Safe)
+    return fail(CONVND_HIP_UNSUPPORTED, "partial counts support masks and counts below 2^31 elements");
+  if (mask == nullptr || counts == nullptr)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "mask and counts must not be null");
+  return hip_check(launch_partial_count(mask_dtype, a, mask, counts, static_cast<hipStream_t>(stream)),
+                   "partial count launch");
+}
+
 int convnd_hip_partial_rescale(convnd_hip_dtype dtype, const void* raw, const void* counts,
                                const void* bias, void* out, int64_t batch, int64_t channels,
                                int64_t positions, int64_t count_batch, int64_t count_channels,

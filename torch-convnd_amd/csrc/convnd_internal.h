@@ -222,6 +222,18 @@ constexpr int kWgradCmBoxVol = 256;
 // Partial-convolution rescale: raw/out [batch][channels][positions], counts
 // [count_batch][count_channels][positions] (count_batch 1 or batch; count_channels divides
 // channels), window = valid samples of a full window.
+// Partial-convolution counts: mask [batch][mask_channels][in...] -> counts
+// [batch][count_channels][out...], zero padding p, stride s, dilation d, kernel k.
+constexpr int kPartialMaxRank = 8;
+// Lanes that share one output in the count kernel (bounds the thread count's range).
+constexpr int64_t kCountLanesMax = 4;
+struct PartialCountArgs {
+  int rank;
+  int64_t batch, mask_channels, count_channels, in_vol, out_vol;
+  int64_t in[kPartialMaxRank], out[kPartialMaxRank], k[kPartialMaxRank], s[kPartialMaxRank],
+      p[kPartialMaxRank], d[kPartialMaxRank], istride[kPartialMaxRank];
+};
+
 struct PartialRescaleArgs {
   int64_t batch, channels, positions, count_batch, count_channels;
   double window;
@@ -293,6 +305,9 @@ struct PrologueParts {
   int64_t pp_batch = 0;
 };
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream);
+// counts = window sums of mask (see PartialCountArgs); float32 counts, float64 for float64.
+hipError_t launch_partial_count(convnd_hip_dtype mask_dtype, const PartialCountArgs& a,
+                                const void* mask, void* counts, hipStream_t stream);
 // out = partial-convolution rescale of raw (see PartialRescaleArgs); out may alias raw.
 hipError_t launch_partial_rescale(convnd_hip_dtype dtype, const PartialRescaleArgs& a,
                                   const void* raw, const void* counts, const void* bias,

@@ -117,6 +117,135 @@ hipError_t launch_typed(const PartialRescaleArgs& a, const void* raw, const void
   return hipGetLastError();
 }
 
+// Window sums of a validity map (a depthwise all-ones convolution, zero padding). Four
+// adjacent lanes share one (image, count channel, output position): they split the first
+// axis's in-bounds taps and add their sums with lane shuffles. Each count channel sums its
+// mask_channels / count_channels map channels. Taps are walked from the first to the last
+// in-bounds index per axis (no bounds checks in the loop); the last axis four loads at a
+// time so several are in flight. RANK is a template parameter so every per-axis array
+// stays in registers.
+constexpr int kCountLanes = static_cast<int>(kCountLanesMax);
+
+template <typename T, typename C, int RANK>
+__global__ __launch_bounds__(kThreads) void partial_count_kernel(PartialCountArgs a,
+                                                                 const T* __restrict__ mask,
+                                                                 C* __restrict__ counts) {
+  // 32-bit index arithmetic: the host admits masks and counts below 2^31 elements.
+  const int total = static_cast<int>(a.batch * a.count_channels * a.out_vol);
+  const int out_vol = static_cast<int>(a.out_vol);
+  const int count_channels = static_cast<int>(a.count_channels);
+  const int mask_channels = static_cast<int>(a.mask_channels);
+  const int in_vol = static_cast<int>(a.in_vol);
+  const int per_group = mask_channels / count_channels;
+  const int sub = static_cast<int>(threadIdx.x) % kCountLanes;
+  const int stride = static_cast<int>(gridDim.x) * (kThreads / kCountLanes);
+  for (int i = static_cast<int>((blockIdx.x * kThreads + threadIdx.x) / kCountLanes); i < total;
+       i += stride) {
+    const int rest = i / out_vol;
+    int o = i - rest * out_vol;
+    const int q = rest % count_channels;
+    const int n = rest / count_channels;
+    int first[RANK], last[RANK], step[RANK];
+    int start_offset = 0;
+    bool empty = false;
+#pragma unroll
+    for (int ax = RANK - 1; ax >= 0; --ax) {
+      const int out_a = static_cast<int>(a.out[ax]);
+      const int oa = o % out_a;
+      o /= out_a;
+      const int d = static_cast<int>(a.d[ax]);
+      const int start = oa * static_cast<int>(a.s[ax]) - static_cast<int>(a.p[ax]);
+      // First tap j with start + j*d >= 0, last with start + j*d <= in - 1.
+      const int lo = start >= 0 ? 0 : (d == 1 ? -start : (-start + d - 1) / d);
+      const int room = static_cast<int>(a.in[ax]) - 1 - start;
+      const int kmax = static_cast<int>(a.k[ax]) - 1;
+      const int reach = d == 1 ? room : room / d;
+      const int hi = room < 0 ? -1 : (reach < kmax ? reach : kmax);
+      first[ax] = lo;
+      last[ax] = hi;
+      step[ax] = d * static_cast<int>(a.istride[ax]);
+      empty = empty || hi < lo;
+      start_offset += (start + lo * d) * static_cast<int>(a.istride[ax]);
+    }
+    C sum = C(0);
+    if (!empty) {
+      const int nl = last[RANK - 1] - first[RANK - 1] + 1;
+      const int sl = step[RANK - 1];
+      for (int ch = q * per_group; ch < (q + 1) * per_group; ++ch) {
+        const T* base = mask + static_cast<size_t>(n * mask_channels + ch) * in_vol + start_offset;
+        for (int j0 = first[0] + sub; j0 <= last[0]; j0 += kCountLanes) {
+          const T* p0 = base + (j0 - first[0]) * step[0];
+          if constexpr (RANK == 1) {
+            sum += static_cast<C>(p0[0]);
+          } else {
+            int j[RANK];
+#pragma unroll
+            for (int ax = 1; ax < RANK - 1; ++ax) j[ax] = first[ax];
+            int off = 0;
+            bool carry = false;
+            while (!carry) {
+              const T* pl = p0 + off;
+              for (int t = 0; t < nl; t += 4) {
+                const C v0 = static_cast<C>(pl[t * sl]);
+                const C v1 = t + 1 < nl ? static_cast<C>(pl[(t + 1) * sl]) : C(0);
+                const C v2 = t + 2 < nl ? static_cast<C>(pl[(t + 2) * sl]) : C(0);
+                const C v3 = t + 3 < nl ? static_cast<C>(pl[(t + 3) * sl]) : C(0);
+                sum += (v0 + v1) + (v2 + v3);
+              }
+              carry = true;
+#pragma unroll
+              for (int ax = RANK - 2; ax >= 1; --ax) {
+                if (carry) {
+                  if (j[ax] < last[ax]) {
+                    ++j[ax];
+                    off += step[ax];
+                    carry = false;
+                  } else {
+                    off -= (last[ax] - first[ax]) * step[ax];
+                    j[ax] = first[ax];
+                  }
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+    // The four lanes of an output are adjacent in one wave and leave the loop together.
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    if (sub == 0) counts[i] = sum;
+  }
+}
+
+template <typename T, typename C>
+hipError_t launch_count_typed(const PartialCountArgs& a, const void* mask, void* counts,
+                              hipStream_t stream) {
+  const int64_t total = a.batch * a.count_channels * a.out_vol;
+  const int64_t blocks = std::min<int64_t>((total * kCountLanes + kThreads - 1) / kThreads, 65536);
+  const auto* m = static_cast<const T*>(mask);
+  auto* c = static_cast<C*>(counts);
+  switch (a.rank) {
+#define CONVND_PARTIAL_COUNT_RANK(R)                                                          \
+  case R:                                                                                    \
+    hipLaunchKernelGGL((partial_count_kernel<T, C, R>), dim3(blocks), dim3(kThreads), 0,     \
+                       stream, a, m, c);                                                     \
+    break;
+    CONVND_PARTIAL_COUNT_RANK(1)
+    CONVND_PARTIAL_COUNT_RANK(2)
+    CONVND_PARTIAL_COUNT_RANK(3)
+    CONVND_PARTIAL_COUNT_RANK(4)
+    CONVND_PARTIAL_COUNT_RANK(5)
+    CONVND_PARTIAL_COUNT_RANK(6)
+    CONVND_PARTIAL_COUNT_RANK(7)
+    CONVND_PARTIAL_COUNT_RANK(8)
+#undef CONVND_PARTIAL_COUNT_RANK
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_partial_rescale(convnd_hip_dtype dtype, const PartialRescaleArgs& a,
@@ -131,6 +260,21 @@ hipError_t launch_partial_rescale(convnd_hip_dtype dtype, const PartialRescaleAr
       return launch_typed<_Float16, float>(a, raw, counts, bias, out, stream);
     case CONVND_HIP_BFLOAT16:
       return launch_typed<__bf16, float>(a, raw, counts, bias, out, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_partial_count(convnd_hip_dtype mask_dtype, const PartialCountArgs& a,
+                                const void* mask, void* counts, hipStream_t stream) {
+  switch (mask_dtype) {
+    case CONVND_HIP_FLOAT32:
+      return launch_count_typed<float, float>(a, mask, counts, stream);
+    case CONVND_HIP_FLOAT64:
+      return launch_count_typed<double, double>(a, mask, counts, stream);
+    case CONVND_HIP_FLOAT16:
+      return launch_count_typed<_Float16, float>(a, mask, counts, stream);
+    case CONVND_HIP_BFLOAT16:
+      return launch_count_typed<__bf16, float>(a, mask, counts, stream);
   }
   return hipErrorInvalidValue;
 }

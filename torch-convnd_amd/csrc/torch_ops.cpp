@@ -262,6 +262,44 @@ at::Tensor partial_rescale_device(const at::Tensor& raw, const at::Tensor& count
   return out;
 }
 
+// torch_convnd::partial_count: window sums of a validity map (see convnd_hip_partial_count).
+at::Tensor partial_count_device(const at::Tensor& mask, at::IntArrayRef kernel,
+                                at::IntArrayRef stride, at::IntArrayRef padding,
+                                at::IntArrayRef dilation, int64_t count_channels) {
+  const auto type = mask.scalar_type();
+  TORCH_CHECK(type == at::kFloat || type == at::kDouble || type == at::kHalf ||
+                  type == at::kBFloat16,
+              "partial_count supports float16, bfloat16, float32 and float64 masks");
+  const int64_t rank = mask.dim() - 2;
+  TORCH_CHECK(rank >= 1 && static_cast<int64_t>(kernel.size()) == rank &&
+                  static_cast<int64_t>(stride.size()) == rank &&
+                  static_cast<int64_t>(padding.size()) == rank &&
+                  static_cast<int64_t>(dilation.size()) == rank,
+              "kernel, stride, padding and dilation must match the mask's spatial rank");
+  convnd_hip_problem problem{};
+  problem.rank = rank;
+  problem.batch = mask.size(0);
+  problem.channels = mask.size(1);
+  problem.groups = count_channels;
+  problem.output_channels = count_channels;
+  std::vector<int64_t> shape = {mask.size(0), count_channels};
+  for (int64_t a = 0; a < rank; ++a) {
+    problem.input[a] = mask.size(a + 2);
+    problem.kernel[a] = kernel[a];
+    problem.stride[a] = stride[a];
+    problem.padding[a] = padding[a];
+    problem.dilation[a] = dilation[a];
+    const int64_t span = dilation[a] * (kernel[a] - 1) + 1;
+    shape.push_back(std::max<int64_t>(0, (mask.size(a + 2) + 2 * padding[a] - span) / std::max<int64_t>(1, stride[a]) + 1));
+  }
+  const c10::OptionalDeviceGuard guard(mask.device());
+  const auto m = mask.contiguous();
+  auto counts = at::empty(shape, mask.options().dtype(type == at::kDouble ? at::kDouble : at::kFloat));
+  raise_status(convnd_hip_partial_count(&problem, to_dtype(type), m.const_data_ptr(),
+                                        counts.mutable_data_ptr(), current_stream(mask)));
+  return counts;
+}
+
 at::Tensor partial_rescale_cpu(const at::Tensor& raw, const at::Tensor& counts,
                                const std::optional<at::Tensor>& bias, double window) {
   check_rescale(raw, counts, bias, window);
@@ -297,6 +335,7 @@ TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
   library.impl("conv_nd", &torch_convnd_hip::conv_nd_device);
   library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_device);
   library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_device);
+  library.impl("partial_count", &torch_convnd_hip::partial_count_device);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {

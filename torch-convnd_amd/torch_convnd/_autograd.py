@@ -124,6 +124,15 @@ def _fake_rescale(raw, counts, bias, window):
     return torch.empty_like(raw, memory_format=torch.contiguous_format)
 
 
+def _fake_count(mask, kernel, stride, padding, dilation, count_channels):
+    out = [
+        (n + 2 * p - d * (k - 1) - 1) // s + 1
+        for n, k, s, p, d in zip(mask.shape[2:], kernel, stride, padding, dilation)
+    ]
+    dtype = torch.float64 if mask.dtype == torch.float64 else torch.float32
+    return mask.new_empty((mask.shape[0], count_channels, *out), dtype=dtype)
+
+
 def _setup_rescale(ctx, inputs, output):
     raw, counts, bias, window = inputs
     ctx.save_for_backward(counts)
@@ -142,14 +151,15 @@ def _rescale_backward(ctx, grad):
         zero = grad.new_zeros(channels) if ctx.has_bias else None
         grad_raw = torch.ops.torch_convnd.partial_rescale.default(grad.contiguous(), counts, zero, ctx.window)
     if ctx.has_bias and ctx.needs_input_grad[2]:
-        # sum over images and positions of grad * update: one batched matrix-vector product
-        # per image and count channel (a plain reduction over the broadcast product is
-        # several times slower on the GPU).
+        # sum over images and positions of grad * update, in the gradient's dtype as the
+        # reference's autograd does, accumulated in float32 (float64 for float64) along the
+        # contiguous positions first: a reduction over the broadcast product's outer and
+        # inner axes at once, or a matrix-vector product, is several times slower here.
         batch, groups = grad.shape[0], counts.shape[1]
-        update = counts.clamp(0, 1).reshape(counts.shape[0], groups, -1, 1)
-        g = grad.to(counts.dtype).reshape(batch, groups, channels // groups, -1)
-        per_image = torch.matmul(g, update.expand(batch, -1, -1, -1))
-        grad_bias = per_image.sum(dim=0).reshape(channels).to(ctx.bias_dtype)
+        update = counts.clamp(0, 1).to(grad.dtype).reshape(counts.shape[0], groups, 1, -1)
+        g = grad.reshape(batch, groups, channels // groups, -1)
+        acc = torch.float64 if grad.dtype == torch.float64 else torch.float32
+        grad_bias = (g * update).sum(dim=3, dtype=acc).sum(dim=0).reshape(channels).to(ctx.bias_dtype)
     return grad_raw, None, grad_bias, None
 
 
@@ -157,6 +167,7 @@ def register_training() -> None:
     torch.library.register_fake("torch_convnd::conv_nd")(_fake_forward)
     torch.library.register_fake("torch_convnd::conv_nd_backward")(_fake_backward)
     torch.library.register_fake("torch_convnd::partial_rescale")(_fake_rescale)
+    torch.library.register_fake("torch_convnd::partial_count")(_fake_count)
     torch.library.register_autograd(
         "torch_convnd::partial_rescale", _rescale_backward, setup_context=_setup_rescale
     )

@@ -73,6 +73,11 @@ def ensure_native_definitions():
             "partial_rescale(Tensor raw, Tensor counts, Tensor? bias, float window) -> Tensor"
         )
         library.impl("partial_rescale", _lazy_rescale, "CompositeExplicitAutograd")
+        # Its counting pass (window sums of the validity map), gfx950 only.
+        library.define(
+            "partial_count(Tensor mask, int[] kernel, int[] stride, int[] padding, "
+            "int[] dilation, int count_channels) -> Tensor"
+        )
         library.impl("conv_nd", _lazy_forward, "CompositeExplicitAutograd")
         library.impl("conv_nd_backward", _lazy_backward, "CompositeExplicitAutograd")
         if HAS_NATIVE_AUTOGRAD:

@@ -134,6 +134,21 @@ def _mask_free_counts(spatial, kernel, stride, dilation, pairs, dtype, device):
     return _cached_counts(spatial, kernel, stride, dilation, pairs, dtype, device, stream)
 
 
+def _use_native_count(valid, pairs, padding_mode, backend):
+    """The gfx950 counting kernel takes symmetric zero padding and ranks up to 8."""
+    return (
+        valid is not None
+        and is_rocm_device(valid.device)
+        and backend != "torch"
+        and not transforms_active()
+        and not is_compiling()
+        and padding_mode == "zeros"
+        and all(left == right for left, right in pairs)
+        and 1 <= len(pairs) <= 8
+        and valid.numel() < 2**31 // 4
+    )
+
+
 def _use_fused_rescale(raw, backend):
     if raw.dtype.is_complex or transforms_active():
         return False
@@ -255,6 +270,7 @@ def partial_forward(
         else:
             valid = torch.ones((1, 1, *spatial), dtype=exact, device=input.device)
         data = input
+        valid_source, count_channels = valid, 1
     else:
         width = channels if multi_channel else 1
         if mask.shape[1] not in (1, width):
@@ -265,17 +281,26 @@ def partial_forward(
             )
         cast = mask.to(real)
         data = input * cast
-        valid = mask.detach().to(exact).expand(mask.shape[0], width, *spatial)
+        valid_source = mask.detach().expand(mask.shape[0], width, *spatial)
+        count_channels = groups if multi_channel else 1
+        window = math.prod(kernel) * (channels // groups if multi_channel else 1)
+    output = _execute(data, weight, None, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend)
+    if counts is None and _use_native_count(valid_source, pairs, padding_mode, backend):
+        # One gfx950 pass: window sums (and the per-group channel sums of multi-channel
+        # masks) straight from the mask, in its own dtype.
+        source = valid_source
+        if exact == torch.float64 and source.dtype != torch.float64:
+            source = source.to(torch.float64)
+        counts = torch.ops.torch_convnd.partial_count(
+            source, list(kernel), list(stride), [left for left, _ in pairs], list(dilation), count_channels
+        )
+    if counts is None and mask is not None:
+        valid = valid_source.to(exact)
         if multi_channel:
             # Each group's channels are summed first, so the count stays depthwise.
-            per_group = channels // groups
-            valid = valid.reshape(mask.shape[0], groups, per_group, -1).sum(2).reshape(
+            valid = valid.reshape(mask.shape[0], groups, channels // groups, -1).sum(2).reshape(
                 mask.shape[0], groups, *spatial
             )
-            window = math.prod(kernel) * per_group
-        else:
-            window = math.prod(kernel)
-    output = _execute(data, weight, None, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend)
     if counts is None:
         count_channels = valid.shape[1]
         ones = torch.ones((count_channels, 1, *kernel), dtype=exact, device=input.device)
