@@ -264,8 +264,9 @@ def test_partial_gpu_empty_batch_and_opcheck():
         ((2, 4, 5, 6, 4, 7), (3, 2, 3, 2), (1, 2, 1, 3), (1, 0, 2, 1), (1, 1, 2, 1), 2),
         ((1, 3, 4, 3, 5, 4, 3), (2, 3, 2, 2, 3), (2, 1, 1, 2, 1), (1, 1, 0, 1, 2), (1, 2, 1, 1, 1), 1),
         ((3, 6, 7, 9), (3, 4), (2, 1), (3, 1), (2, 2), 3),
+        ((2, 4, 9, 7, 8), (5, 6, 3), (1, 1, 2), (2, 3, 1), (1, 1, 1), 4),
     ],
-    ids=["rank4_groups2", "rank5", "rank2_wide_padding"],
+    ids=["rank4_groups2", "rank5", "rank2_wide_padding", "rank3_long_taps"],
 )
 def test_count_kernel_matches_ones_convolution(mask_dtype, geometry):
     # Window sums of a fractional validity map against the float64 depthwise all-ones

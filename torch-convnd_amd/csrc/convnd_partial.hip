@@ -126,6 +126,17 @@ hipError_t launch_typed(const PartialRescaleArgs& a, const void* raw, const void
 // stays in registers.
 constexpr int kCountLanes = static_cast<int>(kCountLanesMax);
 
+// Sum of p[0], p[stride], ... over the first min(n, 4) of them (n >= 1); the loads are
+// independent so they are in flight together.
+template <typename T, typename C>
+__device__ inline C load4(const T* p, int n, int stride) {
+  const C v0 = static_cast<C>(p[0]);
+  const C v1 = n > 1 ? static_cast<C>(p[stride]) : C(0);
+  const C v2 = n > 2 ? static_cast<C>(p[2 * stride]) : C(0);
+  const C v3 = n > 3 ? static_cast<C>(p[3 * stride]) : C(0);
+  return (v0 + v1) + (v2 + v3);
+}
+
 template <typename T, typename C, int RANK>
 __global__ __launch_bounds__(kThreads) void partial_count_kernel(PartialCountArgs a,
                                                                  const T* __restrict__ mask,
@@ -177,24 +188,33 @@ __global__ __launch_bounds__(kThreads) void partial_count_kernel(PartialCountArg
           const T* p0 = base + (j0 - first[0]) * step[0];
           if constexpr (RANK == 1) {
             sum += static_cast<C>(p0[0]);
+          } else if constexpr (RANK == 2) {
+            for (int t = 0; t < nl; t += 4) sum += load4<T, C>(p0 + t * sl, nl - t, sl);
           } else {
+            // Axes 1 .. RANK-3 by an odometer; the last two axes' taps in blocks of 4 x 4
+            // predicated loads, issued together.
+            const int n2 = last[RANK - 2] - first[RANK - 2] + 1;
+            const int s2 = step[RANK - 2];
             int j[RANK];
 #pragma unroll
-            for (int ax = 1; ax < RANK - 1; ++ax) j[ax] = first[ax];
+            for (int ax = 1; ax < RANK - 2; ++ax) j[ax] = first[ax];
             int off = 0;
             bool carry = false;
             while (!carry) {
               const T* pl = p0 + off;
-              for (int t = 0; t < nl; t += 4) {
-                const C v0 = static_cast<C>(pl[t * sl]);
-                const C v1 = t + 1 < nl ? static_cast<C>(pl[(t + 1) * sl]) : C(0);
-                const C v2 = t + 2 < nl ? static_cast<C>(pl[(t + 2) * sl]) : C(0);
-                const C v3 = t + 3 < nl ? static_cast<C>(pl[(t + 3) * sl]) : C(0);
-                sum += (v0 + v1) + (v2 + v3);
+              for (int u = 0; u < n2; u += 4) {
+                for (int t = 0; t < nl; t += 4) {
+                  const T* q0 = pl + u * s2 + t * sl;
+                  const C a0 = load4<T, C>(q0, nl - t, sl);
+                  const C a1 = u + 1 < n2 ? load4<T, C>(q0 + s2, nl - t, sl) : C(0);
+                  const C a2 = u + 2 < n2 ? load4<T, C>(q0 + 2 * s2, nl - t, sl) : C(0);
+                  const C a3 = u + 3 < n2 ? load4<T, C>(q0 + 3 * s2, nl - t, sl) : C(0);
+                  sum += (a0 + a1) + (a2 + a3);
+                }
               }
               carry = true;
 #pragma unroll
-              for (int ax = RANK - 2; ax >= 1; --ax) {
+              for (int ax = RANK - 3; ax >= 1; --ax) {
                 if (carry) {
                   if (j[ax] < last[ax]) {
                     ++j[ax];
