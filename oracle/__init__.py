@@ -9,6 +9,8 @@ this package, and only as the checker (or, for the baseline, the thing timed on 
 * ``torch_path``: restatement of the reference's ``backend="torch"`` CPU path
   (src/torch_convnd/_decomposition.py:11-103, selection src/torch_convnd/_dispatch.py:41-65),
   used as the CPU baseline.
+* ``partial``: float64 numpy restatement of partial convolution
+  (src/torch_convnd/functional.py:203-231,444-633), the checker of ``partial_conv_nd``.
 
 Parity status of each function (how it is pinned) is listed in tests/test_oracle.py.
 """
