@@ -286,6 +286,11 @@ def main():
         help="measure partial convolution on the C2 shape instead (bf16, bias, a 30%% hole "
         "mask): the fused gfx950 rescale kernel against its HBM roofline, the same rescale as "
         "PyTorch elementwise ops, and partial_conv_nd forward and forward+backward")
+    parser.add_argument(
+        "--epilogue", action="store_true",
+        help="measure the C2 bf16 forward followed by GELU (inference, no autograd): "
+        "conv_nd then torch.nn.functional.gelu against conv_nd(activation='gelu') with the "
+        "activation fused into the epilogue")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -312,6 +317,28 @@ def main():
         return
     if args.partial:
         print(json.dumps(measure_partial(torch, device, args.steps, args.warmup)), flush=True)
+        return
+    if args.epilogue:
+        x, w, b = make_inputs(torch, torch.bfloat16, device)
+
+        def unfused():
+            y = torch_convnd.conv_nd(x, w, b, STRIDE, "same", DILATION, GROUPS, backend="native")
+            return torch.nn.functional.gelu(y)
+
+        def fused():
+            return torch_convnd.conv_nd(x, w, b, STRIDE, "same", DILATION, GROUPS, backend="native",
+                                        activation="gelu")
+
+        with torch.no_grad():
+            diff = (fused().float() - unfused().float()).abs().max().item()
+            unfused_ms = _timed_ms(torch, unfused, args.steps, args.warmup)
+            fused_ms = _timed_ms(torch, fused, args.steps, args.warmup)
+        print(json.dumps({
+            "metric": "C2 bf16 forward + GELU (inference)", "steps": args.steps, "warmup": args.warmup,
+            "unfused_us": round(unfused_ms * 1e3, 2), "fused_us": round(fused_ms * 1e3, 2),
+            "fused_tflops": round(forward_flops() / (fused_ms * 1e-3) / 1e12, 1),
+            "max_abs_diff_vs_unfused": diff,
+        }), flush=True)
         return
     if args.calibration_copy_mib > 0:
         src = torch.ones(args.calibration_copy_mib << 18, dtype=torch.float32, device=device)

@@ -36,6 +36,16 @@ typedef enum convnd_hip_dtype {
   CONVND_HIP_BFLOAT16 = 3
 } convnd_hip_dtype;
 
+/* Activation fused into the forward epilogue (convnd_hip_forward_act). GELU is the exact
+ * (erf) form, GELU_TANH its tanh approximation, as torch.nn.functional.gelu with
+ * approximate="none" / "tanh". */
+typedef enum convnd_hip_activation {
+  CONVND_HIP_ACT_NONE = 0,
+  CONVND_HIP_ACT_RELU = 1,
+  CONVND_HIP_ACT_GELU = 2,
+  CONVND_HIP_ACT_GELU_TANH = 3
+} convnd_hip_activation;
+
 typedef enum convnd_hip_status {
   CONVND_HIP_SUCCESS = 0,
   CONVND_HIP_INVALID_ARGUMENT = 1, /* geometry/shape/dtype rejected; see convnd_hip_last_error */
@@ -87,6 +97,18 @@ size_t convnd_hip_forward_workspace_size(const convnd_hip_problem* problem,
 int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                        const void* input, const void* weight, const void* bias, void* output,
                        void* workspace, size_t workspace_size, void* stream);
+
+/* output = act(conv(input, weight) + bias), the activation applied in the GEMM epilogue
+ * (in fp32, fp64 for fp64) before the single rounding to the element type; with
+ * CONVND_HIP_ACT_NONE it is convnd_hip_forward. Kernels without a fused epilogue (the
+ * direct fallback) apply it in one more elementwise pass. Same workspace as
+ * convnd_hip_forward. No reference counterpart: the reference runs the activation as a
+ * separate PyTorch launch after its bias epilogue (src/torch_convnd/csrc/convnd.cpp:337-341;
+ * README.md:129-138 shows the Conv4d -> GELU -> Conv4d stack). */
+int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                           const void* input, const void* weight, const void* bias,
+                           void* output, int activation, void* workspace,
+                           size_t workspace_size, void* stream);
 
 /* Device scratch bytes convnd_hip_backward needs for the requested gradients. */
 size_t convnd_hip_backward_workspace_size(const convnd_hip_problem* problem,

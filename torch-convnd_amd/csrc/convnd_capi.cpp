@@ -1367,6 +1367,16 @@ const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_d
 int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                        const void* input, const void* weight, const void* bias, void* output,
                        void* workspace, size_t workspace_size, void* stream_ptr) {
+  return convnd_hip_forward_act(problem, dtype, input, weight, bias, output, CONVND_HIP_ACT_NONE,
+                                workspace, workspace_size, stream_ptr);
+}
+
+int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                           const void* input, const void* weight, const void* bias,
+                           void* output, int activation, void* workspace,
+                           size_t workspace_size, void* stream_ptr) {
+  if (activation < CONVND_HIP_ACT_NONE || activation > CONVND_HIP_ACT_GELU_TANH)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "activation must be none, relu, gelu or gelu_tanh");
   Geom g;
   int st = prepare(problem, dtype, &g);
   if (st != CONVND_HIP_SUCCESS) return st;
@@ -1377,9 +1387,12 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
     return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
                 "device workspace is smaller than convnd_hip_forward_workspace_size");
   if (!f.ig.ok) {
-    return hip_check(launch_direct_forward(dtype, to_direct(g), input, weight, bias, output,
-                                           stream),
-                     "direct forward kernel");
+    st = hip_check(launch_direct_forward(dtype, to_direct(g), input, weight, bias, output, stream),
+                   "direct forward kernel");
+    if (st != CONVND_HIP_SUCCESS || activation == CONVND_HIP_ACT_NONE) return st;
+    return hip_check(launch_activation(dtype, output, g.batch * g.out_channels * g.out_vol,
+                                       activation, stream),
+                     "activation pass");
   }
   char* ws = static_cast<char*>(workspace);
   IgemmArgs A = f.ig.args;
@@ -1403,6 +1416,7 @@ int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype
   A.wpk = wpk;
   A.bias = bias;
   A.out = output;
+  A.act = activation;
   const auto ev = timing_begin(0, stream);
   st = hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
                  "implicit GEMM forward");

@@ -337,6 +337,7 @@ void igemm_kernel(IgemmArgs A) {
   // least 4 positions on a unit output step they are adjacent: one 8-byte store for 16-bit
   // O, 16 bytes for float. Otherwise every position has its own offset and bounds check.
   O* out = static_cast<O*>(A.out);
+  const int act = A.act;
   const size_t chan0 = (size_t)n * A.cout_total + (size_t)g * A.cout_g;
   O* obox = out + box.out_origin;
   if (A.packed_ok && (flags & 2)) {
@@ -349,7 +350,7 @@ void igemm_kernel(IgemmArgs A) {
       for (int nb = 0; nb < NB; ++nb) {
         O v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(acc[mb][nb][i] + bias_v[mb]);
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], act));
         O* dst = orow + posout[(wn * NB + nb) * 16 + 4 * lg];
         if constexpr (sizeof(O) == 2) {
           uint2 w;
@@ -387,7 +388,8 @@ void igemm_kernel(IgemmArgs A) {
       for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (off[nb][i] >= 0) orow[off[nb][i]] = static_cast<O>(acc[mb][nb][i] + bias_v[mb]);
+          if (off[nb][i] >= 0)
+            orow[off[nb][i]] = static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], act));
       }
     }
   }

@@ -42,6 +42,7 @@ struct IgemmArgs {
   void* out;         // [N][cout_total][out_vol], channels-first
   int rank;
   int mode;          // 0: forward convolution, 1: input gradient of a forward convolution
+  int act;           // forward epilogue activation (convnd_hip_activation), 0 elsewhere
   int batch, groups, nphase;
   int cin_g, cout_g;          // GEMM reduction channels / output channels per group
   int cin_total, cout_total;
@@ -222,6 +223,23 @@ constexpr int kWgradCmBoxVol = 256;
 // Partial-convolution rescale: raw/out [batch][channels][positions], counts
 // [count_batch][count_channels][positions] (count_batch 1 or batch; count_channels divides
 // channels), window = valid samples of a full window.
+// Forward epilogue activations (convnd_hip_activation), applied to conv + bias in fp32
+// (fp64 for fp64 outputs) before the single rounding to the output type.
+template <typename F>
+__device__ inline F epilogue_act(F v, int act) {
+  if (act == CONVND_HIP_ACT_RELU) return v < F(0) ? F(0) : v;
+  if (act == CONVND_HIP_ACT_GELU) return F(0.5) * v * (F(1) + erf(v * F(0.70710678118654752440)));
+  if (act == CONVND_HIP_ACT_GELU_TANH) {
+    const F inner = F(0.79788456080286535588) * (v + F(0.044715) * v * v * v);
+    return F(0.5) * v * (F(1) + tanh(inner));
+  }
+  return v;
+}
+
+// y[i] = act(y[i]) for the n elements of y (outputs of the kernels without a fused epilogue).
+hipError_t launch_activation(convnd_hip_dtype dtype, void* y, int64_t n, int act,
+                             hipStream_t stream);
+
 // Partial-convolution counts: mask [batch][mask_channels][in...] -> counts
 // [batch][count_channels][out...], zero padding p, stride s, dilation d, kernel k.
 constexpr int kPartialMaxRank = 8;

@@ -299,4 +299,39 @@ hipError_t launch_partial_count(convnd_hip_dtype mask_dtype, const PartialCountA
   return hipErrorInvalidValue;
 }
 
+namespace {
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kThreads) void activation_kernel(T* __restrict__ y, int64_t n, int act) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    y[i] = static_cast<T>(epilogue_act(static_cast<F>(y[i]), act));
+}
+
+template <typename T, typename F>
+hipError_t launch_activation_typed(void* y, int64_t n, int act, hipStream_t stream) {
+  const int64_t blocks = std::min<int64_t>((n + kThreads - 1) / kThreads, 65536);
+  hipLaunchKernelGGL((activation_kernel<T, F>), dim3(blocks), dim3(kThreads), 0, stream,
+                     static_cast<T*>(y), n, act);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_activation(convnd_hip_dtype dtype, void* y, int64_t n, int act,
+                             hipStream_t stream) {
+  if (n <= 0 || act == CONVND_HIP_ACT_NONE) return hipSuccess;
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32:
+      return launch_activation_typed<float, float>(y, n, act, stream);
+    case CONVND_HIP_FLOAT64:
+      return launch_activation_typed<double, double>(y, n, act, stream);
+    case CONVND_HIP_FLOAT16:
+      return launch_activation_typed<_Float16, float>(y, n, act, stream);
+    case CONVND_HIP_BFLOAT16:
+      return launch_activation_typed<__bf16, float>(y, n, act, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
 }  // namespace convnd

@@ -218,6 +218,64 @@ Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& inpu
                                     groups, output_mask);
 }
 
+// torch_convnd::conv_nd_act: act(conv + bias) with the activation fused into the forward
+// epilogue (convnd_hip_forward_act); forward only (the Python frontend uses it where no
+// gradient is recorded).
+int activation_code(c10::string_view activation) {
+  if (activation == "none") return CONVND_HIP_ACT_NONE;
+  if (activation == "relu") return CONVND_HIP_ACT_RELU;
+  if (activation == "gelu") return CONVND_HIP_ACT_GELU;
+  if (activation == "gelu_tanh") return CONVND_HIP_ACT_GELU_TANH;
+  TORCH_CHECK(false, "activation must be 'none', 'relu', 'gelu' or 'gelu_tanh'");
+}
+
+at::Tensor conv_nd_act_device(const at::Tensor& input, const at::Tensor& weight,
+                              const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                              at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                              int64_t workspace_bytes, c10::string_view activation) {
+  const int act = activation_code(activation);
+  const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
+                    bias->size(0) == problem.output_channels &&
+                    bias->device() == input.device() &&
+                    bias->scalar_type() == input.scalar_type(),
+                "bias must match output channels, device and dtype");
+  }
+  const auto shape = output_shape(problem, input);
+  check_workspace(problem, input.element_size(), workspace_bytes);
+  const c10::OptionalDeviceGuard guard(input.device());
+  auto output = at::empty(shape, input.options());
+  if (problem.batch == 0) return output;
+  const auto x = input.contiguous();
+  const auto w = weight.contiguous();
+  std::optional<at::Tensor> b;
+  if (bias.has_value()) b = bias->contiguous();
+  const auto dtype = to_dtype(input.scalar_type());
+  const size_t ws_bytes = convnd_hip_forward_workspace_size(&problem, dtype);
+  auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
+  raise_status(convnd_hip_forward_act(&problem, dtype, x.const_data_ptr(), w.const_data_ptr(),
+                                      b.has_value() ? b->const_data_ptr() : nullptr,
+                                      output.mutable_data_ptr(), act,
+                                      ws_bytes ? workspace.mutable_data_ptr() : nullptr, ws_bytes,
+                                      current_stream(input)));
+  return output;
+}
+
+at::Tensor conv_nd_act_cpu(const at::Tensor& input, const at::Tensor& weight,
+                           const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                           at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                           int64_t workspace_bytes, c10::string_view activation) {
+  const int act = activation_code(activation);
+  auto y = conv_nd_cpu(input, weight, bias, stride, padding, dilation, groups, workspace_bytes);
+  if (act == CONVND_HIP_ACT_NONE) return y;
+  const auto ct = input.scalar_type() == at::kDouble ? at::kDouble : at::kFloat;
+  auto v = y.to(ct);
+  if (act == CONVND_HIP_ACT_RELU) v = at::relu(v);
+  else v = at::gelu(v, act == CONVND_HIP_ACT_GELU ? "none" : "tanh");
+  return v.to(input.scalar_type());
+}
+
 // torch_convnd::partial_rescale: shapes as convnd_hip_partial_rescale documents, raw
 // [N, C, *spatial], counts [1 or N, C or a divisor of C, *spatial] in float32 (float64 for
 // float64 raw), bias [C] or None.
@@ -336,6 +394,7 @@ TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
   library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_device);
   library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_device);
   library.impl("partial_count", &torch_convnd_hip::partial_count_device);
+  library.impl("conv_nd_act", &torch_convnd_hip::conv_nd_act_device);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {
@@ -347,6 +406,7 @@ TORCH_LIBRARY_IMPL(torch_convnd, CPU, library) {
   library.impl("conv_nd", &torch_convnd_hip::conv_nd_cpu);
   library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_cpu);
   library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_cpu);
+  library.impl("conv_nd_act", &torch_convnd_hip::conv_nd_act_cpu);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, AutocastCPU, library) {

@@ -124,6 +124,10 @@ def _fake_rescale(raw, counts, bias, window):
     return torch.empty_like(raw, memory_format=torch.contiguous_format)
 
 
+def _fake_act(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, activation):
+    return _fake_forward(input, weight, bias, stride, padding, dilation, groups, workspace_bytes)
+
+
 def _fake_count(mask, kernel, stride, padding, dilation, count_channels):
     out = [
         (n + 2 * p - d * (k - 1) - 1) // s + 1
@@ -168,6 +172,7 @@ def register_training() -> None:
     torch.library.register_fake("torch_convnd::conv_nd_backward")(_fake_backward)
     torch.library.register_fake("torch_convnd::partial_rescale")(_fake_rescale)
     torch.library.register_fake("torch_convnd::partial_count")(_fake_count)
+    torch.library.register_fake("torch_convnd::conv_nd_act")(_fake_act)
     torch.library.register_autograd(
         "torch_convnd::partial_rescale", _rescale_backward, setup_context=_setup_rescale
     )

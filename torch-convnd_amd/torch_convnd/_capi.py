@@ -26,6 +26,7 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_timing_read",
     "convnd_hip_partial_rescale",
     "convnd_hip_partial_count",
+    "convnd_hip_forward_act",
 )
 
 
@@ -82,6 +83,8 @@ def bind(library: ctypes.CDLL) -> ctypes.CDLL:
     library.convnd_hip_timing_enable.argtypes = [ctypes.c_int]
     library.convnd_hip_timing_read.restype = ctypes.c_int
     library.convnd_hip_timing_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)]
+    library.convnd_hip_forward_act.restype = ctypes.c_int
+    library.convnd_hip_forward_act.argtypes = [P, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, vp, sz, vp]
     library.convnd_hip_partial_count.restype = ctypes.c_int
     library.convnd_hip_partial_count.argtypes = [P, ctypes.c_int, vp, vp, vp]
     library.convnd_hip_partial_rescale.restype = ctypes.c_int

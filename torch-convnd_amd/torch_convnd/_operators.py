@@ -46,6 +46,13 @@ def _lazy_backward(
     )
 
 
+def _lazy_act(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, activation):
+    _load_for(input)
+    return torch.ops.torch_convnd.conv_nd_act.default(
+        input, weight, bias, stride, padding, dilation, groups, workspace_bytes, activation
+    )
+
+
 def _lazy_rescale(raw, counts, bias, window):
     _load_for(raw)
     return torch.ops.torch_convnd.partial_rescale.default(raw, counts, bias, window)
@@ -73,6 +80,12 @@ def ensure_native_definitions():
             "partial_rescale(Tensor raw, Tensor counts, Tensor? bias, float window) -> Tensor"
         )
         library.impl("partial_rescale", _lazy_rescale, "CompositeExplicitAutograd")
+        # Forward with the activation fused into the epilogue; no reference counterpart.
+        library.define(
+            "conv_nd_act(Tensor input, Tensor weight, Tensor? bias, int[] stride, int[] padding, "
+            "int[] dilation, int groups, int workspace_bytes, str activation) -> Tensor"
+        )
+        library.impl("conv_nd_act", _lazy_act, "CompositeExplicitAutograd")
         # Its counting pass (window sums of the validity map), gfx950 only.
         library.define(
             "partial_count(Tensor mask, int[] kernel, int[] stride, int[] padding, "

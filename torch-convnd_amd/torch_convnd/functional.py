@@ -74,8 +74,16 @@ def conv_nd(
     padding_mode: str = "zeros",
     workspace_bytes: int = DEFAULT_WORKSPACE_BYTES,
     backend: str = "auto",
+    activation: str | None = None,
 ) -> Tensor:
     """Full (non-separable) dense convolution over ``weight.ndim - 2`` spatial axes.
+
+    ``activation`` ("relu", "gelu", "gelu_tanh"; default None) applies that activation to
+    the result, as ``F.relu`` / ``F.gelu(approximate="none" | "tanh")`` would (an extension;
+    the reference has no such argument). On a ROCm GPU, outside autograd recording,
+    autocast and transforms, with symmetric zero padding, it is fused into the gfx950
+    forward epilogue (``torch_convnd::conv_nd_act``); otherwise it runs after the
+    convolution.
 
     ``backend="auto"`` uses PyTorch convolutions for ranks 1-3 and the gfx950 kernels for
     rank >= 4 on a ROCm GPU; ``native`` forces the gfx950 kernels, ``torch`` the portable
@@ -108,9 +116,48 @@ def conv_nd(
         return output.squeeze(0) if unbatched else output
     amp = _check_arguments(input, weight, stride, padding, dilation, groups)
     _check_bias(input, weight, bias, amp)
+    if activation is not None and activation not in _ACTIVATIONS:
+        raise ValueError(f"Invalid activation {activation!r}; expected 'relu', 'gelu' or 'gelu_tanh'")
     pairs = padding_pairs(padding, weight.shape[2:], stride, dilation)
+    if activation is not None and _fused_activation_ok(input, weight, bias, rank, backend, padding_mode, pairs, amp):
+        from . import _build
+
+        if not _build._LOADED:
+            _build.load_native()
+        output = torch.ops.torch_convnd.conv_nd_act(
+            input, weight, bias, list(stride), [left for left, _ in pairs], list(dilation), groups,
+            workspace_bytes, activation,
+        )
+        return output.squeeze(0) if unbatched else output
     output = _execute(input, weight, bias, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend)
+    if activation == "relu":
+        output = torch.nn.functional.relu(output)
+    elif activation is not None:
+        output = torch.nn.functional.gelu(output, approximate="tanh" if activation == "gelu_tanh" else "none")
     return output.squeeze(0) if unbatched else output
+
+
+_ACTIVATIONS = ("relu", "gelu", "gelu_tanh")
+
+
+def _fused_activation_ok(input, weight, bias, rank, backend, padding_mode, pairs, amp):
+    """Whether conv_nd's activation can run in the gfx950 epilogue (forward only)."""
+    from ._compat import is_compiling, is_rocm_device, transforms_active
+
+    if backend == "torch" or amp or input.dtype.is_complex or not is_rocm_device(input.device):
+        return False
+    if rank < 4 and backend != "native":
+        return False
+    if padding_mode != "zeros" or any_true([left != right for left, right in pairs]):
+        return False
+    if transforms_active() or is_compiling() or torch.jit.is_tracing():
+        return False
+    if input.dtype != weight.dtype or (bias is not None and bias.dtype != input.dtype):
+        return False
+    recording = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (input, weight, bias)
+    )
+    return not recording
 
 
 def _execute(input, weight, bias, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend):
