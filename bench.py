@@ -35,9 +35,44 @@ METRIC = "Conv4d fwd & fwd+bwd TFLOP/s at 1 GPU (bf16) + % of MFMA/HBM roofline"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD published)
 PEAK_HBM_GBS = 8000.0
 
+PEAK_FP32_TFLOPS = 157.3  # MI355X fp32 MFMA (AMD published)
+
 X_SHAPE = (2, 32, 16, 16, 16, 16)
 W_SHAPE = (64, 32, 3, 3, 3, 3)
 STRIDE, PADDING, DILATION, GROUPS = (1,) * 4, (1,) * 4, (1,) * 4, 1
+
+# x shape, w shape, stride, padding, dilation, groups, bias, dtype name,
+# and the rooflines reported for it (the first is the bound).
+CONFIGS = {
+    "C1": ((4, 2, 8, 8, 8, 16), (8, 2, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True, "float32",
+           ("fp32_mfma", "hbm")),
+    "C2": (X_SHAPE, W_SHAPE, STRIDE, PADDING, DILATION, GROUPS, True, "bfloat16", ("bf16_mfma",)),
+    "C3": ((1, 16, 12, 12, 12, 12, 12), (32, 16, 3, 3, 3, 3, 3), (1,) * 5, (1,) * 5, (1,) * 5, 1, True,
+           "bfloat16", ("bf16_mfma",)),
+    "C4_fp32": ((1, 8, 8, 8, 8, 8, 8, 8), (16, 8, 3, 3, 3, 3, 3, 3), (1,) * 6, (1,) * 6, (1,) * 6, 1, True,
+                "float32", ("fp32_mfma",)),
+    "C4_bf16": ((1, 8, 8, 8, 8, 8, 8, 8), (16, 8, 3, 3, 3, 3, 3, 3), (1,) * 6, (1,) * 6, (1,) * 6, 1, True,
+                "bfloat16", ("bf16_mfma",)),
+    "C5": ((2, 64, 24, 24, 24, 12), (128, 16, 3, 3, 3, 5), (2, 2, 2, 1), (1, 1, 1, 4), (1, 1, 1, 2), 4, False,
+           "bfloat16", ("bf16_mfma", "hbm")),
+}
+PEAKS = {"bf16_mfma": (PEAK_BF16_TFLOPS, "TFLOP/s"), "fp32_mfma": (PEAK_FP32_TFLOPS, "TFLOP/s"),
+         "hbm": (PEAK_HBM_GBS, "GB/s")}
+
+
+def config_work(name):
+    """(forward FLOP, forward bytes, forward+backward bytes) of a config: FLOP = 2 N P Co
+    (C/g) taps; bytes = |x| + |W| + |y| (+|b|) forward and |dY| + |x| + |W| + |dx| + |dW|
+    backward, in the config's element size."""
+    xs, ws, stride, padding, dilation, groups, bias, dtype, _ = CONFIGS[name]
+    out = [(n + 2 * p - d * (k - 1) - 1) // s + 1
+           for n, k, s, p, d in zip(xs[2:], ws[2:], stride, padding, dilation)]
+    el = 4 if dtype == "float32" else 2
+    nx, nw, ny = math.prod(xs), math.prod(ws), xs[0] * ws[0] * math.prod(out)
+    flops = 2 * xs[0] * math.prod(out) * ws[0] * ws[1] * math.prod(ws[2:])
+    fwd_bytes = el * (nx + nw + ny + (ws[0] if bias else 0))
+    bwd_bytes = el * (ny + nx + nw + nx + nw)
+    return flops, fwd_bytes, fwd_bytes + bwd_bytes
 
 
 def forward_flops(x_shape=X_SHAPE, w_shape=W_SHAPE):
@@ -113,7 +148,7 @@ def cpu_baseline(torch):
     same C2 problem, bf16 with fp32 partial accumulation; median of timed fwd+bwd runs."""
     from oracle import torch_path
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = cpu_threads()
     previous = torch.get_num_threads()
     torch.set_num_threads(cores)
     try:
@@ -126,29 +161,118 @@ def cpu_baseline(torch):
             y = torch_path.torch_backend_conv(x, w, b, STRIDE, PADDING, DILATION, GROUPS)
             torch.autograd.grad(y, (x, w, b), dy)
 
-        start = time.perf_counter()
-        run()  # warmup
-        first = time.perf_counter() - start
-        iterations = max(3, min(50, int(10.0 / max(first, 1e-3))))
-        times = []
-        for _ in range(iterations):
-            t0 = time.perf_counter()
-            run()
-            times.append(time.perf_counter() - t0)
-        median = statistics.median(times)
+        def forward():
+            with torch.no_grad():
+                torch_path.torch_backend_conv(x, w, b, STRIDE, PADDING, DILATION, GROUPS)
+
+        def median_s(fn, budget_s):
+            start = time.perf_counter()
+            fn()  # warmup
+            first = time.perf_counter() - start
+            iterations = max(3, min(50, int(budget_s / max(first, 1e-3))))
+            times = []
+            for _ in range(iterations):
+                t0 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t0)
+            return statistics.median(times), iterations
+
+        median, iterations = median_s(run, 10.0)
+        fwd_median, fwd_iterations = median_s(forward, 3.0)
         return {
             "value": round(3 * forward_flops() / median / 1e12, 6),
             "unit": "TFLOP/s",
             "cores": cores,
             "kind": "port",
+            "fwd_bwd_ms": round(median * 1e3, 2),
+            "fwd_ms": round(fwd_median * 1e3, 2),
+            "fwd_tflops": round(forward_flops() / fwd_median / 1e12, 6),
+            "affinity_cores": len(os.sched_getaffinity(0)),
             "sample": (
                 f"full C2 problem, fwd + full bwd (dx, dW, db) for a fixed dY, bf16, median of "
-                f"{iterations} runs after 1 warmup ({median * 1e3:.0f} ms each); "
-                f"torch {torch.__version__}, {_cpu_model()}"
+                f"{iterations} runs after 1 warmup ({median * 1e3:.0f} ms each); forward alone "
+                f"median of {fwd_iterations} runs; {cores} threads; torch {torch.__version__}, "
+                f"{_cpu_model()}"
             ),
         }
     finally:
         torch.set_num_threads(previous)
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: the cores this process may run on, capped by the
+    host's per-job thread allowance when OMP_NUM_THREADS sets one (a shared GPU box gives each
+    GPU's job a CPU share and exports it there)."""
+    cores = len(os.sched_getaffinity(0))
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        share = 0
+    return min(cores, share) if share > 0 else cores
+
+
+def measure_configs(torch, device, iterations=30, warmup=5):
+    """Every BASELINE config at full size through conv_nd(backend="native"): forward alone
+    and forward + full backward (dx, dW, db) for a resident synthetic dY; each the median of
+    `iterations` calls timed with their own HIP event pair after `warmup` calls (warm caches:
+    every working set is below the 256 MB Infinity Cache and nothing is flushed)."""
+    import torch_convnd
+    from torch_convnd import _build, _capi
+
+    lib = _build.hip_library()
+    out = {}
+    for name, (xs, ws, stride, padding, dilation, groups, bias, dtype_name, roofs) in CONFIGS.items():
+        dtype = getattr(torch, dtype_name)
+        x, w, b = make_inputs(torch, dtype, device, xs, ws)
+        if not bias:
+            b = None
+        leaves = [t.detach().requires_grad_() for t in (x, w, b) if t is not None]
+
+        def conv(*ts):
+            return torch_convnd.conv_nd(ts[0], ts[1], ts[2] if len(ts) > 2 else None, stride, padding,
+                                        dilation, groups, backend="native")
+
+        y = conv(*leaves)
+        dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(5)).to(dtype).to(device)
+        del y
+
+        def fwd():
+            with torch.no_grad():
+                conv(*(x, w, b)[: len(leaves)])
+
+        def step():
+            torch.autograd.grad(conv(*leaves), leaves, dy)
+
+        times = {}
+        for label, fn in (("fwd", fwd), ("fwd_bwd", step)):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            pairs = []
+            for _ in range(iterations):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                pairs.append((e0, e1))
+            torch.cuda.synchronize()
+            times[label] = statistics.median(a.elapsed_time(b_) for a, b_ in pairs)
+        flops, fwd_bytes, step_bytes = config_work(name)
+        entry = {"dtype": dtype_name,
+                 "plans": list(_capi.plan_names(lib, xs, ws, stride, padding, dilation, groups, dtype))}
+        for label, work_flops, work_bytes in (("fwd", flops, fwd_bytes), ("fwd_bwd", 3 * flops, step_bytes)):
+            ms = times[label]
+            tflops = work_flops / (ms * 1e-3) / 1e12
+            entry[f"{label}_ms"] = round(ms, 4)
+            entry[f"{label}_tflops"] = round(tflops, 2)
+            for roof in roofs:
+                peak, unit = PEAKS[roof]
+                achieved = tflops if unit == "TFLOP/s" else work_bytes / (ms * 1e-3) / 1e9
+                entry[f"{label}_frac_{roof}"] = round(achieved / peak, 4)
+        entry["bound"] = roofs[0]
+        out[name] = entry
+        del x, w, b, leaves, dy
+    return out
 
 
 def _cpu_model():
@@ -273,6 +397,8 @@ def main():
     parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-configs", action="store_true",
+                        help="skip the per-config fwd / fwd+bwd timings of C1-C5")
     parser.add_argument(
         "--calibration-copy-mib", type=int, default=0,
         help="first run a plain elementwise copy of this many MiB three times (the known-size "
@@ -453,7 +579,17 @@ def main():
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
         },
         "correctness_gate_worst": round(gate, 4),
+        "timing": {
+            "value": "wall clock between synchronisations over the timed steps, no events",
+            "fwd_ms": "wall clock of forward-only calls, no events",
+            "roofline": "HIP events recorded around every launch of the kernel on its launch "
+            "stream in a separate region, averaged",
+            "configs": "median of 30 calls after 5 warmups, one HIP event pair per call",
+            "cache": "warm: every working set is below the 256 MB Infinity Cache; no flush",
+        },
     }
+    if not args.no_configs:
+        result["configs"] = measure_configs(torch, device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)

@@ -46,6 +46,22 @@ def oracle_backward(dy, x, w, stride, padding, dilation, groups):
     return torch.from_numpy(dx), torch.from_numpy(dw), torch.from_numpy(db)
 
 
+def error_stats(actual, expected, dtype):
+    """Measured error against the tolerance of ``dtype``: max |a-e|, the largest
+    |a-e| / (atol + rtol*|e|) (<= 1 passes), relative L2, and the atol used."""
+    tol = TOLERANCE[dtype]
+    a = actual.detach().double().cpu()
+    e = expected.detach().double().cpu()
+    rms = e.pow(2).mean().sqrt().item() if e.numel() else 0.0
+    atol = tol["atol"] * max(1.0, rms) if "atol" in tol else tol["atol_rms"] * rms
+    err = (a - e).abs()
+    ratio = (err / (atol + tol["rtol"] * e.abs())).max().item() if e.numel() else 0.0
+    norm = e.norm().item()
+    rel = (a - e).norm().item() / norm if norm > 0 else 0.0
+    return {"max_abs": err.max().item() if e.numel() else 0.0, "ratio": ratio, "rel_l2": rel,
+            "atol": atol, "rms": rms}
+
+
 def assert_close(actual, expected, dtype, what=""):
     """Elementwise |a-e| <= atol + rtol*|e| plus a relative-L2 bound."""
     tol = TOLERANCE[dtype]

@@ -71,8 +71,15 @@ def test_full_size_parity(name, dtype):
 
     ref_in = [t.double().requires_grad_() if t is not None else None for t in (x, w, b)]
     ref_y = helpers.frames_reference(*ref_in, stride, padding, dilation, groups)
-    helpers.assert_close(y, ref_y, dtype, f"{name} forward")
     ref_grads = torch.autograd.grad(ref_y, [t for t in ref_in if t is not None], dy.double())
+    # One line per tensor with the measured error (ratio: worst |err| / (atol + rtol |ref|)).
+    for what, got, want in zip(("forward", "grad_input", "grad_weight", "grad_bias"), (y, *grads),
+                               (ref_y, *ref_grads)):
+        st = helpers.error_stats(got, want, dtype)
+        print(f"[errors] {name} {str(dtype)[6:]} {what} max_abs={st['max_abs']:.3e} "
+              f"ratio={st['ratio']:.3f} rel_l2={st['rel_l2']:.3e} atol={st['atol']:.3e} "
+              f"rms={st['rms']:.3e}", flush=True)
+    helpers.assert_close(y, ref_y, dtype, f"{name} forward")
     for what, got, want in zip(("grad_input", "grad_weight", "grad_bias"), grads, ref_grads):
         helpers.assert_close(got, want, dtype, f"{name} {what}")
     if dtype in (torch.bfloat16, torch.float16):

@@ -73,7 +73,9 @@ def test_vmap_over_input_batch(dtype):
     g = torch.Generator().manual_seed(3)
     xs = torch.randn(3, 2, 8, 4, 3, 5, 6, generator=g).to(dtype).cuda()
     _, w, b = _problem(dtype)
-    # The rule folds the vmap batch into the op's batch (a different plan than per slice).
+    # conv_nd under vmap takes the portable decomposition (functorch transforms are active);
+    # it is compared with per-slice native calls. The operator's own vmap rule is covered by
+    # test_gpu_contract.test_vmap_through_the_operator_rule.
     got = torch.func.vmap(lambda x: _conv(x, w, b))(xs)
     want = torch.stack([_conv(x, w, b) for x in xs])
     helpers.assert_close(got, want, dtype, "vmap over the input batch")

@@ -284,3 +284,40 @@ def test_count_kernel_matches_ones_convolution(mask_dtype, geometry):
     assert got.dtype == (torch.float64 if mask_dtype == torch.float64 else torch.float32)
     tol = 1e-12 if mask_dtype == torch.float64 else 1e-5
     torch.testing.assert_close(got.cpu().double(), torch.from_numpy(want), rtol=tol, atol=tol)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bool, torch.uint8, torch.int64, torch.float16, torch.float64],
+                         ids=lambda d: str(d).split(".")[1])
+@pytest.mark.parametrize("input_dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_masks_of_any_real_dtype_gpu(dtype, input_dtype):
+    # The reference's tests/test_partial_api.py:194-204 on the gfx950 path (rank 4): a mask of
+    # any real dtype marks the same samples as its float32 copy, bit for bit.
+    print(f"[partial] mask dtype {dtype} input {input_dtype}", flush=True)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 3, 5, 4, 6, 7, generator=g).to(input_dtype).cuda()
+    w = torch.randn(4, 3, 3, 3, 3, 3, generator=g).to(input_dtype).cuda()
+    holes = (torch.rand(2, 1, 5, 4, 6, 7, generator=g) > 0.4).cuda()
+    expected = partial_conv_nd(x, w, padding=1, mask=holes.float(), backend="native")
+    actual = partial_conv_nd(x, w, padding=1, mask=holes.to(dtype), backend="native")
+    assert torch.equal(actual.output, expected.output) and torch.equal(actual.mask, expected.mask)
+    assert actual.mask.dtype == input_dtype
+
+
+@pytest.mark.parametrize("act", ["relu", "gelu", "gelu_tanh"])
+def test_partial_padding_mode_applies_activation(act):
+    # conv_nd(padding_mode="partial", activation=...) is the activation of the rescaled
+    # partial convolution; an unknown activation is rejected on that path too.
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(1, 2, 4, 4, 4, 5, generator=g, dtype=torch.float64)
+    w = torch.randn(3, 2, 3, 3, 3, 3, generator=g, dtype=torch.float64)
+    b = torch.randn(3, generator=g, dtype=torch.float64)
+    plain = conv_nd(x, w, b, padding=1, padding_mode="partial", backend="torch")
+    fn = {"relu": torch.nn.functional.relu,
+          "gelu": lambda t: torch.nn.functional.gelu(t),
+          "gelu_tanh": lambda t: torch.nn.functional.gelu(t, approximate="tanh")}[act]
+    got = conv_nd(x, w, b, padding=1, padding_mode="partial", backend="torch", activation=act)
+    torch.testing.assert_close(got, fn(plain), rtol=0, atol=0)
+    assert plain.min() < 0
+    with pytest.raises(ValueError, match="Invalid activation"):
+        conv_nd(x, w, b, padding=1, padding_mode="partial", activation="bogus")

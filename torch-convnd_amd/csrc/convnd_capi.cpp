@@ -13,6 +13,7 @@
 #include <cstring>
 #include <limits>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -1214,45 +1215,127 @@ BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool g
   return cached_plan(cache, plan_key(g, dt, kind), [&] { return make_backward(g, dt, gi, gw, gb); });
 }
 
-// Geometry tables of an implicit-GEMM plan in device memory: built on the host and copied
-// once per (plan, device) on first use, then shared by every call with that plan (they are
-// never written again, so concurrent calls on any stream may read them). The copy is
-// synchronous, so the first call of a geometry must not be under stream capture. The
-// memory lives as long as the process.
-template <typename Build>
-const void* device_tables(const std::string& key, size_t bytes, Build&& build) {
-  static std::mutex lock;
-  static std::unordered_map<std::string, const void*> map;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  const std::string k = key + std::string(reinterpret_cast<const char*>(&dev), sizeof(dev));
-  std::lock_guard<std::mutex> guard(lock);
-  auto it = map.find(k);
-  if (it != map.end()) return it->second;
-  std::vector<unsigned char> host(bytes, 0);
-  build(host.data());
-  void* d = nullptr;
-  if (hipMalloc(&d, host.size()) != hipSuccess) return nullptr;
-  if (hipMemcpy(d, host.data(), host.size(), hipMemcpyHostToDevice) != hipSuccess) {
-    (void)hipFree(d);
-    return nullptr;
+// Geometry tables of a plan in device memory, one copy per (plan, device), shared by every
+// call with that plan (never written again, so calls on any stream may read them).
+//   * Fill: the host-built bytes go to a pinned host buffer and from there to the device with
+//     hipMemcpyAsync on the calling stream, so no call synchronises the host; an event
+//     recorded after the copy orders calls on other streams behind it until it has completed.
+//   * Bounds: at most kTableEntries entries and kTableBytes bytes per process; the least
+//     recently used entry is dropped when a new one would exceed either. An entry's memory is
+//     released with its last holder (calls hold their entry until their kernels are enqueued;
+//     hipFree / hipHostFree wait for queued work that may still read it).
+//   * Graph capture: a miss while the calling stream captures is an error (the copy would only
+//     run when the graph is launched); the first call of a geometry runs outside capture, as
+//     torch.cuda.graph's warm-up does.
+constexpr size_t kTableEntries = 128;
+constexpr size_t kTableBytes = size_t{256} << 20;
+
+struct DeviceTables {
+  void* dev = nullptr;
+  void* host = nullptr;
+  size_t bytes = 0;
+  hipEvent_t ready = nullptr;
+  hipStream_t filled_on = nullptr;
+  bool done = false;
+  uint64_t last_use = 0;
+  ~DeviceTables() {
+    if (ready != nullptr) (void)hipEventDestroy(ready);
+    if (dev != nullptr) (void)hipFree(dev);
+    if (host != nullptr) (void)hipHostFree(host);
   }
-  map.emplace(k, d);
-  return d;
+};
+using TablesRef = std::shared_ptr<DeviceTables>;
+
+struct TableCache {
+  std::mutex lock;
+  std::unordered_map<std::string, TablesRef> map;
+  size_t bytes = 0;
+  uint64_t clock = 0;
+};
+
+// Never destroyed: entries alive at exit are left to process teardown rather than freed after
+// the HIP runtime has shut down.
+TableCache& table_cache() {
+  static TableCache* cache = new TableCache();
+  return *cache;
 }
 
-const void* igemm_device_tables(const std::string& key, const IgemmArgs& A) {
-  return device_tables(key, static_cast<size_t>(A.tab_bytes),
+template <typename Build>
+TablesRef device_tables(const std::string& key, size_t bytes, hipStream_t stream, Build&& build) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: hipGetDevice failed");
+    return nullptr;
+  }
+  const std::string k = key + std::string(reinterpret_cast<const char*>(&dev), sizeof(dev));
+  TableCache& c = table_cache();
+  std::lock_guard<std::mutex> guard(c.lock);
+  auto it = c.map.find(k);
+  if (it != c.map.end()) {
+    DeviceTables& e = *it->second;
+    e.last_use = ++c.clock;
+    if (!e.done && stream != e.filled_on) {
+      const hipError_t q = hipEventQuery(e.ready);
+      if (q == hipErrorNotReady) (void)hipGetLastError();  // not an error: clear the record
+      if (q == hipSuccess) {
+        e.done = true;
+      } else if (q != hipErrorNotReady || hipStreamWaitEvent(stream, e.ready, 0) != hipSuccess) {
+        fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: waiting for their upload failed");
+        return nullptr;
+      }
+    }
+    return it->second;
+  }
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess ||
+      capture != hipStreamCaptureStatusNone) {
+    fail(CONVND_HIP_UNSUPPORTED,
+         "the first call of a convolution geometry cannot be captured into a graph; run it "
+         "once outside capture first");
+    return nullptr;
+  }
+  // Drop least recently used entries until the new one fits both bounds.
+  while (!c.map.empty() && (c.map.size() >= kTableEntries || c.bytes + bytes > kTableBytes)) {
+    auto victim = c.map.begin();
+    for (auto j = c.map.begin(); j != c.map.end(); ++j)
+      if (j->second->last_use < victim->second->last_use) victim = j;
+    c.bytes -= victim->second->bytes;
+    c.map.erase(victim);
+  }
+  auto e = std::make_shared<DeviceTables>();
+  e->bytes = bytes;
+  if (hipHostMalloc(&e->host, bytes, hipHostMallocDefault) != hipSuccess ||
+      hipMalloc(&e->dev, bytes) != hipSuccess ||
+      hipEventCreateWithFlags(&e->ready, hipEventDisableTiming) != hipSuccess) {
+    fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: device allocation failed");
+    return nullptr;
+  }
+  std::memset(e->host, 0, bytes);
+  build(static_cast<unsigned char*>(e->host));
+  if (hipMemcpyAsync(e->dev, e->host, bytes, hipMemcpyHostToDevice, stream) != hipSuccess ||
+      hipEventRecord(e->ready, stream) != hipSuccess) {
+    fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: upload failed");
+    return nullptr;
+  }
+  e->filled_on = stream;
+  e->last_use = ++c.clock;
+  c.bytes += bytes;
+  c.map.emplace(k, e);
+  return e;
+}
+
+TablesRef igemm_device_tables(const std::string& key, const IgemmArgs& A, hipStream_t stream) {
+  return device_tables(key, static_cast<size_t>(A.tab_bytes), stream,
                        [&](unsigned char* h) { igemm_build_tables(A, h); });
 }
 
-const void* wgrad_device_tables(const std::string& key, const WgradArgs& A) {
-  return device_tables(key, static_cast<size_t>(A.tab_bytes),
+TablesRef wgrad_device_tables(const std::string& key, const WgradArgs& A, hipStream_t stream) {
+  return device_tables(key, static_cast<size_t>(A.tab_bytes), stream,
                        [&](unsigned char* h) { wgrad_build_tables(A, h); });
 }
 
-const void* wgrad_cm_device_tables(const std::string& key, const WgradCmArgs& A) {
-  return device_tables(key, static_cast<size_t>(A.tab_bytes),
+TablesRef wgrad_cm_device_tables(const std::string& key, const WgradCmArgs& A, hipStream_t stream) {
+  return device_tables(key, static_cast<size_t>(A.tab_bytes), stream,
                        [&](unsigned char* h) { wgrad_cm_build_tables(A, h); });
 }
 
@@ -1398,9 +1481,9 @@ int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype d
   IgemmArgs A = f.ig.args;
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
-  A.tables = igemm_device_tables(plan_key(g, dtype, 0), A);
-  if (A.tables == nullptr)
-    return fail(CONVND_HIP_LAUNCH_FAILED, "implicit GEMM geometry tables: device allocation failed");
+  const TablesRef tables = igemm_device_tables(plan_key(g, dtype, 0), A, stream);
+  if (tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+  A.tables = tables->dev;
   // Input staging, weight packing and the geometry tables in one launch.
   PrologueParts pp;
   pp.sa = &f.ig.stage;
@@ -1474,12 +1557,12 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   WgradCmArgs CA{};
   float* sums = fused_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
   PrologueParts pp;
+  TablesRef dx_tables, dw_tables;  // held until the kernels that read them are enqueued
   if (mfma_dx) {
     DA = b.dg.args;
-    DA.tables = igemm_device_tables(plan_key(g, dtype, 64), DA);
-    if (DA.tables == nullptr)
-      return fail(CONVND_HIP_LAUNCH_FAILED,
-                  "implicit GEMM geometry tables: device allocation failed");
+    dx_tables = igemm_device_tables(plan_key(g, dtype, 64), DA, stream);
+    if (dx_tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+    DA.tables = dx_tables->dev;
     DA.in = ws + b.off_dy_stage;
     DA.wpk = ws + b.off_wpk;
     DA.bias = nullptr;
@@ -1496,10 +1579,9 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   if (mfma_dw && b.wg.cm) {
     WA = b.wg.args;
     CA = b.wg.cm_args;
-    CA.tables = wgrad_cm_device_tables(plan_key(g, dtype, 66), CA);
-    if (CA.tables == nullptr)
-      return fail(CONVND_HIP_LAUNCH_FAILED,
-                  "weight-gradient geometry tables: device allocation failed");
+    dw_tables = wgrad_cm_device_tables(plan_key(g, dtype, 66), CA, stream);
+    if (dw_tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+    CA.tables = dw_tables->dev;
     CA.x = ws + b.off_x_stage;
     CA.dy = grad_output;
     pp.pp = &b.wg.ppad;
@@ -1519,10 +1601,9 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     }
   } else if (mfma_dw) {
     WA = b.wg.args;
-    WA.tables = wgrad_device_tables(plan_key(g, dtype, 65), WA);
-    if (WA.tables == nullptr)
-      return fail(CONVND_HIP_LAUNCH_FAILED,
-                  "weight-gradient geometry tables: device allocation failed");
+    dw_tables = wgrad_device_tables(plan_key(g, dtype, 65), WA, stream);
+    if (dw_tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+    WA.tables = dw_tables->dev;
     WA.x = ws + b.off_x_stage;
     WA.dy = grad_output;
     WA.partial = reinterpret_cast<float*>(ws + b.off_partial);

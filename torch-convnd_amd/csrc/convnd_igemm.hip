@@ -406,9 +406,7 @@ hipError_t igemm_dispatch(int mb, int nb, const IgemmArgs& a, size_t lds, hipStr
 #define CONVND_IGEMM_CASE(MBV, NBV, WMV)                                                 \
   if (mb == MBV && nb == NBV && a.wm == WMV) {                                           \
     auto fn = igemm_kernel<T, O, MBV, NBV, WMV>;                                         \
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),              \
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,     \
-                                         static_cast<int>(lds));                         \
+    hipError_t err = ensure_dynamic_lds<igemm_kernel<T, O, MBV, NBV, WMV>>(lds);         \
     if (err != hipSuccess) return err;                                                   \
     hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                             \
     return hipGetLastError();                                                            \

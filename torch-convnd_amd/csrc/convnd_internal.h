@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -266,6 +267,28 @@ struct PlanarPadArgs {
   int in_vol, pvol;
   unsigned src_bytes;  // size of the source tensor (loads past it read zero)
 };
+
+// Raises Kernel's dynamic-LDS limit on the current device to at least `bytes`. The attribute
+// stays set for the process, so launches after the first one on a device make no runtime call.
+constexpr int kMaxDevices = 64;
+template <auto Kernel>
+hipError_t ensure_dynamic_lds(size_t bytes) {
+  static std::atomic<int> limit[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const int want = static_cast<int>(bytes);
+  if (dev >= 0 && dev < kMaxDevices && limit[dev].load(std::memory_order_relaxed) >= want)
+    return hipSuccess;
+  err = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, want);
+  if (err == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    int seen = limit[dev].load(std::memory_order_relaxed);
+    while (seen < want && !limit[dev].compare_exchange_weak(seen, want)) {
+    }
+  }
+  return err;
+}
 
 // ---- kernel launchers (defined in the .hip files) -------------------------------------
 

@@ -349,9 +349,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_reduce_kernel(const f32x4* par
 template <typename T, int MB, int STG, bool MULTI>
 hipError_t wgrad_launch(const WgradArgs& a, size_t lds, hipStream_t s) {
   auto fn = wgrad_kernel<T, MB, STG, MULTI>;
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(lds));
+  hipError_t err = ensure_dynamic_lds<wgrad_kernel<T, MB, STG, MULTI>>(lds);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(fn, dim3(a.npc * a.ncq * a.groups * a.mgroups), dim3(kThreads), lds, s, a);
   return hipGetLastError();

@@ -331,9 +331,7 @@ hipError_t wgrad_cm_dispatch(int mb, const WgradCmArgs& a, size_t lds, hipStream
 #define CONVND_WGRAD_CM_CASE(MBV, NTV)                                               \
   if (mb == MBV && a.nt == NTV) {                                                    \
     auto fn = wgrad_cm_kernel<T, MBV, NTV>;                                          \
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),          \
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                         static_cast<int>(lds));                     \
+    hipError_t err = ensure_dynamic_lds<wgrad_cm_kernel<T, MBV, NTV>>(lds);          \
     if (err != hipSuccess) return err;                                               \
     hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                         \
     return hipGetLastError();                                                        \

@@ -105,19 +105,21 @@ def conv_nd(
     if not isinstance(padding, str):
         padding = _tuple(padding, rank, "padding")
     _check_options(padding_mode, workspace_bytes, backend)
+    if activation is not None and activation not in _ACTIVATIONS:
+        raise ValueError(f"Invalid activation {activation!r}; expected 'relu', 'gelu' or 'gelu_tanh'")
     if padding_mode == "partial":
-        # Zero padding with partial-convolution rescaling: the mask-free partial convolution.
+        # Zero padding with partial-convolution rescaling: the mask-free partial convolution,
+        # then the activation on the rescaled result.
         from .partial import partial_forward
 
         output, _ = partial_forward(
             input, weight, bias, stride, padding, dilation, groups, mask=None, multi_channel=False,
             padding_mode="zeros", workspace_bytes=workspace_bytes, backend=backend, need_update=False,
         )
+        output = _apply_activation(output, activation)
         return output.squeeze(0) if unbatched else output
     amp = _check_arguments(input, weight, stride, padding, dilation, groups)
     _check_bias(input, weight, bias, amp)
-    if activation is not None and activation not in _ACTIVATIONS:
-        raise ValueError(f"Invalid activation {activation!r}; expected 'relu', 'gelu' or 'gelu_tanh'")
     pairs = padding_pairs(padding, weight.shape[2:], stride, dilation)
     if activation is not None and _fused_activation_ok(input, weight, bias, rank, backend, padding_mode, pairs, amp):
         from . import _build
@@ -130,14 +132,20 @@ def conv_nd(
         )
         return output.squeeze(0) if unbatched else output
     output = _execute(input, weight, bias, stride, pairs, dilation, groups, padding_mode, workspace_bytes, backend)
-    if activation == "relu":
-        output = torch.nn.functional.relu(output)
-    elif activation is not None:
-        output = torch.nn.functional.gelu(output, approximate="tanh" if activation == "gelu_tanh" else "none")
+    output = _apply_activation(output, activation)
     return output.squeeze(0) if unbatched else output
 
 
 _ACTIVATIONS = ("relu", "gelu", "gelu_tanh")
+
+
+def _apply_activation(output, activation):
+    """The activation as a separate PyTorch op (paths without the fused epilogue)."""
+    if activation == "relu":
+        return torch.nn.functional.relu(output)
+    if activation is not None:
+        return torch.nn.functional.gelu(output, approximate="tanh" if activation == "gelu_tanh" else "none")
+    return output
 
 
 def _fused_activation_ok(input, weight, bias, rank, backend, padding_mode, pairs, amp):

@@ -29,6 +29,8 @@ from ._geometry import DEFAULT_WORKSPACE_BYTES, _tuple, any_true, has_rank
 from ._padding import padding_pairs
 
 _REAL = {torch.complex64: torch.float32, torch.complex128: torch.float64, torch.complex32: torch.float16}
+# Mask dtypes the gfx950 count kernel reads directly.
+_COUNT_MASK_DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
 class PartialConvOutput(NamedTuple):
@@ -288,9 +290,11 @@ def partial_forward(
     if counts is None and _use_native_count(valid_source, pairs, padding_mode, backend):
         # One gfx950 pass: window sums (and the per-group channel sums of multi-channel
         # masks) straight from the mask, in its own dtype.
+        # The kernel reads float16/bfloat16/float32/float64 maps; bool and integer masks
+        # (any real dtype is a valid mask) are converted to the count type first.
         source = valid_source
-        if exact == torch.float64 and source.dtype != torch.float64:
-            source = source.to(torch.float64)
+        if (exact == torch.float64 and source.dtype != torch.float64) or source.dtype not in _COUNT_MASK_DTYPES:
+            source = source.to(exact)
         counts = torch.ops.torch_convnd.partial_count(
             source, list(kernel), list(stride), [left for left, _ in pairs], list(dilation), count_channels
         )
