@@ -134,3 +134,27 @@ def test_validation_messages():
         _op_backward(y[:, :1], x, w, (1,) * 4, (0,) * 4, (1,) * 4, 1, [True] * 3)
     with pytest.raises(RuntimeError, match="bias must match"):
         _op_forward(x, w, torch.randn(3), (1,) * 4, (0,) * 4, (1,) * 4, 1)
+
+
+def test_vmap_rule_of_the_operator():
+    # torch.func.vmap over the operator itself runs its registered rule (the reference's
+    # src/torch_convnd/_autograd.py:93-134): an input-only vmap batch folded into the
+    # operator's batch, batched weights one slice at a time, and an empty vmap batch.
+    g = torch.Generator().manual_seed(61)
+    xs = torch.randn(3, 2, 3, 4, 3, 5, 4, generator=g, dtype=torch.float64)
+    w = torch.randn(5, 3, 2, 3, 2, 2, generator=g, dtype=torch.float64)
+    b = torch.randn(5, generator=g, dtype=torch.float64)
+    args = ([1] * 4, [1, 0, 1, 1], [1] * 4, 1, 1 << 30)
+    op = torch.ops.torch_convnd.conv_nd.default
+    got = torch.func.vmap(lambda x: op(x, w, b, *args))(xs)
+    assert got.shape == (3, 2, 5, 5, 1, 6, 5)
+    for i in range(3):
+        want = helpers.oracle_forward(xs[i], w, b, (1,) * 4, (1, 0, 1, 1), (1,) * 4, 1)
+        helpers.assert_close(got[i], want, torch.float64, f"vmap input slice {i}")
+    ws = torch.stack([w, 2 * w])
+    got = torch.func.vmap(lambda ww: op(xs[0], ww, b, *args))(ws)
+    for i, ww in enumerate((w, 2 * w)):
+        want = helpers.oracle_forward(xs[0], ww, b, (1,) * 4, (1, 0, 1, 1), (1,) * 4, 1)
+        helpers.assert_close(got[i], want, torch.float64, f"vmap weight slice {i}")
+    empty = torch.func.vmap(lambda x: op(x, w, b, *args))(xs[:0])
+    assert empty.shape == (0, 2, 5, 5, 1, 6, 5)

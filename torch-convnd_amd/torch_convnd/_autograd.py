@@ -95,7 +95,7 @@ def _backward_backward(ctx, ggi, ggw, ggb):
 
 def _vmap_forward(info, in_dims, input, weight, bias, stride, padding, dilation, groups, workspace_bytes):
     conv = torch.ops.torch_convnd.conv_nd.default
-    x_dim, w_dim, b_dim = in_dims
+    x_dim, w_dim, b_dim = in_dims[:3]  # one entry per operator argument; the rest are ints
     if x_dim is not None and w_dim is None and b_dim is None:
         # Only the input is batched: fold the vmap batch into the convolution batch.
         moved = input.movedim(x_dim, 0)
