@@ -158,6 +158,24 @@ int convnd_hip_partial_rescale(convnd_hip_dtype dtype, const void* raw, const vo
                                int64_t positions, int64_t count_batch, int64_t count_channels,
                                double window, void* stream);
 
+/* Bytes of the device scratch array convnd_hip_forward_noalloc uses, one per GPU (64 MiB). */
+#define CONVND_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* convnd_hip_forward without a workspace and without any device allocation: the staged
+ * input, the packed weights and the geometry tables live in a file-scope device array of
+ * CONVND_HIP_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until the process
+ * ends; the call itself makes no hipMalloc / hipFree. Problems whose scratch needs exceed it
+ * fail with CONVND_HIP_WORKSPACE_TOO_SMALL and a message naming the size. Every call on one
+ * GPU shares that GPU's array and leaves its contents behind (each call rewrites all it
+ * reads), so calls that overlap on one GPU (other streams, other threads) race: serialise
+ * them. Same results as convnd_hip_forward (the same kernels).
+ * No counterpart in the reference (src/torch_convnd/csrc/convnd.cpp:326 allocates per call):
+ * for callers that cannot allocate device memory -- code under stream capture, serving loops
+ * that must not allocate, harnesses that forbid hipMalloc. */
+int convnd_hip_forward_noalloc(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                               const void* input, const void* weight, const void* bias,
+                               void* output, void* stream);
+
 /* Which kernel family convnd_hip_forward / convnd_hip_backward would use, as a short
  * string ("mfma", "direct", ...) for diagnostics and tests. `which`: 0 forward,
  * 1 input gradient, 2 weight gradient. No reference counterpart (diagnostic only). */

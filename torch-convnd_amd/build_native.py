@@ -34,6 +34,7 @@ HIP_SOURCES = (
     "convnd_wgrad.hip",
     "convnd_wgrad_cm.hip",
     "convnd_partial.hip",
+    "convnd_static.hip",
     "convnd_capi.cpp",
 )
 OFFLOAD_ARCH = os.environ.get("TORCH_CONVND_OFFLOAD_ARCH", "gfx950")

@@ -1390,6 +1390,54 @@ int prepare(const convnd_hip_problem* problem, convnd_hip_dtype dtype, Geom* g) 
   return CONVND_HIP_SUCCESS;
 }
 
+// The forward launch sequence over a prepared geometry and plan. The implicit GEMM reads
+// its geometry tables from `tables` (a device copy), or, when that is null, from
+// `tables_at`, which the table kernel fills first. `ws` holds the workspace regions of f.
+// `timed`: bracket the GEMM with the diagnostic timing events.
+int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, const void* input,
+                const void* weight, const void* bias, void* output, int activation, char* ws,
+                const void* tables, void* tables_at, bool timed, hipStream_t stream) {
+  int st;
+  if (!f.ig.ok) {
+    st = hip_check(launch_direct_forward(dtype, to_direct(g), input, weight, bias, output, stream),
+                   "direct forward kernel");
+    if (st != CONVND_HIP_SUCCESS || activation == CONVND_HIP_ACT_NONE) return st;
+    return hip_check(launch_activation(dtype, output, g.batch * g.out_channels * g.out_vol,
+                                       activation, stream),
+                     "activation pass");
+  }
+  IgemmArgs A = f.ig.args;
+  if (tables == nullptr) {
+    st = hip_check(launch_igemm_tables(A, tables_at, stream), "geometry tables");
+    if (st != CONVND_HIP_SUCCESS) return st;
+    tables = tables_at;
+  }
+  A.tables = tables;
+  void* staged = ws + f.off_stage;
+  void* wpk = ws + f.off_wpk;
+  // Input staging and weight packing in one launch.
+  PrologueParts pp;
+  pp.sa = &f.ig.stage;
+  pp.src = input;
+  pp.staged = staged;
+  pp.batch = g.batch;
+  pp.ig = &A;
+  pp.w = weight;
+  pp.wpk = wpk;
+  st = hip_check(launch_prologue(dtype, pp, stream), "input staging and weight packing");
+  if (st != CONVND_HIP_SUCCESS) return st;
+  A.in = staged;
+  A.wpk = wpk;
+  A.bias = bias;
+  A.out = output;
+  A.act = activation;
+  const auto ev = timed ? timing_begin(0, stream) : std::pair<hipEvent_t, hipEvent_t>{};
+  st = hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
+                 "implicit GEMM forward");
+  if (timed) timing_end(ev, stream);
+  return st;
+}
+
 }  // namespace
 }  // namespace convnd
 
@@ -1461,7 +1509,7 @@ int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype d
   if (activation < CONVND_HIP_ACT_NONE || activation > CONVND_HIP_ACT_GELU_TANH)
     return fail(CONVND_HIP_INVALID_ARGUMENT, "activation must be none, relu, gelu or gelu_tanh");
   Geom g;
-  int st = prepare(problem, dtype, &g);
+  const int st = prepare(problem, dtype, &g);
   if (st != CONVND_HIP_SUCCESS) return st;
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   if (g.batch == 0) return CONVND_HIP_SUCCESS;
@@ -1469,42 +1517,41 @@ int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype d
   if (workspace_size < f.bytes || (f.bytes > 0 && workspace == nullptr))
     return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
                 "device workspace is smaller than convnd_hip_forward_workspace_size");
-  if (!f.ig.ok) {
-    st = hip_check(launch_direct_forward(dtype, to_direct(g), input, weight, bias, output, stream),
-                   "direct forward kernel");
-    if (st != CONVND_HIP_SUCCESS || activation == CONVND_HIP_ACT_NONE) return st;
-    return hip_check(launch_activation(dtype, output, g.batch * g.out_channels * g.out_vol,
-                                       activation, stream),
-                     "activation pass");
+  TablesRef tables;  // held until the kernels that read them are enqueued
+  if (f.ig.ok) {
+    tables = igemm_device_tables(plan_key(g, dtype, 0), f.ig.args, stream);
+    if (tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
   }
-  char* ws = static_cast<char*>(workspace);
-  IgemmArgs A = f.ig.args;
-  void* staged = ws + f.off_stage;
-  void* wpk = ws + f.off_wpk;
-  const TablesRef tables = igemm_device_tables(plan_key(g, dtype, 0), A, stream);
-  if (tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
-  A.tables = tables->dev;
-  // Input staging, weight packing and the geometry tables in one launch.
-  PrologueParts pp;
-  pp.sa = &f.ig.stage;
-  pp.src = input;
-  pp.staged = staged;
-  pp.batch = g.batch;
-  pp.ig = &A;
-  pp.w = weight;
-  pp.wpk = wpk;
-  st = hip_check(launch_prologue(dtype, pp, stream), "input staging and weight packing");
+  return run_forward(g, dtype, f, input, weight, bias, output, activation,
+                     static_cast<char*>(workspace), tables ? tables->dev : nullptr, nullptr, true,
+                     stream);
+}
+
+int convnd_hip_forward_noalloc(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                               const void* input, const void* weight, const void* bias,
+                               void* output, void* stream_ptr) {
+  Geom g;
+  const int st = prepare(problem, dtype, &g);
   if (st != CONVND_HIP_SUCCESS) return st;
-  A.in = staged;
-  A.wpk = wpk;
-  A.bias = bias;
-  A.out = output;
-  A.act = activation;
-  const auto ev = timing_begin(0, stream);
-  st = hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
-                 "implicit GEMM forward");
-  timing_end(ev, stream);
-  return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (g.batch == 0) return CONVND_HIP_SUCCESS;
+  const ForwardSetup f = setup_forward(g, dtype);
+  if (!f.ig.ok)  // the direct kernels use no scratch
+    return run_forward(g, dtype, f, input, weight, bias, output, CONVND_HIP_ACT_NONE, nullptr,
+                       nullptr, nullptr, false, stream);
+  // Scratch: [geometry tables | the workspace regions of convnd_hip_forward].
+  const size_t tab = align_up(static_cast<size_t>(f.ig.args.tab_bytes));
+  if (tab + f.bytes > kNoAllocScratchBytes)
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "convnd_hip_forward_noalloc: this problem needs " + std::to_string(tab + f.bytes) +
+                    " bytes of device scratch, more than its fixed " +
+                    std::to_string(kNoAllocScratchBytes) + " bytes; use convnd_hip_forward");
+  void* scratch = nullptr;
+  const int sst = hip_check(noalloc_scratch(&scratch), "device scratch address");
+  if (sst != CONVND_HIP_SUCCESS) return sst;
+  char* base = static_cast<char*>(scratch);
+  return run_forward(g, dtype, f, input, weight, bias, output, CONVND_HIP_ACT_NONE, base + tab,
+                     nullptr, base, false, stream);
 }
 
 int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,

@@ -1,8 +1,9 @@
 // Tap geometry of the implicit GEMM, shared by the host planner and the kernels.
 //
 // The planner builds the geometry tables (IgemmArgs::tables) once per plan with the
-// functions below and copies them to device memory owned by the plan; the kernels only
-// read them. Everything here is plain integer arithmetic, compiled for host and device.
+// functions below and uploads them to device memory it keeps per plan and device; the
+// allocation-free forward builds the implicit-GEMM tables on the device with the same
+// per-entry code. The kernels only read them. Plain integer arithmetic throughout.
 #pragma once
 
 #include <vector>
@@ -205,30 +206,44 @@ inline size_t igemm_table_layout(IgemmArgs& A) {
   return at;
 }
 
-// Fills the geometry tables (host memory of igemm_table_layout(A) bytes).
-inline void igemm_build_tables(const IgemmArgs& A, unsigned char* tab) {
+// The geometry tables as independent entries, so that the host (igemm_build_tables) and a
+// device kernel fill them with the same code. Entry e in order:
+//   [0, nphase*4)            one (phase, lane group): its tap row, tail entry and packing map;
+//   [.., + nphase*boxes)     one IgemmBox record;
+//   [.., + box_vol)          one box-position record;
+//   [.., + rows)             one halo-row record.
+__host__ __device__ inline long igemm_table_entries(const IgemmArgs& A) {
+  return (long)A.nphase * 4 + (long)A.nphase * A.boxes + A.box_vol + A.rows;
+}
+
+__host__ __device__ inline void igemm_table_entry(const IgemmArgs& A, unsigned char* tab, long e) {
   const int R = A.rank;
   const int cb = A.coord_bits;
-  for (int phase = 0; phase < A.nphase; ++phase) {
+  if (e < (long)A.nphase * 4) {
+    const int phase = static_cast<int>(e / 4), lg = static_cast<int>(e % 4);
     AxisTaps ax[kFastRank];
     const int ntaps = phase_axes(A, phase, ax);
     const int kf = ntaps * A.cc / 32, kcn = (ntaps * A.cc + 31) / 32;
-    for (int lg = 0; lg < 4; ++lg) {
-      int* row = reinterpret_cast<int*>(tab + A.tab_taps) + (phase * 4 + lg) * A.tap_row;
-      for (int k = 0; k < A.tap_row; ++k)
-        row[k] = kf > 0 ? igemm_tap_offset(A, ax, ntaps, k < kf ? k : kf - 1, lg) : 0;
-      reinterpret_cast<int*>(tab + A.tab_tail)[phase * 4 + lg] =
-          kcn > kf ? igemm_tap_offset(A, ax, ntaps, kf, lg) : -1;
-      for (int k = 0; k < A.kc_max; ++k) {
-        int* e = reinterpret_cast<int*>(tab + A.tab_pack) + ((phase * A.kc_max + k) * 4 + lg) * 2;
-        igemm_pack_entry(A, ax, ntaps, k, lg, &e[0], &e[1]);
-      }
+    int* row = reinterpret_cast<int*>(tab + A.tab_taps) + (phase * 4 + lg) * A.tap_row;
+    for (int k = 0; k < A.tap_row; ++k)
+      row[k] = kf > 0 ? igemm_tap_offset(A, ax, ntaps, k < kf ? k : kf - 1, lg) : 0;
+    reinterpret_cast<int*>(tab + A.tab_tail)[phase * 4 + lg] =
+        kcn > kf ? igemm_tap_offset(A, ax, ntaps, kf, lg) : -1;
+    for (int k = 0; k < A.kc_max; ++k) {
+      int* p = reinterpret_cast<int*>(tab + A.tab_pack) + ((phase * A.kc_max + k) * 4 + lg) * 2;
+      igemm_pack_entry(A, ax, ntaps, k, lg, &p[0], &p[1]);
     }
-    for (int bx = 0; bx < A.boxes; ++bx)
-      reinterpret_cast<IgemmBox*>(tab + A.tab_box)[phase * A.boxes + bx] =
-          igemm_box_entry(A, phase, bx);
+    return;
   }
-  for (int q = 0; q < A.box_vol; ++q) {
+  e -= (long)A.nphase * 4;
+  if (e < (long)A.nphase * A.boxes) {
+    const int phase = static_cast<int>(e / A.boxes), bx = static_cast<int>(e % A.boxes);
+    reinterpret_cast<IgemmBox*>(tab + A.tab_box)[phase * A.boxes + bx] = igemm_box_entry(A, phase, bx);
+    return;
+  }
+  e -= (long)A.nphase * A.boxes;
+  if (e < A.box_vol) {
+    const int q = static_cast<int>(e);
     int qq = q, halo = 0, orel = 0, ostr = 1;
     unsigned long long c = 0;
     for (int a = R - 1; a >= 0; --a) {
@@ -239,13 +254,16 @@ inline void igemm_build_tables(const IgemmArgs& A, unsigned char* tab) {
       ostr *= A.out_size[a];
       c |= static_cast<unsigned long long>(qa) << (a * cb);
     }
-    int* e = reinterpret_cast<int*>(tab + A.tab_pos) + q * 4;
-    e[0] = halo * 16;
-    e[1] = orel;
-    e[2] = static_cast<int>(c & 0xffffffffu);
-    e[3] = static_cast<int>(c >> 32);
+    int* p = reinterpret_cast<int*>(tab + A.tab_pos) + q * 4;
+    p[0] = halo * 16;
+    p[1] = orel;
+    p[2] = static_cast<int>(c & 0xffffffffu);
+    p[3] = static_cast<int>(c >> 32);
+    return;
   }
-  for (int r = 0; r < A.rows; ++r) {
+  e -= A.box_vol;
+  if (e < A.rows) {
+    const int r = static_cast<int>(e);
     int rem = r, lpos = 0, irel = 0, istr = A.last_size;
     unsigned long long h = 0;
     for (int a = R - 2; a >= 0; --a) {
@@ -256,12 +274,18 @@ inline void igemm_build_tables(const IgemmArgs& A, unsigned char* tab) {
       istr *= A.in_size[a];
       h |= static_cast<unsigned long long>(ha) << (a * 8);
     }
-    int* e = reinterpret_cast<int*>(tab + A.tab_rows) + r * 4;
-    e[0] = lpos;
-    e[1] = irel;
-    e[2] = static_cast<int>(h & 0xffffffffu);
-    e[3] = static_cast<int>(h >> 32);
+    int* p = reinterpret_cast<int*>(tab + A.tab_rows) + r * 4;
+    p[0] = lpos;
+    p[1] = irel;
+    p[2] = static_cast<int>(h & 0xffffffffu);
+    p[3] = static_cast<int>(h >> 32);
   }
+}
+
+// Fills the geometry tables (host memory of igemm_table_layout(A) bytes).
+inline void igemm_build_tables(const IgemmArgs& A, unsigned char* tab) {
+  const long n = igemm_table_entries(A);
+  for (long e = 0; e < n; ++e) igemm_table_entry(A, tab, e);
 }
 
 }  // namespace convnd

@@ -395,6 +395,12 @@ hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& 
                                hipStream_t stream, const float* bias_sums = nullptr,
                                int64_t nsum = 0, int64_t channels = 0, void* db = nullptr);
 hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream);
+// Allocation-free forward: bytes of the per-device static scratch array, its device address
+// on the current device (looked up once per device), and the kernel that writes the implicit
+// GEMM's geometry tables (igemm_table_layout(a) bytes) into device memory.
+constexpr size_t kNoAllocScratchBytes = CONVND_HIP_NOALLOC_SCRATCH_BYTES;
+hipError_t noalloc_scratch(void** ptr);
+hipError_t launch_igemm_tables(const IgemmArgs& a, void* tables, hipStream_t stream);
 hipError_t launch_reduce_partials(convnd_hip_dtype dtype, const float* partial, void* out,
                                   int64_t count, int64_t parts, hipStream_t stream);
 
