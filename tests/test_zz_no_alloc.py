@@ -55,7 +55,8 @@ def _forward_pair(lib, x_shape, w_shape, stride, padding, dilation, groups, bias
 @pytest.mark.parametrize(
     ("first", "second", "dtype"),
     [
-        # C2 at full size, then a smaller C2-like problem (other geometry tables, fewer boxes).
+        # C2 at full size, then a smaller C2-like problem (other geometry tables, fewer boxes);
+        # the input is staged straight from the caller's tensor (direct staging).
         (((2, 32, 16, 16, 16, 16), (64, 32, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True),
          ((1, 32, 5, 6, 4, 8), (64, 32, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True), torch.bfloat16),
         # Split-precision fp32 with stride, dilation and groups, then a smaller one.
@@ -88,16 +89,18 @@ def test_noalloc_direct_kernel_and_empty_batch(lib):
 
 
 def test_noalloc_rejects_problems_beyond_its_scratch(lib):
-    # 64 MiB of scratch: a bf16 input of 4 x 64 x 32^4 elements (512 MiB when staged) on the
-    # MFMA plan is refused before anything is launched (real buffers all the same).
+    # 64 MiB of scratch: 1024 -> 1024 channels with a 3^4 kernel pack 164 MiB of weight
+    # fragments, so the MFMA plan is refused before anything is launched (real buffers all the
+    # same).
     print("[noalloc] size limit", flush=True)
-    x_shape, w_shape = (4, 64, 32, 32, 32, 32), (64, 64, 3, 3, 3, 3)
+    x_shape, w_shape = (1, 1024, 4, 4, 4, 4), (1024, 1024, 3, 3, 3, 3)
     one = (1,) * 4
     assert _capi.plan_names(lib, x_shape, w_shape, one, one, one, 1, torch.bfloat16)[0] == "mfma"
+    problem = _capi.Problem.make(x_shape, w_shape, one, one, one, 1)
+    assert lib.convnd_hip_forward_workspace_size(ctypes.byref(problem), _capi.BFLOAT16) > _capi.NOALLOC_SCRATCH_BYTES
     x = torch.zeros(x_shape, dtype=torch.bfloat16, device="cuda")
     w = torch.zeros(w_shape, dtype=torch.bfloat16, device="cuda")
-    y = torch.zeros((4, 64, 32, 32, 32, 32), dtype=torch.bfloat16, device="cuda")
-    problem = _capi.Problem.make(x_shape, w_shape, one, one, one, 1)
+    y = torch.zeros((1, 1024, 4, 4, 4, 4), dtype=torch.bfloat16, device="cuda")
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     st = lib.convnd_hip_forward_noalloc(ctypes.byref(problem), _capi.BFLOAT16, _ptr(x), _ptr(w), None,
                                         _ptr(y), stream)

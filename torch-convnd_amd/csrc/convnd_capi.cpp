@@ -227,6 +227,8 @@ AxisPhaseHost grad_axis(const Geom& g, int a, int r) {
 struct IgemmPlan {
   bool ok = false;
   int mb = 1, nb = 4;
+  int waves = 4;  // waves per workgroup
+  int occ = 1;    // resident workgroups per CU
   IgemmArgs args{};
   size_t lds = 0;
   size_t wpk_elems = 0;
@@ -343,11 +345,12 @@ int64_t choose_pitches(int R, const int* box, const int* sigma, const int* hext,
 
 // Optional launch-plan override for tuning sweeps, read once per process from
 // CONVND_HIP_FWD_PLAN / CONVND_HIP_DGRAD_PLAN / CONVND_HIP_WGRAD_PLAN, e.g.
-// "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8" (the weight gradient reads box and occ).
+// "mb=2,nb=8,wm=2,cc=16,box=2x2x8x8,ds=1" (ds: direct staging of the implicit GEMM's halo
+// from the channels-first operand, 0 or 1; the weight gradient reads box, occ and cm).
 // Any subset of the keys may be given; the planner then searches only plans matching it and
 // ignores the override when none does.
 struct PlanFilter {
-  int mb = 0, nb = 0, wm = 0, cc = 0, occ = 0, cm = -1;
+  int mb = 0, nb = 0, wm = 0, cc = 0, occ = 0, cm = -1, ds = -1, nbuf = 0, waves = 0;
   std::vector<int> box;
   bool active = false;
 };
@@ -381,6 +384,9 @@ PlanFilter parse_filter(const char* text) {
         if (key == "cc") f.cc = v;
         if (key == "occ") f.occ = v;
         if (key == "cm") f.cm = v;
+        if (key == "ds") f.ds = v;
+        if (key == "nbuf") f.nbuf = v;
+        if (key == "waves") f.waves = v;
       }
     }
     pos = end + 1;
@@ -447,6 +453,25 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
   }
   const int mtiles = (gemm_cout + 15) / 16;
   const PlanFilter& filter = plan_filter(mode);
+  // Direct staging (16-bit data): the kernel reads the caller's channels-first tensor and
+  // double-buffers the chunk halos; otherwise (split-precision fp32, or halos too large to
+  // double-buffer) a prologue copies the operand octet-major first, which costs its HBM
+  // traffic (read + write of the operand) ahead of the kernel.
+  // Staging variants {direct, halo buffers}: direct with two alternating buffers (staging
+  // overlapped with the MFMAs) or one, or the octet-major copy with one.
+  std::vector<std::pair<bool, int>> staging_options;
+  // Measured on MI355X: two buffers (chunks of one octet to fit occupancy 2) have not beaten
+  // one so far, so they are tried only on request (nbuf=2).
+  // Input gradients of strided convolutions (several stride phases) measured slower with
+  // direct staging: octet copy there unless requested.
+  if (is_half(dt) && filter.ds != 0 && (nphase == 1 || filter.ds == 1)) {
+    if (filter.nbuf == 2) staging_options.push_back({true, 2});
+    if (filter.nbuf != 2) staging_options.push_back({true, 1});
+  }
+  if (filter.ds != 1 && filter.nbuf != 2) staging_options.push_back({false, 1});
+  const double copy_clk =
+      2.0 * 2.0 * double(g.batch) * (mode == 0 ? g.in_vol : g.out_vol) * gemm_cin * g.groups *
+      (2.4e9 / 5.0e12);
 
   // Channel chunk: 8, 16, 32 or 64 channels dividing gemm_cin (octet planes per chunk are
   // a power of two).
@@ -464,9 +489,15 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
   };
   std::map<std::vector<int>, PitchMemo> pitch_memo;
   double best = -1.0;
-  for (const auto& tile : kTiles) {
-    const int mb = tile[0], nb = tile[1], wm = tile[2], wn = 4 / wm;
-    if (!igemm_tile_supported(mb, nb, wm)) continue;
+  for (const auto& staging : staging_options)
+  for (const auto& tile : kTiles)
+  for (const int waves : {4, 8}) {
+    const bool direct = staging.first;
+    const int nbuf = staging.second;
+    const int mb = tile[0], nb = tile[1], wm = tile[2], wn = waves / wm;
+    // Eight-wave workgroups (one per CU, two waves per SIMD) exist for direct staging.
+    if ((waves == 8 && !direct) || !igemm_tile_supported(mb, nb, wm, waves)) continue;
+    if (filter.waves && filter.waves != waves) continue;
     // Cover the output channels without idle waves: the waves' M extent may exceed the
     // channel count by less than one wave's share.
     if ((wm - 1) * mb >= mtiles || (mb > 1 && (mb / 2) >= mtiles)) continue;
@@ -505,6 +536,10 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
           useful *= J[a];
         }
         if (noct * hvol * 16 > kLdsBudget) return;
+        // Direct staging moves whole runs of 8 last-axis elements per task and writes them
+        // row by row; with halo rows shorter than two runs its tasks are mostly partial and
+        // its LDS writes collide (measured about twice as costly as the octet copy there).
+        const double short_rows = direct && hext[R - 1] < 16 ? 2.0 : 1.0;
         // Row validity masks hold 64 halo coordinates per axis; coordinates are packed in
         // bytes in the row table.
         for (int a = 0; a < R; ++a)
@@ -523,8 +558,8 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         const int64_t plane_pos = hit->second.plane_pos;
         const int64_t plane_bytes = align_up(plane_pos * 16);
         const int tap_row = static_cast<int>((kc + kTapPad + 3) / 4 * 4);
-        const int64_t lds = noct * plane_bytes + align_up(rows * 8) + align_up(box_vol * 4) +
-                            align_up(16 * tap_row);
+        const int64_t lds = nbuf * noct * plane_bytes + align_up(rows * 8) +
+                            align_up(box_vol * 4) + align_up(16 * tap_row);
         if (rows > (int64_t{1} << 20)) return;
         // Epilogue stores: a lane writes 4 consecutive positions at once when they are
         // adjacent in the output (box rows of at least 4, unit output step on the last axis).
@@ -533,7 +568,10 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         const bool grid_ok = boxes <= (int64_t{1} << 30) && g.groups * mgroups <= 65535 &&
                              g.batch * nphase <= 65535;
         if (lds > kLdsBudget || !grid_ok) return;
-        const int occ = occupancy(lds, reg_waves);
+        // Resident workgroups per CU (an eight-wave one fills the register budget of two waves
+        // per SIMD by itself) and waves per SIMD on the CU.
+        const int occ = waves == 8 ? 1 : occupancy(lds, reg_waves);
+        const int simd_waves = occ * waves / 4;
         // Clocks per K32 step of one workgroup: MFMA issue on each SIMD, B-fragment LDS
         // reads (4 cycles per wave read when conflict-free; cc == 8 puts four taps of one
         // plane in a K32 step, which costs a second cycle), A-fragment reads through the
@@ -542,25 +580,41 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         const double mfma = mb * nb * 16.0;
         const double ldsc = 4.0 * nb * 4.0 * lds_factor;
         const double l1 = 4.0 * mb * 1024.0 / 64.0;
-        const double step = std::max(mfma * occ, std::max(ldsc, l1) * occ) / occ;
-        const double eff = occ >= 2 ? 0.75 : 0.55;
+        const double step = std::max(mfma, std::max(ldsc, l1)) * (waves / 4);
+        // Issue efficiency of the main loop: two waves per SIMD hide each other's load
+        // latency; one wave per SIMD stalls on its own loads (measured on MI355X: the same
+        // input-gradient problem ran 1.7x slower with one wave per SIMD).
+        const double eff = simd_waves >= 2 ? 0.75 : 0.35;
         const double core = double(nchunk) * kc * step / eff;
-        const double stage = double(nchunk) * (noct * hvol * 16.0 / 64.0 + 1500.0);
+        // Direct staging: only the first chunk's halo is exposed (the rest is loaded during
+        // the previous chunk's MFMAs), each chunk still pays its LDS writes and a barrier.
+        const double stage =
+            short_rows *
+            (nbuf == 2 ? (noct * hvol * 16.0 / 64.0 + 1500.0) + double(nchunk) * (noct * hvol * 16.0 / 256.0 + 300.0)
+                       : double(nchunk) * (noct * hvol * 16.0 / 64.0 + 1500.0));
         // Epilogue: one store per lane of `run` output values.
         const double out_bytes = double(wm) * mb * 16 * box_vol * out_es;
         const double epilogue = out_bytes / (4.0 * out_es * run) + 400.0;
-        const double per_wg = core + (occ >= 2 ? 0.25 : 1.0) * stage + epilogue;
+        // CU time of one round of resident workgroups: their MFMA work shares the SIMDs;
+        // a second resident workgroup hides most of the other's staging, but the two do not
+        // get even issue (measured on MI355X: the younger one finishes its main loop about a
+        // quarter later, alone); a lone workgroup (eight waves, or four at one wave per SIMD)
+        // exposes its staging.
+        const double exposed = occ >= 2 ? 0.25 * stage * occ : stage;
+        const double per_round = occ * core + exposed + occ * epilogue + (occ >= 2 ? 0.1 * core : 0.0);
         const int64_t wgs = boxes * g.groups * mgroups * g.batch * nphase;
         const int64_t slots = 256 * occ;
         const double rounds = double((wgs + slots - 1) / slots);
         // Work in padded boxes beyond the tensor is paid for as well (included via boxes).
-        const double cost = rounds * per_wg * (occ >= 2 ? 1.0 : 1.0);
+        const double cost = rounds * per_round + (direct ? 0.0 : copy_clk);
         (void)useful;
         if (best >= 0 && cost >= best) return;
         best = cost;
         plan.ok = true;
         plan.mb = mb;
         plan.nb = nb;
+        plan.waves = waves;
+        plan.occ = occ;
         plan.cost = cost;
         plan.conflict = conflict;
         IgemmArgs& A = plan.args;
@@ -616,6 +670,10 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.packed_ok = run == 4 ? 1 : 0;
         A.coord_bits = R <= 4 ? 16 : 8;
         A.tap_row = tap_row;
+        A.direct = direct ? 1 : 0;
+        A.nbuf = nbuf;
+        A.waves = waves;
+        A.nrun = (hext[R - 1] + 14) / 8;  // bound; the exact count is set below
         plan.lds = static_cast<size_t>(lds);
       });
     }
@@ -631,6 +689,22 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
       return plan;
     }
     A.in_bytes = static_cast<int>(static_cast<uint32_t>(plan.staged_elems * 2));
+    // Direct staging reads the caller's tensor (the same element count): no copy to stage.
+    // Runs of 8 per halo row: the most any box along the last axis needs, in any phase.
+    if (A.direct) {
+      plan.staged_elems = 0;
+      int most = 0;
+      for (int phase = 0; phase < A.nphase; ++phase) {
+        for (int bx = 0; bx < A.nbox[R - 1]; ++bx) {
+          const IgemmBox B = igemm_box_entry(A, phase, bx);
+          const int corg = B.corg;
+          const int jlo = corg > 0 ? (corg >> 3) : 0;
+          const int clast = std::min(corg + A.hlast, A.last_size) - 1;
+          if (clast >= jlo * 8) most = std::max(most, (clast >> 3) - jlo + 1);
+        }
+      }
+      A.nrun = std::max(most, 1);
+    }
     // Geometry tables (built and copied to the device once per plan and device).
     const size_t at = igemm_table_layout(A);
     if (at > (size_t)kI32Safe) {
@@ -1415,18 +1489,21 @@ int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, co
   A.tables = tables;
   void* staged = ws + f.off_stage;
   void* wpk = ws + f.off_wpk;
-  // Input staging and weight packing in one launch.
+  // Weight packing, and the octet-major input copy unless the kernel stages the halo
+  // straight from the input, in one launch.
   PrologueParts pp;
-  pp.sa = &f.ig.stage;
-  pp.src = input;
-  pp.staged = staged;
-  pp.batch = g.batch;
+  if (!A.direct) {
+    pp.sa = &f.ig.stage;
+    pp.src = input;
+    pp.staged = staged;
+    pp.batch = g.batch;
+  }
   pp.ig = &A;
   pp.w = weight;
   pp.wpk = wpk;
   st = hip_check(launch_prologue(dtype, pp, stream), "input staging and weight packing");
   if (st != CONVND_HIP_SUCCESS) return st;
-  A.in = staged;
+  A.in = A.direct ? input : staged;
   A.wpk = wpk;
   A.bias = bias;
   A.out = output;
@@ -1585,8 +1662,9 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     }
     return CONVND_HIP_SUCCESS;
   }
-  // The bias gradient rides on the channels-last copy of grad_output when the input
-  // gradient makes one; otherwise it reads grad_output on its own.
+  // The bias gradient's channel sums come from the backward prologue launch when the input
+  // gradient runs on MFMA (its octet-major grad_output copy writes them, or, with direct
+  // staging, a sums part of the same launch); otherwise grad_output is reduced on its own.
   const bool fused_bias = gb && gi && b.dg.ok && is_half(dtype);
   if (gb && !fused_bias) {
     st = hip_check(launch_grad_bias(dtype, g.batch, g.out_channels, g.out_vol, grad_output,
@@ -1610,15 +1688,25 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     dx_tables = igemm_device_tables(plan_key(g, dtype, 64), DA, stream);
     if (dx_tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
     DA.tables = dx_tables->dev;
-    DA.in = ws + b.off_dy_stage;
+    DA.in = DA.direct ? grad_output : static_cast<const void*>(ws + b.off_dy_stage);
     DA.wpk = ws + b.off_wpk;
     DA.bias = nullptr;
     DA.out = grad_input;
-    pp.sa = &b.dg.stage;
-    pp.src = grad_output;
-    pp.staged = ws + b.off_dy_stage;
-    pp.sums = sums;
-    pp.batch = g.batch;
+    if (DA.direct) {
+      if (sums != nullptr) {
+        pp.sum_src = grad_output;
+        pp.sum_out = sums;
+        pp.sum_batch = g.batch;
+        pp.sum_channels = g.out_channels;
+        pp.sum_volume = g.out_vol;
+      }
+    } else {
+      pp.sa = &b.dg.stage;
+      pp.src = grad_output;
+      pp.staged = ws + b.off_dy_stage;
+      pp.sums = sums;
+      pp.batch = g.batch;
+    }
     pp.ig = &DA;
     pp.w = weight;
     pp.wpk = ws + b.off_wpk;
@@ -1677,10 +1765,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   // The bias gradient from the staging sums rides in the weight-gradient reduction's launch
   // when there is one.
   const bool bias_in_reduce = fused_bias && mfma_dw;
+  const int64_t nsum = mfma_dx && DA.direct ? prologue_sum_blocks(g.batch, g.out_vol)
+                                            : octet_sum_blocks(g.batch, g.out_vol);
   if (fused_bias && !bias_in_reduce) {
-    st = hip_check(launch_grad_bias_from_sums(dtype, sums,
-                                              octet_sum_blocks(g.batch, g.out_vol),
-                                              g.out_channels, grad_bias, stream),
+    st = hip_check(launch_grad_bias_from_sums(dtype, sums, nsum, g.out_channels, grad_bias, stream),
                    "bias gradient");
     if (st != CONVND_HIP_SUCCESS) return st;
   }
@@ -1709,15 +1797,13 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       if (b.wg.cm) {
         st = hip_check(bias_in_reduce
                            ? launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream,
-                                                    sums, octet_sum_blocks(g.batch, g.out_vol),
-                                                    g.out_channels, grad_bias)
+                                                    sums, nsum, g.out_channels, grad_bias)
                            : launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream),
                        "weight-gradient reduction");
       } else {
         st = hip_check(bias_in_reduce
                            ? launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream, sums,
-                                                 octet_sum_blocks(g.batch, g.out_vol),
-                                                 g.out_channels, grad_bias)
+                                                 nsum, g.out_channels, grad_bias)
                            : launch_wgrad_reduce(dtype, b.wg.mb, WA, grad_weight, stream),
                        "weight-gradient reduction");
       }
@@ -1756,8 +1842,10 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
              std::to_string(A.nphase) + ",\"cc\":" + std::to_string(A.cc) +
              ",\"nchunk\":" + std::to_string(A.nchunk) + ",\"kc_max\":" +
              std::to_string(A.kc_max) + ",\"mgroups\":" + std::to_string(A.mgroups) +
-             ",\"lds\":" + std::to_string(p.lds) + ",\"occupancy\":" +
-             std::to_string(occupancy(static_cast<int64_t>(p.lds), igemm_reg_waves(p.mb, p.nb))) +
+             ",\"lds\":" + std::to_string(p.lds) + ",\"direct\":" + std::to_string(A.direct) +
+             ",\"nbuf\":" + std::to_string(A.nbuf) + ",\"nrun\":" + std::to_string(A.nrun) +
+             ",\"occupancy\":" +
+             std::to_string(p.occ) + ",\"waves\":" + std::to_string(p.waves) +
              ",\"workgroups\":" +
              std::to_string((int64_t)A.boxes * A.groups * A.mgroups * A.batch * A.nphase) + "}";
     }

@@ -2,8 +2,8 @@
 // for the stride phases of the input gradient.
 //
 //   * A workgroup owns a box of output positions (a power-of-two extent per axis) and a
-//     group of output channels. Its four waves are arranged WM along the channels and 4/WM
-//     along the positions; each wave accumulates MB x NB fragments of 16 x 16.
+//     group of output channels. Its W waves (4 or 8) are arranged WM along the channels and
+//     W/WM along the positions; each wave accumulates MB x NB fragments of 16 x 16.
 //   * The GEMM input is staged per call into octet-major planes (8 channels = 16 bytes per
 //     position). The region the box reads through every tap (the halo) is copied once per
 //     channel chunk into LDS: one plane per octet of 8 channels, 16 bytes per position,
@@ -42,10 +42,11 @@ constexpr int igemm_waves = MB * NB >= 32 ? 1 : 2;
 // T: GEMM operand type; O: output and bias type (T, or float for split-precision fp32).
 // Every per-axis quantity comes from the geometry tables (IgemmArgs::tables), so the
 // kernel body is the same for every rank.
-template <typename T, typename O, int MB, int NB, int WM>
-__global__ __launch_bounds__(kThreads)
+template <typename T, typename O, int MB, int NB, int WM, bool DS, int W>
+__global__ __launch_bounds__(64 * W)
 __attribute__((amdgpu_waves_per_eu(igemm_waves<MB, NB>, igemm_waves<MB, NB>)))
 void igemm_kernel(IgemmArgs A) {
+  constexpr int kWT = 64 * W;  // threads of the workgroup
   using M = Mfma16<T>;
   using frag = typename M::frag;
   extern __shared__ __align__(16) unsigned char lds[];
@@ -77,24 +78,25 @@ void igemm_kernel(IgemmArgs A) {
   const int KC = box.kc;
   const int KF = box.kf;
 
-  // LDS: [octet planes | rows: input offset (-1 outside the input), LDS position offset |
-  // output offset of every box position (read by the epilogue; kept out of registers
-  // during the main loop) | the phase's tap offsets, 4 lane groups x tap_row].
-  int* rowin = reinterpret_cast<int*>(lds + A.halo_bytes);
+  // LDS: [octet planes (DS: nbuf sets, alternating per channel chunk) | rows: input offset
+  // (-1 outside the input), LDS position offset | output offset of every box position (read
+  // by the epilogue; kept out of registers during the main loop) | the phase's tap offsets,
+  // 4 lane groups x tap_row].
+  int* rowin = reinterpret_cast<int*>(lds + (DS ? A.nbuf : 1) * A.halo_bytes);
   int* rowlds = rowin + A.rows;
   int* posout = rowlds + A.rows;
   int* ltaps = posout + ((A.box_vol + 3) & ~3);
   const int4* pt = reinterpret_cast<const int4*>(tab + A.tab_pos);
-  for (int q = tid; q < A.box_vol; q += kThreads) posout[q] = pt[q].y;
+  for (int q = tid; q < A.box_vol; q += kWT) posout[q] = pt[q].y;
   {
     const int* gt = reinterpret_cast<const int*>(tab + A.tab_taps) + phase * 4 * A.tap_row;
-    for (int i = tid; i < 4 * A.tap_row; i += kThreads) ltaps[i] = gt[i];
+    for (int i = tid; i < 4 * A.tap_row; i += kWT) ltaps[i] = gt[i];
   }
   {
     const int4* rt = reinterpret_cast<const int4*>(tab + A.tab_rows);
     const unsigned long long lo = box.lo, hi = box.hi;
     const int in_base = box.in_base;
-    for (int r = tid; r < A.rows; r += kThreads) {
+    for (int r = tid; r < A.rows; r += kWT) {
       const int4 e = rt[r];
       const unsigned long long h =
           static_cast<unsigned>(e.z) | (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
@@ -126,16 +128,10 @@ void igemm_kernel(IgemmArgs A) {
     }
   }
 
-  // Staging walk: item = ((row * noct) + octet) * hlast + column, 256 items apart per
-  // thread; the division happens once and every later item updates incrementally.
   const int hlast = A.hlast;
   const int corg = box.corg;
   const int last_size = A.last_size;
-  const int items = A.rows * A.noct * hlast;
-  const int rp0 = tid / hlast, c0 = tid - (tid / hlast) * hlast;
-  const int drp = kThreads / hlast, dc = kThreads - drp * hlast;
   const int onoct = A.noct - 1;
-
   const T* in = static_cast<const T*>(A.in);
   const frag* wp = static_cast<const frag*>(A.wpk);
   f32x4 acc[MB][NB];
@@ -145,92 +141,14 @@ void igemm_kernel(IgemmArgs A) {
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const size_t wstep = (size_t)A.mtiles_padded * 64;  // fragments per K32 step
-  // Halo staging in batches of items per thread: the loads of a batch (branch-free buffer
-  // loads; entries outside the input read zero through an offset past the buffer) are all
-  // in flight before the first LDS store. The first kPreBatch items of the next chunk are
-  // loaded into registers before the current chunk's MFMA loop and stored after it, so
-  // their latency hides behind the MFMAs; the rest go in batches of kStageBatch.
-  constexpr int kPreBatch = 4;
-  constexpr int kStageBatch = 8;
   constexpr unsigned kPast = 0xffffffe0u;  // past every staged tensor (planner: < kPast bytes)
-  // Octet planes of this image and group: [cin_total/8][in_vol][8], addressed in bytes from
-  // the staged tensor's base.
   const __amdgpu_buffer_rsrc_t srsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(in), 0, A.in_bytes, 0x00020000);
-  const unsigned img_base =
-      static_cast<unsigned>(((size_t)n * (A.cin_total >> 3) + (size_t)(g * (A.cin_g >> 3))) *
-                            A.in_vol * 16);
-  u32x4 pre[kPreBatch];
-  auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v, auto nbatch) {
-    const unsigned cbase = img_base + static_cast<unsigned>(ck * A.noct) * A.in_vol * 16u;
-#pragma unroll
-    for (int u = 0; u < decltype(nbatch)::value; ++u) {
-      const int it = it0 + u * kThreads;
-      const int r = rp >> A.log2_noct;
-      const int o = rp & onoct;
-      const int ro = it < items ? rowin[r < A.rows ? r : 0] : -1;
-      const int cl = corg + c;
-      const bool ok = ro >= 0 && cl >= 0 && cl < last_size;
-      const unsigned off =
-          ok ? cbase + static_cast<unsigned>(o * A.in_vol + ro + cl) * 16u : kPast;
-      v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
-      c += dc;
-      rp += drp;
-      if (c >= hlast) {
-        c -= hlast;
-        ++rp;
-      }
-    }
-  };
-  auto stage_store = [&](int it0, int rp, int c, const u32x4* v, auto nbatch) {
-#pragma unroll
-    for (int u = 0; u < decltype(nbatch)::value; ++u) {
-      const int it = it0 + u * kThreads;
-      if (it < items) {
-        const int r = rp >> A.log2_noct;
-        const int o = rp & onoct;
-        *reinterpret_cast<u32x4*>(lds + o * A.plane_bytes + (rowlds[r] + c) * 16) = v[u];
-      }
-      c += dc;
-      rp += drp;
-      if (c >= hlast) {
-        c -= hlast;
-        ++rp;
-      }
-    }
-  };
-  // Position of item it0 + n * kThreads in the walk, from the position of it0.
-  auto advance = [&](int& rp, int& c, auto nbatch) {
-#pragma unroll
-    for (int u = 0; u < decltype(nbatch)::value; ++u) {
-      c += dc;
-      rp += drp;
-      if (c >= hlast) {
-        c -= hlast;
-        ++rp;
-      }
-    }
-  };
-  using PreN = std::integral_constant<int, kPreBatch>;
-  using StageN = std::integral_constant<int, kStageBatch>;
-  __syncthreads();  // row tables in LDS
-  stage_load(0, tid, rp0, c0, pre, PreN{});
-  for (int ck = 0; ck < A.nchunk; ++ck) {
-    {
-      // Chunk ck: the first kPreBatch items are in `pre`; the rest is loaded and stored here.
-      stage_store(tid, rp0, c0, pre, PreN{});
-      int rp = rp0, c = c0;
-      advance(rp, c, PreN{});
-      for (int it0 = tid + kPreBatch * kThreads; it0 < items; it0 += kStageBatch * kThreads) {
-        u32x4 v[kStageBatch];
-        stage_load(ck, it0, rp, c, v, StageN{});
-        stage_store(it0, rp, c, v, StageN{});
-        advance(rp, c, StageN{});
-      }
-    }
-    __syncthreads();
-    if (ck + 1 < A.nchunk) stage_load(ck + 1, tid, rp0, c0, pre, PreN{});
 
+  // MFMAs of channel chunk ck over the halo planes at hb. `issue` runs once, after the first
+  // weight fragments and B fragments are requested and before the loop (the next chunk's
+  // staging loads go there, behind this chunk's first weight loads in the load queue).
+  auto mma_chunk = [&](int ck, const unsigned char* hb, auto&& issue) {
     const frag* wck = wp +
                       ((size_t)((phase * A.groups + g) * A.nchunk + ck) * A.kc_max) * wstep +
                       (size_t)mt0 * 64 + lane;
@@ -254,13 +172,16 @@ void igemm_kernel(IgemmArgs A) {
       int4 t = *reinterpret_cast<const int4*>(tp);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
-        b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t.x);
+        b0[nb] = *reinterpret_cast<const frag*>(hb + pbase[nb] + t.x);
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
       // One step: B fragments of the next step into bn (tap offset tn), weights of step
       // ks into al, MFMAs of the current step (bc, ac).
       auto step = [&](frag* bn, int tn, frag* al, int ks, const frag* bc, const frag* ac) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          bn[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + tn);
+          bn[nb] = *reinterpret_cast<const frag*>(hb + pbase[nb] + tn);
         const size_t ws = wstep_at(ks);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) al[mb] = wck[ws + mb * 64];
@@ -286,7 +207,7 @@ void igemm_kernel(IgemmArgs A) {
         if (left >= 2) {
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            b1[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t.y);
+            b1[nb] = *reinterpret_cast<const frag*>(hb + pbase[nb] + t.y);
         }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
@@ -297,7 +218,7 @@ void igemm_kernel(IgemmArgs A) {
         if (left >= 3) {
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            b0[nb] = *reinterpret_cast<const frag*>(lds + pbase[nb] + t.z);
+            b0[nb] = *reinterpret_cast<const frag*>(hb + pbase[nb] + t.z);
         }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
@@ -310,6 +231,8 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(b0[nb], a2[mb], acc[mb][nb]);
       }
+    } else {
+      issue();
     }
     if (KC > KF) {
       // The partial last step holds k-groups past the phase's last tap (offset -1): their
@@ -320,7 +243,7 @@ void igemm_kernel(IgemmArgs A) {
       for (int mb = 0; mb < MB; ++mb) at[mb] = wck[(size_t)KF * wstep + mb * 64];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(lds + pbase[nb] + (tail_tap < 0 ? 0 : tail_tap));
+        u32x4 v = *reinterpret_cast<const u32x4*>(hb + pbase[nb] + (tail_tap < 0 ? 0 : tail_tap));
         if (tail_tap < 0) v = u32x4{0u, 0u, 0u, 0u};
         bt[nb] = __builtin_bit_cast(frag, v);
       }
@@ -329,7 +252,220 @@ void igemm_kernel(IgemmArgs A) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = M::run(bt[nb], at[mb], acc[mb][nb]);
     }
-    if (ck + 1 < A.nchunk) __syncthreads();  // every wave is done reading this chunk's halo
+  };
+
+  if constexpr (DS) {
+    // Halo staged straight from the channels-first operand [N][cin_total][in_vol]. A task
+    // (halo row r, run jj, octet o; octet fastest) loads the run of 8 consecutive last-axis
+    // elements starting at input column 8*(jlo + jj) for the octet's 8 channels (eight
+    // 16-byte loads, zero past the tensor or for rows outside it), transposes the 8 x 8
+    // block in registers (v_perm) and writes each column inside the halo and the input as
+    // one 16-byte position of the octet plane. Halo columns outside the input's last axis
+    // are never written by a task: they are cleared once, in every buffer. With two buffers
+    // they alternate per chunk: the next chunk's loads are issued inside this chunk's MFMA loop
+    // setup and written after it, so staging overlaps the MFMAs (nbuf 2; with nbuf 1 the
+    // loads still overlap, the writes wait for the chunk's last reads).
+    constexpr int kPf = MB * NB >= 32 ? 2 : 1;  // tasks per thread held in registers
+    const int nrun = A.nrun;
+    const int ntask = A.rows * nrun * A.noct;
+    const int jlo = corg > 0 ? (corg >> 3) : 0;
+    const int clast = (corg + hlast < last_size ? corg + hlast : last_size) - 1;
+    const int nrun_box = clast >= jlo * 8 ? (clast >> 3) - jlo + 1 : 0;
+    const unsigned img_chan = static_cast<unsigned>(n * A.cin_total + g * A.cin_g);
+    const unsigned in_vol = static_cast<unsigned>(A.in_vol);
+    const unsigned in_bytes = static_cast<unsigned>(A.in_bytes);
+    auto task_load = [&](int ck, int t, u32x4* v) {
+      const int o = t & onoct;
+      const int rt = t >> A.log2_noct;
+      const int r = rt / nrun;
+      const int jj = rt - r * nrun;
+      const int ro = (t < ntask && jj < nrun_box) ? rowin[r] : -1;
+      const unsigned chan = img_chan + static_cast<unsigned>(ck * A.cc + o * 8);
+      const unsigned pos = static_cast<unsigned>(ro + (jlo + jj) * 8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const unsigned off = ro >= 0 ? ((chan + i) * in_vol + pos) * 2u : kPast;
+        v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
+        // The buffer's range check is per dword: a dword straddling the tensor's end reads
+        // zero, valid half included. A run that crosses the end loads element by element.
+        if (off < in_bytes && off + 16u > in_bytes) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const unsigned lo = __builtin_amdgcn_raw_buffer_load_b16(srsrc, off + 4u * k, 0, 0);
+            const unsigned hi = __builtin_amdgcn_raw_buffer_load_b16(srsrc, off + 4u * k + 2u, 0, 0);
+            v[i][k] = lo | (hi << 16);
+          }
+        }
+      }
+    };
+    auto task_store = [&](int t, const u32x4* v, unsigned char* buf) {
+      const int o = t & onoct;
+      const int rt = t >> A.log2_noct;
+      const int r = rt / nrun;
+      const int jj = rt - r * nrun;
+      if (t >= ntask || jj >= nrun_box) return;
+      const int c0 = (jlo + jj) * 8;
+      unsigned char* rowp = buf + o * A.plane_bytes + (rowlds[r] - corg) * 16;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + e;
+        if (c >= corg && c <= clast) {
+          const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const int d = e >> 1;
+          u32x4 w;
+          w.x = __builtin_amdgcn_perm(v[1][d], v[0][d], sel);
+          w.y = __builtin_amdgcn_perm(v[3][d], v[2][d], sel);
+          w.z = __builtin_amdgcn_perm(v[5][d], v[4][d], sel);
+          w.w = __builtin_amdgcn_perm(v[7][d], v[6][d], sel);
+          *reinterpret_cast<u32x4*>(rowp + c * 16) = w;
+        }
+      }
+    };
+    // Tasks past the ones held in registers: loaded and written in place (not overlapped).
+    auto stage_rest = [&](int ck, unsigned char* buf) {
+      for (int t = tid + kPf * kWT; t < ntask; t += kWT) {
+        u32x4 v[8];
+        task_load(ck, t, v);
+        task_store(t, v, buf);
+      }
+    };
+    __syncthreads();  // row tables in LDS
+    {
+      const int zl = corg < 0 ? (-corg < hlast ? -corg : hlast) : 0;
+      const int rstart = last_size - corg > zl ? last_size - corg : zl;  // first right column
+      const int zr = hlast > rstart ? hlast - rstart : 0;
+      const int zc = zl + zr;
+      const int nz = A.nbuf * A.noct * A.rows * zc;
+      for (int i = tid; i < nz; i += kWT) {
+        const int col = i % zc;
+        const int rest = i / zc;
+        const int r = rest % A.rows;
+        const int bo = rest / A.rows;  // buffer * noct + octet
+        const int hp = col < zl ? col : rstart + (col - zl);
+        *reinterpret_cast<u32x4*>(lds + bo * A.plane_bytes + (rowlds[r] + hp) * 16) =
+            u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    u32x4 pf[kPf][8];
+#pragma unroll
+    for (int q = 0; q < kPf; ++q) task_load(0, tid + q * kWT, pf[q]);
+#pragma unroll
+    for (int q = 0; q < kPf; ++q) task_store(tid + q * kWT, pf[q], lds);
+    stage_rest(0, lds);
+    __syncthreads();
+    // nbuf 2: chunk ck reads buffer ck & 1 while the next chunk goes to the other one;
+    // nbuf 1: one buffer, rewritten after every wave is done with it.
+    const int alt = A.nbuf == 2 ? A.halo_bytes : 0;
+    for (int ck = 0; ck < A.nchunk; ++ck) {
+      unsigned char* cur = lds + (ck & 1) * alt;
+      unsigned char* nxt = lds + ((ck + 1) & 1) * alt;
+      const bool more = ck + 1 < A.nchunk;
+      mma_chunk(ck, cur, [&]() {
+        if (more) {
+#pragma unroll
+          for (int q = 0; q < kPf; ++q) task_load(ck + 1, tid + q * kWT, pf[q]);
+        }
+      });
+      if (more) {
+        if (A.nbuf == 1) __syncthreads();  // every wave is done reading the buffer
+#pragma unroll
+        for (int q = 0; q < kPf; ++q) task_store(tid + q * kWT, pf[q], nxt);
+        stage_rest(ck + 1, nxt);
+        __syncthreads();  // next chunk's halo written
+      }
+    }
+  } else {
+    // Staging walk over the octet-major copy: item = ((row * noct) + octet) * hlast +
+    // column, 256 items apart per thread; the division happens once and every later item
+    // updates incrementally.
+    const int items = A.rows * A.noct * hlast;
+    const int rp0 = tid / hlast, c0 = tid - (tid / hlast) * hlast;
+    const int drp = kWT / hlast, dc = kWT - drp * hlast;
+    // Halo staging in batches of items per thread: the loads of a batch (branch-free buffer
+    // loads; entries outside the input read zero through an offset past the buffer) are all
+    // in flight before the first LDS store. The first kPreBatch items of the next chunk are
+    // loaded into registers before the current chunk's MFMA loop and stored after it, so
+    // their latency hides behind the MFMAs; the rest go in batches of kStageBatch.
+    constexpr int kPreBatch = 4;
+    constexpr int kStageBatch = 8;
+    // Octet planes of this image and group: [cin_total/8][in_vol][8], addressed in bytes from
+    // the staged tensor's base.
+    const unsigned img_base =
+        static_cast<unsigned>(((size_t)n * (A.cin_total >> 3) + (size_t)(g * (A.cin_g >> 3))) *
+                              A.in_vol * 16);
+    u32x4 pre[kPreBatch];
+    auto stage_load = [&](int ck, int it0, int rp, int c, u32x4* v, auto nbatch) {
+      const unsigned cbase = img_base + static_cast<unsigned>(ck * A.noct) * A.in_vol * 16u;
+#pragma unroll
+      for (int u = 0; u < decltype(nbatch)::value; ++u) {
+        const int it = it0 + u * kWT;
+        const int r = rp >> A.log2_noct;
+        const int o = rp & onoct;
+        const int ro = it < items ? rowin[r < A.rows ? r : 0] : -1;
+        const int cl = corg + c;
+        const bool ok = ro >= 0 && cl >= 0 && cl < last_size;
+        const unsigned off =
+            ok ? cbase + static_cast<unsigned>(o * A.in_vol + ro + cl) * 16u : kPast;
+        v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
+        c += dc;
+        rp += drp;
+        if (c >= hlast) {
+          c -= hlast;
+          ++rp;
+        }
+      }
+    };
+    auto stage_store = [&](int it0, int rp, int c, const u32x4* v, auto nbatch) {
+#pragma unroll
+      for (int u = 0; u < decltype(nbatch)::value; ++u) {
+        const int it = it0 + u * kWT;
+        if (it < items) {
+          const int r = rp >> A.log2_noct;
+          const int o = rp & onoct;
+          *reinterpret_cast<u32x4*>(lds + o * A.plane_bytes + (rowlds[r] + c) * 16) = v[u];
+        }
+        c += dc;
+        rp += drp;
+        if (c >= hlast) {
+          c -= hlast;
+          ++rp;
+        }
+      }
+    };
+    // Position of item it0 + n * kWT in the walk, from the position of it0.
+    auto advance = [&](int& rp, int& c, auto nbatch) {
+#pragma unroll
+      for (int u = 0; u < decltype(nbatch)::value; ++u) {
+        c += dc;
+        rp += drp;
+        if (c >= hlast) {
+          c -= hlast;
+          ++rp;
+        }
+      }
+    };
+    using PreN = std::integral_constant<int, kPreBatch>;
+    using StageN = std::integral_constant<int, kStageBatch>;
+    __syncthreads();  // row tables in LDS
+    stage_load(0, tid, rp0, c0, pre, PreN{});
+    for (int ck = 0; ck < A.nchunk; ++ck) {
+      {
+        // Chunk ck: the first kPreBatch items are in `pre`; the rest is loaded and stored here.
+        stage_store(tid, rp0, c0, pre, PreN{});
+        int rp = rp0, c = c0;
+        advance(rp, c, PreN{});
+        for (int it0 = tid + kPreBatch * kWT; it0 < items; it0 += kStageBatch * kWT) {
+          u32x4 v[kStageBatch];
+          stage_load(ck, it0, rp, c, v, StageN{});
+          stage_store(it0, rp, c, v, StageN{});
+          advance(rp, c, StageN{});
+        }
+      }
+      __syncthreads();
+      if (ck + 1 < A.nchunk) stage_load(ck + 1, tid, rp0, c0, pre, PreN{});
+      mma_chunk(ck, lds, []() {});
+      if (ck + 1 < A.nchunk) __syncthreads();  // every wave is done reading this chunk's halo
+    }
   }
 
   // Epilogue: straight from the accumulators. A lane's four values are box positions
@@ -395,33 +531,54 @@ void igemm_kernel(IgemmArgs A) {
   }
 }
 
-// The compiled implicit-GEMM tiles: (MB, NB, WM).
+// The compiled implicit-GEMM tiles: (MB, NB, WM) with four waves per workgroup, and the
+// eight-wave ones (direct staging, 16-bit data): one workgroup of two waves per SIMD per CU,
+// whose waves are issued evenly where two four-wave workgroups sharing a CU are not (the
+// older one's waves run ahead and the other finishes alone).
 #define CONVND_IGEMM_TILES(X)                                                             \
   X(1, 2, 1) X(1, 4, 1) X(1, 8, 1) X(2, 2, 1) X(2, 4, 1) X(2, 8, 1) X(4, 2, 1) X(4, 4, 1) \
   X(4, 8, 1) X(1, 4, 2) X(1, 8, 2) X(2, 4, 2) X(2, 8, 2) X(1, 4, 4) X(1, 8, 4)
+#define CONVND_IGEMM_TILES8(X) \
+  X(4, 4, 1) X(2, 4, 1) X(4, 2, 1) X(2, 8, 1) X(1, 8, 1) X(1, 4, 1) X(1, 2, 1) X(2, 2, 1)
 
-template <typename T, typename O>
+template <typename T, typename O, bool DS>
 hipError_t igemm_dispatch(int mb, int nb, const IgemmArgs& a, size_t lds, hipStream_t s) {
   const dim3 grid(a.boxes, a.groups * a.mgroups, a.batch * a.nphase);
 #define CONVND_IGEMM_CASE(MBV, NBV, WMV)                                                 \
-  if (mb == MBV && nb == NBV && a.wm == WMV) {                                           \
-    auto fn = igemm_kernel<T, O, MBV, NBV, WMV>;                                         \
-    hipError_t err = ensure_dynamic_lds<igemm_kernel<T, O, MBV, NBV, WMV>>(lds);         \
+  if (mb == MBV && nb == NBV && a.wm == WMV && a.waves == 4) {                           \
+    auto fn = igemm_kernel<T, O, MBV, NBV, WMV, DS, 4>;                                  \
+    hipError_t err = ensure_dynamic_lds<igemm_kernel<T, O, MBV, NBV, WMV, DS, 4>>(lds);  \
     if (err != hipSuccess) return err;                                                   \
-    hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                             \
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, a);                                  \
     return hipGetLastError();                                                            \
   }
   CONVND_IGEMM_TILES(CONVND_IGEMM_CASE)
 #undef CONVND_IGEMM_CASE
+  if constexpr (DS) {
+#define CONVND_IGEMM_CASE8(MBV, NBV, WMV)                                                \
+  if (mb == MBV && nb == NBV && a.wm == WMV && a.waves == 8) {                           \
+    auto fn = igemm_kernel<T, O, MBV, NBV, WMV, DS, 8>;                                  \
+    hipError_t err = ensure_dynamic_lds<igemm_kernel<T, O, MBV, NBV, WMV, DS, 8>>(lds);  \
+    if (err != hipSuccess) return err;                                                   \
+    hipLaunchKernelGGL(fn, grid, dim3(512), lds, s, a);                                  \
+    return hipGetLastError();                                                            \
+  }
+    CONVND_IGEMM_TILES8(CONVND_IGEMM_CASE8)
+#undef CONVND_IGEMM_CASE8
+  }
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-bool igemm_tile_supported(int mb, int nb, int wm) {
+bool igemm_tile_supported(int mb, int nb, int wm, int waves) {
 #define CONVND_IGEMM_HAS(MBV, NBV, WMV) \
   if (mb == MBV && nb == NBV && wm == WMV) return true;
-  CONVND_IGEMM_TILES(CONVND_IGEMM_HAS)
+  if (waves == 4) {
+    CONVND_IGEMM_TILES(CONVND_IGEMM_HAS)
+  } else if (waves == 8) {
+    CONVND_IGEMM_TILES8(CONVND_IGEMM_HAS)
+  }
 #undef CONVND_IGEMM_HAS
   return false;
 }
@@ -430,11 +587,13 @@ hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs&
                         size_t lds_bytes, hipStream_t stream) {
   if (a.boxes == 0 || a.batch == 0) return hipSuccess;
   if (dtype == CONVND_HIP_BFLOAT16)
-    return igemm_dispatch<__bf16, __bf16>(mb, nb, a, lds_bytes, stream);
+    return a.direct ? igemm_dispatch<__bf16, __bf16, true>(mb, nb, a, lds_bytes, stream)
+                    : igemm_dispatch<__bf16, __bf16, false>(mb, nb, a, lds_bytes, stream);
   if (dtype == CONVND_HIP_FLOAT16)
-    return igemm_dispatch<_Float16, _Float16>(mb, nb, a, lds_bytes, stream);
-  if (dtype == CONVND_HIP_FLOAT32 && a.split_c > 0)
-    return igemm_dispatch<__bf16, float>(mb, nb, a, lds_bytes, stream);
+    return a.direct ? igemm_dispatch<_Float16, _Float16, true>(mb, nb, a, lds_bytes, stream)
+                    : igemm_dispatch<_Float16, _Float16, false>(mb, nb, a, lds_bytes, stream);
+  if (dtype == CONVND_HIP_FLOAT32 && a.split_c > 0 && !a.direct)
+    return igemm_dispatch<__bf16, float, false>(mb, nb, a, lds_bytes, stream);
   return hipErrorInvalidValue;
 }
 

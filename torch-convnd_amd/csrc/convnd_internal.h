@@ -85,6 +85,14 @@ struct IgemmArgs {
   int last_size;     // input extent of the last axis
   int packed_ok;     // interior boxes store 4 adjacent outputs per lane
   int coord_bits;    // field width of box coordinates (16 when rank <= 4, else 8)
+  // Direct staging: the halo is read straight from the channels-first operand
+  // [N][cin_total][in_vol] (16-bit data; `in` is the caller's tensor) in runs of 8 last-axis
+  // elements, nrun runs per halo row at most (over every box and phase), into nbuf (1 or 2)
+  // alternating sets of octet planes.
+  int direct;
+  int nrun;
+  int nbuf;
+  int waves;  // waves per workgroup (4, or 8 with direct staging)
 };
 
 constexpr int kTapPad = 8;
@@ -310,8 +318,11 @@ struct PadArgs {
 };
 
 // Channel partial sums written by the GEMM-input copy: sums[c * octet_sum_blocks(N, V) +
-// block], one per channel and run of positions.
+// block], one per channel and run of positions; by the prologue's sums part: the same layout
+// with prologue_sum_blocks(N, V) per channel (runs of kSumRun positions).
 int64_t octet_sum_blocks(int64_t batch, int64_t volume);
+constexpr int64_t kSumRun = 8192;
+int64_t prologue_sum_blocks(int64_t batch, int64_t volume);
 
 // One launch for the staging passes that precede the MFMA kernels; each part is optional
 // (null pointers skip it) and runs on its own range of workgroups:
@@ -321,7 +332,8 @@ int64_t octet_sum_blocks(int64_t batch, int64_t volume);
 //   octets:     zero-padded octet-major input for the weight gradient (pad);
 //   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg);
 //   planar pad: zero-padded channels-first input for the channel-major weight gradient
-//               (pp, 16-bit data).
+//               (pp, 16-bit data);
+//   sums:       channel partial sums of a channels-first 16-bit tensor (bias gradient).
 struct IgemmArgs;
 struct WgradArgs;
 struct PrologueParts {
@@ -344,6 +356,11 @@ struct PrologueParts {
   const PlanarPadArgs* pp = nullptr;  // zero-padded channels-first input (x -> x_pp)
   void* x_pp = nullptr;
   int64_t pp_batch = 0;
+  // Channel partial sums of a channels-first 16-bit tensor [sum_batch][sum_channels]
+  // [sum_volume] in the layout of the GEMM-input copy's sums (octet_sum_blocks per channel).
+  const void* sum_src = nullptr;
+  float* sum_out = nullptr;
+  int64_t sum_batch = 0, sum_channels = 0, sum_volume = 0;
 };
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream);
 // counts = window sums of mask (see PartialCountArgs); float32 counts, float64 for float64.
@@ -370,9 +387,10 @@ hipError_t launch_grad_bias(convnd_hip_dtype dtype, int64_t batch, int64_t chann
                             int64_t chunks, hipStream_t stream);
 hipError_t launch_igemm(convnd_hip_dtype dtype, int mb, int nb, const IgemmArgs& a,
                         size_t lds_bytes, hipStream_t stream);
-// Whether launch_igemm has a compiled kernel for this wave tile (mb x nb fragments) and
-// wave arrangement (wm waves along output channels).
-bool igemm_tile_supported(int mb, int nb, int wm);
+// Whether launch_igemm has a compiled kernel for this wave tile (mb x nb fragments), wave
+// arrangement (wm waves along output channels) and workgroup size (waves: 4, or 8 with direct
+// staging).
+bool igemm_tile_supported(int mb, int nb, int wm, int waves);
 // stg: staging slots per thread (8, 16 or 24); multi: the item's staging takes
 // several batches of 8 slots (only the first is prefetched).
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,

@@ -59,6 +59,13 @@ struct DevPrologue {
   void* x_pp;
   int64_t e_total;
   int e_blocks;
+  // Channel partial sums of a channels-first 16-bit tensor (bias gradient): block (image,
+  // channel, run of kSumRun positions) -> f_sums[c * (batch * f_nrun) + n * f_nrun + run].
+  const void* f_src;
+  float* f_sums;
+  int64_t f_channels, f_volume;
+  int f_nrun, f_blocks;
+  bool f_vec;  // 16-byte loads: volume a multiple of 8 and a 16-byte aligned source
 };
 
 // SPLIT: fp32 sources (split-precision copies and packing).
@@ -96,10 +103,49 @@ void prologue_kernel(DevPrologue P) {
     return;
   }
   b -= P.d_blocks;
+  if (b < P.e_blocks) {
+    if constexpr (!SPLIT) {
+      stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
+                                 static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b,
+                                 P.e_blocks);
+    }
+    return;
+  }
+  b -= P.e_blocks;
   if constexpr (!SPLIT) {
-    stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
-                               static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b,
-                               P.e_blocks);
+    if (b < P.f_blocks) {
+      const int run = b % P.f_nrun;
+      const int64_t rc = b / P.f_nrun;
+      const int64_t c = rc % P.f_channels;
+      const int64_t n = rc / P.f_channels;
+      const unsigned short* src =
+          static_cast<const unsigned short*>(P.f_src) + (n * P.f_channels + c) * P.f_volume;
+      const int64_t p0 = (int64_t)run * kSumRun;
+      const int64_t pend = p0 + kSumRun < P.f_volume ? p0 + kSumRun : P.f_volume;
+      auto widen16 = [&](unsigned h) {
+        return P.is_bf16 ? __builtin_bit_cast(float, h << 16)
+                         : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+      };
+      float acc = 0.f;
+      if (P.f_vec) {
+        for (int64_t q = p0 + 8 * (int64_t)threadIdx.x; q < pend; q += 8 * kThreads) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(src + q);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc += widen16(v[k] & 0xffffu) + widen16(v[k] >> 16);
+        }
+      } else {
+        for (int64_t q = p0 + threadIdx.x; q < pend; q += kThreads) acc += widen16(src[q]);
+      }
+      // Fixed-order reduction: lanes by xor shuffles, then the four waves in order.
+      for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+      if ((threadIdx.x & 63) == 0) smem.red[0][threadIdx.x >> 6] = acc;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const float total = ((smem.red[0][0] + smem.red[0][1]) + smem.red[0][2]) + smem.red[0][3];
+        const int64_t nsum = P.f_nrun * (P.f_blocks / (P.f_nrun * P.f_channels));
+        P.f_sums[c * nsum + n * P.f_nrun + run] = total;
+      }
+    }
   }
 }
 
@@ -283,6 +329,19 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     P.e_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
     total += P.e_blocks;
   }
+  if (p.sum_out != nullptr && p.sum_src != nullptr && p.sum_batch > 0 && p.sum_channels > 0) {
+    if (split) return hipErrorInvalidValue;
+    P.f_src = p.sum_src;
+    P.f_sums = p.sum_out;
+    P.f_channels = p.sum_channels;
+    P.f_volume = p.sum_volume;
+    P.f_nrun = static_cast<int>((p.sum_volume + kSumRun - 1) / kSumRun);
+    P.f_vec = p.sum_volume % 8 == 0 && reinterpret_cast<uintptr_t>(p.sum_src) % 16 == 0;
+    const int64_t blocks = p.sum_batch * p.sum_channels * P.f_nrun;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    P.f_blocks = static_cast<int>(blocks);
+    total += P.f_blocks;
+  }
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(total));
@@ -298,6 +357,10 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
 
 int64_t octet_sum_blocks(int64_t batch, int64_t volume) {
   return batch * ((volume + stage::kOctRun - 1) / stage::kOctRun);
+}
+
+int64_t prologue_sum_blocks(int64_t batch, int64_t volume) {
+  return batch * ((volume + kSumRun - 1) / kSumRun);
 }
 
 hipError_t launch_grad_bias_from_sums(convnd_hip_dtype dtype, const float* sums, int64_t nsum,
