@@ -841,7 +841,7 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
         const int tpc = (ntiles + ncq - 1) / ncq;
         if ((ntiles + tpc - 1) / tpc != ncq) continue;  // same split as a smaller ncq
         int nt = (tpc + 3) / 4;
-        while (nt <= 8 && !wgrad_cm_supported(mb, nt)) ++nt;
+        while (nt <= 8 && !wgrad_cm_supported(mb, nt, 4)) ++nt;
         if (nt > 8) continue;
         if (nt == prev_nt) continue;
         prev_nt = nt;
@@ -865,10 +865,14 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
         const int64_t lds = lds_items + ipc * 8;
         if (lds > dyn_budget) continue;
         if (npc * per_chunk_wgs > INT32_MAX) continue;
+        for (const int waves : {8, 4}) {
+        if (!wgrad_cm_supported(mb, nt, waves)) continue;
+        if (filter.waves && filter.waves != waves) continue;
         // Per item, clocks of one CU: MFMA issue of one wave (MB x NT per K32 step) and the
         // LDS fragment reads of four waves (128 B/clock) against the item's loads straight
         // into LDS (~64 B/clock/CU of L2 traffic), which overlap, plus barriers.
-        const double mfma = double(ksteps) * mb * nt * 16.0 / 0.8;
+        // Two waves per SIMD (eight-wave workgroups) issue MFMAs more evenly.
+        const double mfma = double(ksteps) * mb * nt * 16.0 / (waves == 8 ? 0.9 : 0.8);
         const double ldsr = double(ksteps) * (mb + nt) * 32.0;
         const double stage = (double(xi) * 1024 + double(dyt_bytes)) / 64.0;
         const double per_item = std::max(std::max(mfma, ldsr), stage) + 800.0;
@@ -918,6 +922,7 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
         C.items = static_cast<int>(items);
         C.items_per_pc = static_cast<int>(ipc);
         C.lds_items = static_cast<int>(lds_items);
+        C.waves = waves;
         PlanarPadArgs& P = plan.ppad;
         std::memset(&P, 0, sizeof(P));
         P.rank = R;
@@ -952,6 +957,7 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
           ovol *= D.out_size[a];
         }
         D.out_vol = ovol;
+        }
       }
     });
   }
@@ -1856,7 +1862,8 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
     } else if (p.cm) {
       const WgradCmArgs& C = p.cm_args;
       text = "{\"kernel\":\"mfma_wgrad_cm\",\"mb\":" + std::to_string(p.mb) +
-             ",\"nt\":" + std::to_string(C.nt) + ",\"box\":" + join(C.box, C.rank) +
+             ",\"nt\":" + std::to_string(C.nt) + ",\"waves\":" + std::to_string(C.waves) +
+             ",\"box\":" + join(C.box, C.rank) +
              ",\"items\":" + std::to_string(C.items) + ",\"npc\":" + std::to_string(C.npc) +
              ",\"items_per_pc\":" + std::to_string(C.items_per_pc) +
              ",\"ncq\":" + std::to_string(C.ncq) + ",\"mgroups\":" +

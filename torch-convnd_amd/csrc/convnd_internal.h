@@ -222,6 +222,7 @@ struct WgradCmArgs {
   //              workgroup).
   const void* tables;
   int tab_chunk, tab_col, tab_cid, tab_run, tab_xsrc, tab_dsrc, tab_item, tab_bytes;
+  int waves;  // waves per workgroup: 4 (one per SIMD) or 8 (two per SIMD, K steps split)
 };
 
 // LDS bytes of one item buffer of the channel-major weight gradient (two per workgroup).
@@ -396,8 +397,8 @@ bool igemm_tile_supported(int mb, int nb, int wm, int waves);
 hipError_t launch_wgrad_mfma(convnd_hip_dtype dtype, int mb, int stg, bool multi,
                              const WgradArgs& a, size_t lds_bytes, hipStream_t stream);
 // Channel-major weight gradient: mb tiles of 16 output channels and nt column tiles per
-// wave (wgrad_cm_supported lists the compiled pairs).
-bool wgrad_cm_supported(int mb, int nt);
+// wave, 4 or 8 waves per workgroup (wgrad_cm_supported lists the compiled combinations).
+bool wgrad_cm_supported(int mb, int nt, int waves);
 hipError_t launch_wgrad_cm(convnd_hip_dtype dtype, int mb, const WgradCmArgs& a,
                            size_t lds_bytes, hipStream_t stream);
 int64_t wgrad_cm_partial_slots(int mb, const WgradCmArgs& a);

@@ -78,7 +78,7 @@ void prologue_kernel(DevPrologue P) {
   int b = blockIdx.x;
   if (b < P.b_blocks) {
     stage::igemm_pack_blocks<T, W>(P.ig, static_cast<const W*>(P.w), static_cast<T*>(P.wpk),
-                                   P.units, b, P.b_blocks);
+                                   static_cast<int>(P.units), b, P.b_blocks);
     return;
   }
   b -= P.b_blocks;
@@ -281,6 +281,7 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     P.w = p.w;
     P.wpk = p.wpk;
     P.units = (int64_t)a.nphase * a.groups * a.nchunk * a.kc_max * a.mtiles_padded * 64;
+    if (P.units > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit unit indices
     const int64_t blocks = (P.units + kThreads - 1) / kThreads;
     P.b_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
     total += P.b_blocks;
@@ -325,6 +326,7 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     P.xpp_src = p.x;
     P.x_pp = p.x_pp;
     P.e_total = p.pp_batch * p.pp->channels * (p.pp->pvol / 8);
+    if (P.e_total > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit run indices
     const int64_t blocks = (P.e_total + kThreads - 1) / kThreads;
     P.e_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
     total += P.e_blocks;

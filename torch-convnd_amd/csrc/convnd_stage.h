@@ -20,13 +20,12 @@ namespace stage {
 // channel ci % split_c of the fp32 weight (zero past kSplitProducts copies).
 template <typename T, typename S>
 __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w, T* wpk,
-                                                  int64_t units, int block, int nblocks) {
+                                                  int units, int block, int nblocks) {
   const int* pmap = reinterpret_cast<const int*>(static_cast<const char*>(A.tables) + A.tab_pack);
-  for (int64_t u = block * (int64_t)kThreads + threadIdx.x; u < units;
-       u += (int64_t)nblocks * kThreads) {
-    int64_t r = u;
-    const int lane = r & 63;
-    r >>= 6;
+  for (int u = block * kThreads + static_cast<int>(threadIdx.x); u < units; u += nblocks * kThreads) {
+    // 32-bit index arithmetic (the host keeps units below 2^31).
+    int r = u >> 6;
+    const int lane = u & 63;
     const int mt = r % A.mtiles_padded;
     r /= A.mtiles_padded;
     const int kc = r % A.kc_max;
@@ -34,14 +33,14 @@ __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w
     const int ck = r % A.nchunk;
     r /= A.nchunk;
     const int g = r % A.groups;
-    const int phase = (int)(r / A.groups);
+    const int phase = r / A.groups;
     const int m = mt * 16 + (lane & 15);
     const int* pe = pmap + ((phase * A.kc_max + kc) * 4 + (lane >> 4)) * 2;
     const int tflat = pe[0];
     const int ci0 = ck * A.cc + pe[1];
-    T vals[8];
+    unsigned short bits[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vals[i] = static_cast<T>(0.f);
+    for (int i = 0; i < 8; ++i) bits[i] = 0;
     if (m < A.cout_g && tflat >= 0) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -56,15 +55,16 @@ __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w
             A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
                         : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
         if constexpr (sizeof(S) == 4) {
-          vals[i] = __builtin_bit_cast(T, bf16_part_bits(w[widx], part));
+          bits[i] = bf16_part_bits(w[widx], part);
         } else {
-          vals[i] = w[widx];
+          bits[i] = __builtin_bit_cast(unsigned short, w[widx]);
         }
       }
     }
-    T* dst = wpk + u * 8;
+    u32x4 out;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = vals[i];
+    for (int j = 0; j < 4; ++j) out[j] = bits[2 * j] | (static_cast<unsigned>(bits[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4*>(wpk + (size_t)u * 8) = out;  // one 16-byte fragment store
   }
 }
 
@@ -378,12 +378,14 @@ __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<unsigned short*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes),
       0x00020000);
-  for (int64_t t = block * (int64_t)kThreads + threadIdx.x; t < total;
-       t += (int64_t)nblocks * kThreads) {
-    const int64_t row = t / chunks;  // (image, channel, padded row)
-    const int u0 = static_cast<int>(t - row * chunks) * 8 - pad_last;
-    const int64_t nc = row / rows_per_img;
-    int rem = static_cast<int>(row - nc * rows_per_img);
+  // 32-bit index arithmetic: the padded copy and the source hold fewer than 2^31 elements
+  // (the planner checks both).
+  const int ntotal = static_cast<int>(total);
+  for (int t = block * kThreads + static_cast<int>(threadIdx.x); t < ntotal; t += nblocks * kThreads) {
+    const int row = t / chunks;  // (image, channel, padded row)
+    const int u0 = (t - row * chunks) * 8 - pad_last;
+    const int nc = row / rows_per_img;
+    int rem = row - nc * rows_per_img;
     int srow = 0, istr = in_last;
     bool ok = true;
 #pragma unroll
@@ -396,7 +398,7 @@ __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
         istr *= P.in[a];
       }
     }
-    const int64_t base = nc * P.in_vol + srow;
+    const int64_t base = (int64_t)nc * P.in_vol + srow;
     // One 16-byte load at the (2-byte-aligned) first element when it lies wholly inside the
     // source; elements outside the row are masked to zero. At the source's two ends (a load
     // there would start before it or end past it) the elements are read one by one.
@@ -425,7 +427,7 @@ __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
         for (int j = 0; j < 4; ++j) w[j] = v[2 * j] | (static_cast<unsigned>(v[2 * j + 1]) << 16);
       }
     }
-    *reinterpret_cast<u32x4*>(dst + t * 8) = w;
+    *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = w;
   }
 }
 

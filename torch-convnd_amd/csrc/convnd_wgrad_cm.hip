@@ -20,7 +20,8 @@
 //     slot r ^ (co % 16) so the 16 rows of an A fragment read distinct bank slots.
 //   * Loads go straight to LDS (no registers, no stores): two item buffers in LDS alternate,
 //     the MFMAs of one item running while the next item's loads land in the other buffer.
-//     One workgroup per CU (one wave per SIMD). Each workgroup writes fp32 partial sums of
+//     One workgroup per CU: four waves (one per SIMD), or eight (two per SIMD) that split
+//     each item's K steps between the two waves of a column set. Each workgroup writes fp32 partial sums of
 //     its range of items; a second pass adds them in a fixed order into the weight layout
 //     (deterministic, no atomics).
 
@@ -38,9 +39,10 @@ constexpr unsigned kCmPast = 0xffffffe0u;
 // LDS per item buffer (grad_output tile, then the input runs); two buffers alternate, one
 // read by the MFMAs while the loads of the next item land in the other.
 constexpr int kCmBuf = kWgradCmBuffer;
-// Load instructions per wave whose per-lane source offsets stay in registers.
-constexpr int kXi = 16;
-constexpr int kDi = 8;
+// Load instructions per wave whose per-lane source offsets stay in registers (four waves;
+// eight waves issue half as many each).
+constexpr int kXi4 = 16;
+constexpr int kDi4 = 8;
 // Of which issued per K step (eight steps per item).
 constexpr int kXs = 2;
 constexpr int kDs = 1;
@@ -63,9 +65,15 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, unsigned ch
 // Waits until every load this wave issued has landed (vmcnt 0; expcnt, lgkmcnt untouched).
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
-template <typename T, int MB, int NT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// W waves per workgroup: 4 (one per SIMD), or 8 (two per SIMD; wave w computes column set
+// w % 4 over K steps [4 (w / 4), 4 (w / 4) + 4) of every item, the two halves added through
+// LDS at the end).
+template <typename T, int MB, int NT, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
 void wgrad_cm_kernel(WgradCmArgs A) {
+  constexpr int kWT = 64 * W;
+  constexpr int kXi = W == 8 ? kXi4 / 2 : kXi4;
+  constexpr int kDi = W == 8 ? kDi4 / 2 : kDi4;
   using M = Mfma16<T>;
   using frag = typename M::frag;
   extern __shared__ __align__(16) unsigned char lds[];
@@ -75,6 +83,8 @@ void wgrad_cm_kernel(WgradCmArgs A) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+  const int cw = wave & 3;    // column set
+  const int kh = wave >> 2;   // half of the item's K steps (eight waves)
   const int nl = lane & 15;
   const int lg = lane >> 4;
   // Consecutive workgroup ids go round-robin to the eight XCDs; give each XCD a contiguous
@@ -104,15 +114,15 @@ void wgrad_cm_kernel(WgradCmArgs A) {
   // the workgroup's item records (LDS).
   int colb[NT];
   {
-    const int* ct = reinterpret_cast<const int*>(tab + A.tab_col) + ((size_t)(cq * 4 + wave) * NT) * 16 + nl;
+    const int* ct = reinterpret_cast<const int*>(tab + A.tab_col) + ((size_t)(cq * 4 + cw) * NT) * 16 + nl;
 #pragma unroll
     for (int j = 0; j < NT; ++j) colb[j] = ct[j * 16] + A.dyt_bytes;
     const int* rt = reinterpret_cast<const int*>(tab + A.tab_run);
-    for (int q = tid; q < kBoxVol / 8; q += kThreads) runl[q] = rt[q];
+    for (int q = tid; q < kBoxVol / 8; q += kWT) runl[q] = rt[q];
     const int* gi = reinterpret_cast<const int*>(tab + A.tab_item) + (size_t)it0 * 2;
-    for (int q = tid; q < nitems * 2; q += kThreads) items[q] = gi[q];
+    for (int q = tid; q < nitems * 2; q += kWT) items[q] = gi[q];
   }
-  // Load instructions of this wave: m = wave + 4 i. Input runs: slot m*64 + lane of the
+  // Load instructions of this wave: m = wave + W i. Input runs: slot m*64 + lane of the
   // chunk's runs; grad_output: slot m*64 + lane of the tile (rows past the group's output
   // channels read zero).
   const int* xs = reinterpret_cast<const int*>(tab + A.tab_xsrc) + (size_t)cq * A.xi * 64;
@@ -122,17 +132,17 @@ void wgrad_cm_kernel(WgradCmArgs A) {
   int xoff[kXi], doff[kDi];
 #pragma unroll
   for (int i = 0; i < kXi; ++i) {
-    const int m = wave + 4 * i;
+    const int m = wave + W * i;
     xoff[i] = m < A.xi ? xs[m * 64 + lane] : -1;
   }
 #pragma unroll
   for (int i = 0; i < kDi; ++i) {
-    const int m = wave + 4 * i;
+    const int m = wave + W * i;
     const int sl = m * 64 + lane;
     doff[i] = m < A.di && sl / nruns < co_valid ? ds[sl] : -1;
   }
-  const int xwave = (A.xi - wave + 3) / 4;  // this wave's input-run instructions
-  const int dwave = (A.di - wave + 3) / 4;
+  const int xwave = (A.xi - wave + W - 1) / W;  // this wave's input-run instructions
+  const int dwave = (A.di - wave + W - 1) / W;
 
   const T* x = static_cast<const T*>(A.x);
   const T* dy = static_cast<const T*>(A.dy);
@@ -145,7 +155,7 @@ void wgrad_cm_kernel(WgradCmArgs A) {
 
   // Loads of item k into buf, issued a few at a time between the MFMA steps of the current
   // item (past the last item: loads that read zero): per K step up to kXs input-run and kDs
-  // grad_output instructions of this wave (m = wave + 4 i, in order); the per-lane offsets
+  // grad_output instructions of this wave (m = wave + W i, in order); the per-lane offsets
   // of the next ones rotate into fixed registers so the loop stays rolled.
   struct Bases {
     int xb, db;
@@ -194,8 +204,11 @@ void wgrad_cm_kernel(WgradCmArgs A) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[mb][j] = M::run(a[mb], b[j], acc[mb][j]);
     };
+    // This wave's K steps of the item: all eight (four waves), or one half (eight waves).
+    constexpr int kMine = W == 8 ? kSteps / 2 : kSteps;
+    const int k0 = W == 8 ? kh * kMine : 0;
     frag a0[MB], a1[MB], b0[NT], b1[NT];
-    read_ab(0, a0, b0);
+    read_ab(k0, a0, b0);
     // Per K step: up to kXs input-run and kDs grad_output load instructions, then the
     // offsets of the next ones rotate into the fixed registers.
     auto issue = [&]() {
@@ -203,18 +216,18 @@ void wgrad_cm_kernel(WgradCmArgs A) {
       for (int u = 0; u < kXs; ++u) {
         if (u < xleft) {
           const unsigned o = xq[u] >= 0 && nb.live ? static_cast<unsigned>(nb.xb + xq[u]) * 2u : kCmPast;
-          load_lds16(xr, nbuf + A.dyt_bytes + (xm + 4 * u) * 1024, o);
+          load_lds16(xr, nbuf + A.dyt_bytes + (xm + W * u) * 1024, o);
         }
       }
 #pragma unroll
       for (int u = 0; u < kDs; ++u) {
         if (u < dleft) {
           const unsigned o = dq[u] >= 0 && nb.live ? static_cast<unsigned>(nb.db + dq[u]) * 2u : kCmPast;
-          load_lds16(dr, nbuf + (dm + 4 * u) * 1024, o);
+          load_lds16(dr, nbuf + (dm + W * u) * 1024, o);
         }
       }
-      xm += 4 * kXs;
-      dm += 4 * kDs;
+      xm += W * kXs;
+      dm += W * kDs;
       xleft -= kXs;
       dleft -= kDs;
 #pragma unroll
@@ -222,12 +235,12 @@ void wgrad_cm_kernel(WgradCmArgs A) {
 #pragma unroll
       for (int i = 0; i + kDs < kDi; ++i) dq[i] = dq[i + kDs];
     };
-    for (int kc = 0; kc < kSteps; kc += 2) {
+    for (int kc = k0; kc < k0 + kMine; kc += 2) {
       issue();
       read_ab(kc + 1, a1, b1);
       mfmas(a0, b0);
       issue();
-      read_ab(kc + 2 < kSteps ? kc + 2 : kSteps - 1, a0, b0);
+      read_ab(kc + 2 < k0 + kMine ? kc + 2 : k0 + kMine - 1, a0, b0);
       mfmas(a1, b1);
     }
   };
@@ -239,14 +252,14 @@ void wgrad_cm_kernel(WgradCmArgs A) {
     for (int i = 0; i < kXi; ++i) {
       if (i < xwave) {
         const unsigned o = xoff[i] >= 0 && b0.live ? static_cast<unsigned>(b0.xb + xoff[i]) * 2u : kCmPast;
-        load_lds16(xr, cm_buf0 + A.dyt_bytes + (wave + 4 * i) * 1024, o);
+        load_lds16(xr, cm_buf0 + A.dyt_bytes + (wave + W * i) * 1024, o);
       }
     }
 #pragma unroll
     for (int i = 0; i < kDi; ++i) {
       if (i < dwave) {
         const unsigned o = doff[i] >= 0 && b0.live ? static_cast<unsigned>(b0.db + doff[i]) * 2u : kCmPast;
-        load_lds16(dr, cm_buf0 + (wave + 4 * i) * 1024, o);
+        load_lds16(dr, cm_buf0 + (wave + W * i) * 1024, o);
       }
     }
   }
@@ -264,9 +277,29 @@ void wgrad_cm_kernel(WgradCmArgs A) {
     __syncthreads();
   }
 
-  // Partial sums as each lane's accumulators: [pc][tile][wave][mb][j][lane] x 4 floats.
+  if constexpr (W == 8) {
+    // The second K half's accumulators go through LDS (waves 4, 5 in buffer 0, waves 6, 7 in
+    // buffer 1; the item loop has ended and every wave passed its last barrier) and are added
+    // to the first half's, waves 0-3, in a fixed order.
+    static_assert(MB * NT * 64 * 16 * 2 <= kCmBuf, "second-half accumulators fit an item buffer");
+    unsigned char* pair_buf = (cw & 2) ? cm_buf1 : cm_buf0;
+    f32x4* slot = reinterpret_cast<f32x4*>(pair_buf) + ((size_t)(cw & 1) * MB * NT) * 64 + lane;
+    if (kh == 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) slot[(mb * NT + j) * 64] = acc[mb][j];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[mb][j] += slot[(mb * NT + j) * 64];
+  }
+  // Partial sums as each lane's accumulators: [pc][tile][column set][mb][j][lane] x 4 floats.
   f32x4* part = reinterpret_cast<f32x4*>(A.partial) +
-                ((((size_t)pc * ntiles + tile) * 4 + wave) * MB * NT) * 64 + lane;
+                ((((size_t)pc * ntiles + tile) * 4 + cw) * MB * NT) * 64 + lane;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -285,16 +318,17 @@ __global__ __launch_bounds__(kThreads) void wgrad_cm_reduce_kernel(const f32x4* 
     stage::bias_from_sums<T>(bs, blockIdx.x - rblocks);
     return;
   }
-  const int64_t s = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+  // 32-bit slot arithmetic (the launcher keeps nslots below 2^31).
+  const int s = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
   if (s >= nslots) return;
-  const int lane = static_cast<int>(s & 63);
-  int64_t r = s >> 6;
-  const int j = static_cast<int>(r % A.nt);
+  const int lane = s & 63;
+  int r = s >> 6;
+  const int j = r % A.nt;
   r /= A.nt;
-  const int mb = static_cast<int>(r % mbv);
+  const int mb = r % mbv;
   r /= mbv;
-  const int wave = static_cast<int>(r % 4);
-  const int tile = static_cast<int>(r / 4);
+  const int wave = r & 3;
+  const int tile = r >> 2;
   const int cq = tile % A.ncq;
   const int zq = tile / A.ncq;
   const int g = zq / A.mgroups;
@@ -321,32 +355,48 @@ __global__ __launch_bounds__(kThreads) void wgrad_cm_reduce_kernel(const f32x4* 
   }
 }
 
-// The compiled (MB, NT) pairs: accumulators MB * NT * 4 registers (at most 128).
+// The compiled (MB, NT) pairs: accumulators MB * NT * 4 registers (at most 128); with eight
+// waves per workgroup (two per SIMD, 256 registers each) the pairs that fit them unspilled.
 #define CONVND_WGRAD_CM_TILES(X) \
   X(4, 4) X(4, 5) X(4, 6) X(4, 7) X(4, 8) X(2, 4) X(2, 6) X(2, 8) X(1, 4) X(1, 8)
+#define CONVND_WGRAD_CM_TILES8(X) X(4, 4) X(2, 4) X(2, 6) X(2, 8) X(1, 8)
 
 template <typename T>
 hipError_t wgrad_cm_dispatch(int mb, const WgradCmArgs& a, size_t lds, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.npc * a.ncq * a.groups * a.mgroups));
 #define CONVND_WGRAD_CM_CASE(MBV, NTV)                                               \
-  if (mb == MBV && a.nt == NTV) {                                                    \
-    auto fn = wgrad_cm_kernel<T, MBV, NTV>;                                          \
-    hipError_t err = ensure_dynamic_lds<wgrad_cm_kernel<T, MBV, NTV>>(lds);          \
+  if (mb == MBV && a.nt == NTV && a.waves == 4) {                                    \
+    auto fn = wgrad_cm_kernel<T, MBV, NTV, 4>;                                       \
+    hipError_t err = ensure_dynamic_lds<wgrad_cm_kernel<T, MBV, NTV, 4>>(lds);       \
     if (err != hipSuccess) return err;                                               \
-    hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, s, a);                         \
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, a);                              \
     return hipGetLastError();                                                        \
   }
   CONVND_WGRAD_CM_TILES(CONVND_WGRAD_CM_CASE)
 #undef CONVND_WGRAD_CM_CASE
+#define CONVND_WGRAD_CM_CASE8(MBV, NTV)                                              \
+  if (mb == MBV && a.nt == NTV && a.waves == 8) {                                    \
+    auto fn = wgrad_cm_kernel<T, MBV, NTV, 8>;                                       \
+    hipError_t err = ensure_dynamic_lds<wgrad_cm_kernel<T, MBV, NTV, 8>>(lds);       \
+    if (err != hipSuccess) return err;                                               \
+    hipLaunchKernelGGL(fn, grid, dim3(512), lds, s, a);                              \
+    return hipGetLastError();                                                        \
+  }
+  CONVND_WGRAD_CM_TILES8(CONVND_WGRAD_CM_CASE8)
+#undef CONVND_WGRAD_CM_CASE8
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-bool wgrad_cm_supported(int mb, int nt) {
+bool wgrad_cm_supported(int mb, int nt, int waves) {
 #define CONVND_WGRAD_CM_HAS(MBV, NTV) \
   if (mb == MBV && nt == NTV) return true;
-  CONVND_WGRAD_CM_TILES(CONVND_WGRAD_CM_HAS)
+  if (waves == 4) {
+    CONVND_WGRAD_CM_TILES(CONVND_WGRAD_CM_HAS)
+  } else if (waves == 8) {
+    CONVND_WGRAD_CM_TILES8(CONVND_WGRAD_CM_HAS)
+  }
 #undef CONVND_WGRAD_CM_HAS
   return false;
 }
@@ -367,6 +417,7 @@ hipError_t launch_wgrad_cm_reduce(convnd_hip_dtype dtype, int mb, const WgradCmA
                                   void* dw, hipStream_t stream, const float* bias_sums,
                                   int64_t nsum, int64_t channels, void* db) {
   const int64_t nslots = wgrad_cm_partial_slots(mb, a);
+  if (nslots > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit slot indices
   const int64_t rblocks = (nslots + kThreads - 1) / kThreads;
   stage::BiasSums bs{bias_sums, db, static_cast<int>(nsum), static_cast<int>(channels)};
   const int64_t bblocks = bias_sums != nullptr ? channels : 0;
