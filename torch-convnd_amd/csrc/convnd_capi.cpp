@@ -670,6 +670,10 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
         A.packed_ok = run == 4 ? 1 : 0;
         A.coord_bits = R <= 4 ? 16 : 8;
         A.tap_row = tap_row;
+        A.div_mt = make_fast_div(static_cast<unsigned>(A.mtiles_padded));
+        A.div_kc = make_fast_div(static_cast<unsigned>(A.kc_max));
+        A.div_nchunk = make_fast_div(static_cast<unsigned>(A.nchunk));
+        A.div_groups = make_fast_div(static_cast<unsigned>(A.groups));
         A.direct = direct ? 1 : 0;
         A.nbuf = nbuf;
         A.waves = waves;
@@ -942,7 +946,10 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
           P.in[a] = static_cast<int>(g.in[a]);
           P.pe[a] = pe[a];
           P.pad[a] = static_cast<int>(g.p[a]);
+          P.div_pe[a] = make_fast_div(static_cast<unsigned>(pe[a]));
         }
+        P.div_chunks = make_fast_div(static_cast<unsigned>(pe[R - 1] / 8));
+        P.div_rows = make_fast_div(static_cast<unsigned>(pvol / pe[R - 1]));
         // grad_output as the padded copy's source/destination sees it.
         WgradArgs& D = plan.args;
         std::memset(&D, 0, sizeof(D));
@@ -1283,7 +1290,12 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
     const size_t fused = (gi && b.dg.ok && is_half(dt))
                              ? (size_t)octet_sum_blocks(g.batch, g.out_vol) * sizeof(float)
                              : 0;
-    b.off_bias = L.take((size_t)g.out_channels * std::max(fused, kBiasChunks * sizeof(double)));
+    // Or one float per position chunk of the channel-major weight gradient, which adds them.
+    const size_t cm = (gw && b.wg.ok && b.wg.cm && is_half(dt))
+                          ? (size_t)b.wg.cm_args.npc * sizeof(float)
+                          : 0;
+    b.off_bias = L.take((size_t)g.out_channels *
+                        std::max(std::max(fused, cm), kBiasChunks * sizeof(double)));
   }
   b.bytes = L.total;
   return b;
@@ -1668,11 +1680,13 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     }
     return CONVND_HIP_SUCCESS;
   }
-  // The bias gradient's channel sums come from the backward prologue launch when the input
-  // gradient runs on MFMA (its octet-major grad_output copy writes them, or, with direct
-  // staging, a sums part of the same launch); otherwise grad_output is reduced on its own.
-  const bool fused_bias = gb && gi && b.dg.ok && is_half(dtype);
-  if (gb && !fused_bias) {
+  // The bias gradient's channel sums: the channel-major weight gradient adds them from the
+  // grad_output tiles it stages anyway; else the backward prologue launch writes them when the
+  // input gradient runs on MFMA (its octet-major grad_output copy, or, with direct staging, a
+  // sums part of the same launch); otherwise grad_output is reduced on its own.
+  const bool cm_bias = gb && gw && b.wg.ok && b.wg.cm && is_half(dtype);
+  const bool fused_bias = gb && !cm_bias && gi && b.dg.ok && is_half(dtype);
+  if (gb && !fused_bias && !cm_bias) {
     st = hip_check(launch_grad_bias(dtype, g.batch, g.out_channels, g.out_vol, grad_output,
                                     grad_bias, reinterpret_cast<float*>(ws + b.off_bias),
                                     kBiasChunks, stream),
@@ -1725,6 +1739,7 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     CA.tables = dw_tables->dev;
     CA.x = ws + b.off_x_stage;
     CA.dy = grad_output;
+    CA.bias_part = cm_bias ? reinterpret_cast<float*>(ws + b.off_bias) : nullptr;
     pp.pp = &b.wg.ppad;
     pp.x = input;
     pp.x_pp = ws + b.off_x_stage;
@@ -1801,7 +1816,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
       timing_end(ev, stream);
       if (st != CONVND_HIP_SUCCESS) return st;
       if (b.wg.cm) {
-        st = hip_check(bias_in_reduce
+        st = hip_check(cm_bias ? launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream,
+                                                        CA.bias_part, CA.npc, g.out_channels,
+                                                        grad_bias)
+                       : bias_in_reduce
                            ? launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream,
                                                     sums, nsum, g.out_channels, grad_bias)
                            : launch_wgrad_cm_reduce(dtype, b.wg.mb, CA, grad_weight, stream),

@@ -28,6 +28,25 @@ struct DirectGeom {
   int64_t in[kMaxRank], out[kMaxRank], k[kMaxRank], s[kMaxRank], p[kMaxRank], d[kMaxRank];
 };
 
+// Division of a non-negative 31-bit integer by an invariant divisor d >= 1 as a multiply and
+// a shift: with l = ceil(log2 d), p = 31 + l and m = ceil(2^p / d) (m < 2^32), floor(x / d) =
+// (x m) >> p for every 0 <= x < 2^31, since x m / 2^p exceeds x / d by less than x / 2^p <=
+// 2^-l <= 1 / d, which never reaches the next integer.
+struct FastDiv {
+  unsigned m;
+  int p;
+};
+inline FastDiv make_fast_div(unsigned d) {
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  const int p = 31 + l;
+  const unsigned long long m = ((1ull << p) + d - 1) / d;
+  return FastDiv{static_cast<unsigned>(m), p};
+}
+__host__ __device__ __forceinline__ int fast_div(int x, FastDiv f) {
+  return static_cast<int>((static_cast<unsigned long long>(static_cast<unsigned>(x)) * f.m) >> f.p);
+}
+
 // Arguments of the box-tiled implicit GEMM (forward, or one family of stride phases of
 // the input gradient). All sizes fit int32; the planner checks that.
 //
@@ -93,6 +112,8 @@ struct IgemmArgs {
   int nrun;
   int nbuf;
   int waves;  // waves per workgroup (4, or 8 with direct staging)
+  // Divisions of the weight-packing unit index by mtiles_padded, kc_max, nchunk and groups.
+  FastDiv div_mt, div_kc, div_nchunk, div_groups;
 };
 
 constexpr int kTapPad = 8;
@@ -223,6 +244,9 @@ struct WgradCmArgs {
   const void* tables;
   int tab_chunk, tab_col, tab_cid, tab_run, tab_xsrc, tab_dsrc, tab_item, tab_bytes;
   int waves;  // waves per workgroup: 4 (one per SIMD) or 8 (two per SIMD, K steps split)
+  // Bias gradient partial sums [cout_total][npc] over each position chunk's items (null: not
+  // computed here).
+  float* bias_part;
 };
 
 // LDS bytes of one item buffer of the channel-major weight gradient (two per workgroup).
@@ -275,6 +299,10 @@ struct PlanarPadArgs {
   int in[kFastRank], pe[kFastRank], pad[kFastRank];
   int in_vol, pvol;
   unsigned src_bytes;  // size of the source tensor (loads past it read zero)
+  // Divisions of the copy's run index: by pe[a] (a < rank - 1), by the runs per row
+  // (pe[rank-1] / 8) and by the rows per (image, channel) (pvol / pe[rank-1]).
+  FastDiv div_pe[kFastRank];
+  FastDiv div_chunks, div_rows;
 };
 
 // Raises Kernel's dynamic-LDS limit on the current device to at least `bytes`. The attribute

@@ -26,8 +26,8 @@ namespace {
 // ---- fused prologue ----------------------------------------------------------------------
 
 struct DevPrologue {
-  // Weight packing of the implicit GEMM (reads the plan's geometry tables): first in block
-  // order (the longest-running blocks), so they overlap the copies.
+  // Weight packing of the implicit GEMM (the input gradient's reads the plan's geometry
+  // tables).
   IgemmArgs ig;
   const void* w;
   void* wpk;
@@ -68,7 +68,56 @@ struct DevPrologue {
   bool f_vec;  // 16-byte loads: volume a multiple of 8 and a 16-byte aligned source
 };
 
-// SPLIT: fp32 sources (split-precision copies and packing).
+// Channel partial sum of a 16-bit channels-first tensor: block (image, channel, run of
+// kSumRun positions) -> f_sums[c][n * f_nrun + run]. A whole run with 16-byte loads has
+// each thread's loads in flight together.
+__device__ __forceinline__ void channel_sum_block(const DevPrologue& P, int b,
+                                                  stage::OctetSmem* smem) {
+  const int run = b % P.f_nrun;
+  const int64_t rc = b / P.f_nrun;
+  const int64_t c = rc % P.f_channels;
+  const int64_t n = rc / P.f_channels;
+  const unsigned short* src =
+      static_cast<const unsigned short*>(P.f_src) + (n * P.f_channels + c) * P.f_volume;
+  const int64_t p0 = (int64_t)run * kSumRun;
+  const int64_t pend = p0 + kSumRun < P.f_volume ? p0 + kSumRun : P.f_volume;
+  auto widen16 = [&](unsigned h) {
+    return P.is_bf16 ? __builtin_bit_cast(float, h << 16)
+                     : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+  };
+  float acc = 0.f;
+  constexpr int kPer = kSumRun / (8 * kThreads);  // 16-byte loads per thread in a whole run
+  if (P.f_vec && pend - p0 == kSumRun) {
+    u32x4 v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      v[j] = *reinterpret_cast<const u32x4*>(src + p0 + 8 * ((int64_t)j * kThreads + threadIdx.x));
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc += widen16(v[j][k] & 0xffffu) + widen16(v[j][k] >> 16);
+  } else if (P.f_vec) {
+    for (int64_t q = p0 + 8 * (int64_t)threadIdx.x; q < pend; q += 8 * kThreads) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src + q);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc += widen16(v[k] & 0xffffu) + widen16(v[k] >> 16);
+    }
+  } else {
+    for (int64_t q = p0 + threadIdx.x; q < pend; q += kThreads) acc += widen16(src[q]);
+  }
+  // Fixed-order reduction: lanes by xor shuffles, then the four waves in order.
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if ((threadIdx.x & 63) == 0) smem->red[0][threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float total = ((smem->red[0][0] + smem->red[0][1]) + smem->red[0][2]) + smem->red[0][3];
+    const int64_t nsum = P.f_nrun * (P.f_blocks / (P.f_nrun * P.f_channels));
+    P.f_sums[c * nsum + n * P.f_nrun + run] = total;
+  }
+}
+
+// SPLIT: fp32 sources (split-precision copies and packing). Block order: channel sums and
+// weight packing first (latency-bound blocks with few bytes each), then the copies.
 template <typename T, bool SPLIT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void prologue_kernel(DevPrologue P) {
@@ -76,6 +125,13 @@ void prologue_kernel(DevPrologue P) {
   using S = typename std::conditional<SPLIT, float, unsigned short>::type;
   using W = typename std::conditional<SPLIT, float, T>::type;
   int b = blockIdx.x;
+  if constexpr (!SPLIT) {
+    if (b < P.f_blocks) {
+      channel_sum_block(P, b, &smem);
+      return;
+    }
+  }
+  b -= P.f_blocks;
   if (b < P.b_blocks) {
     stage::igemm_pack_blocks<T, W>(P.ig, static_cast<const W*>(P.w), static_cast<T*>(P.wpk),
                                    static_cast<int>(P.units), b, P.b_blocks);
@@ -103,49 +159,10 @@ void prologue_kernel(DevPrologue P) {
     return;
   }
   b -= P.d_blocks;
-  if (b < P.e_blocks) {
-    if constexpr (!SPLIT) {
-      stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
-                                 static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b,
-                                 P.e_blocks);
-    }
-    return;
-  }
-  b -= P.e_blocks;
   if constexpr (!SPLIT) {
-    if (b < P.f_blocks) {
-      const int run = b % P.f_nrun;
-      const int64_t rc = b / P.f_nrun;
-      const int64_t c = rc % P.f_channels;
-      const int64_t n = rc / P.f_channels;
-      const unsigned short* src =
-          static_cast<const unsigned short*>(P.f_src) + (n * P.f_channels + c) * P.f_volume;
-      const int64_t p0 = (int64_t)run * kSumRun;
-      const int64_t pend = p0 + kSumRun < P.f_volume ? p0 + kSumRun : P.f_volume;
-      auto widen16 = [&](unsigned h) {
-        return P.is_bf16 ? __builtin_bit_cast(float, h << 16)
-                         : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
-      };
-      float acc = 0.f;
-      if (P.f_vec) {
-        for (int64_t q = p0 + 8 * (int64_t)threadIdx.x; q < pend; q += 8 * kThreads) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(src + q);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) acc += widen16(v[k] & 0xffffu) + widen16(v[k] >> 16);
-        }
-      } else {
-        for (int64_t q = p0 + threadIdx.x; q < pend; q += kThreads) acc += widen16(src[q]);
-      }
-      // Fixed-order reduction: lanes by xor shuffles, then the four waves in order.
-      for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-      if ((threadIdx.x & 63) == 0) smem.red[0][threadIdx.x >> 6] = acc;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        const float total = ((smem.red[0][0] + smem.red[0][1]) + smem.red[0][2]) + smem.red[0][3];
-        const int64_t nsum = P.f_nrun * (P.f_blocks / (P.f_nrun * P.f_channels));
-        P.f_sums[c * nsum + n * P.f_nrun + run] = total;
-      }
-    }
+    if (b < P.e_blocks)
+      stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
+                                 static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b);
   }
 }
 
@@ -281,9 +298,9 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     P.w = p.w;
     P.wpk = p.wpk;
     P.units = (int64_t)a.nphase * a.groups * a.nchunk * a.kc_max * a.mtiles_padded * 64;
-    if (P.units > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit unit indices
-    const int64_t blocks = (P.units + kThreads - 1) / kThreads;
-    P.b_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
+    if (P.units * 8 > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit element indices
+    const int64_t blocks = (P.units * 8 + kThreads - 1) / kThreads;
+    P.b_blocks = static_cast<int>(blocks < 8192 ? blocks : 8192);
     total += P.b_blocks;
   }
   if (p.staged != nullptr && p.sa != nullptr && p.batch > 0 && p.sa->pvol > 0) {
@@ -327,8 +344,8 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     P.x_pp = p.x_pp;
     P.e_total = p.pp_batch * p.pp->channels * (p.pp->pvol / 8);
     if (P.e_total > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit run indices
-    const int64_t blocks = (P.e_total + kThreads - 1) / kThreads;
-    P.e_blocks = static_cast<int>(blocks < 4096 ? blocks : 4096);
+    const int64_t per = (int64_t)stage::kPlanarRuns * kThreads;
+    P.e_blocks = static_cast<int>((P.e_total + per - 1) / per);
     total += P.e_blocks;
   }
   if (p.sum_out != nullptr && p.sum_src != nullptr && p.sum_batch > 0 && p.sum_channels > 0) {

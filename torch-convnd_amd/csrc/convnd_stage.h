@@ -21,50 +21,61 @@ namespace stage {
 template <typename T, typename S>
 __device__ __forceinline__ void igemm_pack_blocks(const IgemmArgs& A, const S* w, T* wpk,
                                                   int units, int block, int nblocks) {
+  // One thread per element (8 per fragment, consecutive): the gathers of a wave are spread
+  // over many blocks, one load and one 2-byte store per thread.
   const int* pmap = reinterpret_cast<const int*>(static_cast<const char*>(A.tables) + A.tab_pack);
-  for (int u = block * kThreads + static_cast<int>(threadIdx.x); u < units; u += nblocks * kThreads) {
-    // 32-bit index arithmetic (the host keeps units below 2^31).
+  const int elems = units * 8;  // the host keeps this below 2^31
+  for (int e = block * kThreads + static_cast<int>(threadIdx.x); e < elems; e += nblocks * kThreads) {
+    const int u = e >> 3;
+    const int i = e & 7;
     int r = u >> 6;
     const int lane = u & 63;
-    const int mt = r % A.mtiles_padded;
-    r /= A.mtiles_padded;
-    const int kc = r % A.kc_max;
-    r /= A.kc_max;
-    const int ck = r % A.nchunk;
-    r /= A.nchunk;
-    const int g = r % A.groups;
-    const int phase = r / A.groups;
+    int q = fast_div(r, A.div_mt);
+    const int mt = r - q * A.mtiles_padded;
+    r = q;
+    q = fast_div(r, A.div_kc);
+    const int kc = r - q * A.kc_max;
+    r = q;
+    q = fast_div(r, A.div_nchunk);
+    const int ck = r - q * A.nchunk;
+    r = q;
+    const int phase = fast_div(r, A.div_groups);
+    const int g = r - phase * A.groups;
     const int m = mt * 16 + (lane & 15);
-    const int* pe = pmap + ((phase * A.kc_max + kc) * 4 + (lane >> 4)) * 2;
-    const int tflat = pe[0];
-    const int ci0 = ck * A.cc + pe[1];
-    unsigned short bits[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) bits[i] = 0;
-    if (m < A.cout_g && tflat >= 0) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int ci = ci0 + i, part = 0;
-        if constexpr (sizeof(S) == 4) {
-          const int sp = ci / A.split_c;
-          if (sp >= kSplitProducts) continue;
-          ci -= sp * A.split_c;
-          part = split_other_part(sp);
-        }
-        const int64_t widx =
-            A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
-                        : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
-        if constexpr (sizeof(S) == 4) {
-          bits[i] = bf16_part_bits(w[widx], part);
-        } else {
-          bits[i] = __builtin_bit_cast(unsigned short, w[widx]);
-        }
+    // Tap and channel of the lane's k-group: for the forward convolution (one phase, every
+    // tap in row-major order) k-group kk / 8 of the chunk is tap kk / cc, channel kk % cc;
+    // the input gradient's phases read the plan's map.
+    int tflat, chan;
+    if (A.mode == 0) {
+      const int kk = kc * 32 + (lane >> 4) * 8;
+      tflat = kk >> (3 + A.log2_noct);  // cc = 8 << log2_noct
+      chan = kk - (tflat << (3 + A.log2_noct));
+      if (tflat >= A.k_vol) tflat = -1;
+    } else {
+      const int* pe = pmap + ((phase * A.kc_max + kc) * 4 + (lane >> 4)) * 2;
+      tflat = pe[0];
+      chan = pe[1];
+    }
+    int ci = ck * A.cc + chan + i, part = 0;
+    bool live = m < A.cout_g && tflat >= 0;
+    if constexpr (sizeof(S) == 4) {
+      const int sp = ci / A.split_c;
+      live = live && sp < kSplitProducts;
+      ci -= sp * A.split_c;
+      part = split_other_part(sp);
+    }
+    unsigned short bits = 0;
+    if (live) {
+      const int64_t widx =
+          A.mode == 0 ? ((int64_t)(g * A.wk_cout_g + m) * A.wk_cin_g + ci) * A.k_vol + tflat
+                      : ((int64_t)(g * A.wk_cout_g + ci) * A.wk_cin_g + m) * A.k_vol + tflat;
+      if constexpr (sizeof(S) == 4) {
+        bits = bf16_part_bits(w[widx], part);
+      } else {
+        bits = __builtin_bit_cast(unsigned short, w[widx]);
       }
     }
-    u32x4 out;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = bits[2 * j] | (static_cast<unsigned>(bits[2 * j + 1]) << 16);
-    *reinterpret_cast<u32x4*>(wpk + (size_t)u * 8) = out;  // one 16-byte fragment store
+    reinterpret_cast<unsigned short*>(wpk)[e] = bits;
   }
 }
 
@@ -356,78 +367,127 @@ __device__ __forceinline__ void pad_dy16_blocks(const Src* src, unsigned short* 
   }
 }
 
-// Zero-padded channels-first copy (PlanarPadArgs), 16-bit elements: each thread writes 8
-// consecutive elements of a destination row (pe[rank-1] is a multiple of 8) as one 16-byte
-// store.
+// Zero-padded channels-first copy (PlanarPadArgs), 16-bit elements: run t of 8 consecutive
+// elements of a destination row (pe[rank-1] is a multiple of 8) is one 16-byte store. A block
+// covers 2 kThreads consecutive runs, two per thread (both loads in flight before the stores;
+// consecutive threads write consecutive runs); the index divisions are multiply-shifts.
+constexpr int kPlanarRuns = 2;
 __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
                                                     unsigned short* dst,
                                                     const PlanarPadArgs& P, int64_t total,
-                                                    int block, int nblocks) {
+                                                    int block) {
   const int R = P.rank;
-  int pe_last = 8, in_last = 1, pad_last = 0;
+  int in_last = 1, pad_last = 0;
 #pragma unroll
   for (int a = 0; a < kFastRank; ++a) {
     if (a == R - 1) {
-      pe_last = P.pe[a];
       in_last = P.in[a];
       pad_last = P.pad[a];
     }
   }
-  const int chunks = pe_last >> 3;
-  const int rows_per_img = P.pvol / pe_last;
+  const int chunks = P.pe[R - 1] >> 3;
+  const int rows_per_img = P.pvol / P.pe[R - 1];
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<unsigned short*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes),
       0x00020000);
   // 32-bit index arithmetic: the padded copy and the source hold fewer than 2^31 elements
   // (the planner checks both).
   const int ntotal = static_cast<int>(total);
-  for (int t = block * kThreads + static_cast<int>(threadIdx.x); t < ntotal; t += nblocks * kThreads) {
-    const int row = t / chunks;  // (image, channel, padded row)
+  u32x4 w[kPlanarRuns];
+#pragma unroll
+  for (int q = 0; q < kPlanarRuns; ++q) {
+    const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
+    w[q] = u32x4{0u, 0u, 0u, 0u};
+    if (t >= ntotal) continue;
+    const int row = fast_div(t, P.div_chunks);  // (image, channel, padded row)
     const int u0 = (t - row * chunks) * 8 - pad_last;
-    const int nc = row / rows_per_img;
+    const int nc = fast_div(row, P.div_rows);
     int rem = row - nc * rows_per_img;
     int srow = 0, istr = in_last;
     bool ok = true;
 #pragma unroll
     for (int a = kFastRank - 2; a >= 0; --a) {
       if (a < R - 1) {
-        const int u = rem % P.pe[a] - P.pad[a];
-        rem /= P.pe[a];
+        const int qa = fast_div(rem, P.div_pe[a]);
+        const int u = rem - qa * P.pe[a] - P.pad[a];
+        rem = qa;
         ok = ok && u >= 0 && u < P.in[a];
         srow += u * istr;
         istr *= P.in[a];
       }
     }
-    const int64_t base = (int64_t)nc * P.in_vol + srow;
-    // One 16-byte load at the (2-byte-aligned) first element when it lies wholly inside the
-    // source; elements outside the row are masked to zero. At the source's two ends (a load
-    // there would start before it or end past it) the elements are read one by one.
-    const int64_t first = base + u0;
+    // The run's 8 source elements start at `first` (any element offset): the two aligned
+    // 16-byte chunks that cover them are loaded (a chunk before the source or past its end
+    // reads zero) and the run is shifted out of them; elements outside the row are masked to
+    // zero.
+    const int64_t first = (int64_t)nc * P.in_vol + srow + u0;
     const int lo_i = -u0 < 0 ? 0 : (-u0 > 8 ? 8 : -u0);
     const int hi_i = in_last - u0 < 0 ? 0 : (in_last - u0 > 8 ? 8 : in_last - u0);
-    u32x4 w = u32x4{0u, 0u, 0u, 0u};
     if (ok && lo_i < hi_i) {
-      if (first >= 0 && (first + 8) * 2 <= static_cast<int64_t>(P.src_bytes)) {
-        w = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, static_cast<unsigned>(first * 2), 0, 0));
-        const unsigned bits = ((1u << hi_i) - 1u) & ~((1u << lo_i) - 1u);
+      const int64_t chunk = first >= 0 ? first >> 3 : -((7 - first) >> 3);  // floor(first / 8)
+      const int o = static_cast<int>(first - chunk * 8);                   // 0 .. 7
+      // A chunk that straddles the source's end loads element by element (the buffer's range
+      // check is per dword: a dword straddling the end would read zero, valid half included).
+      auto load16 = [&](int64_t c) {
+        const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
+        if (c >= 0 && (c + 1) * 16 > nbytes && c * 16 < nbytes) {
+          u32x4 r;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          w[j] &= ((bits >> (2 * j)) & 1u ? 0x0000ffffu : 0u) |
-                  ((bits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
-      } else {
-        unsigned short v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const bool in = i >= lo_i && i < hi_i;
-          const unsigned off = in ? static_cast<unsigned>((first + i) * 2) : 0xfffffff0u;
-          v[i] = __builtin_amdgcn_raw_buffer_load_b16(sr, off, 0, 0);
+          for (int k = 0; k < 4; ++k) {
+            const unsigned off = static_cast<unsigned>(c * 16 + 4 * k);
+            const unsigned lo = __builtin_amdgcn_raw_buffer_load_b16(sr, off, 0, 0);
+            const unsigned hi = __builtin_amdgcn_raw_buffer_load_b16(sr, off + 2u, 0, 0);
+            r[k] = lo | (hi << 16);
+          }
+          return r;
         }
+        const unsigned off = c >= 0 && c * 16 < nbytes ? static_cast<unsigned>(c * 16) : 0xfffffff0u;
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
+      };
+      const u32x4 c0 = load16(chunk);
+      const u32x4 c1 = o > 0 ? load16(chunk + 1) : u32x4{0u, 0u, 0u, 0u};
+      const unsigned d[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+      // Dword j of the run: bytes 2 o + 4 j .. +3 of the 32 loaded bytes.
+      u32x4 v;
+      const int dw = o >> 1;
+      if (o & 1) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = v[2 * j] | (static_cast<unsigned>(v[2 * j + 1]) << 16);
+        for (int j = 0; j < 4; ++j) {
+          unsigned lo = d[0], hi = d[1];
+#pragma unroll
+          for (int k = 1; k < 4; ++k)
+            if (dw == k) {
+              lo = d[k + j];
+              hi = d[k + j + 1];
+            }
+          if (dw == 0) {
+            lo = d[j];
+            hi = d[j + 1];
+          }
+          v[j] = __builtin_amdgcn_alignbyte(hi, lo, 2);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          unsigned x = d[j];
+#pragma unroll
+          for (int k = 1; k < 4; ++k)
+            if (dw == k) x = d[k + j];
+          v[j] = x;
+        }
       }
+      const unsigned bits = ((1u << hi_i) - 1u) & ~((1u << lo_i) - 1u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[j] &= ((bits >> (2 * j)) & 1u ? 0x0000ffffu : 0u) |
+                ((bits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+      w[q] = v;
     }
-    *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = w;
+  }
+#pragma unroll
+  for (int q = 0; q < kPlanarRuns; ++q) {
+    const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
+    if (t < ntotal) *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = w[q];
   }
 }
 

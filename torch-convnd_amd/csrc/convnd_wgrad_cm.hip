@@ -62,6 +62,16 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, unsigned ch
       r, (__attribute__((address_space(3))) void*)(dst), 16, voff, 0, 0, 0);
 }
 
+// A 16-bit element (the low half of h) as float.
+template <typename T>
+__device__ __forceinline__ float widen16(unsigned h) {
+  if constexpr (sizeof(T) == 2 && __is_same(T, __bf16)) {
+    return __builtin_bit_cast(float, h << 16);
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+  }
+}
+
 // Waits until every load this wave issued has landed (vmcnt 0; expcnt, lgkmcnt untouched).
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
@@ -245,6 +255,34 @@ void wgrad_cm_kernel(WgradCmArgs A) {
     }
   };
 
+  // Bias gradient (A.bias_part set): the column chunks of a workgroup row set share its
+  // grad_output rows out, chunk cq summing rows [r0, r1) of each item's tile from LDS, one
+  // 16-byte run of 8 positions per thread and slot (q = tid + kWT i: row r0 + q / 32 of the
+  // tile, run q % 32); the per-thread sums are added over the runs of a row in a fixed order
+  // at the end and written as this position chunk's partial sum of the channel.
+  constexpr int kRuns = kBoxVol / 8;
+  constexpr int kBs = MB * 16 * kRuns / kWT;  // slots per thread
+  const int r0 = (cq * MB * 16) / A.ncq;
+  const int r1 = ((cq + 1) * MB * 16) / A.ncq;
+  const int nbs = (r1 - r0) * kRuns;
+  float bsum[kBs];
+#pragma unroll
+  for (int i = 0; i < kBs; ++i) bsum[i] = 0.f;
+  auto sum_bias = [&](const unsigned char* buf) {
+    if (A.bias_part == nullptr) return;
+#pragma unroll
+    for (int i = 0; i < kBs; ++i) {
+      const int q = tid + kWT * i;
+      if (q < nbs) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(buf + (r0 + q / kRuns) * rowb + (q % kRuns) * 16);
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t += widen16<T>(v[k] & 0xffffu) + widen16<T>(v[k] >> 16);
+        bsum[i] += t;
+      }
+    }
+  };
+
   __syncthreads();  // run table and item records in LDS
   {
     const Bases b0 = bases(0);
@@ -269,12 +307,26 @@ void wgrad_cm_kernel(WgradCmArgs A) {
   // are waited for (by every wave, then a barrier) after the MFMAs.
   for (int k = 0; k < nitems; k += 2) {
     compute(cm_buf0, cm_buf1, k + 1);
+    sum_bias(cm_buf0);
     wait_loads();
     __syncthreads();
     if (k + 1 >= nitems) break;
     compute(cm_buf1, cm_buf0, k + 2);
+    sum_bias(cm_buf1);
     wait_loads();
     __syncthreads();
+  }
+  if (A.bias_part != nullptr) {
+    // Rows of 32 runs: lanes 0-31 and 32-63 of a wave hold one row each per slot.
+#pragma unroll
+    for (int i = 0; i < kBs; ++i) {
+      float t = bsum[i];
+      for (int m = 16; m >= 1; m >>= 1) t += __shfl_xor(t, m);
+      const int q = tid + kWT * i;
+      const int row = r0 + q / kRuns;
+      if ((lane & 31) == 0 && q < nbs && co0 + row < A.cout_g)
+        A.bias_part[(size_t)(g * A.cout_g + co0 + row) * A.npc + pc] = t;
+    }
   }
 
   if constexpr (W == 8) {
@@ -307,45 +359,56 @@ void wgrad_cm_kernel(WgradCmArgs A) {
 }
 
 // dW from the partial sums: slot s = ((((tile*4 + wave)*MB + mb)*NT + j)*64 + lane) holds
-// four output channels of one column; the npc partials are added in order, eight loads in
-// flight. Blocks past the reduction's: the bias gradient from the staging pass's sums.
+// four output channels of one column. A block covers 64 consecutive slots (lane = slot): its
+// wave w adds the partials w, w + 4, w + 8, ... (loads in flight eight at a time), and the
+// four waves' sums are added in order through LDS (a fixed order: deterministic). Blocks past
+// the reduction's: the bias gradient from the staging pass's sums.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void wgrad_cm_reduce_kernel(const f32x4* part, T* dw,
                                                                    WgradCmArgs A, int mbv,
                                                                    int64_t nslots, int rblocks,
                                                                    stage::BiasSums bs) {
+  static_assert(kThreads == 256, "four waves per block");
   if (static_cast<int>(blockIdx.x) >= rblocks) {
     stage::bias_from_sums<T>(bs, blockIdx.x - rblocks);
     return;
   }
+  __shared__ f32x4 wsum[3][64];
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
   // 32-bit slot arithmetic (the launcher keeps nslots below 2^31).
-  const int s = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
-  if (s >= nslots) return;
-  const int lane = s & 63;
+  const int s = static_cast<int>(blockIdx.x) * 64 + lane;
+  const bool live = s < nslots;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i0 = wave; i0 < A.npc; i0 += 32) {
+    f32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = i0 + 4 * k;
+      v[k] = live && i < A.npc ? part[(int64_t)i * nslots + s] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (i0 + 4 * k < A.npc) acc += v[k];
+  }
+  if (wave > 0) wsum[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave > 0 || !live) return;
+  acc = ((acc + wsum[0][lane]) + wsum[1][lane]) + wsum[2][lane];
   int r = s >> 6;
   const int j = r % A.nt;
   r /= A.nt;
   const int mb = r % mbv;
   r /= mbv;
-  const int wave = r & 3;
+  const int cw = r & 3;
   const int tile = r >> 2;
   const int cq = tile % A.ncq;
   const int zq = tile / A.ncq;
   const int g = zq / A.mgroups;
   const int mg = zq % A.mgroups;
   const int col = reinterpret_cast<const int*>(static_cast<const char*>(A.tables) +
-                                               A.tab_cid)[((cq * 4 + wave) * A.nt + j) * 16 + (lane & 15)];
+                                               A.tab_cid)[((cq * 4 + cw) * A.nt + j) * 16 + (lane & 15)];
   if (col < 0) return;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int i = 0;
-  for (; i + 8 <= A.npc; i += 8) {
-    f32x4 v[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = part[(int64_t)(i + k) * nslots + s];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) acc += v[k];
-  }
-  for (; i < A.npc; ++i) acc += part[(int64_t)i * nslots + s];
   const int co_base = mg * mbv * 16 + mb * 16 + 4 * (lane >> 4);
   const int64_t per_co = (int64_t)A.cin_g * A.k_vol;
 #pragma unroll
@@ -418,7 +481,7 @@ hipError_t launch_wgrad_cm_reduce(convnd_hip_dtype dtype, int mb, const WgradCmA
                                   int64_t nsum, int64_t channels, void* db) {
   const int64_t nslots = wgrad_cm_partial_slots(mb, a);
   if (nslots > 0x7fffffff) return hipErrorInvalidValue;  // 32-bit slot indices
-  const int64_t rblocks = (nslots + kThreads - 1) / kThreads;
+  const int64_t rblocks = (nslots + 63) / 64;  // 64 slots per block
   stage::BiasSums bs{bias_sums, db, static_cast<int>(nsum), static_cast<int>(channels)};
   const int64_t bblocks = bias_sums != nullptr ? channels : 0;
   if (bias_sums != nullptr && nsum > INT32_MAX) return hipErrorInvalidValue;
