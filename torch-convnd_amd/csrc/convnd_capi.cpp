@@ -105,22 +105,30 @@ int build_geometry(const convnd_hip_problem* pr, Geom* g) {
   return CONVND_HIP_SUCCESS;
 }
 
-// Axes with one sample, one tap and no padding contribute coordinate 0 only; dropping
-// them changes no volume or layout (the reference does the same,
-// src/torch_convnd/csrc/convnd.h:29-48). One axis is always kept.
+// An axis of one sample read by a one-tap kernel without padding only ever contributes
+// coordinate 0 (its output extent is 1 for any stride and dilation), so it is squeezed out of
+// the geometry: volumes and memory layouts are unchanged and more problems fit the kernels'
+// rank limit. At least one axis stays: the last one when every axis is such a unit axis. (The
+// reference applies the same rule before its index arithmetic,
+// src/torch_convnd/csrc/convnd.h:29-48.)
 Geom drop_unit_axes(const Geom& g) {
-  Geom r = g;
-  r.rank = 0;
+  int kept[kMaxRank];
+  int n = 0;
   for (int a = 0; a < g.rank; ++a) {
     const bool unit = g.in[a] == 1 && g.k[a] == 1 && g.p[a] == 0;
-    if (unit && (r.rank > 0 || a + 1 < g.rank)) continue;
-    r.in[r.rank] = g.in[a];
-    r.out[r.rank] = g.out[a];
-    r.k[r.rank] = g.k[a];
-    r.s[r.rank] = g.s[a];
-    r.p[r.rank] = g.p[a];
-    r.d[r.rank] = g.d[a];
-    ++r.rank;
+    if (!unit) kept[n++] = a;
+  }
+  if (n == 0) kept[n++] = g.rank - 1;
+  Geom r = g;
+  r.rank = n;
+  for (int i = 0; i < n; ++i) {
+    const int a = kept[i];
+    r.in[i] = g.in[a];
+    r.out[i] = g.out[a];
+    r.k[i] = g.k[a];
+    r.s[i] = g.s[a];
+    r.p[i] = g.p[a];
+    r.d[i] = g.d[a];
   }
   return r;
 }

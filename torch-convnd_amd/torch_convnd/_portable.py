@@ -5,8 +5,8 @@ src/torch_convnd/_decomposition.py:11-103 and the selection in
 src/torch_convnd/_dispatch.py:41-50). It is never used for a ROCm GPU tensor with
 ``backend="native"``/``"auto"`` outside a transform: those go to the gfx950 kernels.
 
-* Rank 4 with ordinary metadata: one batched ``F.conv3d`` per tap of the first spatial
-  axis. Low-precision partial results are summed in fp32 and rounded once at the end.
+* Rank 4 with ordinary metadata: one batched ``F.conv3d`` whose channels stack the first
+  spatial axis's taps (input frames ``o*s0 + t*d0`` as channel ``c*k0 + t``).
 * Everything else: output positions in tiles bounded by ``workspace_bytes``; each tile
   gathers its patch matrix with integer index arithmetic (padding never materialised,
   so huge padding/stride metadata stays cheap) and contracts it with one matmul per group.
@@ -32,32 +32,30 @@ def _output_shape(spatial, kernel, stride, padding, dilation):
     return shape
 
 
-def conv4d_by_frames(input, weight, bias, stride, padding, dilation, groups):
-    """Rank-4 convolution as a sum over the first axis's taps of batched 3-D convolutions.
+def conv4d_stacked_taps(input, weight, bias, stride, padding, dilation, groups):
+    """Rank-4 convolution as one batched 3-D convolution whose channels carry the first
+    spatial axis's taps.
 
-    Exact (not separable): tap ``t`` of axis 0 convolves the frames ``o*s0 + t*d0`` of the
-    axis-0-padded input with the 3-D kernel ``weight[:, :, t]``.
+    Output frame ``o`` of axis 0 reads the input frames ``o*s0 + t*d0`` (``t < k0``) of the
+    axis-0-padded input. Those ``k0`` frames become ``C*k0`` channels of one 3-D sample,
+    ordered (channel, tap) so that every group's channels stay contiguous; the weight
+    ``[Co, C/g, k0, k1, k2, k3]`` read as ``[Co, (C/g)*k0, k1, k2, k3]`` has the same order.
+    Exact: every product of an output is summed in the one 3-D reduction (in fp32 for 16-bit
+    data), and the bias is added there once.
     """
     batch, channels = input.shape[:2]
-    extent = (input.shape[2] + 2 * padding[0] - dilation[0] * (weight.shape[2] - 1) - 1) // stride[0] + 1
-    if extent <= 0:
+    taps0 = weight.shape[2]
+    frames = (input.shape[2] + 2 * padding[0] - dilation[0] * (taps0 - 1) - 1) // stride[0] + 1
+    if frames <= 0:
         raise RuntimeError("kernel exceeds padded input")
     source = F.pad(input, (0, 0, 0, 0, 0, 0, padding[0], padding[0])) if padding[0] else input
-    total = None
-    result_dtype = input.dtype
-    for tap in range(weight.shape[2]):
-        first = tap * dilation[0]
-        frames = source[:, :, first : first + (extent - 1) * stride[0] + 1 : stride[0]]
-        frames = frames.transpose(1, 2).reshape(batch * extent, channels, *input.shape[3:])
-        partial = F.conv3d(frames, weight[:, :, tap], None, stride[1:], padding[1:], dilation[1:], groups)
-        result_dtype = partial.dtype
-        partial = partial.reshape(batch, extent, *partial.shape[1:]).transpose(1, 2)
-        if partial.dtype in (torch.float16, torch.bfloat16):
-            partial = partial.float()
-        total = partial if total is None else total + partial
-    if bias is not None:
-        total = total + bias.to(total.dtype).reshape(1, -1, 1, 1, 1, 1)
-    return total.to(result_dtype)
+    span = dilation[0] * (taps0 - 1) + 1
+    # [N, C, frames, D1, D2, D3, span] windows along axis 0, of which every d0-th is a tap.
+    windows = source.unfold(2, span, stride[0])[..., :: dilation[0]]
+    stacked = windows.permute(0, 2, 1, 6, 3, 4, 5).reshape(batch * frames, channels * taps0, *input.shape[3:])
+    kernel = weight.reshape(weight.shape[0], weight.shape[1] * taps0, *weight.shape[3:])
+    out = F.conv3d(stacked, kernel, bias, stride[1:], padding[1:], dilation[1:], groups)
+    return out.reshape(batch, frames, *out.shape[1:]).transpose(1, 2).contiguous()
 
 
 def _patch_offsets(start, length, spatial, out_shape, kernel, stride, padding, dilation, device):
@@ -121,5 +119,5 @@ def portable_convolution(input, weight, bias, stride, padding, dilation, groups,
         and padding[0] <= input.shape[2]
         and small_metadata
     ):
-        return conv4d_by_frames(input, weight, bias, stride, padding, dilation, groups)
+        return conv4d_stacked_taps(input, weight, bias, stride, padding, dilation, groups)
     return tiled_patch_conv(input, weight, bias, stride, padding, dilation, groups, workspace_bytes)
