@@ -136,12 +136,19 @@ def test_float64_and_odd_channels_plans(lib):
     import torch
 
     c1 = ((4, 2, 8, 8, 8, 16), (8, 2, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1)
-    # bf16: the forward contracts over 2 input channels (direct); the input gradient over 8
-    # output channels (an MFMA octet); the weight gradient stages the input with its
-    # channels zero-padded to an octet.
-    assert _capi.plan_names(lib, *c1, torch.bfloat16) == ("direct", "mfma", "mfma")
-    # fp32 runs as split precision on the bf16 MFMA: 6 x 2 channels padded to 16.
-    assert _capi.plan_names(lib, *c1, torch.float32) == ("mfma", "mfma", "mfma")
+    # 2 x 8 channels: the tiny-channel vector-ALU kernels, in every precision.
+    for dtype in (torch.bfloat16, torch.float32, torch.float64):
+        assert _capi.plan_names(lib, *c1, dtype) == ("tiny",) * 3
+        for plan in _capi.plan_details(lib, *c1, dtype):
+            assert plan["kernel"] == "tiny" and plan["lds"] <= 160 * 1024, plan
+    # More channels: fp32 runs as split precision on the bf16 MFMA (6 x 8 channels).
+    c4 = ((1, 8, 4, 4, 4, 4, 4, 4), (16, 8, 3, 3, 3, 3, 3, 3), (1,) * 6, (1,) * 6, (1,) * 6, 1)
+    assert _capi.plan_names(lib, *c4, torch.float32) == ("mfma", "mfma", "mfma")
+    # float64 with few input channels per group runs tiny where its weights and halo fit LDS
+    # (rank 3, 27 taps), else direct (rank 6: 729 taps of weights per staged channel).
+    r3 = ((2, 8, 8, 8, 8), (16, 8, 3, 3, 3), (1,) * 3, (1,) * 3, (1,) * 3, 1)
+    assert _capi.plan_names(lib, *r3, torch.float64) == ("tiny",) * 3
+    assert _capi.plan_names(lib, *c4, torch.float64) == ("direct",) * 3
     assert _capi.plan_names(lib, *BASELINE["C2"], torch.float64) == ("direct",) * 3
     # fp32 with more than 64 channels per group in the GEMM-input role stays direct.
     wide = ((1, 72, 4, 4, 4, 8), (8, 72, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1)

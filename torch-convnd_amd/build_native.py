@@ -35,6 +35,7 @@ HIP_SOURCES = (
     "convnd_wgrad_cm.hip",
     "convnd_partial.hip",
     "convnd_static.hip",
+    "convnd_tiny.hip",
     "convnd_capi.cpp",
 )
 OFFLOAD_ARCH = os.environ.get("TORCH_CONVND_OFFLOAD_ARCH", "gfx950")

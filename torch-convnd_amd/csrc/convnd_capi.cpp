@@ -1210,7 +1210,164 @@ struct Layout {
   }
 };
 
+// Tiny-channel vector-ALU convolution (convnd_tiny.hip). Preferred over the implicit GEMM
+// for layers whose per-group channel product is small (a 16 x 16 MFMA tile would mostly
+// multiply padding, and the layer is bound by memory and launch latency) and for float64
+// (no float64 MFMA path here) with few input channels per group.
+struct TinyPlan {
+  bool ok = false;
+  TinyArgs args{};
+  size_t lds = 0;        // forward / input-gradient kernel
+  size_t wlds = 0;       // weight-gradient kernel (mode 0 plans)
+  int64_t part = 0;      // weight-gradient partial sums (accumulation-type elements)
+  int64_t bpart = 0;     // bias-gradient partial sums
+};
+
+constexpr int kTinyMaxChannels = 16;   // input channels per group staged in LDS
+constexpr int64_t kTinyLds = 160 * 1024;
+
+bool tiny_preferred(const Geom& g, convnd_hip_dtype dt) {
+  if (g.cin_g > kTinyMaxChannels) return false;
+  if (dt == CONVND_HIP_FLOAT64) return true;
+  return g.cin_g * g.cout_g <= 32;
+}
+
+// mode 0: forward geometry (and the weight gradient's); mode 1: input gradient of a stride-1
+// convolution as a convolution of grad_output.
+TinyPlan plan_tiny(const Geom& g, convnd_hip_dtype dt, int mode) {
+  TinyPlan plan;
+  const int R = g.rank;
+  if (R > kFastRank || !fits_int32(g) || g.batch > 65535) return plan;
+  const int64_t cig = mode == 0 ? g.cin_g : g.cout_g;
+  const int64_t cog = mode == 0 ? g.cout_g : g.cin_g;
+  if (cig > kTinyMaxChannels || cig < 1 || cog < 1) return plan;
+  int64_t in_size[kFastRank], out_size[kFastRank], pad[kFastRank], stride[kFastRank];
+  for (int a = 0; a < R; ++a) {
+    if (mode == 1 && g.s[a] != 1) return plan;
+    in_size[a] = mode == 0 ? g.in[a] : g.out[a];
+    out_size[a] = mode == 0 ? g.out[a] : g.in[a];
+    pad[a] = mode == 0 ? g.p[a] : (g.k[a] - 1) * g.d[a] - g.p[a];
+    stride[a] = mode == 0 ? g.s[a] : 1;
+  }
+  // Forward kernel: one wave per cpw output channels, at most 8 waves per workgroup; weight
+  // gradient: all output channels of the group in one tile of cot.
+  // Forward kernel: jw waves of cpw output channels each, times csplit slices of the input
+  // channels (their sums added through LDS), at most 8 waves.
+  const int cpw = cog >= 16 ? 4 : (cog >= 8 ? 2 : 1);
+  const int64_t jw = std::min<int64_t>(8, (cog + cpw - 1) / cpw);
+  int64_t csplit = 1;
+  while (csplit * 2 <= cig && jw * csplit * 2 <= 8) csplit *= 2;
+  const int64_t waves = jw * csplit;
+  const int64_t ctiles = (cog + jw * cpw - 1) / (jw * cpw);
+  const int cot = cog <= 4 ? 4 : (cog <= 8 ? 8 : 16);
+  if (g.groups * ctiles > 65535) return plan;  // grid y
+  const int64_t acc = dt == CONVND_HIP_FLOAT64 ? 8 : 4;
+  // Box of output positions: power-of-two extents filled from the last axis (coalesced
+  // stores), at most 64 positions (one per lane), shrunk while the grid would leave CUs idle.
+  int b[kFastRank];
+  {
+    int64_t rem = 64;
+    for (int a = R - 1; a >= 0; --a) {
+      int64_t e = 1;
+      while (e < out_size[a] && e < rem) e *= 2;
+      b[a] = static_cast<int>(e);
+      rem /= e;
+    }
+  }
+  auto count = [&](const int* bb, int64_t* boxes, int64_t* vol) {
+    *boxes = 1;
+    *vol = 1;
+    for (int a = 0; a < R; ++a) {
+      *boxes *= (out_size[a] + bb[a] - 1) / bb[a];
+      *vol *= bb[a];
+    }
+  };
+  int64_t boxes, box_vol;
+  count(b, &boxes, &box_vol);
+  while (box_vol > 64 && boxes * g.groups * ctiles * g.batch < 1024) {
+    int big = -1;
+    for (int a = 0; a < R; ++a)
+      if (b[a] > 1 && (big < 0 || b[a] * (a == R - 1 ? 1 : 4) > b[big] * (big == R - 1 ? 1 : 4))) big = a;
+    if (big < 0) break;
+    b[big] /= 2;
+    count(b, &boxes, &box_vol);
+  }
+  if (boxes > INT32_MAX / 2) return plan;
+  TinyArgs& A = plan.args;
+  std::memset(&A, 0, sizeof(A));
+  int64_t halo = 1;
+  for (int a = R - 1; a >= 0; --a) {
+    const int64_t h = (b[a] - 1) * stride[a] + (g.k[a] - 1) * g.d[a] + 1;
+    if (h > 4096) return plan;
+    A.hext[a] = static_cast<int>(h);
+    A.hpitch[a] = static_cast<int>(halo);
+    halo *= h;
+    if (halo > (1 << 20)) return plan;
+  }
+  if (g.k_vol > kTinyMaxTaps) return plan;
+  const int64_t red_at = (cig * halo + 3) / 4 * 4;
+  const int64_t lds = (red_at + (csplit - 1) * jw * 64 * cpw) * acc;
+  const int64_t wlds = cig * halo * acc + box_vol * cot * acc + g.k_vol * 4 + box_vol * 4;
+  if (lds > kTinyLds || (mode == 0 && cog <= 16 && wlds > kTinyLds)) return plan;
+  A.mode = mode;
+  A.rank = R;
+  A.batch = static_cast<int>(g.batch);
+  A.groups = static_cast<int>(g.groups);
+  A.cig = static_cast<int>(cig);
+  A.cog = static_cast<int>(cog);
+  A.cin_total = static_cast<int>(cig * g.groups);
+  A.cout_total = static_cast<int>(cog * g.groups);
+  A.cpw = cpw;
+  A.waves = static_cast<int>(waves);
+  A.csplit = static_cast<int>(csplit);
+  A.red_at = static_cast<int>(red_at);
+  A.cot = cot;
+  A.ctiles = static_cast<int>(ctiles);
+  int64_t ivol = 1, ovol = 1;
+  for (int a = 0; a < R; ++a) {
+    A.k[a] = static_cast<int>(g.k[a]);
+    A.s[a] = static_cast<int>(stride[a]);
+    A.p[a] = static_cast<int>(pad[a]);
+    A.d[a] = static_cast<int>(g.d[a]);
+    A.in_size[a] = static_cast<int>(in_size[a]);
+    A.out_size[a] = static_cast<int>(out_size[a]);
+    A.box[a] = b[a];
+    A.box_shift[a] = 0;
+    while ((1 << A.box_shift[a]) < b[a]) ++A.box_shift[a];
+    A.nbox[a] = static_cast<int>((out_size[a] + b[a] - 1) / b[a]);
+    A.div_hext[a] = make_fast_div(static_cast<unsigned>(A.hext[a]));
+    A.div_k[a] = make_fast_div(static_cast<unsigned>(A.k[a]));
+    ivol *= in_size[a];
+    ovol *= out_size[a];
+  }
+  A.box_vol = static_cast<int>(box_vol);
+  A.halo_vol = static_cast<int>(halo);
+  A.k_vol = static_cast<int>(g.k_vol);
+  A.in_vol = static_cast<int>(ivol);
+  A.out_vol = static_cast<int>(ovol);
+  A.boxes = static_cast<int>(boxes);
+  A.div_halo = make_fast_div(static_cast<unsigned>(halo));
+  for (int t = 0; t < A.k_vol; ++t) {
+    int r = t, off = 0;
+    for (int a = R - 1; a >= 0; --a) {
+      off += (r % A.k[a]) * A.d[a] * A.hpitch[a];
+      r /= A.k[a];
+    }
+    A.toff[t] = off;
+  }
+  plan.ok = true;
+  plan.lds = static_cast<size_t>(lds);
+  if (mode == 0 && cog <= 16 && wlds <= kTinyLds) {
+    plan.wlds = static_cast<size_t>(wlds);
+    const int64_t nblk = g.batch * boxes * g.groups;
+    plan.part = nblk * cog * cig * g.k_vol;
+    plan.bpart = nblk * cog;
+  }
+  return plan;
+}
+
 struct ForwardSetup {
+  TinyPlan tiny;
   IgemmPlan ig;
   size_t off_stage = 0, off_wpk = 0;
   size_t bytes = 0;
@@ -1249,7 +1406,8 @@ Setup cached_plan(PlanCache<Setup>& cache, const std::string& key, Make&& make) 
 
 ForwardSetup make_forward(const Geom& g, convnd_hip_dtype dt) {
   ForwardSetup f;
-  f.ig = plan_igemm(g, dt, 0);
+  if (tiny_preferred(g, dt)) f.tiny = plan_tiny(g, dt, 0);
+  if (!f.tiny.ok) f.ig = plan_igemm(g, dt, 0);
   Layout L;
   if (f.ig.ok) {
     // Staged operands and packed weights are 16-bit (bf16 parts for split-precision fp32).
@@ -1261,6 +1419,8 @@ ForwardSetup make_forward(const Geom& g, convnd_hip_dtype dt) {
 }
 
 struct BackwardSetup {
+  TinyPlan tdx, tdw;  // tiny-channel input and weight gradients
+  size_t off_tpart = 0, off_tbpart = 0;
   IgemmPlan dg;
   WgradPlan wg;
   size_t off_dy_stage = 0, off_wpk = 0, off_x_stage = 0, off_partial = 0, off_bias = 0;
@@ -1277,14 +1437,26 @@ BackwardSetup make_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool gw
   BackwardSetup b;
   const int64_t es = element_size(dt);
   Layout L;
-  if (gi && g.batch > 0) {
+  const bool tiny = tiny_preferred(g, dt);
+  if (gi && g.batch > 0 && tiny) b.tdx = plan_tiny(g, dt, 1);
+  if (gi && g.batch > 0 && !b.tdx.ok) {
     b.dg = plan_igemm(g, dt, 1);
     if (b.dg.ok) {
       b.off_dy_stage = L.take(b.dg.staged_elems * 2);
       b.off_wpk = L.take(b.dg.wpk_elems * 2);
     }
   }
-  if (gw && g.batch > 0) {
+  if (gw && g.batch > 0 && tiny) {
+    b.tdw = plan_tiny(g, dt, 0);
+    if (b.tdw.ok && b.tdw.wlds > 0) {
+      const size_t acc = dt == CONVND_HIP_FLOAT64 ? 8 : 4;
+      b.off_tpart = L.take(b.tdw.part * acc);
+      b.off_tbpart = L.take(b.tdw.bpart * acc);
+    } else {
+      b.tdw.ok = false;
+    }
+  }
+  if (gw && g.batch > 0 && !b.tdw.ok) {
     b.wg = plan_wgrad(g, dt);
     if (b.wg.ok) {
       b.off_x_stage = L.take(b.wg.staged_elems * 2);
@@ -1498,6 +1670,20 @@ int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, co
                 const void* weight, const void* bias, void* output, int activation, char* ws,
                 const void* tables, void* tables_at, bool timed, hipStream_t stream) {
   int st;
+  if (f.tiny.ok) {
+    TinyArgs T = f.tiny.args;
+    T.in = input;
+    T.w = weight;
+    T.bias = bias;
+    T.out = output;
+    const auto ev = timed ? timing_begin(0, stream) : std::pair<hipEvent_t, hipEvent_t>{};
+    st = hip_check(launch_tiny_conv(dtype, T, f.tiny.lds, stream), "tiny-channel forward");
+    if (timed) timing_end(ev, stream);
+    if (st != CONVND_HIP_SUCCESS || activation == CONVND_HIP_ACT_NONE) return st;
+    return hip_check(launch_activation(dtype, output, g.batch * g.out_channels * g.out_vol,
+                                       activation, stream),
+                     "activation pass");
+  }
   if (!f.ig.ok) {
     st = hip_check(launch_direct_forward(dtype, to_direct(g), input, weight, bias, output, stream),
                    "direct forward kernel");
@@ -1592,10 +1778,14 @@ const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_d
                                  int which) {
   Geom g;
   if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return "invalid";
+  if (which < 0 || which > 2) return "invalid";
+  if (tiny_preferred(g, dtype)) {
+    const TinyPlan t = plan_tiny(g, dtype, which == 1 ? 1 : 0);
+    if (t.ok && (which != 2 || t.wlds > 0)) return "tiny";
+  }
   if (which == 0) return plan_igemm(g, dtype, 0).ok ? "mfma" : "direct";
   if (which == 1) return plan_igemm(g, dtype, 1).ok ? "mfma" : "direct";
-  if (which == 2) return plan_wgrad(g, dtype).ok ? "mfma" : "direct";
-  return "invalid";
+  return plan_wgrad(g, dtype).ok ? "mfma" : "direct";
 }
 
 int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
@@ -1692,9 +1882,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   // grad_output tiles it stages anyway; else the backward prologue launch writes them when the
   // input gradient runs on MFMA (its octet-major grad_output copy, or, with direct staging, a
   // sums part of the same launch); otherwise grad_output is reduced on its own.
+  const bool tiny_bias = gb && gw && b.tdw.ok;
   const bool cm_bias = gb && gw && b.wg.ok && b.wg.cm && is_half(dtype);
-  const bool fused_bias = gb && !cm_bias && gi && b.dg.ok && is_half(dtype);
-  if (gb && !fused_bias && !cm_bias) {
+  const bool fused_bias = gb && !cm_bias && !tiny_bias && gi && b.dg.ok && is_half(dtype);
+  if (gb && !fused_bias && !cm_bias && !tiny_bias) {
     st = hip_check(launch_grad_bias(dtype, g.batch, g.out_channels, g.out_vol, grad_output,
                                     grad_bias, reinterpret_cast<float*>(ws + b.off_bias),
                                     kBiasChunks, stream),
@@ -1801,7 +1992,17 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                    "bias gradient");
     if (st != CONVND_HIP_SUCCESS) return st;
   }
-  if (gi) {
+  if (gi && b.tdx.ok) {
+    TinyArgs T = b.tdx.args;
+    T.in = grad_output;
+    T.w = weight;
+    T.bias = nullptr;
+    T.out = grad_input;
+    const auto ev = timing_begin(1, stream);
+    st = hip_check(launch_tiny_conv(dtype, T, b.tdx.lds, stream), "tiny-channel input gradient");
+    timing_end(ev, stream);
+    if (st != CONVND_HIP_SUCCESS) return st;
+  } else if (gi) {
     if (mfma_dx) {
       const auto ev = timing_begin(1, stream);
       st = hip_check(launch_igemm(dtype, b.dg.mb, b.dg.nb, DA, b.dg.lds, stream),
@@ -1814,7 +2015,18 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     }
     if (st != CONVND_HIP_SUCCESS) return st;
   }
-  if (gw) {
+  if (gw && b.tdw.ok) {
+    TinyArgs T = b.tdw.args;
+    T.in = input;
+    T.w = weight;
+    T.dy = grad_output;
+    const auto ev = timing_begin(2, stream);
+    st = hip_check(launch_tiny_wgrad(dtype, T, b.tdw.wlds, ws + b.off_tpart, ws + b.off_tbpart,
+                                     grad_weight, tiny_bias ? grad_bias : nullptr, stream),
+                   "tiny-channel weight gradient");
+    timing_end(ev, stream);
+    if (st != CONVND_HIP_SUCCESS) return st;
+  } else if (gw) {
     if (mfma_dw) {
       const auto ev = timing_begin(2, stream);
       st = hip_check(b.wg.cm ? launch_wgrad_cm(dtype, b.wg.mb, CA, b.wg.lds, stream)
@@ -1860,7 +2072,17 @@ int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype
     for (int i = 0; i < n; ++i) out += (i ? "," : "") + std::to_string(v[i]);
     return out + "]";
   };
-  if (which == 0 || which == 1) {
+  const TinyPlan tp = tiny_preferred(g, dtype) && which >= 0 && which <= 2
+                          ? plan_tiny(g, dtype, which == 1 ? 1 : 0)
+                          : TinyPlan{};
+  if (tp.ok && (which != 2 || tp.wlds > 0)) {
+    const TinyArgs& T = tp.args;
+    text = "{\"kernel\":\"tiny\",\"box\":" + join(T.box, T.rank) + ",\"halo\":" +
+           join(T.hext, T.rank) + ",\"cpw\":" + std::to_string(T.cpw) + ",\"waves\":" +
+           std::to_string(T.waves) + ",\"cot\":" + std::to_string(T.cot) + ",\"lds\":" +
+           std::to_string(which == 2 ? tp.wlds : tp.lds) + ",\"workgroups\":" +
+           std::to_string((int64_t)T.boxes * T.groups * (which == 2 ? 1 : T.ctiles) * T.batch) + "}";
+  } else if (which == 0 || which == 1) {
     const IgemmPlan p = plan_igemm(g, dtype, which);
     if (!p.ok) {
       text = "{\"kernel\":\"direct\"}";

@@ -47,6 +47,43 @@ __host__ __device__ __forceinline__ int fast_div(int x, FastDiv f) {
   return static_cast<int>((static_cast<unsigned long long>(static_cast<unsigned>(x)) * f.m) >> f.p);
 }
 
+constexpr int kTinyMaxTaps = 512;
+// Tiny-channel convolution on the vector ALUs (convnd_tiny.hip): a workgroup per (box of
+// output positions, group and tile of output channels, image); halo of the group's cig input
+// channels in LDS. Mode 0: forward convolution (also the weight
+// gradient's geometry, with dy set); mode 1: input gradient of a stride-1 convolution as a
+// convolution of grad_output (in) with the flipped, transposed weights. All sizes int32.
+struct TinyArgs {
+  const void* in;    // [batch][cin_total][in_vol]
+  const void* w;     // the convolution's weight [cout][cin_g][k_vol] (both modes)
+  const void* bias;  // [cout_total] or null (mode 0)
+  void* out;         // [batch][cout_total][out_vol]
+  const void* dy;    // weight gradient: grad_output [batch][cout_total][out_vol]
+  int mode, rank, batch, groups;
+  int cig, cog;                 // reduction / output channels per group (the kernel's roles)
+  int cin_total, cout_total;
+  int cpw, waves, ctiles;       // forward kernel: output channels per wave (1, 2 or 4), waves
+                                // per workgroup, workgroup tiles per group
+  int csplit, red_at;           // input-channel slices per workgroup (waves = slots x slices)
+                                // and the LDS element offset of their sums
+  int cot;                      // weight gradient: output channels per workgroup (4, 8, 16)
+  int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
+  int in_size[kFastRank], out_size[kFastRank];
+  int box[kFastRank], box_shift[kFastRank], nbox[kFastRank];
+  int hext[kFastRank], hpitch[kFastRank];
+  int box_vol, halo_vol, k_vol, in_vol, out_vol, boxes;
+  FastDiv div_halo, div_hext[kFastRank], div_k[kFastRank];
+  // Halo offset (positions) of every tap, sum over the axes of t_a d_a hpitch_a: read by the
+  // forward kernel with uniform (scalar) loads from the kernel arguments.
+  int toff[kTinyMaxTaps];
+};
+hipError_t launch_tiny_conv(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, hipStream_t s);
+// Weight gradient (and bias gradient when db is set) of a mode-0 TinyArgs: per-workgroup
+// partial sums into part / bpart (tiny_wgrad_part_elems accumulation-type elements), then a
+// fixed-order reduction into dw / db.
+hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, void* part,
+                             void* bpart, void* dw, void* db, hipStream_t s);
+
 // Arguments of the box-tiled implicit GEMM (forward, or one family of stride phases of
 // the input gradient). All sizes fit int32; the planner checks that.
 //

@@ -1,0 +1,472 @@
+// Tiny-channel N-d convolution on the vector ALUs (gfx950): layers with a few input and
+// output channels per group, where a matrix-core GEMM would run mostly on padding and the work
+// is bound by memory and launch latency, not by arithmetic.
+//
+//   * tiny_conv_kernel: a workgroup owns a box of at most 64 output positions of one image
+//     (one per lane) and a tile of output channels of one group, CPW per wave. It stages the
+//     box's input halo for every input channel of the group into LDS (widened to the
+//     accumulation type, zero outside the input); each lane then accumulates its position's CPW
+//     outputs with FMAs, per (input channel, tap) one LDS read of its input value, the weights
+//     being the same for every lane of the wave (uniform loads through the scalar cache). The
+//     bias is added at the end. The same kernel computes the input gradient of a stride-1
+//     convolution as a convolution of grad_output with the flipped, transposed weights
+//     (mode 1).
+//   * tiny_wgrad_kernel: a workgroup owns a box of output positions of one image and one group:
+//     it stages the input halo and the grad_output tile, and each thread owns one (input channel,
+//     tap) column, accumulating all output channels over the box's positions; it writes these
+//     partial sums (and the grad_output sums of the box, for the bias gradient) per workgroup.
+//   * tiny_reduce_kernel: adds the workgroups' partial sums in a fixed order into dW and db.
+// Every sum has a fixed order, so results are bitwise repeatable. Semantics follow the
+// reference's im2col map (src/torch_convnd/csrc/convnd.h:57-104): input coordinate =
+// o*stride - pad + t*dilation, out-of-range coordinates read as zero.
+
+#include "convnd_internal.h"
+#include "convnd_types.h"
+
+namespace convnd {
+namespace {
+
+template <typename T>
+using TinyAcc = typename Acc<T>::type;
+
+// Box coordinates of position q (power-of-two extents, last axis fastest).
+__device__ __forceinline__ void tiny_box_coords(const TinyArgs& A, int q, int* c) {
+#pragma unroll
+  for (int a = kFastRank - 1; a >= 0; --a) {
+    if (a < A.rank) {
+      c[a] = q & (A.box[a] - 1);
+      q >>= A.box_shift[a];
+    }
+  }
+}
+
+// Stages the input halo of box bx of image n, input channels [c0, c0 + cig) of the tensor, into
+// xh[c][h] (h over the halo, last axis fastest). Eight elements per thread and pass, their loads
+// all issued before the first store (a load outside the input reads element 0 and is replaced
+// by zero), so each thread waits for memory once per pass.
+template <typename T>
+__device__ __forceinline__ void tiny_stage_halo(const TinyArgs& A, const T* in, int n, int c0,
+                                                const int* origin, TinyAcc<T>* xh) {
+  using Acc = TinyAcc<T>;
+  constexpr int kBatch = 8;
+  const int total = A.cig * A.halo_vol;
+  const int nt = blockDim.x;
+  for (int e0 = threadIdx.x; e0 < total; e0 += kBatch * nt) {
+    T raw[kBatch];
+    bool keep[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int e = e0 + u * nt;
+      const int c = fast_div(e, A.div_halo);
+      int h = e - c * A.halo_vol;
+      int off = 0, stride = 1;
+      bool ok = e < total;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < A.rank) {
+          const int q = fast_div(h, A.div_hext[a]);
+          const int ha = h - q * A.hext[a];
+          h = q;
+          const int x = origin[a] * A.s[a] - A.p[a] + ha;
+          ok = ok && x >= 0 && x < A.in_size[a];
+          off += x * stride;
+          stride *= A.in_size[a];
+        }
+      }
+      keep[u] = ok;
+      raw[u] = in[ok ? ((size_t)n * A.cin_total + c0 + c) * A.in_vol + off : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int e = e0 + u * nt;
+      if (e < total) xh[e] = keep[u] ? widen<Acc>(raw[u]) : Acc(0);
+    }
+  }
+}
+
+// LDS offset (in the halo, positions) of every tap: sum over the axes of t_a * d_a * hpitch_a.
+__device__ __forceinline__ void tiny_tap_offsets(const TinyArgs& A, int* toff) {
+  for (int t = threadIdx.x; t < A.k_vol; t += blockDim.x) {
+    int r = t, off = 0;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      if (a < A.rank) {
+        const int q = fast_div(r, A.div_k[a]);
+        off += (r - q * A.k[a]) * A.d[a] * A.hpitch[a];
+        r = q;
+      }
+    }
+    toff[t] = off;
+  }
+}
+
+// One lane per box position (box_vol <= 64) and one wave per CPW output channels: the
+// wave's weights are the same for all its lanes, so they come through the scalar cache
+// (uniform loads), and each (input channel, tap) costs one LDS read of the lane's input value
+// and CPW FMAs.
+template <typename T, int CPW>
+__global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
+  using Acc = TinyAcc<T>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  Acc* xh = reinterpret_cast<Acc*>(smem);  // [cig][halo_vol]
+  const int bx = blockIdx.x;
+  const int g = blockIdx.y / A.ctiles;
+  const int tile = blockIdx.y - g * A.ctiles;
+  const int n = blockIdx.z;
+  int origin[kFastRank];
+  {
+    int r = bx;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      origin[a] = 0;
+      if (a < A.rank) {
+        const int q = r / A.nbox[a];
+        origin[a] = (r - q * A.nbox[a]) * A.box[a];
+        r = q;
+      }
+    }
+  }
+  tiny_stage_halo<T>(A, static_cast<const T*>(A.in), n, g * A.cig, origin, xh);
+  __syncthreads();
+
+  // Wave w: output channels of slot w % jw, input channels of slice w / jw (the slices'
+  // sums are added through LDS at the end, in slice order).
+  const int q = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int jw = A.waves / A.csplit;
+  const int jwave = wave % jw;
+  const int cs = wave / jw;
+  const int j0 = (tile * jw + jwave) * CPW;  // first output channel (in the group) of the wave
+  int bc[kFastRank];
+  tiny_box_coords(A, q, bc);
+  int posoff = 0, outoff = 0, ostride = 1;
+  bool inside = q < A.box_vol;
+#pragma unroll
+  for (int a = kFastRank - 1; a >= 0; --a) {
+    if (a < A.rank) {
+      posoff += bc[a] * A.s[a] * A.hpitch[a];
+      const int o = origin[a] + bc[a];
+      inside = inside && o < A.out_size[a];
+      outoff += o * ostride;
+      ostride *= A.out_size[a];
+    }
+  }
+  const bool wave_live = j0 < A.cog;
+  const int c_lo = cs * A.cig / A.csplit;
+  const int c_hi = (cs + 1) * A.cig / A.csplit;
+  // Weights W(j, c, t): forward w[g cog + j][c][t]; input gradient w[g cig + c][j][K - 1 - t]
+  // (the kernel's reduction channels are the convolution's output channels). A channel past
+  // the group's reads channel j0 and is not stored. Taps go in chunks of 8: the chunk's tap
+  // offsets (kernel arguments) and weights are uniform scalar loads, then 8 LDS reads of the
+  // lane's input values, then the 8 x CPW FMAs.
+  const T* w = static_cast<const T*>(A.w);
+  int jj[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) jj[i] = j0 + i < A.cog ? j0 + i : j0;
+  Acc acc[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) acc[i] = 0;
+  constexpr int kChunk = 8;
+  const int kv = A.k_vol;
+  for (int c = wave_live && inside ? c_lo : c_hi; c < c_hi; ++c) {
+    const Acc* xc = xh + (size_t)c * A.halo_vol + posoff;
+    const T* wr[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; ++i)
+      wr[i] = A.mode == 0 ? w + ((size_t)(g * A.cog + jj[i]) * A.cig + c) * kv
+                          : w + ((size_t)(g * A.cig + c) * A.cog + jj[i]) * kv;
+    int t0 = 0;
+    if (A.mode == 0) {
+      for (; t0 + kChunk <= kv; t0 += kChunk) {
+        Acc v[kChunk];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) v[u] = xc[A.toff[t0 + u]];
+#pragma unroll
+        for (int i = 0; i < CPW; ++i)
+#pragma unroll
+          for (int u = 0; u < kChunk; ++u) acc[i] += v[u] * widen<Acc>(wr[i][t0 + u]);
+      }
+    } else {
+      for (; t0 + kChunk <= kv; t0 += kChunk) {
+        Acc v[kChunk];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) v[u] = xc[A.toff[t0 + u]];
+        const int back = kv - kChunk - t0;  // taps K-1-t0-u = back + (kChunk-1-u)
+#pragma unroll
+        for (int i = 0; i < CPW; ++i)
+#pragma unroll
+          for (int u = 0; u < kChunk; ++u) acc[i] += v[u] * widen<Acc>(wr[i][back + (kChunk - 1 - u)]);
+      }
+    }
+    for (int t = t0; t < kv; ++t) {
+      const Acc v = xc[A.toff[t]];
+      const int tw = A.mode == 0 ? t : kv - 1 - t;
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) acc[i] += v * widen<Acc>(wr[i][tw]);
+    }
+  }
+  if (A.csplit > 1) {
+    Acc* red = xh + A.red_at;  // [csplit - 1][jw][64][CPW]
+    if (cs > 0) {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) red[(((cs - 1) * jw + jwave) * 64 + q) * CPW + i] = acc[i];
+    }
+    __syncthreads();
+    if (cs > 0) return;
+    for (int k = 0; k + 1 < A.csplit; ++k) {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) acc[i] += red[((k * jw + jwave) * 64 + q) * CPW + i];
+    }
+  }
+  if (!wave_live || !inside) return;
+  T* out = static_cast<T*>(A.out);
+  const T* bias = static_cast<const T*>(A.bias);
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    if (j0 + i < A.cog) {
+      const int co = g * A.cog + j0 + i;
+      Acc v = acc[i];
+      if (bias != nullptr) v += widen<Acc>(bias[co]);
+      out[((size_t)n * A.cout_total + co) * A.out_vol + outoff] = narrow<T>(v);
+    }
+  }
+}
+
+// Partial sums of one workgroup (image n, box bx, group g): part[blk][co][c][t] for the group's
+// output channels co, input channels c, taps t, and bpart[blk][co] (grad_output summed over the
+// box) where blk = (n * boxes + bx) * groups + g.
+template <typename T, int COG>
+__global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAcc<T>* part,
+                                                              TinyAcc<T>* bpart) {
+  using Acc = TinyAcc<T>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  // [box_vol][COG] grad_output tile first (16-byte aligned rows of COG), then the halo.
+  Acc* dyt = reinterpret_cast<Acc*>(smem);
+  Acc* xh = dyt + (size_t)A.box_vol * COG;                // [cig][halo_vol]
+  int* toff = reinterpret_cast<int*>(xh + (size_t)A.cig * A.halo_vol);  // [k_vol]
+  int* posl = toff + A.k_vol;                             // [box_vol]
+  const int bx = blockIdx.x;
+  const int g = blockIdx.y;
+  const int n = blockIdx.z;
+  int origin[kFastRank];
+  {
+    int r = bx;
+#pragma unroll
+    for (int a = kFastRank - 1; a >= 0; --a) {
+      origin[a] = 0;
+      if (a < A.rank) {
+        const int q = r / A.nbox[a];
+        origin[a] = (r - q * A.nbox[a]) * A.box[a];
+        r = q;
+      }
+    }
+  }
+  const T* x = static_cast<const T*>(A.in);
+  const T* dy = static_cast<const T*>(A.dy);
+  tiny_stage_halo<T>(A, x, n, g * A.cig, origin, xh);
+  tiny_tap_offsets(A, toff);
+  // grad_output tile [q][co] (zero outside the output and past the group's channels) and the
+  // halo offset of every box position.
+  // (box_vol * COG <= 64 * 16 entries: at most four per thread, loads first.)
+  {
+    constexpr int kPer = (64 * COG + kThreads - 1) / kThreads;
+    T raw[kPer];
+    bool keep[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + u * kThreads;
+      const int q = e / COG;
+      const int j = e - q * COG;
+      int bc[kFastRank];
+      tiny_box_coords(A, q, bc);
+      int posoff = 0, outoff = 0, ostride = 1;
+      bool inside = e < A.box_vol * COG && j < A.cog;
+#pragma unroll
+      for (int a = kFastRank - 1; a >= 0; --a) {
+        if (a < A.rank) {
+          posoff += bc[a] * A.s[a] * A.hpitch[a];
+          const int o = origin[a] + bc[a];
+          inside = inside && o < A.out_size[a];
+          outoff += o * ostride;
+          ostride *= A.out_size[a];
+        }
+      }
+      keep[u] = inside;
+      raw[u] = dy[inside ? ((size_t)n * A.cout_total + g * A.cog + j) * A.out_vol + outoff : 0];
+      if (j == 0 && e < A.box_vol * COG) posl[q] = posoff;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + u * kThreads;
+      if (e < A.box_vol * COG) dyt[e] = keep[u] ? widen<Acc>(raw[u]) : Acc(0);
+    }
+  }
+  __syncthreads();
+  const int blk = (n * A.boxes + bx) * A.groups + g;
+  const int ncol = A.cig * A.k_vol;
+  for (int col = threadIdx.x; col < ncol; col += kThreads) {
+    const int c = col / A.k_vol;
+    const int t = col - c * A.k_vol;
+    const Acc* xc = xh + (size_t)c * A.halo_vol + toff[t];
+    Acc acc[COG];
+#pragma unroll
+    for (int j = 0; j < COG; ++j) acc[j] = 0;
+    typedef Acc acc4 __attribute__((ext_vector_type(4)));
+    for (int q = 0; q < A.box_vol; ++q) {
+      const Acc v = xc[posl[q]];
+      const acc4* dq = reinterpret_cast<const acc4*>(dyt + q * COG);
+#pragma unroll
+      for (int j4 = 0; j4 < COG / 4; ++j4) {
+        const acc4 d = dq[j4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[4 * j4 + k] += d[k] * v;
+      }
+    }
+    Acc* pc = part + (size_t)blk * A.cog * ncol;
+#pragma unroll
+    for (int j = 0; j < COG; ++j)
+      if (j < A.cog) pc[(size_t)j * ncol + col] = acc[j];
+  }
+  if (bpart != nullptr && (int)threadIdx.x < A.cog) {
+    const int j = threadIdx.x;
+    Acc s = 0;
+    for (int q = 0; q < A.box_vol; ++q) s += dyt[q * COG + j];
+    bpart[(size_t)blk * A.cog + j] = s;
+  }
+}
+
+// dW[g cog + co][c][t] = sum over the workgroups blk of image/box of part[blk][co][c][t] (blocks
+// of group g only), and db likewise from bpart. A block covers 16 consecutive output elements
+// (the lane's low 4 bits) and splits the workgroups into 16 interleaved sets (the thread's high
+// bits), eight loads in flight per thread; the 16 set sums are added in order through LDS
+// (fixed order: deterministic).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void tiny_reduce_kernel(TinyArgs A, const TinyAcc<T>* part,
+                                                               const TinyAcc<T>* bpart, T* dw,
+                                                               T* db) {
+  using Acc = TinyAcc<T>;
+  __shared__ Acc red[16][16];
+  const int ncol = A.cig * A.k_vol;
+  const int per_group = A.cog * ncol;
+  const int nw = A.groups * per_group;
+  const int nb = db != nullptr ? A.groups * A.cog : 0;
+  const int el = threadIdx.x & 15;
+  const int set = threadIdx.x >> 4;
+  const int e = blockIdx.x * 16 + el;
+  const int nblk = A.batch * A.boxes;
+  // Element e: a weight (e < nw) or a bias channel; its partials are at stride `stride` from
+  // `base`, one per workgroup blk = b * groups + g.
+  const Acc* src = nullptr;
+  size_t stride = 0;
+  if (e < nw) {
+    const int g = e / per_group;
+    src = part + (size_t)g * per_group + (e - g * per_group);
+    stride = (size_t)A.groups * per_group;
+  } else if (e < nw + nb) {
+    const int f = e - nw;
+    const int g = f / A.cog;
+    src = bpart + (size_t)g * A.cog + (f - g * A.cog);
+    stride = (size_t)A.groups * A.cog;
+  }
+  Acc acc = 0;
+  if (src != nullptr) {
+    for (int b0 = set; b0 < nblk; b0 += 16 * 8) {
+      Acc v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int b = b0 + 16 * k;
+        v[k] = b < nblk ? src[(size_t)b * stride] : Acc(0);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (b0 + 16 * k < nblk) acc += v[k];
+    }
+  }
+  red[set][el] = acc;
+  __syncthreads();
+  if (set != 0 || src == nullptr) return;
+  for (int k = 1; k < 16; ++k) acc += red[k][el];
+  if (e < nw) {
+    dw[e] = narrow<T>(acc);
+  } else {
+    db[e - nw] = narrow<T>(acc);
+  }
+}
+
+template <typename T, int CPW>
+hipError_t tiny_launch(const TinyArgs& a, size_t lds, hipStream_t s) {
+  if (lds > 64 * 1024) {
+    const hipError_t err = ensure_dynamic_lds<tiny_conv_kernel<T, CPW>>(lds);
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL((tiny_conv_kernel<T, CPW>), dim3(a.boxes, a.groups * a.ctiles, a.batch),
+                     dim3(64 * a.waves), lds, s, a);
+  return hipGetLastError();
+}
+
+template <typename T, int COG>
+hipError_t tiny_wgrad_launch(const TinyArgs& a, size_t lds, void* part, void* bpart, void* dw,
+                             void* db, hipStream_t s) {
+  using Acc = TinyAcc<T>;
+  if (lds > 64 * 1024) {
+    const hipError_t err = ensure_dynamic_lds<tiny_wgrad_kernel<T, COG>>(lds);
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL((tiny_wgrad_kernel<T, COG>), dim3(a.boxes, a.groups, a.batch), dim3(kThreads),
+                     lds, s, a, static_cast<Acc*>(part), static_cast<Acc*>(bpart));
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int64_t n = (int64_t)a.groups * a.cog * a.cig * a.k_vol + (db != nullptr ? a.groups * a.cog : 0);
+  hipLaunchKernelGGL((tiny_reduce_kernel<T>), dim3(static_cast<unsigned>((n + 15) / 16)),
+                     dim3(kThreads), 0, s, a, static_cast<const Acc*>(part),
+                     static_cast<const Acc*>(bpart), static_cast<T*>(dw), static_cast<T*>(db));
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t tiny_dispatch(const TinyArgs& a, size_t lds, hipStream_t s) {
+  switch (a.cpw) {
+    case 1: return tiny_launch<T, 1>(a, lds, s);
+    case 2: return tiny_launch<T, 2>(a, lds, s);
+    case 4: return tiny_launch<T, 4>(a, lds, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t tiny_wgrad_dispatch(const TinyArgs& a, size_t lds, void* part, void* bpart, void* dw,
+                               void* db, hipStream_t s) {
+  switch (a.cot) {
+    case 4: return tiny_wgrad_launch<T, 4>(a, lds, part, bpart, dw, db, s);
+    case 8: return tiny_wgrad_launch<T, 8>(a, lds, part, bpart, dw, db, s);
+    case 16: return tiny_wgrad_launch<T, 16>(a, lds, part, bpart, dw, db, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_tiny_conv(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, hipStream_t s) {
+  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32: return tiny_dispatch<float>(a, lds, s);
+    case CONVND_HIP_FLOAT64: return tiny_dispatch<double>(a, lds, s);
+    case CONVND_HIP_FLOAT16: return tiny_dispatch<_Float16>(a, lds, s);
+    case CONVND_HIP_BFLOAT16: return tiny_dispatch<__bf16>(a, lds, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, void* part,
+                             void* bpart, void* dw, void* db, hipStream_t s) {
+  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32: return tiny_wgrad_dispatch<float>(a, lds, part, bpart, dw, db, s);
+    case CONVND_HIP_FLOAT64: return tiny_wgrad_dispatch<double>(a, lds, part, bpart, dw, db, s);
+    case CONVND_HIP_FLOAT16: return tiny_wgrad_dispatch<_Float16>(a, lds, part, bpart, dw, db, s);
+    case CONVND_HIP_BFLOAT16: return tiny_wgrad_dispatch<__bf16>(a, lds, part, bpart, dw, db, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace convnd
