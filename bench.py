@@ -211,7 +211,7 @@ def cpu_threads():
     return min(cores, share) if share > 0 else cores
 
 
-def measure_configs(torch, device, iterations=30, warmup=5):
+def measure_configs(torch, device, iterations=30, warmup=5, only=None):
     """Every BASELINE config at full size through conv_nd(backend="native"): forward alone
     and forward + full backward (dx, dW, db) for a resident synthetic dY; each the median of
     `iterations` calls timed with their own HIP event pair after `warmup` calls (warm caches:
@@ -222,6 +222,8 @@ def measure_configs(torch, device, iterations=30, warmup=5):
     lib = _build.hip_library()
     out = {}
     for name, (xs, ws, stride, padding, dilation, groups, bias, dtype_name, roofs) in CONFIGS.items():
+        if only is not None and name not in only:
+            continue
         dtype = getattr(torch, dtype_name)
         x, w, b = make_inputs(torch, dtype, device, xs, ws)
         if not bias:
@@ -399,6 +401,9 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-configs", action="store_true",
                         help="skip the per-config fwd / fwd+bwd timings of C1-C5")
+    parser.add_argument("--configs", default="",
+                        help="comma-separated subset of C1,C2,C3,C4_fp32,C4_bf16,C5 for the "
+                        "per-config timings (default: all)")
     parser.add_argument(
         "--calibration-copy-mib", type=int, default=0,
         help="first run a plain elementwise copy of this many MiB three times (the known-size "
@@ -589,7 +594,8 @@ def main():
         },
     }
     if not args.no_configs:
-        result["configs"] = measure_configs(torch, device)
+        only = [c for c in args.configs.split(",") if c] or None
+        result["configs"] = measure_configs(torch, device, only=only)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)
