@@ -182,6 +182,14 @@ int convnd_hip_forward_noalloc(const convnd_hip_problem* problem, convnd_hip_dty
 const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                                  int which);
 
+/* Diagnostic, no counterpart in the reference: plans the forward and every gradient of a
+ * problem, builds their geometry tables in host memory and checks every entry against the
+ * buffer the kernels index with it (LDS halo and staging regions, tap prefetch rows, output
+ * offsets, weight-packing map, weight-gradient columns and load sources). Touches no GPU.
+ * Returns CONVND_HIP_SUCCESS, or CONVND_HIP_LAUNCH_FAILED with the first violation in
+ * convnd_hip_last_error(). Used by the host-only sanitizer build of the tests. */
+int convnd_hip_plan_check(const convnd_hip_problem* problem, convnd_hip_dtype dtype);
+
 /* JSON description of the launch plan (kernel family, box shape, channel chunk, LDS bytes,
  * occupancy, workgroups) written to `buffer` (NUL-terminated, truncated to `length`).
  * `which`: 0 forward, 1 input gradient, 2 weight gradient. Diagnostic only, no reference

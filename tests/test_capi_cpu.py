@@ -186,3 +186,33 @@ def test_timing_read_rejects_unknown_kernel(lib):
     assert lib.convnd_hip_timing_read(9, ctypes.byref(total), ctypes.byref(count)) == _capi.INVALID_ARGUMENT
     assert lib.convnd_hip_timing_read(0, ctypes.byref(total), ctypes.byref(count)) == _capi.SUCCESS
     assert count.value == 0
+
+
+def test_plan_check_baseline_and_random_geometries(lib):
+    """convnd_hip_plan_check (host-built tables checked against the buffers the kernels
+    index) passes for every BASELINE config and seeded random geometries in every dtype,
+    and reports validation failures with the validator's status."""
+    import random
+
+    dtypes = (_capi.FLOAT32, _capi.FLOAT64, _capi.FLOAT16, _capi.BFLOAT16)
+    for name, args in BASELINE.items():
+        p = problem(*args)
+        for dtype in dtypes:
+            assert lib.convnd_hip_plan_check(ctypes.byref(p), dtype) == _capi.SUCCESS, (
+                name, dtype, lib.convnd_hip_last_error().decode())
+    rng = random.Random(5)
+    for case in range(60):
+        rank = rng.randint(1, 5)
+        k = [rng.randint(1, 4) for _ in range(rank)]
+        d = [rng.randint(1, 2) for _ in range(rank)]
+        s = [rng.randint(1, 3) for _ in range(rank)]
+        pad = [rng.randint(0, (k[a] - 1) * d[a]) for a in range(rank)]
+        size = [max(rng.randint(1, 10), (k[a] - 1) * d[a] + 1 - 2 * pad[a], 1) for a in range(rank)]
+        g = rng.choice((1, 1, 2))
+        cig, cog = rng.choice((1, 2, 3, 8, 16, 32)), rng.choice((1, 4, 8, 16, 64))
+        p = problem((rng.randint(1, 2), cig * g, *size), (cog * g, cig, *k), s, pad, d, g)
+        for dtype in dtypes:
+            assert lib.convnd_hip_plan_check(ctypes.byref(p), dtype) == _capi.SUCCESS, (
+                case, dtype, lib.convnd_hip_last_error().decode())
+    bad = problem((1, 4, 6), (6, 2, 3), groups=3)
+    assert lib.convnd_hip_plan_check(ctypes.byref(bad), _capi.BFLOAT16) == _capi.INVALID_ARGUMENT

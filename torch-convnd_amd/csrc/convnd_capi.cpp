@@ -2061,6 +2061,151 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
   return CONVND_HIP_SUCCESS;
 }
 
+}  // extern "C"
+
+namespace convnd {
+namespace {
+
+// Checks of the plan checker: every geometry-table entry against the buffer the kernels index
+// with it. Each returns an empty string or the first violation found.
+std::string check_igemm_tables(const IgemmArgs& A0, size_t lds_bytes, const char* what) {
+  IgemmArgs A = A0;
+  const size_t bytes = igemm_table_layout(A);
+  std::vector<unsigned char> tab(bytes);
+  igemm_build_tables(A, tab.data());
+  auto fail_at = [&](const std::string& m) { return std::string(what) + ": " + m; };
+  const int positions_per_plane = A.plane_bytes / 16;
+  const int nbuf = A.direct ? A.nbuf : 1;
+  // LDS carve-up: halo buffers, row tables (2 ints per row), box output offsets, taps.
+  const size_t lds_need = (size_t)nbuf * A.halo_bytes + (size_t)A.rows * 8 +
+                          (size_t)((A.box_vol + 3) & ~3) * 4 + (size_t)4 * A.tap_row * 4;
+  if (lds_need > lds_bytes) return fail_at("LDS layout exceeds the plan's LDS size");
+  const int4* pos = reinterpret_cast<const int4*>(tab.data() + A.tab_pos);
+  const int4* rows = reinterpret_cast<const int4*>(tab.data() + A.tab_rows);
+  int max_pos = 0;
+  for (int q = 0; q < A.box_vol; ++q) {
+    if (pos[q].x < 0 || pos[q].x % 16 != 0) return fail_at("box position offset invalid");
+    max_pos = std::max(max_pos, pos[q].x);
+  }
+  for (int r = 0; r < A.rows; ++r)
+    if (rows[r].x < 0 || rows[r].x + A.hlast > positions_per_plane)
+      return fail_at("halo row past its LDS plane");
+  const int* taps = reinterpret_cast<const int*>(tab.data() + A.tab_taps);
+  const int* tail = reinterpret_cast<const int*>(tab.data() + A.tab_tail);
+  const int* pack = reinterpret_cast<const int*>(tab.data() + A.tab_pack);
+  const IgemmBox* boxes = reinterpret_cast<const IgemmBox*>(tab.data() + A.tab_box);
+  for (int ph = 0; ph < A.nphase; ++ph) {
+    for (int lg = 0; lg < 4; ++lg) {
+      const int* row = taps + (ph * 4 + lg) * A.tap_row;
+      for (int k = 0; k < A.tap_row; ++k)
+        if (row[k] < 0 || max_pos + row[k] + 16 > A.halo_bytes)
+          return fail_at("tap offset reads past the halo");
+      const int t = tail[ph * 4 + lg];
+      if (t < -1 || (t >= 0 && max_pos + t + 16 > A.halo_bytes))
+        return fail_at("tail tap offset reads past the halo");
+      for (int k = 0; k < A.kc_max; ++k) {
+        const int* e = pack + ((ph * A.kc_max + k) * 4 + lg) * 2;
+        if (e[0] < -1 || e[0] >= A.k_vol || (e[0] >= 0 && (e[1] < 0 || e[1] + 8 > A.cc)))
+          return fail_at("weight-packing map entry out of range");
+      }
+    }
+    const unsigned long long guard = A.coord_bits == 16 ? kGuard16 : kGuard8;
+    const unsigned long long ones = A.coord_bits == 16 ? kOnes16 : kOnes8;
+    for (int bx = 0; bx < A.boxes; ++bx) {
+      const IgemmBox& B = boxes[ph * A.boxes + bx];
+      if (B.flags & 1) continue;
+      if (B.kc > A.kc_max || B.kf > B.kc || B.kf < 0)
+        return fail_at("box K steps exceed the plan");
+      if (B.kf + 4 > A.tap_row) return fail_at("tap prefetch reads past the tap row");
+      for (int q = 0; q < A.box_vol; ++q) {
+        const unsigned long long c =
+            static_cast<unsigned>(pos[q].z) | (static_cast<unsigned long long>(static_cast<unsigned>(pos[q].w)) << 32);
+        const bool stored = (B.flags & 2) != 0 || swar_all_less(c, B.lim, guard, ones);
+        if (!stored) continue;
+        const int64_t o = (int64_t)B.out_origin + pos[q].y;
+        // Interior boxes with packed stores write runs of 4 adjacent outputs from positions
+        // 4j: those must be contiguous.
+        const bool packed = A.packed_ok && (B.flags & 2) && q % 4 == 0;
+        const int64_t run = packed ? 4 : 1;
+        if (packed)
+          for (int i = 1; i < 4; ++i)
+            if (pos[q + i].y != pos[q].y + i) return fail_at("packed output run not contiguous");
+        if (o < 0 || o + run > A.out_vol)
+          return fail_at("output offset outside the output (phase " + std::to_string(ph) +
+                         ", box " + std::to_string(bx) + ", position " + std::to_string(q) +
+                         ": " + std::to_string(o) + " of " + std::to_string(A.out_vol) +
+                         ", flags " + std::to_string(B.flags) + ")");
+      }
+    }
+  }
+  return "";
+}
+
+std::string check_wgrad_cm_tables(const WgradCmArgs& C0) {
+  WgradCmArgs C = C0;
+  const size_t bytes = wgrad_cm_table_layout(C);
+  std::vector<unsigned char> tab(bytes);
+  wgrad_cm_build_tables(C, tab.data());
+  const std::string what = "weight gradient (channel-major)";
+  if (C.dyt_bytes + C.xi * 1024 > kWgradCmBuffer) return what + ": item does not fit its buffer";
+  const int* col = reinterpret_cast<const int*>(tab.data() + C.tab_col);
+  const int* cid = reinterpret_cast<const int*>(tab.data() + C.tab_cid);
+  const int* run = reinterpret_cast<const int*>(tab.data() + C.tab_run);
+  int max_run = 0;
+  for (int r = 0; r < C.box_vol / 8; ++r) {
+    if (run[r] < 0) return what + ": negative run offset";
+    max_run = std::max(max_run, run[r]);
+  }
+  const size_t lanes = (size_t)C.ncq * 4 * C.nt * 16;
+  for (size_t i = 0; i < lanes; ++i) {
+    if (cid[i] < -1 || cid[i] >= C.cin_g * C.k_vol) return what + ": column id out of range";
+    if (col[i] < 0 || col[i] + max_run + 16 > C.xi * 1024)
+      return what + ": column read past the staged input runs";
+  }
+  const int* xsrc = reinterpret_cast<const int*>(tab.data() + C.tab_xsrc);
+  for (size_t i = 0; i < (size_t)C.ncq * C.xi * 64; ++i)
+    if (xsrc[i] < -1 || xsrc[i] >= C.cin_g * C.pvol) return what + ": input run source out of range";
+  return "";
+}
+
+std::string check_tiny(const TinyPlan& t, const char* what) {
+  const TinyArgs& A = t.args;
+  int max_tap = 0, max_pos = 0;
+  for (int i = 0; i < A.k_vol; ++i) max_tap = std::max(max_tap, A.toff[i]);
+  for (int a = 0; a < A.rank; ++a) max_pos += (A.box[a] - 1) * A.s[a] * A.hpitch[a];
+  if (max_tap + max_pos >= A.halo_vol) return std::string(what) + ": tap reads past the halo";
+  if (A.box_vol > 64 || A.waves > 8 || A.waves < 1) return std::string(what) + ": launch shape";
+  return "";
+}
+
+}  // namespace
+}  // namespace convnd
+
+extern "C" {
+
+int convnd_hip_plan_check(const convnd_hip_problem* problem, convnd_hip_dtype dtype) {
+  Geom g;
+  const int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  if (g.batch == 0) return CONVND_HIP_SUCCESS;
+  std::string bad;
+  const ForwardSetup f = make_forward(g, dtype);
+  if (f.tiny.ok) bad = check_tiny(f.tiny, "forward (tiny)");
+  if (bad.empty() && f.ig.ok) bad = check_igemm_tables(f.ig.args, f.ig.lds, "forward");
+  const BackwardSetup b = make_backward(g, dtype, true, true, true);
+  if (bad.empty() && b.tdx.ok) bad = check_tiny(b.tdx, "input gradient (tiny)");
+  if (bad.empty() && b.tdw.ok) bad = check_tiny(b.tdw, "weight gradient (tiny)");
+  if (bad.empty() && b.dg.ok) bad = check_igemm_tables(b.dg.args, b.dg.lds, "input gradient");
+  if (bad.empty() && b.wg.ok && b.wg.cm) bad = check_wgrad_cm_tables(b.wg.cm_args);
+  if (bad.empty() && b.wg.ok && !b.wg.cm) {
+    WgradArgs W = b.wg.args;
+    std::vector<unsigned char> tab(wgrad_table_layout(W, b.wg.mb));
+    wgrad_build_tables(W, tab.data());
+  }
+  if (!bad.empty()) return fail(CONVND_HIP_LAUNCH_FAILED, "plan check: " + bad);
+  return CONVND_HIP_SUCCESS;
+}
+
 int convnd_hip_plan_describe(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                              int which, char* buffer, size_t length) {
   Geom g;

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_partial_count",
     "convnd_hip_forward_act",
     "convnd_hip_forward_noalloc",
+    "convnd_hip_plan_check",
 )
 
 # Bytes of the per-GPU static scratch of convnd_hip_forward_noalloc (CONVND_HIP_NOALLOC_SCRATCH_BYTES).
@@ -89,6 +90,8 @@ def bind(library: ctypes.CDLL) -> ctypes.CDLL:
     library.convnd_hip_timing_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)]
     library.convnd_hip_forward_act.restype = ctypes.c_int
     library.convnd_hip_forward_act.argtypes = [P, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, vp, sz, vp]
+    library.convnd_hip_plan_check.restype = ctypes.c_int
+    library.convnd_hip_plan_check.argtypes = [P, ctypes.c_int]
     library.convnd_hip_forward_noalloc.restype = ctypes.c_int
     library.convnd_hip_forward_noalloc.argtypes = [P, ctypes.c_int, vp, vp, vp, vp, vp]
     library.convnd_hip_partial_count.restype = ctypes.c_int
