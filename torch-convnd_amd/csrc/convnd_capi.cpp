@@ -848,23 +848,47 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
       if (items > (int64_t{1} << 22)) return;
       const int64_t dyt_bytes = (int64_t)mb * 16 * box_vol * 2;
       const int ksteps = box_vol / 32;
-      int prev_nt = -1;
-      for (int ncq = 1; ncq <= ntiles; ++ncq) {
-        const int tpc = (ntiles + ncq - 1) / ncq;
-        if ((ntiles + tpc - 1) / tpc != ncq) continue;  // same split as a smaller ncq
+      // Column splits: (kvp, cpc, ncq, tpc, channels a chunk spans at most). Dense: the
+      // columns of consecutive channels share tiles and a chunk may span channels.
+      // Channel-aligned (taps padded to whole tiles): a chunk stages one channel's runs,
+      // for halos too large to stage two channels per item.
+      struct Split {
+        int kvp, cpc, ncq, tpc, nch;
+      };
+      std::vector<Split> splits;
+      {
+        int prev_nt = -1;
+        for (int ncq = 1; ncq <= ntiles; ++ncq) {
+          const int tpc = (ntiles + ncq - 1) / ncq;
+          if ((ntiles + tpc - 1) / tpc != ncq) continue;  // same split as a smaller ncq
+          const int nt = (tpc + 3) / 4;
+          if (nt == prev_nt) continue;
+          prev_nt = nt;
+          int nch = 1;
+          for (int cq = 0; cq < ncq; ++cq) {
+            const int c0 = cq * tpc * 16;
+            const int c1 = std::min((cq + 1) * tpc * 16, ncol);
+            if (c0 < c1) nch = std::max(nch, (c1 - 1) / k_vol - c0 / k_vol + 1);
+          }
+          splits.push_back({k_vol, 0, ncq, tpc, nch});
+        }
+        const int kvp = (k_vol + 15) / 16 * 16;
+        const int tch = kvp / 16;
+        // Padding at most an eighth of the columns.
+        if (k_vol % 16 != 0 && (kvp - k_vol) * 8 <= k_vol && (int64_t)cin_g * tch <= 65536) {
+          for (int cpc = 1; cpc <= tch; ++cpc) {
+            const int tpc = (tch + cpc - 1) / cpc;
+            if ((tch + tpc - 1) / tpc != cpc) continue;
+            splits.push_back({kvp, cpc, cin_g * cpc, tpc, 1});
+          }
+        }
+      }
+      for (const Split& sp : splits) {
+        const int ncq = sp.ncq, tpc = sp.tpc, nch = sp.nch;
         int nt = (tpc + 3) / 4;
         while (nt <= 8 && !wgrad_cm_supported(mb, nt, 4)) ++nt;
         if (nt > 8) continue;
-        if (nt == prev_nt) continue;
-        prev_nt = nt;
         if (filter.nb && filter.nb != nt) continue;
-        // Channels a chunk spans (its columns are consecutive in (channel, tap) order).
-        int nch = 1;
-        for (int cq = 0; cq < ncq; ++cq) {
-          const int c0 = cq * tpc * 16;
-          const int c1 = std::min((cq + 1) * tpc * 16, ncol);
-          if (c0 < c1) nch = std::max(nch, (c1 - 1) / k_vol - c0 / k_vol + 1);
-        }
         // Input runs per item in 64-run load instructions (at most 16 per wave), landing
         // after the grad_output tile in one item buffer.
         const int64_t xi = (nch * chpitch / 16 + 63) / 64;
@@ -930,6 +954,9 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
         C.mgroups = mgroups;
         C.ncq = ncq;
         C.nt = nt;
+        C.kvp = sp.kvp;
+        C.tpc = tpc;
+        C.cpc = sp.cpc;
         C.npc = static_cast<int>(npc);
         C.items = static_cast<int>(items);
         C.items_per_pc = static_cast<int>(ipc);

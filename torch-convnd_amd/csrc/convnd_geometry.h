@@ -485,23 +485,37 @@ inline size_t wgrad_cm_table_layout(WgradCmArgs& A) {
   return at;
 }
 
-// Column tiles: chunk cq holds tiles [cq * tpc, (cq + 1) * tpc); wave w of its workgroup the
-// chunk's tiles w * nt .. w * nt + nt - 1.
-inline int wgrad_cm_tiles_per_chunk(const WgradCmArgs& A) {
-  const int ntiles = (A.cin_g * A.k_vol + 15) / 16;
-  return (ntiles + A.ncq - 1) / A.ncq;
+// Column tiles [t0, t1) of chunk cq (see WgradCmArgs::kvp); wave w of its workgroup holds
+// the chunk's tiles t0 + w * nt .. t0 + w * nt + nt - 1 (those below t1).
+inline void wgrad_cm_chunk_tiles(const WgradCmArgs& A, int cq, int* t0, int* t1) {
+  if (A.cpc > 0) {
+    const int tch = A.kvp / 16;
+    const int ch = cq / A.cpc;
+    *t0 = ch * tch + (cq % A.cpc) * A.tpc;
+    *t1 = *t0 + A.tpc < (ch + 1) * tch ? *t0 + A.tpc : (ch + 1) * tch;
+  } else {
+    const int ntiles = (A.cin_g * A.kvp + 15) / 16;
+    *t0 = cq * A.tpc;
+    *t1 = *t0 + A.tpc < ntiles ? *t0 + A.tpc : ntiles;
+  }
+  if (*t1 < *t0) *t1 = *t0;
+}
+
+// Column c of the padded space: its weight column (ci * k_vol + tap), or -1 for padding.
+inline int wgrad_cm_column(const WgradCmArgs& A, int c) {
+  if (c >= A.cin_g * A.kvp) return -1;
+  const int tap = c % A.kvp;
+  return tap < A.k_vol ? (c / A.kvp) * A.k_vol + tap : -1;
 }
 
 // Channels spanned by chunk cq: first (group-relative) and count.
 inline void wgrad_cm_chunk_channels(const WgradCmArgs& A, int cq, int* first, int* count) {
-  const int ncol = A.cin_g * A.k_vol;
-  const int ntiles = (ncol + 15) / 16;
-  const int tpc = wgrad_cm_tiles_per_chunk(A);
-  const int t0 = cq * tpc;
-  const int t1 = t0 + tpc < ntiles ? t0 + tpc : ntiles;
+  int t0, t1;
+  wgrad_cm_chunk_tiles(A, cq, &t0, &t1);
+  const int ncol = A.cin_g * A.kvp;
   const int c_end = t1 * 16 < ncol ? t1 * 16 : ncol;
-  *first = t0 < t1 ? t0 * 16 / A.k_vol : 0;
-  *count = t0 < t1 ? (c_end - 1) / A.k_vol - *first + 1 : 0;
+  *first = t0 < t1 ? t0 * 16 / A.kvp : 0;
+  *count = t0 < t1 ? (c_end - 1) / A.kvp - *first + 1 : 0;
 }
 
 // Halo-row pitch (in rows) of each axis but the last.
@@ -534,15 +548,12 @@ inline int wgrad_cm_tap_offset(const WgradCmArgs& A, int t) {
 // Fills the tables (host memory of wgrad_cm_table_layout(A) bytes).
 inline void wgrad_cm_build_tables(const WgradCmArgs& A, unsigned char* tab) {
   const int R = A.rank;
-  const int ncol = A.cin_g * A.k_vol;
-  const int ntiles = (ncol + 15) / 16;
-  const int tpc = wgrad_cm_tiles_per_chunk(A);
   int* chunk = reinterpret_cast<int*>(tab + A.tab_chunk);
   int* col = reinterpret_cast<int*>(tab + A.tab_col);
   int* cid = reinterpret_cast<int*>(tab + A.tab_cid);
   for (int cq = 0; cq < A.ncq; ++cq) {
-    const int t0 = cq * tpc;
-    const int t1 = t0 + tpc < ntiles ? t0 + tpc : ntiles;
+    int t0, t1;
+    wgrad_cm_chunk_tiles(A, cq, &t0, &t1);
     int ci_lo, nch;
     wgrad_cm_chunk_channels(A, cq, &ci_lo, &nch);
     chunk[2 * cq] = ci_lo;
@@ -554,10 +565,10 @@ inline void wgrad_cm_build_tables(const WgradCmArgs& A, unsigned char* tab) {
         int cols[16], offs[16];
         for (int i = 0; i < 16; ++i) {
           const int c = T * 16 + i;
-          const bool ok = lt < tpc && T < t1 && c < ncol;
-          cols[i] = ok ? c : -1;
-          offs[i] = ok ? (c / A.k_vol - ci_lo) * A.chpitch + wgrad_cm_tap_offset(A, c % A.k_vol)
-                       : 0;
+          const int wc = T < t1 ? wgrad_cm_column(A, c) : -1;
+          cols[i] = wc;
+          offs[i] = wc >= 0 ? (wc / A.k_vol - ci_lo) * A.chpitch + wgrad_cm_tap_offset(A, wc % A.k_vol)
+                            : 0;
         }
         // Lanes 0-7 and 8-15 are read together (eight 16-byte reads per pass): give each
         // half columns on distinct 16-byte bank slots (bits 4-7 of the offset) where possible.

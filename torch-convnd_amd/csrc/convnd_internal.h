@@ -259,6 +259,12 @@ struct WgradCmArgs {
   int dyt_bytes;        // LDS bytes of the grad_output tile (MB * 16 rows of box_vol * 2)
   int xi, di;           // 64-run load instructions per item: input runs, grad_output runs
   int mgroups, ncq, nt; // output-channel groups of 16 * MB, column chunks, tiles per wave
+  // Column space: each input channel's k_vol taps take kvp >= k_vol consecutive columns
+  // (kvp - k_vol padding columns), 16 per tile. cpc == 0: chunk cq holds tiles [cq * tpc,
+  // (cq + 1) * tpc) of the whole space (kvp == k_vol). cpc > 0 (kvp a multiple of 16): every
+  // channel's kvp / 16 tiles split into cpc chunks of at most tpc tiles, chunk cq covering
+  // channel cq / cpc only, so it stages one channel's runs.
+  int kvp, tpc, cpc;
   int npc, items, items_per_pc;
   int lds_items;        // dynamic LDS byte offset of the item records (after the run table)
   int box[kFastRank], nbox[kFastRank], dext[kFastRank], hext[kFastRank], pe[kFastRank];

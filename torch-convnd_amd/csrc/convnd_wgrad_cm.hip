@@ -420,9 +420,10 @@ __global__ __launch_bounds__(kThreads) void wgrad_cm_reduce_kernel(const f32x4* 
 
 // The compiled (MB, NT) pairs: accumulators MB * NT * 4 registers (at most 128); with eight
 // waves per workgroup (two per SIMD, 256 registers each) the pairs that fit them unspilled.
-#define CONVND_WGRAD_CM_TILES(X) \
-  X(4, 4) X(4, 5) X(4, 6) X(4, 7) X(4, 8) X(2, 4) X(2, 6) X(2, 8) X(1, 4) X(1, 8)
-#define CONVND_WGRAD_CM_TILES8(X) X(4, 4) X(2, 4) X(2, 6) X(2, 8) X(1, 8)
+#define CONVND_WGRAD_CM_TILES(X)                                                         \
+  X(4, 4) X(4, 5) X(4, 6) X(4, 7) X(4, 8) X(2, 3) X(2, 4) X(2, 6) X(2, 8) X(1, 3) X(1, 4) \
+  X(1, 6) X(1, 8)
+#define CONVND_WGRAD_CM_TILES8(X) X(4, 4) X(2, 3) X(2, 4) X(2, 6) X(2, 8) X(1, 4) X(1, 6) X(1, 8)
 
 template <typename T>
 hipError_t wgrad_cm_dispatch(int mb, const WgradCmArgs& a, size_t lds, hipStream_t s) {
