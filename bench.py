@@ -60,6 +60,15 @@ PEAKS = {"bf16_mfma": (PEAK_BF16_TFLOPS, "TFLOP/s"), "fp32_mfma": (PEAK_FP32_TFL
          "hbm": (PEAK_HBM_GBS, "GB/s")}
 
 
+CL_CONFIGS = ("C2", "C5")
+
+
+def to_channels_last(t):
+    """Same values, stored [N, *spatial, C]."""
+    order = (0, *range(2, t.dim()), 1)
+    return t.permute(order).contiguous().permute(0, t.dim() - 1, *range(1, t.dim() - 1))
+
+
 def config_work(name):
     """(forward FLOP, forward bytes, forward+backward bytes) of a config: FLOP = 2 N P Co
     (C/g) taps; bytes = |x| + |W| + |y| (+|b|) forward and |dY| + |x| + |W| + |dx| + |dW|
@@ -221,11 +230,17 @@ def measure_configs(torch, device, iterations=30, warmup=5, only=None):
 
     lib = _build.hip_library()
     out = {}
-    for name, (xs, ws, stride, padding, dilation, groups, bias, dtype_name, roofs) in CONFIGS.items():
+    # Channels-last runs of C2 and C5: x and dY stored [N, *spatial, C] (outputs and grad_input
+    # come back in that layout; same kernels, no layout copy in the forward).
+    runs = [(name, name, False) for name in CONFIGS] + [(f"{name}_channels_last", name, True) for name in CL_CONFIGS]
+    for name, base, channels_last in runs:
+        xs, ws, stride, padding, dilation, groups, bias, dtype_name, roofs = CONFIGS[base]
         if only is not None and name not in only:
             continue
         dtype = getattr(torch, dtype_name)
         x, w, b = make_inputs(torch, dtype, device, xs, ws)
+        if channels_last:
+            x = to_channels_last(x)
         if not bias:
             b = None
         leaves = [t.detach().requires_grad_() for t in (x, w, b) if t is not None]
@@ -236,6 +251,8 @@ def measure_configs(torch, device, iterations=30, warmup=5, only=None):
 
         y = conv(*leaves)
         dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(5)).to(dtype).to(device)
+        if channels_last:
+            dy = to_channels_last(dy)
         del y
 
         def fwd():
@@ -259,7 +276,7 @@ def measure_configs(torch, device, iterations=30, warmup=5, only=None):
                 pairs.append((e0, e1))
             torch.cuda.synchronize()
             times[label] = statistics.median(a.elapsed_time(b_) for a, b_ in pairs)
-        flops, fwd_bytes, step_bytes = config_work(name)
+        flops, fwd_bytes, step_bytes = config_work(base)
         entry = {"dtype": dtype_name,
                  "plans": list(_capi.plan_names(lib, xs, ws, stride, padding, dilation, groups, dtype))}
         for label, work_flops, work_bytes in (("fwd", flops, fwd_bytes), ("fwd_bwd", 3 * flops, step_bytes)):
@@ -402,8 +419,8 @@ def main():
     parser.add_argument("--no-configs", action="store_true",
                         help="skip the per-config fwd / fwd+bwd timings of C1-C5")
     parser.add_argument("--configs", default="",
-                        help="comma-separated subset of C1,C2,C3,C4_fp32,C4_bf16,C5 for the "
-                        "per-config timings (default: all)")
+                        help="comma-separated subset of C1,C2,C3,C4_fp32,C4_bf16,C5,"
+                        "C2_channels_last,C5_channels_last for the per-config timings (default: all)")
     parser.add_argument(
         "--calibration-copy-mib", type=int, default=0,
         help="first run a plain elementwise copy of this many MiB three times (the known-size "

@@ -46,6 +46,16 @@ typedef enum convnd_hip_activation {
   CONVND_HIP_ACT_GELU_TANH = 3
 } convnd_hip_activation;
 
+/* Memory layout of the activation tensors of a call (input, output, grad_output and
+ * grad_input; weights are always [output_channels, channels / groups, kernel...]):
+ *   CHANNELS_FIRST  [batch, channels, spatial...]  (the reference's only layout)
+ *   CHANNELS_LAST   [batch, spatial..., channels]  (channels innermost, as PyTorch's
+ *                   channels_last / channels_last_3d memory formats and their N-d analogue) */
+typedef enum convnd_hip_layout {
+  CONVND_HIP_CHANNELS_FIRST = 0,
+  CONVND_HIP_CHANNELS_LAST = 1
+} convnd_hip_layout;
+
 typedef enum convnd_hip_status {
   CONVND_HIP_SUCCESS = 0,
   CONVND_HIP_INVALID_ARGUMENT = 1, /* geometry/shape/dtype rejected; see convnd_hip_last_error */
@@ -126,6 +136,34 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
                         const void* grad_output, const void* input, const void* weight,
                         void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
                         size_t workspace_size, void* stream);
+
+/* Device scratch bytes of convnd_hip_forward_layout / convnd_hip_backward_layout for a
+ * layout (CHANNELS_FIRST: the same as convnd_hip_forward_workspace_size /
+ * convnd_hip_backward_workspace_size). */
+size_t convnd_hip_forward_workspace_size_layout(const convnd_hip_problem* problem,
+                                                convnd_hip_dtype dtype, int layout);
+size_t convnd_hip_backward_workspace_size_layout(const convnd_hip_problem* problem,
+                                                 convnd_hip_dtype dtype, int layout,
+                                                 int need_grad_input, int need_grad_weight,
+                                                 int need_grad_bias);
+
+/* convnd_hip_forward_act / convnd_hip_backward with the activation tensors in `layout`
+ * (convnd_hip_layout). With CHANNELS_LAST the implicit GEMM with direct staging (16-bit data)
+ * reads [batch, spatial..., channels] and writes [batch, out..., output_channels] itself, so
+ * such a forward makes no layout copy; other plans, and the weight gradient (whose kernels
+ * read channels-first operands), run on channels-first copies in the workspace. Results are
+ * the same numbers as the channels-first call. No reference counterpart: the reference makes
+ * every operand contiguous (channels-first) first (src/torch_convnd/csrc/convnd.cpp:317-319,
+ * 377-381). */
+int convnd_hip_forward_layout(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                              int layout, int activation, const void* input, const void* weight,
+                              const void* bias, void* output, void* workspace,
+                              size_t workspace_size, void* stream);
+int convnd_hip_backward_layout(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                               int layout, const void* grad_output, const void* input,
+                               const void* weight, void* grad_input, void* grad_weight,
+                               void* grad_bias, void* workspace, size_t workspace_size,
+                               void* stream);
 
 /* Partial convolution's counts: window sums of a validity map under the convolution's
  * geometry (a depthwise all-ones convolution with symmetric zero padding). Reads

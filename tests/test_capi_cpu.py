@@ -181,6 +181,38 @@ def test_workspace_sizes_without_device(lib):
     assert lib.convnd_hip_forward_workspace_size(ctypes.byref(bad), _capi.BFLOAT16) == 0
 
 
+def test_channels_last_workspace_sizes_without_device(lib):
+    # Channels-first sizes equal the plain queries. Channels-last: the forward of a
+    # direct-staged implicit GEMM (C2 bf16) needs nothing more; a plan that runs on
+    # channels-first copies (fp32 split precision, tiny-channel kernels) adds the input and
+    # output copies; the backward adds the copies its weight gradient reads.
+    first, last = _capi.CHANNELS_FIRST, _capi.CHANNELS_LAST
+    p = problem(*BASELINE["C2"][:2], padding=(1,) * 4)
+    for dt in (_capi.BFLOAT16, _capi.FLOAT32):
+        fwd = lib.convnd_hip_forward_workspace_size(ctypes.byref(p), dt)
+        assert lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(p), dt, first) == fwd
+        bwd = lib.convnd_hip_backward_workspace_size(ctypes.byref(p), dt, 1, 1, 1)
+        assert lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(p), dt, first, 1, 1, 1) == bwd
+    x_bytes, y_bytes = 2 * 32 * 16**4 * 2, 2 * 64 * 16**4 * 2
+    fwd = lib.convnd_hip_forward_workspace_size(ctypes.byref(p), _capi.BFLOAT16)
+    assert lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last) == fwd
+    bwd_cl = lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last, 1, 1, 1)
+    assert bwd_cl >= lib.convnd_hip_backward_workspace_size(ctypes.byref(p), _capi.BFLOAT16, 1, 1, 1) + x_bytes + y_bytes
+    # grad_input alone: the input-gradient GEMM stages channels-last grad_output itself.
+    assert lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last, 1, 0, 0) == \
+        lib.convnd_hip_backward_workspace_size(ctypes.byref(p), _capi.BFLOAT16, 1, 0, 0)
+    fwd32 = lib.convnd_hip_forward_workspace_size(ctypes.byref(p), _capi.FLOAT32)
+    assert lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(p), _capi.FLOAT32, last) >= \
+        fwd32 + 2 * (x_bytes + y_bytes)
+    c1 = problem((4, 2, 8, 8, 8, 16), (8, 2, 3, 3, 3, 3), padding=(1,) * 4)
+    assert lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(c1), _capi.FLOAT32, last) >= \
+        4 * (4 * 2 * 8 * 8 * 8 * 16 + 4 * 8 * 8 * 8 * 8 * 16)
+    # An unknown layout is rejected before any device work.
+    assert lib.convnd_hip_forward_layout(ctypes.byref(p), _capi.BFLOAT16, 7, 0, None, None, None, None,
+                                         None, 0, None) == _capi.INVALID_ARGUMENT
+    assert b"layout" in lib.convnd_hip_last_error()
+
+
 def test_timing_read_rejects_unknown_kernel(lib):
     total, count = ctypes.c_double(), ctypes.c_int64()
     assert lib.convnd_hip_timing_read(9, ctypes.byref(total), ctypes.byref(count)) == _capi.INVALID_ARGUMENT

@@ -158,3 +158,40 @@ def test_vmap_rule_of_the_operator():
         helpers.assert_close(got[i], want, torch.float64, f"vmap weight slice {i}")
     empty = torch.func.vmap(lambda x: op(x, w, b, *args))(xs[:0])
     assert empty.shape == (0, 2, 5, 5, 1, 6, 5)
+
+
+def _channels_last(t):
+    order = (0, *range(2, t.dim()), 1)
+    return t.permute(order).contiguous().permute(0, t.dim() - 1, *range(1, t.dim() - 1))
+
+
+def _is_channels_last(t):
+    return not t.is_contiguous() and t.permute(0, *range(2, t.dim()), 1).is_contiguous()
+
+
+def test_channels_last_outputs_follow_the_input_layout():
+    """A channels-last input gives a channels-last output and grad_input with the values of
+    the channels-first call, on CPU as on the device; the fake (shape) functions agree, so
+    compiled graphs see the strides the kernels produce."""
+    xs, ws, stride, padding, dilation, groups, bias = CASES["r4_strided_dilated"]
+    x, w, b = helpers.seeded_problem(xs, ws, bias, torch.float32, seed=3)
+    y = _op_forward(x, w, b, stride, padding, dilation, groups)
+    y_cl = _op_forward(_channels_last(x), w, b, stride, padding, dilation, groups)
+    assert _is_channels_last(y_cl) and torch.equal(y_cl, y)
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(4))
+    g = _op_backward(dy, x, w, stride, padding, dilation, groups, [True, True, True])
+    g_cl = _op_backward(_channels_last(dy), _channels_last(x), w, stride, padding, dilation, groups,
+                        [True, True, True])
+    assert _is_channels_last(g_cl[0])
+    for got, want in zip(g_cl, g):
+        assert torch.equal(got, want)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    x_cl, dy_cl = _channels_last(x), _channels_last(dy)
+    mode = FakeTensorMode()
+    fx, fw, fdy = mode.from_tensor(x_cl), mode.from_tensor(w), mode.from_tensor(dy_cl)
+    with mode:
+        fy = _op_forward(fx, fw, None, stride, padding, dilation, groups)
+        fg = _op_backward(fdy, fx, fw, stride, padding, dilation, groups, [True, False, False])
+    assert fy.shape == y.shape and fy.stride() == y_cl.stride()
+    assert fg[0].stride() == g_cl[0].stride()

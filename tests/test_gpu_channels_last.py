@@ -1,0 +1,176 @@
+"""Channels-last I/O on the gfx950 path (marked ``gpu``).
+
+A channels-last activation ([N, C, *spatial] stored as [N, *spatial, C]) goes to the native
+operators without a layout copy: the implicit GEMM with direct staging reads it and writes a
+channels-last output (``convnd_hip_forward_layout``); other plans and the weight gradient run
+on channels-first copies. The reference always makes its operands contiguous first
+(src/torch_convnd/csrc/convnd.cpp:317-319, 377-381), so its results for a channels-last input
+are those of the channels-first call. Each case checks exactly that: the channels-last call
+returns the same bits as the channels-first one (same kernels and summation order; copies and
+transposes are exact), in the channels-last layout, and both match the float64 C oracle.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+import helpers
+from torch_convnd import _build, _capi, conv_nd, load_native
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def native():
+    load_native()
+
+
+def channels_last(t):
+    """Same values, memory [N, *spatial, C]."""
+    order = (0, *range(2, t.dim()), 1)
+    back = (0, t.dim() - 1, *range(1, t.dim() - 1))
+    return t.permute(order).contiguous().permute(back)
+
+
+def is_channels_last(t):
+    return not t.is_contiguous() and t.permute(0, *range(2, t.dim()), 1).is_contiguous()
+
+
+CASES = {
+    # name: x shape, w shape, stride, padding, dilation, groups, bias, dtype
+    # direct-staged implicit GEMM forward and input gradient (C2 scaled down)
+    "c2_like_bf16": ((2, 32, 6, 5, 6, 16), (64, 32, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True,
+                     torch.bfloat16),
+    "c2_like_fp16": ((1, 16, 5, 4, 6, 12), (32, 16, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True,
+                     torch.float16),
+    # strided, dilated, grouped (C5 scaled down): strided input gradient on the octet copy,
+    # stored channels-last by the GEMM epilogue
+    "c5_like_bf16": ((2, 64, 10, 8, 8, 12), (128, 16, 3, 3, 3, 5), (2, 2, 2, 1), (1, 1, 1, 4), (1, 1, 1, 2), 4,
+                     False, torch.bfloat16),
+    # rank 6 (C4 scaled down)
+    "c4_like_bf16": ((1, 8, 5, 4, 5, 4, 4, 6), (16, 8, 3, 3, 3, 3, 3, 3), (1,) * 6, (1,) * 6, (1,) * 6, 1, True,
+                     torch.bfloat16),
+    # split-precision fp32 MFMA and the tiny-channel kernels (channels-first copies)
+    "fp32_split": ((1, 16, 4, 5, 4, 8), (32, 16, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True,
+                   torch.float32),
+    "c1_like_fp32_tiny": ((2, 2, 5, 4, 6, 8), (8, 2, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True,
+                          torch.float32),
+    # 64-bit direct kernels
+    "fp64_direct": ((1, 3, 4, 3, 5, 6), (5, 3, 2, 3, 2, 3), (1, 2, 1, 1), (1, 0, 1, 1), (1, 1, 2, 1), 1, True,
+                    torch.float64),
+}
+
+
+def _run(x, w, b, stride, padding, dilation, groups, dy):
+    xs = x.detach().clone().requires_grad_()
+    ws = w.detach().clone().requires_grad_()
+    bs = b.detach().clone().requires_grad_() if b is not None else None
+    y = conv_nd(xs, ws, bs, stride, padding, dilation, groups, backend="native")
+    params = [xs, ws] + ([bs] if bs is not None else [])
+    grads = torch.autograd.grad(y, params, dy)
+    return y, grads
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_channels_last_matches_channels_first_and_oracle(name):
+    x_shape, w_shape, stride, padding, dilation, groups, bias, dtype = CASES[name]
+    print(f"[channels_last] {name} {dtype} x={x_shape} w={w_shape}", flush=True)
+    x, w, b = helpers.seeded_problem(x_shape, w_shape, bias, dtype, seed=21)
+    ref_y = helpers.oracle_forward(x, w, b, stride, padding, dilation, groups)
+    dy = torch.randn(ref_y.shape, generator=torch.Generator().manual_seed(22)).to(dtype)
+    ref_grads = helpers.oracle_backward(dy, x, w, stride, padding, dilation, groups)
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    bd = b.cuda() if b is not None else None
+    y_cf, g_cf = _run(xd, wd, bd, stride, padding, dilation, groups, dyd)
+    y_cl, g_cl = _run(channels_last(xd), wd, bd, stride, padding, dilation, groups, channels_last(dyd))
+    assert is_channels_last(y_cl), f"{name}: output is not channels-last (strides {y_cl.stride()})"
+    assert is_channels_last(g_cl[0]), f"{name}: grad_input is not channels-last"
+    assert torch.equal(y_cl, y_cf), f"{name}: channels-last forward differs from channels-first"
+    for what, got, want in zip(("grad_input", "grad_weight", "grad_bias"), g_cl, g_cf):
+        assert torch.equal(got, want), f"{name}: channels-last {what} differs from channels-first"
+    helpers.assert_close(y_cl, ref_y, dtype, f"{name} channels-last forward")
+    for what, got, want in zip(("grad_input", "grad_weight", "grad_bias"), g_cl, ref_grads):
+        helpers.assert_close(got, want, dtype, f"{name} channels-last {what}")
+
+
+def test_channels_last_mismatched_grad_output_layout():
+    """A channels-first grad_output for a channels-last input still gives the same gradients."""
+    x, w, b = helpers.seeded_problem((1, 16, 4, 5, 4, 8), (32, 16, 3, 3, 3, 3), True, torch.bfloat16, seed=23)
+    xd, wd, bd = x.cuda(), w.cuda(), b.cuda()
+    p = ((1,) * 4, (1,) * 4, (1,) * 4, 1)
+    y = conv_nd(xd, wd, bd, *p, backend="native")
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(24)).to(torch.bfloat16).cuda()
+    _, g_cf = _run(xd, wd, bd, *p, dy)
+    _, g_cl = _run(channels_last(xd), wd, bd, *p, dy)
+    for got, want in zip(g_cl, g_cf):
+        assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("config", ["C2", "C5"])
+def test_channels_last_full_size(config):
+    """BASELINE C2 and C5 at full size: channels-last forward and backward, bit for bit the
+    channels-first results (which the full-size parity tests check against the oracle)."""
+    shapes = {
+        "C2": ((2, 32, 16, 16, 16, 16), (64, 32, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True),
+        "C5": ((2, 64, 24, 24, 24, 12), (128, 16, 3, 3, 3, 5), (2, 2, 2, 1), (1, 1, 1, 4), (1, 1, 1, 2), 4, False),
+    }
+    x_shape, w_shape, stride, padding, dilation, groups, bias = shapes[config]
+    print(f"[channels_last] full size {config}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(25)
+    x = torch.randn(x_shape, generator=gen, device="cuda").to(torch.bfloat16)
+    w = (torch.rand(w_shape, generator=gen, device="cuda") * 0.1 - 0.05).to(torch.bfloat16)
+    b = torch.randn(w_shape[0], generator=gen, device="cuda").to(torch.bfloat16) if bias else None
+    dy = torch.randn(helpers_out_shape(x_shape, w_shape, stride, padding, dilation), generator=gen,
+                     device="cuda").to(torch.bfloat16)
+    y_cf, g_cf = _run(x, w, b, stride, padding, dilation, groups, dy)
+    y_cl, g_cl = _run(channels_last(x), w, b, stride, padding, dilation, groups, channels_last(dy))
+    assert is_channels_last(y_cl) and is_channels_last(g_cl[0])
+    assert torch.equal(y_cl, y_cf)
+    for got, want in zip(g_cl, g_cf):
+        assert torch.equal(got, want)
+
+
+def helpers_out_shape(x_shape, w_shape, stride, padding, dilation):
+    spatial = [(n + 2 * p - d * (k - 1) - 1) // s + 1
+               for n, k, s, p, d in zip(x_shape[2:], w_shape[2:], stride, padding, dilation)]
+    return (x_shape[0], w_shape[0], *spatial)
+
+
+def test_channels_last_c_abi():
+    """convnd_hip_forward_layout / convnd_hip_backward_layout through ctypes on [N, *spatial, C]
+    buffers, against the oracle."""
+    lib = _build.hip_library()
+    x_shape, w_shape = (1, 16, 4, 5, 6, 8), (32, 16, 3, 3, 3, 3)
+    stride, padding, dilation = (1, 1, 2, 1), (1, 1, 1, 1), (1, 1, 1, 2)
+    x, w, b = helpers.seeded_problem(x_shape, w_shape, True, torch.bfloat16, seed=26)
+    ref_y = helpers.oracle_forward(x, w, b, stride, padding, dilation, 1)
+    dy = torch.randn(ref_y.shape, generator=torch.Generator().manual_seed(27)).to(torch.bfloat16)
+    ref_dx, ref_dw, ref_db = helpers.oracle_backward(dy, x, w, stride, padding, dilation, 1)
+    prob = _capi.Problem.make(x_shape, w_shape, stride, padding, dilation, 1)
+    code, last = _capi.dtype_code(torch.bfloat16), _capi.CHANNELS_LAST
+    xd = x.permute(0, 2, 3, 4, 5, 1).contiguous().cuda()     # [N, *spatial, C]
+    dyd = dy.permute(0, 2, 3, 4, 5, 1).contiguous().cuda()
+    wd, bd = w.cuda(), b.cuda()
+    y = torch.empty(dyd.shape, dtype=torch.bfloat16, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    size = lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(prob), code, last)
+    ws = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
+    st = lib.convnd_hip_forward_layout(ctypes.byref(prob), code, last, 0, ctypes.c_void_p(xd.data_ptr()),
+                                       ctypes.c_void_p(wd.data_ptr()), ctypes.c_void_p(bd.data_ptr()),
+                                       ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(ws.data_ptr()), size, stream)
+    assert st == 0, lib.convnd_hip_last_error()
+    dx, dw, db = torch.empty_like(xd), torch.empty_like(wd), torch.empty_like(bd)
+    size = lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(prob), code, last, 1, 1, 1)
+    ws = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
+    st = lib.convnd_hip_backward_layout(ctypes.byref(prob), code, last, ctypes.c_void_p(dyd.data_ptr()),
+                                        ctypes.c_void_p(xd.data_ptr()), ctypes.c_void_p(wd.data_ptr()),
+                                        ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(dw.data_ptr()),
+                                        ctypes.c_void_p(db.data_ptr()), ctypes.c_void_p(ws.data_ptr()), size,
+                                        stream)
+    assert st == 0, lib.convnd_hip_last_error()
+    torch.cuda.synchronize()
+    helpers.assert_close(y.permute(0, 5, 1, 2, 3, 4), ref_y, torch.bfloat16, "C ABI channels-last forward")
+    helpers.assert_close(dx.permute(0, 5, 1, 2, 3, 4), ref_dx, torch.bfloat16, "C ABI channels-last dx")
+    helpers.assert_close(dw, ref_dw, torch.bfloat16, "C ABI channels-last dw")
+    helpers.assert_close(db, ref_db, torch.bfloat16, "C ABI channels-last db")

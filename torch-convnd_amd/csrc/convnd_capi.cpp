@@ -1695,7 +1695,8 @@ int prepare(const convnd_hip_problem* problem, convnd_hip_dtype dtype, Geom* g) 
 // `timed`: bracket the GEMM with the diagnostic timing events.
 int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, const void* input,
                 const void* weight, const void* bias, void* output, int activation, char* ws,
-                const void* tables, void* tables_at, bool timed, hipStream_t stream) {
+                const void* tables, void* tables_at, bool timed, hipStream_t stream,
+                bool channels_last = false) {
   int st;
   if (f.tiny.ok) {
     TinyArgs T = f.tiny.args;
@@ -1747,6 +1748,9 @@ int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, co
   A.bias = bias;
   A.out = output;
   A.act = activation;
+  // Channels-last (only with direct staging, see forward_reads_cl): stage the halo from
+  // [N][in...][C] and store [N][out...][Co].
+  A.in_cl = A.out_cl = channels_last ? 1 : 0;
   const auto ev = timed ? timing_begin(0, stream) : std::pair<hipEvent_t, hipEvent_t>{};
   st = hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
                  "implicit GEMM forward");
@@ -1754,141 +1758,68 @@ int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, co
   return st;
 }
 
-}  // namespace
-}  // namespace convnd
+// ---- channels-last I/O -----------------------------------------------------------------
+// The implicit GEMM with direct staging (16-bit data) reads [N][in...][C] and writes
+// [N][out...][Co] itself. Every other plan runs channels-first on copies in the workspace,
+// made and undone by transposes; so does the weight gradient, whose kernels read
+// channels-first input and grad_output.
+bool forward_reads_cl(const ForwardSetup& f) { return f.ig.ok && f.ig.args.direct != 0; }
 
-using namespace convnd;
-
-extern "C" {
-
-const char* convnd_hip_last_error(void) { return g_error.c_str(); }
-
-int convnd_hip_validate(const convnd_hip_problem* problem, int64_t element_sz,
-                        int64_t workspace_bytes, int64_t* output_sizes) {
-  Geom g;
-  const int st = build_geometry(problem, &g);
-  if (st != CONVND_HIP_SUCCESS) return st;
-  // tile_size (src/torch_convnd/csrc/convnd.cpp:89-100).
-  int64_t rows, per_position;
-  if (!mul_ok(g.channels, g.k_vol, &rows))
-    return fail(CONVND_HIP_INVALID_ARGUMENT, "patch rows overflows int64");
-  if (!mul_ok(std::max<int64_t>(element_sz, 4), rows, &per_position))
-    return fail(CONVND_HIP_INVALID_ARGUMENT, "workspace bytes per position overflows int64");
-  if (workspace_bytes < per_position)
-    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
-                "workspace_bytes is too small for one output position; requires at least " +
-                    std::to_string(per_position));
-  if (output_sizes != nullptr)
-    for (int a = 0; a < g.rank; ++a) output_sizes[a] = g.out[a];
-  g_error.clear();
-  return CONVND_HIP_SUCCESS;
+size_t tensor_bytes(int64_t batch, int64_t channels, int64_t volume, convnd_hip_dtype dt) {
+  return align_up(static_cast<size_t>(batch * channels * volume * element_size(dt)));
 }
 
-size_t convnd_hip_forward_workspace_size(const convnd_hip_problem* problem,
-                                         convnd_hip_dtype dtype) {
-  Geom g;
-  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
-  return setup_forward(g, dtype).bytes;
+size_t cl_forward_extra(const Geom& g, convnd_hip_dtype dt, const ForwardSetup& f) {
+  if (forward_reads_cl(f)) return 0;
+  return tensor_bytes(g.batch, g.channels, g.in_vol, dt) +
+         tensor_bytes(g.batch, g.out_channels, g.out_vol, dt);
 }
 
-size_t convnd_hip_backward_workspace_size(const convnd_hip_problem* problem,
-                                          convnd_hip_dtype dtype, int need_grad_input,
-                                          int need_grad_weight, int need_grad_bias) {
-  Geom g;
-  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
-  return setup_backward(g, dtype, need_grad_input != 0, need_grad_weight != 0,
-                        need_grad_bias != 0)
-      .bytes;
-}
+// Which channels-first copies a channels-last backward needs.
+struct ClBackward {
+  bool dgrad_cl = false;  // the input-gradient GEMM stages grad_output channels-last itself
+  bool dx_epilogue = false;  // the input-gradient GEMM stores grad_input channels-last
+  bool dy_cf = false, x_cf = false, dx_cf = false;
+  size_t off_dy = 0, off_x = 0, off_dx = 0, bytes = 0;
+};
 
-const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
-                                 int which) {
-  Geom g;
-  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return "invalid";
-  if (which < 0 || which > 2) return "invalid";
-  if (tiny_preferred(g, dtype)) {
-    const TinyPlan t = plan_tiny(g, dtype, which == 1 ? 1 : 0);
-    if (t.ok && (which != 2 || t.wlds > 0)) return "tiny";
+ClBackward cl_backward_plan(const Geom& g, convnd_hip_dtype dt, const BackwardSetup& b, bool gi,
+                            bool gw, bool gb) {
+  ClBackward c;
+  const bool mfma_dx = gi && g.batch > 0 && b.dg.ok;
+  c.dgrad_cl = mfma_dx && b.dg.args.direct != 0;
+  c.dx_epilogue = mfma_dx;
+  c.dy_cf = gw || gb || (gi && !c.dgrad_cl);
+  c.x_cf = gw;
+  c.dx_cf = gi && !mfma_dx;
+  size_t at = align_up(b.bytes);
+  if (c.dy_cf) {
+    c.off_dy = at;
+    at += tensor_bytes(g.batch, g.out_channels, g.out_vol, dt);
   }
-  if (which == 0) return plan_igemm(g, dtype, 0).ok ? "mfma" : "direct";
-  if (which == 1) return plan_igemm(g, dtype, 1).ok ? "mfma" : "direct";
-  return plan_wgrad(g, dtype).ok ? "mfma" : "direct";
-}
-
-int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
-                       const void* input, const void* weight, const void* bias, void* output,
-                       void* workspace, size_t workspace_size, void* stream_ptr) {
-  return convnd_hip_forward_act(problem, dtype, input, weight, bias, output, CONVND_HIP_ACT_NONE,
-                                workspace, workspace_size, stream_ptr);
-}
-
-int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
-                           const void* input, const void* weight, const void* bias,
-                           void* output, int activation, void* workspace,
-                           size_t workspace_size, void* stream_ptr) {
-  if (activation < CONVND_HIP_ACT_NONE || activation > CONVND_HIP_ACT_GELU_TANH)
-    return fail(CONVND_HIP_INVALID_ARGUMENT, "activation must be none, relu, gelu or gelu_tanh");
-  Geom g;
-  const int st = prepare(problem, dtype, &g);
-  if (st != CONVND_HIP_SUCCESS) return st;
-  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  if (g.batch == 0) return CONVND_HIP_SUCCESS;
-  const ForwardSetup f = setup_forward(g, dtype);
-  if (workspace_size < f.bytes || (f.bytes > 0 && workspace == nullptr))
-    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
-                "device workspace is smaller than convnd_hip_forward_workspace_size");
-  TablesRef tables;  // held until the kernels that read them are enqueued
-  if (f.ig.ok) {
-    tables = igemm_device_tables(plan_key(g, dtype, 0), f.ig.args, stream);
-    if (tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+  if (c.x_cf) {
+    c.off_x = at;
+    at += tensor_bytes(g.batch, g.channels, g.in_vol, dt);
   }
-  return run_forward(g, dtype, f, input, weight, bias, output, activation,
-                     static_cast<char*>(workspace), tables ? tables->dev : nullptr, nullptr, true,
-                     stream);
+  if (c.dx_cf) {
+    c.off_dx = at;
+    at += tensor_bytes(g.batch, g.channels, g.in_vol, dt);
+  }
+  c.bytes = at;
+  return c;
 }
 
-int convnd_hip_forward_noalloc(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
-                               const void* input, const void* weight, const void* bias,
-                               void* output, void* stream_ptr) {
-  Geom g;
-  const int st = prepare(problem, dtype, &g);
-  if (st != CONVND_HIP_SUCCESS) return st;
-  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  if (g.batch == 0) return CONVND_HIP_SUCCESS;
-  const ForwardSetup f = setup_forward(g, dtype);
-  if (!f.ig.ok)  // the direct kernels use no scratch
-    return run_forward(g, dtype, f, input, weight, bias, output, CONVND_HIP_ACT_NONE, nullptr,
-                       nullptr, nullptr, false, stream);
-  // Scratch: [geometry tables | the workspace regions of convnd_hip_forward].
-  const size_t tab = align_up(static_cast<size_t>(f.ig.args.tab_bytes));
-  if (tab + f.bytes > kNoAllocScratchBytes)
-    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
-                "convnd_hip_forward_noalloc: this problem needs " + std::to_string(tab + f.bytes) +
-                    " bytes of device scratch, more than its fixed " +
-                    std::to_string(kNoAllocScratchBytes) + " bytes; use convnd_hip_forward");
-  void* scratch = nullptr;
-  const int sst = hip_check(noalloc_scratch(&scratch), "device scratch address");
-  if (sst != CONVND_HIP_SUCCESS) return sst;
-  char* base = static_cast<char*>(scratch);
-  return run_forward(g, dtype, f, input, weight, bias, output, CONVND_HIP_ACT_NONE, base + tab,
-                     nullptr, base, false, stream);
-}
-
-int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
-                        const void* grad_output, const void* input, const void* weight,
-                        void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
-                        size_t workspace_size, void* stream_ptr) {
-  Geom g;
-  int st = prepare(problem, dtype, &g);
-  if (st != CONVND_HIP_SUCCESS) return st;
-  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+// The backward launch sequence over a prepared geometry and plan. Channels-last calls pass
+// channels-first copies of grad_output and input (when a consumer needs them) plus
+// dy_cl: grad_output channels-last for an input-gradient GEMM that stages it directly, and
+// dx_cl: the input-gradient GEMM stores grad_input channels-last.
+int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
+                 const void* grad_output, const void* input, const void* weight, void* grad_input,
+                 void* grad_weight, void* grad_bias, char* ws, hipStream_t stream,
+                 const void* dy_cl = nullptr, bool dx_cl = false) {
+  int st = CONVND_HIP_SUCCESS;
   const bool gi = grad_input != nullptr, gw = grad_weight != nullptr,
              gb = grad_bias != nullptr;
-  const BackwardSetup b = setup_backward(g, dtype, gi, gw, gb);
-  if (workspace_size < b.bytes || (b.bytes > 0 && workspace == nullptr))
-    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
-                "device workspace is smaller than convnd_hip_backward_workspace_size");
-  char* ws = static_cast<char*>(workspace);
   const int64_t es = element_size(dtype);
   if (g.batch == 0) {
     // Gradients of an empty batch: dX is empty, dW and db are zero.
@@ -1934,7 +1865,10 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     dx_tables = igemm_device_tables(plan_key(g, dtype, 64), DA, stream);
     if (dx_tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
     DA.tables = dx_tables->dev;
-    DA.in = DA.direct ? grad_output : static_cast<const void*>(ws + b.off_dy_stage);
+    DA.in = DA.direct ? (dy_cl != nullptr ? dy_cl : grad_output)
+                      : static_cast<const void*>(ws + b.off_dy_stage);
+    DA.in_cl = DA.direct && dy_cl != nullptr ? 1 : 0;
+    DA.out_cl = dx_cl ? 1 : 0;
     DA.wpk = ws + b.off_wpk;
     DA.bias = nullptr;
     DA.out = grad_input;
@@ -2086,6 +2020,259 @@ int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtyp
     if (st != CONVND_HIP_SUCCESS) return st;
   }
   return CONVND_HIP_SUCCESS;
+}
+
+}  // namespace
+}  // namespace convnd
+
+using namespace convnd;
+
+extern "C" {
+
+const char* convnd_hip_last_error(void) { return g_error.c_str(); }
+
+int convnd_hip_validate(const convnd_hip_problem* problem, int64_t element_sz,
+                        int64_t workspace_bytes, int64_t* output_sizes) {
+  Geom g;
+  const int st = build_geometry(problem, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  // tile_size (src/torch_convnd/csrc/convnd.cpp:89-100).
+  int64_t rows, per_position;
+  if (!mul_ok(g.channels, g.k_vol, &rows))
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "patch rows overflows int64");
+  if (!mul_ok(std::max<int64_t>(element_sz, 4), rows, &per_position))
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "workspace bytes per position overflows int64");
+  if (workspace_bytes < per_position)
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "workspace_bytes is too small for one output position; requires at least " +
+                    std::to_string(per_position));
+  if (output_sizes != nullptr)
+    for (int a = 0; a < g.rank; ++a) output_sizes[a] = g.out[a];
+  g_error.clear();
+  return CONVND_HIP_SUCCESS;
+}
+
+size_t convnd_hip_forward_workspace_size(const convnd_hip_problem* problem,
+                                         convnd_hip_dtype dtype) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
+  return setup_forward(g, dtype).bytes;
+}
+
+size_t convnd_hip_backward_workspace_size(const convnd_hip_problem* problem,
+                                          convnd_hip_dtype dtype, int need_grad_input,
+                                          int need_grad_weight, int need_grad_bias) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
+  return setup_backward(g, dtype, need_grad_input != 0, need_grad_weight != 0,
+                        need_grad_bias != 0)
+      .bytes;
+}
+
+const char* convnd_hip_plan_name(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                                 int which) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return "invalid";
+  if (which < 0 || which > 2) return "invalid";
+  if (tiny_preferred(g, dtype)) {
+    const TinyPlan t = plan_tiny(g, dtype, which == 1 ? 1 : 0);
+    if (t.ok && (which != 2 || t.wlds > 0)) return "tiny";
+  }
+  if (which == 0) return plan_igemm(g, dtype, 0).ok ? "mfma" : "direct";
+  if (which == 1) return plan_igemm(g, dtype, 1).ok ? "mfma" : "direct";
+  return plan_wgrad(g, dtype).ok ? "mfma" : "direct";
+}
+
+int convnd_hip_forward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                       const void* input, const void* weight, const void* bias, void* output,
+                       void* workspace, size_t workspace_size, void* stream_ptr) {
+  return convnd_hip_forward_act(problem, dtype, input, weight, bias, output, CONVND_HIP_ACT_NONE,
+                                workspace, workspace_size, stream_ptr);
+}
+
+int convnd_hip_forward_act(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                           const void* input, const void* weight, const void* bias,
+                           void* output, int activation, void* workspace,
+                           size_t workspace_size, void* stream_ptr) {
+  if (activation < CONVND_HIP_ACT_NONE || activation > CONVND_HIP_ACT_GELU_TANH)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "activation must be none, relu, gelu or gelu_tanh");
+  Geom g;
+  const int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (g.batch == 0) return CONVND_HIP_SUCCESS;
+  const ForwardSetup f = setup_forward(g, dtype);
+  if (workspace_size < f.bytes || (f.bytes > 0 && workspace == nullptr))
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "device workspace is smaller than convnd_hip_forward_workspace_size");
+  TablesRef tables;  // held until the kernels that read them are enqueued
+  if (f.ig.ok) {
+    tables = igemm_device_tables(plan_key(g, dtype, 0), f.ig.args, stream);
+    if (tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+  }
+  return run_forward(g, dtype, f, input, weight, bias, output, activation,
+                     static_cast<char*>(workspace), tables ? tables->dev : nullptr, nullptr, true,
+                     stream);
+}
+
+int convnd_hip_forward_noalloc(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                               const void* input, const void* weight, const void* bias,
+                               void* output, void* stream_ptr) {
+  Geom g;
+  const int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (g.batch == 0) return CONVND_HIP_SUCCESS;
+  const ForwardSetup f = setup_forward(g, dtype);
+  if (!f.ig.ok)  // the direct kernels use no scratch
+    return run_forward(g, dtype, f, input, weight, bias, output, CONVND_HIP_ACT_NONE, nullptr,
+                       nullptr, nullptr, false, stream);
+  // Scratch: [geometry tables | the workspace regions of convnd_hip_forward].
+  const size_t tab = align_up(static_cast<size_t>(f.ig.args.tab_bytes));
+  if (tab + f.bytes > kNoAllocScratchBytes)
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "convnd_hip_forward_noalloc: this problem needs " + std::to_string(tab + f.bytes) +
+                    " bytes of device scratch, more than its fixed " +
+                    std::to_string(kNoAllocScratchBytes) + " bytes; use convnd_hip_forward");
+  void* scratch = nullptr;
+  const int sst = hip_check(noalloc_scratch(&scratch), "device scratch address");
+  if (sst != CONVND_HIP_SUCCESS) return sst;
+  char* base = static_cast<char*>(scratch);
+  return run_forward(g, dtype, f, input, weight, bias, output, CONVND_HIP_ACT_NONE, base + tab,
+                     nullptr, base, false, stream);
+}
+
+int convnd_hip_backward(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                        const void* grad_output, const void* input, const void* weight,
+                        void* grad_input, void* grad_weight, void* grad_bias, void* workspace,
+                        size_t workspace_size, void* stream_ptr) {
+  Geom g;
+  const int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  const BackwardSetup b = setup_backward(g, dtype, grad_input != nullptr,
+                                         grad_weight != nullptr, grad_bias != nullptr);
+  if (workspace_size < b.bytes || (b.bytes > 0 && workspace == nullptr))
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "device workspace is smaller than convnd_hip_backward_workspace_size");
+  return run_backward(g, dtype, b, grad_output, input, weight, grad_input, grad_weight, grad_bias,
+                      static_cast<char*>(workspace), static_cast<hipStream_t>(stream_ptr));
+}
+
+size_t convnd_hip_forward_workspace_size_layout(const convnd_hip_problem* problem,
+                                                convnd_hip_dtype dtype, int layout) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
+  const ForwardSetup f = setup_forward(g, dtype);
+  if (layout != CONVND_HIP_CHANNELS_LAST) return f.bytes;
+  return align_up(f.bytes) + cl_forward_extra(g, dtype, f);
+}
+
+size_t convnd_hip_backward_workspace_size_layout(const convnd_hip_problem* problem,
+                                                 convnd_hip_dtype dtype, int layout,
+                                                 int need_grad_input, int need_grad_weight,
+                                                 int need_grad_bias) {
+  Geom g;
+  if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
+  const bool gi = need_grad_input != 0, gw = need_grad_weight != 0, gb = need_grad_bias != 0;
+  const BackwardSetup b = setup_backward(g, dtype, gi, gw, gb);
+  if (layout != CONVND_HIP_CHANNELS_LAST) return b.bytes;
+  return cl_backward_plan(g, dtype, b, gi, gw, gb).bytes;
+}
+
+int convnd_hip_forward_layout(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                              int layout, int activation, const void* input, const void* weight,
+                              const void* bias, void* output, void* workspace,
+                              size_t workspace_size, void* stream_ptr) {
+  if (layout != CONVND_HIP_CHANNELS_FIRST && layout != CONVND_HIP_CHANNELS_LAST)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "layout must be channels_first or channels_last");
+  if (layout == CONVND_HIP_CHANNELS_FIRST)
+    return convnd_hip_forward_act(problem, dtype, input, weight, bias, output, activation,
+                                  workspace, workspace_size, stream_ptr);
+  if (activation < CONVND_HIP_ACT_NONE || activation > CONVND_HIP_ACT_GELU_TANH)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "activation must be none, relu, gelu or gelu_tanh");
+  Geom g;
+  int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (g.batch == 0) return CONVND_HIP_SUCCESS;
+  const ForwardSetup f = setup_forward(g, dtype);
+  const size_t need = align_up(f.bytes) + cl_forward_extra(g, dtype, f);
+  if (workspace_size < need || (need > 0 && workspace == nullptr))
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "device workspace is smaller than convnd_hip_forward_workspace_size_layout");
+  TablesRef tables;  // held until the kernels that read them are enqueued
+  if (f.ig.ok) {
+    tables = igemm_device_tables(plan_key(g, dtype, 0), f.ig.args, stream);
+    if (tables == nullptr) return CONVND_HIP_LAUNCH_FAILED;
+  }
+  char* ws = static_cast<char*>(workspace);
+  const void* tab = tables ? tables->dev : nullptr;
+  if (forward_reads_cl(f))
+    return run_forward(g, dtype, f, input, weight, bias, output, activation, ws, tab, nullptr,
+                       true, stream, true);
+  // Channels-first copies: x [N][in][C] -> [N][C][in], then y [N][Co][out] -> [N][out][Co].
+  const int64_t es = element_size(dtype);
+  char* x_cf = ws + align_up(f.bytes);
+  char* y_cf = x_cf + tensor_bytes(g.batch, g.channels, g.in_vol, dtype);
+  st = hip_check(launch_transpose(es, g.batch, g.in_vol, g.channels, input, x_cf, stream),
+                 "channels-last input copy");
+  if (st != CONVND_HIP_SUCCESS) return st;
+  st = run_forward(g, dtype, f, x_cf, weight, bias, y_cf, activation, ws, tab, nullptr, true,
+                   stream);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  return hip_check(launch_transpose(es, g.batch, g.out_channels, g.out_vol, y_cf, output, stream),
+                   "channels-last output copy");
+}
+
+int convnd_hip_backward_layout(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
+                               int layout, const void* grad_output, const void* input,
+                               const void* weight, void* grad_input, void* grad_weight,
+                               void* grad_bias, void* workspace, size_t workspace_size,
+                               void* stream_ptr) {
+  if (layout != CONVND_HIP_CHANNELS_FIRST && layout != CONVND_HIP_CHANNELS_LAST)
+    return fail(CONVND_HIP_INVALID_ARGUMENT, "layout must be channels_first or channels_last");
+  if (layout == CONVND_HIP_CHANNELS_FIRST)
+    return convnd_hip_backward(problem, dtype, grad_output, input, weight, grad_input,
+                               grad_weight, grad_bias, workspace, workspace_size, stream_ptr);
+  Geom g;
+  int st = prepare(problem, dtype, &g);
+  if (st != CONVND_HIP_SUCCESS) return st;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const bool gi = grad_input != nullptr, gw = grad_weight != nullptr,
+             gb = grad_bias != nullptr;
+  const BackwardSetup b = setup_backward(g, dtype, gi, gw, gb);
+  const ClBackward c = cl_backward_plan(g, dtype, b, gi, gw, gb);
+  if (workspace_size < c.bytes || (c.bytes > 0 && workspace == nullptr))
+    return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
+                "device workspace is smaller than convnd_hip_backward_workspace_size_layout");
+  char* ws = static_cast<char*>(workspace);
+  if (g.batch == 0)
+    return run_backward(g, dtype, b, grad_output, input, weight, grad_input, grad_weight,
+                        grad_bias, ws, stream);
+  const int64_t es = element_size(dtype);
+  const void* dy = grad_output;
+  const void* x = input;
+  if (c.dy_cf) {
+    st = hip_check(launch_transpose(es, g.batch, g.out_vol, g.out_channels, grad_output,
+                                    ws + c.off_dy, stream),
+                   "channels-last grad_output copy");
+    if (st != CONVND_HIP_SUCCESS) return st;
+    dy = ws + c.off_dy;
+  }
+  if (c.x_cf) {
+    st = hip_check(launch_transpose(es, g.batch, g.in_vol, g.channels, input, ws + c.off_x,
+                                    stream),
+                   "channels-last input copy");
+    if (st != CONVND_HIP_SUCCESS) return st;
+    x = ws + c.off_x;
+  }
+  void* dx = c.dx_cf ? static_cast<void*>(ws + c.off_dx) : grad_input;
+  st = run_backward(g, dtype, b, dy, x, weight, dx, grad_weight, grad_bias, ws, stream,
+                    c.dgrad_cl ? grad_output : nullptr, c.dx_epilogue);
+  if (st != CONVND_HIP_SUCCESS || !c.dx_cf) return st;
+  return hip_check(launch_transpose(es, g.batch, g.channels, g.in_vol, ws + c.off_dx, grad_input,
+                                    stream),
+                   "channels-last grad_input copy");
 }
 
 }  // extern "C"

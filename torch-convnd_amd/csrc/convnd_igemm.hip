@@ -274,6 +274,11 @@ void igemm_kernel(IgemmArgs A) {
     const unsigned img_chan = static_cast<unsigned>(n * A.cin_total + g * A.cin_g);
     const unsigned in_vol = static_cast<unsigned>(A.in_vol);
     const unsigned in_bytes = static_cast<unsigned>(A.in_bytes);
+    // Channels-last: element (n, position, channel) at (n*in_vol + position)*cin_total + channel;
+    // load i of a task is position i of the run (its 8 channels), not channel i.
+    const bool in_cl = A.in_cl != 0;
+    const unsigned cl_img = static_cast<unsigned>(n) * in_vol;
+    const unsigned cl_stride = static_cast<unsigned>(A.cin_total);
     auto task_load = [&](int ck, int t, u32x4* v) {
       const int o = t & onoct;
       const int rt = t >> A.log2_noct;
@@ -282,9 +287,13 @@ void igemm_kernel(IgemmArgs A) {
       const int ro = (t < ntask && jj < nrun_box) ? rowin[r] : -1;
       const unsigned chan = img_chan + static_cast<unsigned>(ck * A.cc + o * 8);
       const unsigned pos = static_cast<unsigned>(ro + (jlo + jj) * 8);
+      const unsigned cl_chan = static_cast<unsigned>(g * A.cin_g + ck * A.cc + o * 8);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const unsigned off = ro >= 0 ? ((chan + i) * in_vol + pos) * 2u : kPast;
+        const unsigned off =
+            ro < 0 ? kPast
+                   : (in_cl ? ((cl_img + pos + i) * cl_stride + cl_chan) * 2u
+                            : ((chan + i) * in_vol + pos) * 2u);
         v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
         // The buffer's range check is per dword: a dword straddling the tensor's end reads
         // zero, valid half included. A run that crosses the end loads element by element.
@@ -306,6 +315,14 @@ void igemm_kernel(IgemmArgs A) {
       if (t >= ntask || jj >= nrun_box) return;
       const int c0 = (jlo + jj) * 8;
       unsigned char* rowp = buf + o * A.plane_bytes + (rowlds[r] - corg) * 16;
+      if (in_cl) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int c = c0 + e;
+          if (c >= corg && c <= clast) *reinterpret_cast<u32x4*>(rowp + c * 16) = v[e];
+        }
+        return;
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int c = c0 + e;
@@ -476,7 +493,48 @@ void igemm_kernel(IgemmArgs A) {
   const int act = A.act;
   const size_t chan0 = (size_t)n * A.cout_total + (size_t)g * A.cout_g;
   O* obox = out + box.out_origin;
-  if (A.packed_ok && (flags & 2)) {
+  if (A.out_cl) {
+    // Channels-last output: output channel m of position q at
+    // ((n*out_vol + q)*cout_total + g*cout_g + m); sixteen lanes write one position's 16
+    // consecutive channels.
+    const size_t ostride = static_cast<size_t>(A.cout_total);
+    O* ocl = out + ((size_t)n * A.out_vol + box.out_origin) * ostride + (size_t)g * A.cout_g;
+    const bool inside = A.packed_ok && (flags & 2);
+    int off[NB][4];
+    {
+      const unsigned long long lim = box.lim;
+      const unsigned long long guard = A.coord_bits == 16 ? kGuard16 : kGuard8;
+      const unsigned long long ones = A.coord_bits == 16 ? kOnes16 : kOnes8;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int q = (wn * NB + nb) * 16 + 4 * lg + i;
+          if (inside) {
+            off[nb][i] = posout[q];
+          } else {
+            const int4 e = pt[q];
+            const unsigned long long c = static_cast<unsigned>(e.z) |
+                                         (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
+            off[nb][i] = swar_all_less(c, lim, guard, ones) ? e.y : -1;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = (mt0 + mb) * 16 + (lane & 15);
+      if (m >= A.cout_g) continue;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (off[nb][i] >= 0)
+            ocl[(size_t)off[nb][i] * ostride + m] =
+                static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], act));
+      }
+    }
+  } else if (A.packed_ok && (flags & 2)) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const int m = (mt0 + mb) * 16 + (lane & 15);

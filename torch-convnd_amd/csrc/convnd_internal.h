@@ -149,6 +149,10 @@ struct IgemmArgs {
   int nrun;
   int nbuf;
   int waves;  // waves per workgroup (4, or 8 with direct staging)
+  // Channels-last I/O: in_cl, the directly staged operand is [N][in_vol][cin_total] (a halo
+  // run of 8 last-axis positions is eight 16-byte loads of one octet's channels, stored
+  // without a transpose); out_cl, the output is [N][out_vol][cout_total]. 0: channels-first.
+  int in_cl, out_cl;
   // Divisions of the weight-packing unit index by mtiles_padded, kc_max, nchunk and groups.
   FastDiv div_mt, div_kc, div_nchunk, div_groups;
 };
@@ -485,6 +489,10 @@ hipError_t launch_wgrad_reduce(convnd_hip_dtype dtype, int mb, const WgradArgs& 
                                hipStream_t stream, const float* bias_sums = nullptr,
                                int64_t nsum = 0, int64_t channels = 0, void* db = nullptr);
 hipError_t launch_fill_zero(void* dst, int64_t bytes, hipStream_t stream);
+// dst[n][b][a] = src[n][a][b] (batch matrices of a x b elements of element_size 2, 4 or 8
+// bytes): channels-last <-> channels-first copies.
+hipError_t launch_transpose(int64_t element_size, int64_t batch, int64_t a, int64_t b,
+                            const void* src, void* dst, hipStream_t stream);
 // Allocation-free forward: bytes of the per-device static scratch array, its device address
 // on the current device (looked up once per device), and the kernel that writes the implicit
 // GEMM's geometry tables (igemm_table_layout(a) bytes) into device memory.

@@ -11,6 +11,8 @@
 //     transposed copy of grad_output is made).
 //   * reduce_channel_sums: db[c] = sum over the partials of channel c in a fixed order.
 //   * reduce_partials: out[e] = sum_i part[i][e] in a fixed order, four elements per thread.
+//   * transpose: channels-first <-> channels-last copies for channels-last calls whose plan
+//     cannot read or write that layout itself.
 // Every reduction has a fixed summation order, so results are bitwise repeatable.
 
 #include "convnd_internal.h"
@@ -261,7 +263,66 @@ __global__ __launch_bounds__(kThreads) void reduce_partials4_kernel(const float*
     if (e0 + k < count) out[e0 + k] = static_cast<T>(acc[k]);
 }
 
+// ---- channels-first <-> channels-last -----------------------------------------------------
+
+// dst[n][b][a] = src[n][a][b] for each of `batch` matrices of rows x cols = a x b, through a
+// 64 x 64 LDS tile (one element column of padding keeps the transposed reads off one bank).
+// Channels-last to channels-first: a = positions, b = channels; the reverse swaps them.
+// Element type E: 2, 4 or 8 bytes, moved as raw bits.
+template <typename E>
+__global__ __launch_bounds__(kThreads) void transpose_kernel(const E* __restrict__ src,
+                                                             E* __restrict__ dst, int64_t a,
+                                                             int64_t b) {
+  __shared__ E tile[64][65];
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const size_t mat = static_cast<size_t>(a) * static_cast<size_t>(b);
+  const E* s = src + blockIdx.z * mat;
+  E* d = dst + blockIdx.z * mat;
+  const int tx = threadIdx.x & 63;
+  const int ty = threadIdx.x >> 6;  // 0..3
+#pragma unroll
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t ra = a0 + r, cb = b0 + tx;
+    if (ra < a && cb < b) tile[r][tx] = s[ra * b + cb];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t rb = b0 + r, ca = a0 + tx;
+    if (rb < b && ca < a) d[rb * a + ca] = tile[tx][r];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_transpose(int64_t element_size, int64_t batch, int64_t a, int64_t b,
+                            const void* src, void* dst, hipStream_t stream) {
+  if (batch == 0 || a == 0 || b == 0) return hipSuccess;
+  if ((a + 63) / 64 > 0x7fffffff || (b + 63) / 64 > 65535 || batch > 65535)
+    return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((a + 63) / 64), static_cast<unsigned>((b + 63) / 64),
+                  static_cast<unsigned>(batch));
+  switch (element_size) {
+    case 2:
+      hipLaunchKernelGGL((transpose_kernel<unsigned short>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst),
+                         a, b);
+      break;
+    case 4:
+      hipLaunchKernelGGL((transpose_kernel<unsigned>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const unsigned*>(src), static_cast<unsigned*>(dst), a, b);
+      break;
+    case 8:
+      hipLaunchKernelGGL((transpose_kernel<unsigned long long>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const unsigned long long*>(src),
+                         static_cast<unsigned long long*>(dst), a, b);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipStream_t stream) {
   DevPrologue P;

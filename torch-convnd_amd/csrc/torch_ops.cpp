@@ -104,8 +104,69 @@ void check_workspace(const convnd_hip_problem& problem, int64_t element_size,
   raise_status(convnd_hip_validate(&problem, element_size, workspace_bytes, nullptr));
 }
 
+// Channels-last activation tensors: [N, C, spatial...] whose memory is [N, spatial..., C]
+// (channel stride 1, dense in that order). A tensor that is also contiguous (C == 1, or all
+// spatial sizes 1) counts as channels-first.
+std::vector<int64_t> channels_last_order(int64_t dim) {
+  std::vector<int64_t> order = {0};
+  for (int64_t a = 2; a < dim; ++a) order.push_back(a);
+  order.push_back(1);
+  return order;
+}
+
+bool is_channels_last(const at::Tensor& t) {
+  if (t.dim() < 3 || t.is_contiguous()) return false;
+  return t.permute(channels_last_order(t.dim())).is_contiguous();
+}
+
+// An uninitialised tensor of logical shape [N, C, spatial...] laid out channels-last.
+at::Tensor empty_channels_last(at::IntArrayRef shape, const at::TensorOptions& options) {
+  const int64_t dim = static_cast<int64_t>(shape.size());
+  std::vector<int64_t> stored = {shape[0]};
+  for (int64_t a = 2; a < dim; ++a) stored.push_back(shape[a]);
+  stored.push_back(shape[1]);
+  std::vector<int64_t> back = {0, dim - 1};
+  for (int64_t a = 1; a < dim - 1; ++a) back.push_back(a);
+  return at::empty(stored, options).permute(back);
+}
+
+at::Tensor to_channels_last(const at::Tensor& t) {
+  if (is_channels_last(t)) return t;
+  auto out = empty_channels_last(t.sizes(), t.options());
+  out.copy_(t);
+  return out;
+}
+
 void* current_stream(const at::Tensor& tensor) {
   return static_cast<void*>(c10::hip::getCurrentHIPStream(tensor.device().index()).stream());
+}
+
+// The forward on the device in the input's layout: a channels-last input gives a
+// channels-last output with no layout copy on the implicit-GEMM path
+// (convnd_hip_forward_layout); otherwise operands are made contiguous as in the reference
+// (src/torch_convnd/csrc/convnd.cpp:317-319).
+at::Tensor forward_device(const convnd_hip_problem& problem, const at::Tensor& input,
+                          const at::Tensor& weight, const std::optional<at::Tensor>& bias,
+                          const std::vector<int64_t>& shape, int act) {
+  const c10::OptionalDeviceGuard guard(input.device());
+  const bool cl = is_channels_last(input);
+  auto output = cl ? empty_channels_last(shape, input.options()) : at::empty(shape, input.options());
+  if (problem.batch == 0) return output;
+  const auto x = cl ? input : input.contiguous();
+  const auto w = weight.contiguous();
+  std::optional<at::Tensor> b;
+  if (bias.has_value()) b = bias->contiguous();
+  const auto dtype = to_dtype(input.scalar_type());
+  const int layout = cl ? CONVND_HIP_CHANNELS_LAST : CONVND_HIP_CHANNELS_FIRST;
+  const size_t ws_bytes = convnd_hip_forward_workspace_size_layout(&problem, dtype, layout);
+  auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
+  raise_status(convnd_hip_forward_layout(&problem, dtype, layout, act, x.const_data_ptr(),
+                                         w.const_data_ptr(),
+                                         b.has_value() ? b->const_data_ptr() : nullptr,
+                                         output.mutable_data_ptr(),
+                                         ws_bytes ? workspace.mutable_data_ptr() : nullptr,
+                                         ws_bytes, current_stream(input)));
+  return output;
 }
 
 at::Tensor conv_nd_device(const at::Tensor& input, const at::Tensor& weight,
@@ -122,22 +183,7 @@ at::Tensor conv_nd_device(const at::Tensor& input, const at::Tensor& weight,
   }
   const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
-  const c10::OptionalDeviceGuard guard(input.device());
-  auto output = at::empty(shape, input.options());
-  if (problem.batch == 0) return output;
-  const auto x = input.contiguous();
-  const auto w = weight.contiguous();
-  std::optional<at::Tensor> b;
-  if (bias.has_value()) b = bias->contiguous();
-  const auto dtype = to_dtype(input.scalar_type());
-  const size_t ws_bytes = convnd_hip_forward_workspace_size(&problem, dtype);
-  auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
-  raise_status(convnd_hip_forward(&problem, dtype, x.const_data_ptr(), w.const_data_ptr(),
-                                  b.has_value() ? b->const_data_ptr() : nullptr,
-                                  output.mutable_data_ptr(),
-                                  ws_bytes ? workspace.mutable_data_ptr() : nullptr, ws_bytes,
-                                  current_stream(input)));
-  return output;
+  return forward_device(problem, input, weight, bias, shape, CONVND_HIP_ACT_NONE);
 }
 
 Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& input,
@@ -155,26 +201,34 @@ Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& i
   // with four-byte elements (src/torch_convnd/csrc/convnd.cpp:361).
   check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
   const c10::OptionalDeviceGuard guard(input.device());
+  // A channels-last input gets a channels-last grad_input, computed from a channels-last
+  // grad_output (converted when it comes in another layout).
+  const bool cl = is_channels_last(input);
   std::optional<at::Tensor> grad_input, grad_weight, grad_bias;
   if (problem.batch == 0) {
-    if (output_mask[0]) grad_input = at::zeros(input.sizes(), input.options());
+    if (output_mask[0])
+      grad_input = cl ? empty_channels_last(input.sizes(), input.options()).zero_()
+                      : at::zeros(input.sizes(), input.options());
     if (output_mask[1]) grad_weight = at::zeros(weight.sizes(), weight.options());
     if (output_mask[2]) grad_bias = at::zeros({problem.output_channels}, input.options());
     return {grad_input, grad_weight, grad_bias};
   }
-  if (output_mask[0]) grad_input = at::empty(input.sizes(), input.options());
+  if (output_mask[0])
+    grad_input = cl ? empty_channels_last(input.sizes(), input.options())
+                    : at::empty(input.sizes(), input.options());
   if (output_mask[1]) grad_weight = at::empty(weight.sizes(), weight.options());
   if (output_mask[2]) grad_bias = at::empty({problem.output_channels}, input.options());
   if (!output_mask[0] && !output_mask[1] && !output_mask[2]) return {};
-  const auto dy = grad_output.contiguous();
-  const auto x = input.contiguous();
+  const auto dy = cl ? to_channels_last(grad_output) : grad_output.contiguous();
+  const auto x = cl ? input : input.contiguous();
   const auto w = weight.contiguous();
   const auto dtype = to_dtype(input.scalar_type());
-  const size_t ws_bytes = convnd_hip_backward_workspace_size(
-      &problem, dtype, output_mask[0], output_mask[1], output_mask[2]);
+  const int layout = cl ? CONVND_HIP_CHANNELS_LAST : CONVND_HIP_CHANNELS_FIRST;
+  const size_t ws_bytes = convnd_hip_backward_workspace_size_layout(
+      &problem, dtype, layout, output_mask[0], output_mask[1], output_mask[2]);
   auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
-  raise_status(convnd_hip_backward(
-      &problem, dtype, dy.const_data_ptr(), x.const_data_ptr(), w.const_data_ptr(),
+  raise_status(convnd_hip_backward_layout(
+      &problem, dtype, layout, dy.const_data_ptr(), x.const_data_ptr(), w.const_data_ptr(),
       grad_input.has_value() ? grad_input->mutable_data_ptr() : nullptr,
       grad_weight.has_value() ? grad_weight->mutable_data_ptr() : nullptr,
       grad_bias.has_value() ? grad_bias->mutable_data_ptr() : nullptr,
@@ -199,8 +253,10 @@ at::Tensor conv_nd_cpu(const at::Tensor& input, const at::Tensor& weight,
   }
   const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
-  return torch_convnd_cpu::forward(input, weight, bias, shape, stride, padding, dilation,
-                                   groups);
+  auto y = torch_convnd_cpu::forward(input, weight, bias, shape, stride, padding, dilation,
+                                     groups);
+  // Outputs follow the input's layout, as on the device.
+  return is_channels_last(input) ? to_channels_last(y) : y;
 }
 
 Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& input,
@@ -214,8 +270,11 @@ Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& inpu
                   grad_output.layout() == at::kStrided,
               "grad_output must match the convolution output shape, device and dtype");
   check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
-  return torch_convnd_cpu::backward(grad_output, input, weight, stride, padding, dilation,
-                                    groups, output_mask);
+  auto grads = torch_convnd_cpu::backward(grad_output, input, weight, stride, padding, dilation,
+                                          groups, output_mask);
+  if (is_channels_last(input) && std::get<0>(grads).has_value())
+    std::get<0>(grads) = to_channels_last(*std::get<0>(grads));
+  return grads;
 }
 
 // torch_convnd::conv_nd_act: act(conv + bias) with the activation fused into the forward
@@ -244,22 +303,7 @@ at::Tensor conv_nd_act_device(const at::Tensor& input, const at::Tensor& weight,
   }
   const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
-  const c10::OptionalDeviceGuard guard(input.device());
-  auto output = at::empty(shape, input.options());
-  if (problem.batch == 0) return output;
-  const auto x = input.contiguous();
-  const auto w = weight.contiguous();
-  std::optional<at::Tensor> b;
-  if (bias.has_value()) b = bias->contiguous();
-  const auto dtype = to_dtype(input.scalar_type());
-  const size_t ws_bytes = convnd_hip_forward_workspace_size(&problem, dtype);
-  auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
-  raise_status(convnd_hip_forward_act(&problem, dtype, x.const_data_ptr(), w.const_data_ptr(),
-                                      b.has_value() ? b->const_data_ptr() : nullptr,
-                                      output.mutable_data_ptr(), act,
-                                      ws_bytes ? workspace.mutable_data_ptr() : nullptr, ws_bytes,
-                                      current_stream(input)));
-  return output;
+  return forward_device(problem, input, weight, bias, shape, act);
 }
 
 at::Tensor conv_nd_act_cpu(const at::Tensor& input, const at::Tensor& weight,

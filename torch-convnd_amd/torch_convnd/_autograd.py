@@ -19,16 +19,33 @@ def _spatial_output(sizes, kernels, stride, padding, dilation):
     ]
 
 
+def _is_channels_last(tensor):
+    """[N, C, *spatial] stored as [N, *spatial, C] (and not also contiguous), the layout in
+    which the native operators return channels-last outputs and input gradients."""
+    if tensor.dim() < 3 or tensor.is_contiguous():
+        return False
+    return tensor.permute(0, *range(2, tensor.dim()), 1).is_contiguous()
+
+
+def _empty_like_layout(reference, shape):
+    """An empty tensor of ``shape`` in ``reference``'s activation layout (channels-last or
+    contiguous), as the native operators allocate their outputs."""
+    if not _is_channels_last(reference):
+        return reference.new_empty(shape)
+    stored = reference.new_empty([shape[0], *shape[2:], shape[1]])
+    return stored.permute(0, len(shape) - 1, *range(1, len(shape) - 1))
+
+
 def _fake_forward(input, weight, bias, stride, padding, dilation, groups, workspace_bytes):
     spatial = _spatial_output(input.shape[2:], weight.shape[2:], stride, padding, dilation)
-    return input.new_empty([input.shape[0], weight.shape[0], *spatial])
+    return _empty_like_layout(input, [input.shape[0], weight.shape[0], *spatial])
 
 
 def _fake_backward(
     grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
 ):
     contiguous = torch.contiguous_format
-    grad_input = torch.empty_like(input, memory_format=contiguous) if output_mask[0] else None
+    grad_input = _empty_like_layout(input, list(input.shape)) if output_mask[0] else None
     grad_weight = torch.empty_like(weight, memory_format=contiguous) if output_mask[1] else None
     grad_bias = input.new_empty(weight.shape[0]) if output_mask[2] else None
     return grad_input, grad_weight, grad_bias

@@ -29,7 +29,13 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_forward_act",
     "convnd_hip_forward_noalloc",
     "convnd_hip_plan_check",
+    "convnd_hip_forward_workspace_size_layout",
+    "convnd_hip_backward_workspace_size_layout",
+    "convnd_hip_forward_layout",
+    "convnd_hip_backward_layout",
 )
+
+CHANNELS_FIRST, CHANNELS_LAST = 0, 1
 
 # Bytes of the per-GPU static scratch of convnd_hip_forward_noalloc (CONVND_HIP_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -94,6 +100,16 @@ def bind(library: ctypes.CDLL) -> ctypes.CDLL:
     library.convnd_hip_plan_check.argtypes = [P, ctypes.c_int]
     library.convnd_hip_forward_noalloc.restype = ctypes.c_int
     library.convnd_hip_forward_noalloc.argtypes = [P, ctypes.c_int, vp, vp, vp, vp, vp]
+    library.convnd_hip_forward_workspace_size_layout.restype = sz
+    library.convnd_hip_forward_workspace_size_layout.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    library.convnd_hip_backward_workspace_size_layout.restype = sz
+    library.convnd_hip_backward_workspace_size_layout.argtypes = [
+        P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int
+    ]
+    library.convnd_hip_forward_layout.restype = ctypes.c_int
+    library.convnd_hip_forward_layout.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp, vp, vp, sz, vp]
+    library.convnd_hip_backward_layout.restype = ctypes.c_int
+    library.convnd_hip_backward_layout.argtypes = [P, ctypes.c_int, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     library.convnd_hip_partial_count.restype = ctypes.c_int
     library.convnd_hip_partial_count.argtypes = [P, ctypes.c_int, vp, vp, vp]
     library.convnd_hip_partial_rescale.restype = ctypes.c_int
