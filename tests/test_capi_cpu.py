@@ -198,9 +198,11 @@ def test_channels_last_workspace_sizes_without_device(lib):
     assert lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last) == fwd
     bwd_cl = lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last, 1, 1, 1)
     assert bwd_cl >= lib.convnd_hip_backward_workspace_size(ctypes.byref(p), _capi.BFLOAT16, 1, 1, 1) + x_bytes + y_bytes
-    # grad_input alone: the input-gradient GEMM stages channels-last grad_output itself.
-    assert lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last, 1, 0, 0) == \
-        lib.convnd_hip_backward_workspace_size(ctypes.byref(p), _capi.BFLOAT16, 1, 0, 0)
+    # grad_input alone: at most a channels-first grad_output copy (none when the input-gradient
+    # GEMM stages channels-last grad_output itself).
+    alone = lib.convnd_hip_backward_workspace_size(ctypes.byref(p), _capi.BFLOAT16, 1, 0, 0)
+    alone_cl = lib.convnd_hip_backward_workspace_size_layout(ctypes.byref(p), _capi.BFLOAT16, last, 1, 0, 0)
+    assert alone <= alone_cl <= alone + y_bytes + 512
     fwd32 = lib.convnd_hip_forward_workspace_size(ctypes.byref(p), _capi.FLOAT32)
     assert lib.convnd_hip_forward_workspace_size_layout(ctypes.byref(p), _capi.FLOAT32, last) >= \
         fwd32 + 2 * (x_bytes + y_bytes)

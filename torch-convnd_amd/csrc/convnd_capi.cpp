@@ -1763,7 +1763,14 @@ int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, co
 // [N][out...][Co] itself. Every other plan runs channels-first on copies in the workspace,
 // made and undone by transposes; so does the weight gradient, whose kernels read
 // channels-first input and grad_output.
-bool forward_reads_cl(const ForwardSetup& f) { return f.ig.ok && f.ig.args.direct != 0; }
+// Direct channels-last staging loads 16 bytes of each position's channel chunk; when the chunk
+// covers less than half of the position's channels (wide or grouped layers) most of every line
+// goes unused and the channels-first copy is cheaper.
+bool igemm_stages_cl(const IgemmPlan& p) {
+  return p.ok && p.args.direct != 0 && p.args.cc * 2 >= p.args.cin_total;
+}
+
+bool forward_reads_cl(const ForwardSetup& f) { return igemm_stages_cl(f.ig); }
 
 size_t tensor_bytes(int64_t batch, int64_t channels, int64_t volume, convnd_hip_dtype dt) {
   return align_up(static_cast<size_t>(batch * channels * volume * element_size(dt)));
@@ -1787,7 +1794,9 @@ ClBackward cl_backward_plan(const Geom& g, convnd_hip_dtype dt, const BackwardSe
                             bool gw, bool gb) {
   ClBackward c;
   const bool mfma_dx = gi && g.batch > 0 && b.dg.ok;
-  c.dgrad_cl = mfma_dx && b.dg.args.direct != 0;
+  // The weight and bias gradients read a channels-first grad_output copy; the input gradient
+  // then stages from it as well, and reads channels-last grad_output only when it is alone.
+  c.dgrad_cl = mfma_dx && !gw && !gb && igemm_stages_cl(b.dg);
   c.dx_epilogue = mfma_dx;
   c.dy_cf = gw || gb || (gi && !c.dgrad_cl);
   c.x_cf = gw;

@@ -294,6 +294,48 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const E* __restrict
   }
 }
 
+// The same for 16-bit elements when a and b are multiples of 8 and both buffers 16-byte
+// aligned: 16-byte loads of 8 consecutive b elements and 16-byte stores of 8 consecutive a
+// elements (gathered from the tile's column), two of each per thread.
+__global__ __launch_bounds__(kThreads) void transpose16_kernel(const uint4* __restrict__ src,
+                                                               uint4* __restrict__ dst, int64_t a,
+                                                               int64_t b) {
+  constexpr int kPitch = 64 + 8;  // elements per tile row
+  __shared__ __align__(16) unsigned short tile[64 * kPitch];
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const size_t mat = static_cast<size_t>(a) * static_cast<size_t>(b);
+  const unsigned short* s = reinterpret_cast<const unsigned short*>(src) + blockIdx.z * mat;
+  unsigned short* d = reinterpret_cast<unsigned short*>(dst) + blockIdx.z * mat;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int chunk = threadIdx.x + k * kThreads;  // 64 rows x 8 chunks of 8
+    const int r = chunk >> 3, c = (chunk & 7) * 8;
+    const int64_t ra = a0 + r, cb = b0 + c;
+    if (ra < a && cb < b)
+      *reinterpret_cast<uint4*>(&tile[r * kPitch + c]) =
+          *reinterpret_cast<const uint4*>(s + ra * b + cb);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int chunk = threadIdx.x + k * kThreads;  // 64 b-rows x 8 chunks of 8 a elements
+    const int r = chunk >> 3, c = (chunk & 7) * 8;
+    const int64_t rb = b0 + r, ca = a0 + c;
+    if (rb < b && ca < a) {
+      unsigned short e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = tile[(c + i) * kPitch + r];
+      uint4 v;
+      v.x = e[0] | (static_cast<unsigned>(e[1]) << 16);
+      v.y = e[2] | (static_cast<unsigned>(e[3]) << 16);
+      v.z = e[4] | (static_cast<unsigned>(e[5]) << 16);
+      v.w = e[6] | (static_cast<unsigned>(e[7]) << 16);
+      *reinterpret_cast<uint4*>(d + rb * a + ca) = v;
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_transpose(int64_t element_size, int64_t batch, int64_t a, int64_t b,
@@ -303,6 +345,12 @@ hipError_t launch_transpose(int64_t element_size, int64_t batch, int64_t a, int6
     return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>((a + 63) / 64), static_cast<unsigned>((b + 63) / 64),
                   static_cast<unsigned>(batch));
+  if (element_size == 2 && a % 8 == 0 && b % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
+    hipLaunchKernelGGL(transpose16_kernel, grid, dim3(kThreads), 0, stream,
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), a, b);
+    return hipGetLastError();
+  }
   switch (element_size) {
     case 2:
       hipLaunchKernelGGL((transpose_kernel<unsigned short>), grid, dim3(kThreads), 0, stream,
