@@ -174,3 +174,36 @@ def test_channels_last_c_abi():
     helpers.assert_close(dx.permute(0, 5, 1, 2, 3, 4), ref_dx, torch.bfloat16, "C ABI channels-last dx")
     helpers.assert_close(dw, ref_dw, torch.bfloat16, "C ABI channels-last dw")
     helpers.assert_close(db, ref_db, torch.bfloat16, "C ABI channels-last db")
+
+
+def test_channels_last_module_compile_and_autocast():
+    """A channels-last activation through a Conv4d layer: eager, compiled (AOTAutograd with the
+    operator's fake functions, which must report the channels-last strides the kernels
+    produce, or the compiled graph would index the output wrongly) and under autocast, each
+    equal to the channels-first call."""
+    from torch_convnd import Conv4d
+
+    print("[channels_last] Conv4d eager / compiled / autocast", flush=True)
+    torch.manual_seed(902)
+    layer = Conv4d(16, 32, 3, padding=1, device="cuda", dtype=torch.bfloat16, backend="native")
+    x = torch.randn(2, 16, 4, 5, 4, 8, device="cuda").to(torch.bfloat16)
+    x_cl = channels_last(x).requires_grad_()
+    x_cf = x.clone().requires_grad_()
+    y_cf = layer(x_cf)
+    y_cl = layer(x_cl)
+    assert is_channels_last(y_cl) and torch.equal(y_cl, y_cf)
+    (g_cf,) = torch.autograd.grad(y_cf.float().square().sum(), x_cf)
+    (g_cl,) = torch.autograd.grad(y_cl.float().square().sum(), x_cl)
+    assert is_channels_last(g_cl) and torch.equal(g_cl, g_cf)
+    compiled = torch.compile(layer, backend="aot_eager", fullgraph=True)
+    y_comp = compiled(x_cl)
+    assert y_comp.stride() == y_cl.stride() and torch.equal(y_comp, y_cl)
+    # Downstream elementwise work of the compiled graph reads the output through its strides.
+    shifted = torch.compile(lambda t: layer(t) * 2 + 1, backend="aot_eager", fullgraph=True)
+    assert torch.equal(shifted(x_cl), y_cl * 2 + 1)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        layer32 = Conv4d(16, 32, 3, padding=1, device="cuda", backend="native")
+        x32 = x.float()
+        y_ac_cf = layer32(x32)
+        y_ac_cl = layer32(channels_last(x32))
+    assert y_ac_cl.dtype == torch.bfloat16 and torch.equal(y_ac_cl, y_ac_cf)
