@@ -12,6 +12,7 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
+#include <torch/csrc/autograd/custom_function.h>
 
 #include <array>
 #include <limits>
@@ -430,8 +431,178 @@ at::Tensor conv_nd_autocast(const at::Tensor& input, const at::Tensor& weight,
                  workspace_bytes);
 }
 
+// ---- autograd -----------------------------------------------------------------------------
+// The derivative contract of the reference's Python registration (src/torch_convnd/
+// _autograd.py:8-149), as C++ autograd kernels so that a training step spends little host time
+// in the autograd machinery: the forward saves input and weight; the backward calls
+// conv_nd_backward for exactly the gradients autograd needs; conv_nd_backward is itself
+// differentiable (double backward through the same two operators, its terms again forward or
+// backward convolutions, computed with autocast off).
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+using ConvFn = at::Tensor(const at::Tensor&, const at::Tensor&, const std::optional<at::Tensor>&,
+                          at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, int64_t);
+
+const c10::TypedOperatorHandle<ConvFn>& conv_op() {
+  static const auto op =
+      c10::Dispatcher::singleton().findSchemaOrThrow("torch_convnd::conv_nd", "").typed<ConvFn>();
+  return op;
+}
+
+// conv_nd_backward's output_mask is a bool[3]; the typed handle takes it as std::array.
+using BackwardArrayFn = Grads(const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                              at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, int64_t,
+                              std::array<bool, 3>);
+const c10::TypedOperatorHandle<BackwardArrayFn>& backward_op() {
+  static const auto op = c10::Dispatcher::singleton()
+                             .findSchemaOrThrow("torch_convnd::conv_nd_backward", "")
+                             .typed<BackwardArrayFn>();
+  return op;
+}
+
+void save_geometry(AutogradContext* ctx, at::IntArrayRef stride, at::IntArrayRef padding,
+                   at::IntArrayRef dilation, int64_t groups, int64_t workspace_bytes) {
+  ctx->saved_data["stride"] = stride.vec();
+  ctx->saved_data["padding"] = padding.vec();
+  ctx->saved_data["dilation"] = dilation.vec();
+  ctx->saved_data["groups"] = groups;
+  ctx->saved_data["workspace_bytes"] = workspace_bytes;
+}
+
+class ConvNdFunction : public torch::autograd::Function<ConvNdFunction> {
+ public:
+  static at::Tensor forward(AutogradContext* ctx, const at::Tensor& input, const at::Tensor& weight,
+                            const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                            at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                            int64_t workspace_bytes) {
+    save_geometry(ctx, stride, padding, dilation, groups, workspace_bytes);
+    const bool has_bias = bias.has_value() && bias->defined();
+    ctx->saved_data["has_bias"] = has_bias;
+    ctx->save_for_backward({input, weight});
+    at::AutoDispatchBelowADInplaceOrView below;
+    return conv_op().call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes);
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const bool has_bias = ctx->saved_data["has_bias"].toBool();
+    // Edges: input, weight, then bias when one was given.
+    const std::array<bool, 3> mask = {ctx->needs_input_grad(0), ctx->needs_input_grad(1),
+                                      has_bias && ctx->needs_input_grad(2)};
+    const auto stride = ctx->saved_data["stride"].toIntVector();
+    const auto padding = ctx->saved_data["padding"].toIntVector();
+    const auto dilation = ctx->saved_data["dilation"].toIntVector();
+    auto [gi, gw, gb] = backward_op().call(
+        grads[0], saved[0], saved[1], stride, padding, dilation, ctx->saved_data["groups"].toInt(),
+        ctx->saved_data["workspace_bytes"].toInt(), mask);
+    return {gi.value_or(at::Tensor()), gw.value_or(at::Tensor()), gb.value_or(at::Tensor()),
+            at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+class ConvNdBackwardFunction : public torch::autograd::Function<ConvNdBackwardFunction> {
+ public:
+  static variable_list forward(AutogradContext* ctx, const at::Tensor& grad_output,
+                               const at::Tensor& input, const at::Tensor& weight,
+                               at::IntArrayRef stride, at::IntArrayRef padding,
+                               at::IntArrayRef dilation, int64_t groups, int64_t workspace_bytes,
+                               std::array<bool, 3> output_mask) {
+    save_geometry(ctx, stride, padding, dilation, groups, workspace_bytes);
+    ctx->saved_data["mask"] =
+        std::vector<bool>{output_mask[0], output_mask[1], output_mask[2]};
+    ctx->save_for_backward({grad_output, input, weight});
+    at::AutoDispatchBelowADInplaceOrView below;
+    auto [gi, gw, gb] = backward_op().call(grad_output, input, weight, stride, padding, dilation,
+                                           groups, workspace_bytes, output_mask);
+    // Outputs of a custom function must be defined: only the requested gradients are returned
+    // (in order); the caller maps them back to the three optional results.
+    variable_list out;
+    for (const auto& t : {gi, gw, gb})
+      if (t.has_value() && t->defined()) out.push_back(*t);
+    return out;
+  }
+
+  // Second-order terms (the reference's backward of the backward): the backward is bilinear in
+  // (grad_output, input) and in (grad_output, weight).
+  static variable_list backward(AutogradContext* ctx, variable_list ggrads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor &grad_output = saved[0], &input = saved[1], &weight = saved[2];
+    const auto stride = ctx->saved_data["stride"].toIntVector();
+    const auto padding = ctx->saved_data["padding"].toIntVector();
+    const auto dilation = ctx->saved_data["dilation"].toIntVector();
+    const int64_t groups = ctx->saved_data["groups"].toInt();
+    const int64_t ws = ctx->saved_data["workspace_bytes"].toInt();
+    const bool need_go = ctx->needs_input_grad(0), need_x = ctx->needs_input_grad(1),
+               need_w = ctx->needs_input_grad(2);
+    // ggrads holds one entry per returned (requested) gradient, in order.
+    const auto mask = ctx->saved_data["mask"].toBoolList();
+    at::Tensor gg[3];
+    size_t at_ = 0;
+    for (int i = 0; i < 3; ++i)
+      if (mask.get(i) && at_ < ggrads.size()) gg[i] = ggrads[at_++];
+    const at::Tensor &ggi = gg[0], &ggw = gg[1], &ggb = gg[2];
+    at::Tensor gg_output, new_input_grad, new_weight_grad;
+    auto add = [](at::Tensor& total, const at::Tensor& term) {
+      total = total.defined() ? total + term : term;
+    };
+    // Autocast off for these terms, on both device types the operators run on.
+    c10::impl::ExcludeDispatchKeyGuard no_autocast(
+        c10::DispatchKeySet({c10::DispatchKey::AutocastCUDA, c10::DispatchKey::AutocastCPU}));
+    if (ggi.defined()) {
+      if (need_go) add(gg_output, conv_op().call(ggi, weight, std::nullopt, stride, padding,
+                                                 dilation, groups, ws));
+      if (need_w)
+        new_weight_grad = *std::get<1>(backward_op().call(grad_output, ggi, weight, stride, padding,
+                                                          dilation, groups, ws,
+                                                          {false, true, false}));
+    }
+    if (ggw.defined()) {
+      if (need_go) add(gg_output, conv_op().call(input, ggw, std::nullopt, stride, padding,
+                                                 dilation, groups, ws));
+      if (need_x)
+        new_input_grad = *std::get<0>(backward_op().call(grad_output, input, ggw, stride, padding,
+                                                         dilation, groups, ws,
+                                                         {true, false, false}));
+    }
+    if (ggb.defined() && need_go) {
+      std::vector<int64_t> shape(input.dim(), 1);
+      shape[1] = -1;
+      add(gg_output, ggb.reshape(shape).expand_as(grad_output));
+    }
+    return {gg_output, new_input_grad, new_weight_grad, at::Tensor(), at::Tensor(),
+            at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+at::Tensor conv_nd_autograd(const at::Tensor& input, const at::Tensor& weight,
+                            const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
+                            at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                            int64_t workspace_bytes) {
+  return ConvNdFunction::apply(input, weight, bias, stride, padding, dilation, groups,
+                               workspace_bytes);
+}
+
+Grads conv_nd_backward_autograd(const at::Tensor& grad_output, const at::Tensor& input,
+                                const at::Tensor& weight, at::IntArrayRef stride,
+                                at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
+                                int64_t workspace_bytes, std::array<bool, 3> output_mask) {
+  auto out = ConvNdBackwardFunction::apply(grad_output, input, weight, stride, padding, dilation,
+                                           groups, workspace_bytes, output_mask);
+  std::optional<at::Tensor> res[3];
+  size_t at_ = 0;
+  for (int i = 0; i < 3; ++i)
+    if (output_mask[i] && at_ < out.size()) res[i] = out[at_++];
+  return {res[0], res[1], res[2]};
+}
+
 }  // namespace
 }  // namespace torch_convnd_hip
+
+TORCH_LIBRARY_IMPL(torch_convnd, Autograd, library) {
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autograd);
+  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_autograd);
+}
 
 TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
   library.impl("conv_nd", &torch_convnd_hip::conv_nd_device);

@@ -184,6 +184,18 @@ def _rescale_backward(ctx, grad):
     return grad_raw, None, grad_bias, None
 
 
+_PY_AUTOGRAD = None
+
+
+def release_python_autograd() -> None:
+    """Drop the Python autograd registrations of conv_nd / conv_nd_backward (called right
+    before the native library, whose C++ autograd kernels replace them, is loaded)."""
+    global _PY_AUTOGRAD
+    if _PY_AUTOGRAD is not None:
+        _PY_AUTOGRAD._destroy()
+        _PY_AUTOGRAD = None
+
+
 def register_training() -> None:
     torch.library.register_fake("torch_convnd::conv_nd")(_fake_forward)
     torch.library.register_fake("torch_convnd::conv_nd_backward")(_fake_backward)
@@ -193,9 +205,20 @@ def register_training() -> None:
     torch.library.register_autograd(
         "torch_convnd::partial_rescale", _rescale_backward, setup_context=_setup_rescale
     )
-    torch.library.register_autograd("torch_convnd::conv_nd", _backward, setup_context=_setup_context)
+    # The convolution operators' derivatives are registered here for use before the native
+    # library loads; that library carries the same contract as C++ autograd kernels
+    # (torch_ops.cpp), and release_python_autograd() drops these registrations just before it
+    # loads, so a training step does not pay the Python autograd machinery per call.
+    global _PY_AUTOGRAD
+    _PY_AUTOGRAD = torch.library.Library("torch_convnd", "FRAGMENT")
     torch.library.register_autograd(
-        "torch_convnd::conv_nd_backward", _backward_backward, setup_context=_setup_backward_context
+        "torch_convnd::conv_nd", _backward, setup_context=_setup_context, lib=_PY_AUTOGRAD
+    )
+    torch.library.register_autograd(
+        "torch_convnd::conv_nd_backward",
+        _backward_backward,
+        setup_context=_setup_backward_context,
+        lib=_PY_AUTOGRAD,
     )
     if HAS_NATIVE_VMAP:
         torch.library.register_vmap("torch_convnd::conv_nd", _vmap_forward)

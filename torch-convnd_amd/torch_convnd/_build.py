@@ -62,6 +62,9 @@ def load_native(*, with_cuda: bool | None = None, verbose: bool = False) -> None
         from . import _capi
 
         _HIP = _capi.bind(ctypes.CDLL(str(HIP_LIBRARY), mode=ctypes.RTLD_GLOBAL))
+        from ._autograd import release_python_autograd
+
+        release_python_autograd()
         torch.ops.load_library(str(OPS_LIBRARY))
         _WITH_CUDA = torch.version.hip is not None
         _LOADED = True
