@@ -195,3 +195,63 @@ def test_channels_last_outputs_follow_the_input_layout():
         fg = _op_backward(fdy, fx, fw, stride, padding, dilation, groups, [True, False, False])
     assert fy.shape == y.shape and fy.stride() == y_cl.stride()
     assert fg[0].stride() == g_cl[0].stride()
+
+
+def test_direct_call_matches_the_general_path(monkeypatch):
+    """conv_nd's shortcut to the operator (plain batched calls with symmetric zero padding)
+    gives the general path's results and gradients bitwise, and hands every other call
+    (asymmetric 'same' padding, mismatched dtypes, invalid channels, autocast) to the general
+    path, whose errors and results stay the same."""
+    from torch_convnd import functional
+
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 4, 5, 4, 3, 6, generator=gen, dtype=torch.float64)
+    w = torch.randn(6, 2, 3, 2, 3, 3, generator=gen, dtype=torch.float64)
+    b = torch.randn(6, generator=gen, dtype=torch.float64)
+    taken = []
+    real = functional._direct_call
+
+    def spy(*args):
+        out = real(*args)
+        taken.append(out is not None)
+        return out
+
+    monkeypatch.setattr(functional, "_direct_call", spy)
+    for stride, padding, dilation in (
+        (1, 1, 1),
+        ([2, 1, 1, 2], (1, 0, 1, 2), (1, 2, 1, 1)),
+        (1, "same", (1, 2, 1, 1)),  # odd kernels: symmetric 'same'
+        ((1, 1, 1, 1), "valid", 1),
+    ):
+        leaves = [t.clone().requires_grad_() for t in (x, w, b)]
+        y = conv_nd(*leaves, stride=stride, padding=padding, dilation=dilation, groups=2, backend="native")
+        dy = torch.randn(y.shape, generator=gen, dtype=y.dtype)
+        grads = torch.autograd.grad(y, leaves, dy)
+        assert taken[-1]
+        monkeypatch.setattr(functional, "_direct_call", lambda *args: None)
+        leaves2 = [t.clone().requires_grad_() for t in (x, w, b)]
+        y2 = conv_nd(*leaves2, stride=stride, padding=padding, dilation=dilation, groups=2, backend="native")
+        grads2 = torch.autograd.grad(y2, leaves2, dy)
+        monkeypatch.setattr(functional, "_direct_call", spy)
+        assert torch.equal(y, y2)
+        for g1, g2 in zip(grads, grads2):
+            assert torch.equal(g1, g2)
+    # Even kernel with 'same': asymmetric padding, general path (explicit pad first).
+    w_even = torch.randn(6, 2, 2, 2, 3, 3, generator=gen, dtype=torch.float64)
+    y = conv_nd(x, w_even, b, padding="same", groups=2, backend="native")
+    assert not taken[-1] and y.shape[2:] == x.shape[2:]
+    # Mismatched dtype: the general path's error.
+    with pytest.raises(RuntimeError, match="same device and dtype"):
+        conv_nd(x, w.float(), b, padding=1, groups=2, backend="native")
+    assert not taken[-1]
+    # Channels not divisible by groups: the general path's error.
+    with pytest.raises(RuntimeError, match="divisible by groups"):
+        conv_nd(x, w, b, padding=1, groups=3, backend="native")
+    assert not taken[-1]
+    # Autocast: the general path (it casts the operands).
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        y = conv_nd(x.float(), w.float(), b.float(), padding=1, groups=2, backend="native")
+    assert not taken[-1] and y.dtype == torch.bfloat16
+    # The auto backend on CPU at rank 4 keeps the general path's policy (portable).
+    conv_nd(x, w, b, padding=1, groups=2)
+    assert not taken[-1]

@@ -11,7 +11,8 @@ from collections.abc import Sequence
 import torch
 from torch import Tensor
 
-from ._compat import HAS_LIBRARY, is_autocast_enabled
+from . import _build
+from ._compat import HAS_LIBRARY, is_autocast_enabled, is_compiling, is_onnx_exporting, transforms_active
 from ._dispatch import BACKENDS, convolution, ensure_compatible_operator
 from ._geometry import DEFAULT_WORKSPACE_BYTES, _tuple, any_true, has_rank
 from ._padding import apply_padding, padding_pairs
@@ -62,6 +63,103 @@ def _check_bias(input, weight, bias, amp):
         raise RuntimeError("bias must match output channels, device and dtype")
 
 
+# Normalised geometry of calls that can go straight to the operator, per (rank, stride,
+# padding, dilation, kernel sizes) as passed: (stride, implicit padding, dilation) lists, or
+# None for calls that need the general path (asymmetric 'same' padding, invalid values;
+# lists are keyed as tuples, other unhashable arguments take the general path). Bounded:
+# cleared when full.
+_DIRECT_GEOMETRY: dict = {}
+_DIRECT_GEOMETRY_LIMIT = 512
+
+
+def _hashable(value):
+    return tuple(value) if type(value) is list else value
+
+
+def _direct_geometry(rank, stride, padding, dilation, kernel):
+    key = (rank, _hashable(stride), _hashable(padding), _hashable(dilation), kernel)
+    try:
+        return _DIRECT_GEOMETRY[key]
+    except KeyError:
+        pass
+    except TypeError:
+        return None
+    value = None
+    try:
+        strides = _tuple(stride, rank, "stride")
+        dilations = _tuple(dilation, rank, "dilation")
+        pads = padding if isinstance(padding, str) else _tuple(padding, rank, "padding")
+        positive = min(*strides, *dilations) > 0 and (isinstance(pads, str) or min(pads) >= 0)
+        if positive:
+            pairs = padding_pairs(pads, kernel, strides, dilations)
+            if not any_true([left != right for left, right in pairs]):
+                value = (list(strides), [left for left, _ in pairs], list(dilations))
+    except (TypeError, ValueError, RuntimeError):
+        value = None
+    if len(_DIRECT_GEOMETRY) >= _DIRECT_GEOMETRY_LIMIT:
+        _DIRECT_GEOMETRY.clear()
+    _DIRECT_GEOMETRY[key] = value
+    return value
+
+
+def _direct_call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, backend):
+    """The operator call of a plain batched convolution with symmetric zero padding, the
+    same one the general path below ends in, without its per-call argument normalisation;
+    None when any condition of that shortcut fails (the general path then handles the call,
+    errors included): native library loaded, a ROCm GPU with the native or auto backend at
+    rank >= 4 (or native at any rank), or a CPU tensor with the native backend; equal dtypes
+    and devices, valid channels and extents; no autocast, transform, tracing, compiling or
+    ONNX export."""
+    if is_compiling() or not _build._LOADED:
+        return None
+    if workspace_bytes <= 0 or type(groups) is not int or groups <= 0:
+        return None
+    rank = weight.ndim - 2
+    if not 1 <= rank <= 62 or input.ndim != rank + 2:
+        return None
+    device = input.device
+    if device.type == "cuda":
+        if torch.version.hip is None or (backend != "native" and (backend != "auto" or rank < 4)):
+            return None
+    elif device.type != "cpu" or backend != "native":
+        return None
+    dtype = input.dtype
+    if weight.dtype != dtype or dtype.is_complex or weight.device != device:
+        return None
+    out_channels = weight.shape[0]
+    if bias is not None and (
+        bias.dtype != dtype or bias.ndim != 1 or bias.shape[0] != out_channels or bias.device != device
+    ):
+        return None
+    in_channels = input.shape[1]
+    if (
+        in_channels <= 0
+        or out_channels <= 0
+        or in_channels % groups
+        or out_channels % groups
+        or weight.shape[1] * groups != in_channels
+        or min(input.shape[2:]) <= 0
+    ):
+        return None
+    kernel = tuple(weight.shape[2:])
+    if min(kernel) <= 0:
+        return None
+    geometry = _direct_geometry(rank, stride, padding, dilation, kernel)
+    if geometry is None:
+        return None
+    if (
+        is_autocast_enabled(device.type)
+        or torch.jit.is_tracing()
+        or transforms_active()
+        or is_onnx_exporting()
+    ):
+        return None
+    strides, implicit, dilations = geometry
+    return torch.ops.torch_convnd.conv_nd.default(
+        input, weight, bias, strides, implicit, dilations, groups, workspace_bytes
+    )
+
+
 def conv_nd(
     input: Tensor,
     weight: Tensor,
@@ -92,6 +190,10 @@ def conv_nd(
     max(element size, 4) * channels * kernel volume bytes); the implicit-GEMM kernels
     allocate their own small scratch instead of a patch buffer.
     """
+    if padding_mode == "zeros" and activation is None:
+        output = _direct_call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, backend)
+        if output is not None:
+            return output
     rank = weight.ndim - 2
     if not 1 <= rank <= 62:
         raise ValueError("weight must have output/input channels and 1-62 spatial dimensions")
@@ -122,8 +224,6 @@ def conv_nd(
     _check_bias(input, weight, bias, amp)
     pairs = padding_pairs(padding, weight.shape[2:], stride, dilation)
     if activation is not None and _fused_activation_ok(input, weight, bias, rank, backend, padding_mode, pairs, amp):
-        from . import _build
-
         if not _build._LOADED:
             _build.load_native()
         output = torch.ops.torch_convnd.conv_nd_act(
