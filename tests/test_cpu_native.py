@@ -252,6 +252,12 @@ def test_direct_call_matches_the_general_path(monkeypatch):
     with torch.autocast("cpu", dtype=torch.bfloat16):
         y = conv_nd(x.float(), w.float(), b.float(), padding=1, groups=2, backend="native")
     assert not taken[-1] and y.dtype == torch.bfloat16
+    # A bool where an int belongs is refused even after the int's geometry is cached.
+    conv_nd(x, w, b, stride=1, padding=1, groups=2, backend="native")
+    with pytest.raises(TypeError):
+        conv_nd(x, w, b, stride=True, padding=1, groups=2, backend="native")
+    with pytest.raises(ValueError):
+        conv_nd(x, w, b, stride=(1, 1, True, 1), padding=1, groups=2, backend="native")
     # The auto backend on CPU at rank 4 keeps the general path's policy (portable).
     conv_nd(x, w, b, padding=1, groups=2)
     assert not taken[-1]

@@ -73,7 +73,10 @@ _DIRECT_GEOMETRY_LIMIT = 512
 
 
 def _hashable(value):
-    return tuple(value) if type(value) is list else value
+    # With the element types: True == 1 and hashes alike, but only the int is a valid stride.
+    if type(value) is list or type(value) is tuple:
+        return tuple(value), tuple(map(type, value))
+    return value, type(value)
 
 
 def _direct_geometry(rank, stride, padding, dilation, kernel):
