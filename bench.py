@@ -175,10 +175,11 @@ def cpu_baseline(torch):
                 torch_path.torch_backend_conv(x, w, b, STRIDE, PADDING, DILATION, GROUPS)
 
         def median_s(fn, budget_s):
+            fn()  # warmup (first-call allocations)
             start = time.perf_counter()
-            fn()  # warmup
+            fn()  # one run to size the sample to the time budget
             first = time.perf_counter() - start
-            iterations = max(3, min(50, int(budget_s / max(first, 1e-3))))
+            iterations = max(3, min(1000, int(budget_s / max(first, 1e-3))))
             times = []
             for _ in range(iterations):
                 t0 = time.perf_counter()
@@ -199,7 +200,7 @@ def cpu_baseline(torch):
             "affinity_cores": len(os.sched_getaffinity(0)),
             "sample": (
                 f"full C2 problem, fwd + full bwd (dx, dW, db) for a fixed dY, bf16, median of "
-                f"{iterations} runs after 1 warmup ({median * 1e3:.0f} ms each); forward alone "
+                f"{iterations} runs after a warmup and a sizing run ({median * 1e3:.0f} ms each); forward alone "
                 f"median of {fwd_iterations} runs; {cores} threads; torch {torch.__version__}, "
                 f"{_cpu_model()}"
             ),
