@@ -185,13 +185,13 @@ def test_partial_gpu_matches_oracle(dtype, multi_channel):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rank", [4, 5, 9])
+@pytest.mark.parametrize("rank", [4, 5, 9, 16, 42])
 @pytest.mark.parametrize("multi_channel", [False, True])
 def test_partial_gpu_native_matches_portable_with_gradients(rank, multi_channel):
     # The reference's tests/test_partial_native.py:19-80 on the GPU: float64, gradients.
     print(f"[partial] gpu gradients rank {rank} multi={multi_channel}", flush=True)
     g = torch.Generator().manual_seed(rank)
-    if rank == 9:
+    if rank >= 9:
         size, kernel, padding = [1] * rank, [1] * rank, [0] * rank
         for axis, length, taps in ((0, 5, 3), (rank // 2, 4, 2), (rank - 1, 6, 3)):
             size[axis], kernel[axis], padding[axis] = length, taps, 1
