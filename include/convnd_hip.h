@@ -50,10 +50,16 @@ typedef enum convnd_hip_activation {
  * grad_input; weights are always [output_channels, channels / groups, kernel...]):
  *   CHANNELS_FIRST  [batch, channels, spatial...]  (the reference's only layout)
  *   CHANNELS_LAST   [batch, spatial..., channels]  (channels innermost, as PyTorch's
- *                   channels_last / channels_last_3d memory formats and their N-d analogue) */
+ *                   channels_last / channels_last_3d memory formats and their N-d analogue)
+ *   CHANNELS_LAST_INPUT  input channels-last; output, grad_output and grad_input
+ *                   channels-first. This is what the reference operators give a channels-last
+ *                   input: they read it through a contiguous copy and return contiguous
+ *                   results (src/torch_convnd/csrc/convnd.cpp:317-320,377-386). Here the
+ *                   forward GEMM reads the channels-last input itself where it can. */
 typedef enum convnd_hip_layout {
   CONVND_HIP_CHANNELS_FIRST = 0,
-  CONVND_HIP_CHANNELS_LAST = 1
+  CONVND_HIP_CHANNELS_LAST = 1,
+  CONVND_HIP_CHANNELS_LAST_INPUT = 2
 } convnd_hip_layout;
 
 typedef enum convnd_hip_status {
@@ -151,10 +157,14 @@ size_t convnd_hip_backward_workspace_size_layout(const convnd_hip_problem* probl
  * (convnd_hip_layout). With CHANNELS_LAST the implicit GEMM with direct staging (16-bit data)
  * reads [batch, spatial..., channels] and writes [batch, out..., output_channels] itself, so
  * such a forward makes no layout copy; other plans, and the weight gradient (whose kernels
- * read channels-first operands), run on channels-first copies in the workspace. Results are
- * the same numbers as the channels-first call. No reference counterpart: the reference makes
- * every operand contiguous (channels-first) first (src/torch_convnd/csrc/convnd.cpp:317-319,
- * 377-381). */
+ * read channels-first operands), run on channels-first copies in the workspace. With
+ * CHANNELS_LAST_INPUT the same GEMM reads the channels-last input and writes a channels-first
+ * output; the backward is the channels-first one with the weight gradient reading a
+ * channels-first copy of the input. Results are the same numbers as the channels-first call.
+ * CHANNELS_LAST_INPUT is the layout of the reference operators' contract for a channels-last
+ * input (they copy every operand to channels-first and return channels-first results,
+ * src/torch_convnd/csrc/convnd.cpp:317-320,377-386); CHANNELS_LAST has no reference
+ * counterpart. */
 int convnd_hip_forward_layout(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                               int layout, int activation, const void* input, const void* weight,
                               const void* bias, void* output, void* workspace,
@@ -207,9 +217,9 @@ int convnd_hip_partial_rescale(convnd_hip_dtype dtype, const void* raw, const vo
  * GPU shares that GPU's array and leaves its contents behind (each call rewrites all it
  * reads), so calls that overlap on one GPU (other streams, other threads) race: serialise
  * them. Same results as convnd_hip_forward (the same kernels).
- * No counterpart in the reference (src/torch_convnd/csrc/convnd.cpp:326 allocates per call):
- * for callers that cannot allocate device memory -- code under stream capture, serving loops
- * that must not allocate, harnesses that forbid hipMalloc. */
+ * No counterpart in the reference: for callers that cannot allocate device memory -- code
+ * under stream capture, serving loops that must not allocate, harnesses that forbid
+ * hipMalloc. */
 int convnd_hip_forward_noalloc(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                                const void* input, const void* weight, const void* bias,
                                void* output, void* stream);

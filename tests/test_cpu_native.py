@@ -169,20 +169,27 @@ def _is_channels_last(t):
     return not t.is_contiguous() and t.permute(0, *range(2, t.dim()), 1).is_contiguous()
 
 
-def test_channels_last_outputs_follow_the_input_layout():
-    """A channels-last input gives a channels-last output and grad_input with the values of
-    the channels-first call, on CPU as on the device; the fake (shape) functions agree, so
-    compiled graphs see the strides the kernels produce."""
+@pytest.mark.parametrize("preserve", [False, True], ids=["contiguous_contract", "preserve"])
+def test_channels_last_input_layouts(preserve):
+    """A channels-last input gives the values of the channels-first call. The reference
+    operators return a contiguous output and grad_input (src/torch_convnd/csrc/convnd.cpp:
+    317-320,377-386; fake functions src/torch_convnd/_autograd.py:8-26); the layout-following
+    pair (conv_nd_preserve / conv_nd_backward_preserve) returns channels-last ones. The fake
+    (shape) functions report the strides the kernels produce, so compiled graphs agree."""
+    forward = torch.ops.torch_convnd.conv_nd_preserve if preserve else torch.ops.torch_convnd.conv_nd
+    backward = (torch.ops.torch_convnd.conv_nd_backward_preserve if preserve
+                else torch.ops.torch_convnd.conv_nd_backward)
+    expect = _is_channels_last if preserve else (lambda t: t.is_contiguous())
     xs, ws, stride, padding, dilation, groups, bias = CASES["r4_strided_dilated"]
+    geometry = (list(stride), list(padding), list(dilation), groups, 1 << 30)
     x, w, b = helpers.seeded_problem(xs, ws, bias, torch.float32, seed=3)
     y = _op_forward(x, w, b, stride, padding, dilation, groups)
-    y_cl = _op_forward(_channels_last(x), w, b, stride, padding, dilation, groups)
-    assert _is_channels_last(y_cl) and torch.equal(y_cl, y)
+    y_cl = forward(_channels_last(x), w, b, *geometry)
+    assert expect(y_cl) and torch.equal(y_cl, y)
     dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(4))
     g = _op_backward(dy, x, w, stride, padding, dilation, groups, [True, True, True])
-    g_cl = _op_backward(_channels_last(dy), _channels_last(x), w, stride, padding, dilation, groups,
-                        [True, True, True])
-    assert _is_channels_last(g_cl[0])
+    g_cl = backward(_channels_last(dy), _channels_last(x), w, *geometry, [True, True, True])
+    assert expect(g_cl[0]) and g_cl[1].is_contiguous()
     for got, want in zip(g_cl, g):
         assert torch.equal(got, want)
     from torch._subclasses.fake_tensor import FakeTensorMode
@@ -191,10 +198,28 @@ def test_channels_last_outputs_follow_the_input_layout():
     mode = FakeTensorMode()
     fx, fw, fdy = mode.from_tensor(x_cl), mode.from_tensor(w), mode.from_tensor(dy_cl)
     with mode:
-        fy = _op_forward(fx, fw, None, stride, padding, dilation, groups)
-        fg = _op_backward(fdy, fx, fw, stride, padding, dilation, groups, [True, False, False])
+        fy = forward(fx, fw, None, *geometry)
+        fg = backward(fdy, fx, fw, *geometry, [True, False, False])
     assert fy.shape == y.shape and fy.stride() == y_cl.stride()
     assert fg[0].stride() == g_cl[0].stride()
+
+
+def test_memory_format_keyword():
+    """conv_nd(memory_format=...) selects the contract; other formats are rejected."""
+    from torch_convnd import conv_nd
+
+    xs, ws, stride, padding, dilation, groups, bias = CASES["r4_strided_dilated"]
+    x, w, b = helpers.seeded_problem(xs, ws, bias, torch.float64, seed=5)
+    x_cl = _channels_last(x)
+    for backend in ("native", "torch"):
+        y = conv_nd(x, w, b, stride, padding, dilation, groups, backend=backend)
+        kept = conv_nd(x_cl, w, b, stride, padding, dilation, groups, backend=backend,
+                       memory_format=torch.preserve_format)
+        assert _is_channels_last(kept) and torch.allclose(kept, y, rtol=1e-12, atol=1e-12)
+    y_default = conv_nd(x_cl, w, b, stride, padding, dilation, groups, backend="native")
+    assert y_default.is_contiguous()
+    with pytest.raises(ValueError, match="memory_format"):
+        conv_nd(x, w, b, stride, padding, dilation, groups, memory_format=torch.channels_last)
 
 
 def test_direct_call_matches_the_general_path(monkeypatch):

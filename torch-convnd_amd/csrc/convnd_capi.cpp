@@ -1517,15 +1517,22 @@ BackwardSetup setup_backward(const Geom& g, convnd_hip_dtype dt, bool gi, bool g
 // Geometry tables of a plan in device memory, one copy per (plan, device), shared by every
 // call with that plan (never written again, so calls on any stream may read them).
 //   * Fill: the host-built bytes go to a pinned host buffer and from there to the device with
-//     hipMemcpyAsync on the calling stream, so no call synchronises the host; an event
-//     recorded after the copy orders calls on other streams behind it until it has completed.
+//     hipMemcpyAsync on a per-device upload stream (non-blocking, so it is not ordered behind
+//     the caller's queued kernels), and the host waits for that copy alone before the entry is
+//     published. The tables are therefore complete before any kernel that reads them is
+//     enqueued, on any stream, and no later call queries or waits for anything. Only the first
+//     call of a geometry waits, for the copy of a few tens of KB.
 //   * Bounds: at most kTableEntries entries and kTableBytes bytes per process; the least
 //     recently used entry is dropped when a new one would exceed either. An entry's memory is
 //     released with its last holder (calls hold their entry until their kernels are enqueued;
-//     hipFree / hipHostFree wait for queued work that may still read it).
+//     hipFree waits for queued work that may still read it).
 //   * Graph capture: a miss while the calling stream captures is an error (the copy would only
 //     run when the graph is launched); the first call of a geometry runs outside capture, as
-//     torch.cuda.graph's warm-up does.
+//     torch.cuda.graph's warm-up does. A hit while the stream captures pins the entry: a
+//     captured graph keeps the tables' device address in its kernel arguments, so a pinned
+//     entry is never evicted (it stays until the process ends, outside both bounds).
+//   * Evicted entries are released after the cache lock is dropped (hipFree synchronises the
+//     device).
 constexpr size_t kTableEntries = 128;
 constexpr size_t kTableBytes = size_t{256} << 20;
 
@@ -1533,12 +1540,9 @@ struct DeviceTables {
   void* dev = nullptr;
   void* host = nullptr;
   size_t bytes = 0;
-  hipEvent_t ready = nullptr;
-  hipStream_t filled_on = nullptr;
-  bool done = false;
+  bool pinned = false;  // read by a captured graph: never evicted
   uint64_t last_use = 0;
   ~DeviceTables() {
-    if (ready != nullptr) (void)hipEventDestroy(ready);
     if (dev != nullptr) (void)hipFree(dev);
     if (host != nullptr) (void)hipHostFree(host);
   }
@@ -1548,8 +1552,10 @@ using TablesRef = std::shared_ptr<DeviceTables>;
 struct TableCache {
   std::mutex lock;
   std::unordered_map<std::string, TablesRef> map;
-  size_t bytes = 0;
+  size_t bytes = 0;           // of the unpinned entries
+  size_t pinned_entries = 0;
   uint64_t clock = 0;
+  std::map<int, hipStream_t> upload;  // per device, created on first use, kept until exit
 };
 
 // Never destroyed: entries alive at exit are left to process teardown rather than freed after
@@ -1567,56 +1573,64 @@ TablesRef device_tables(const std::string& key, size_t bytes, hipStream_t stream
     return nullptr;
   }
   const std::string k = key + std::string(reinterpret_cast<const char*>(&dev), sizeof(dev));
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+    fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: hipStreamIsCapturing failed");
+    return nullptr;
+  }
+  const bool capturing = capture != hipStreamCaptureStatusNone;
   TableCache& c = table_cache();
+  std::vector<TablesRef> evicted;  // released after the lock (declared first: destroyed last)
   std::lock_guard<std::mutex> guard(c.lock);
   auto it = c.map.find(k);
   if (it != c.map.end()) {
     DeviceTables& e = *it->second;
     e.last_use = ++c.clock;
-    if (!e.done && stream != e.filled_on) {
-      const hipError_t q = hipEventQuery(e.ready);
-      if (q == hipErrorNotReady) (void)hipGetLastError();  // not an error: clear the record
-      if (q == hipSuccess) {
-        e.done = true;
-      } else if (q != hipErrorNotReady || hipStreamWaitEvent(stream, e.ready, 0) != hipSuccess) {
-        fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: waiting for their upload failed");
-        return nullptr;
-      }
+    if (capturing && !e.pinned) {
+      e.pinned = true;
+      c.bytes -= e.bytes;  // pinned entries are outside the bounds
+      c.pinned_entries += 1;
     }
     return it->second;
   }
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &capture) != hipSuccess ||
-      capture != hipStreamCaptureStatusNone) {
+  if (capturing) {
     fail(CONVND_HIP_UNSUPPORTED,
          "the first call of a convolution geometry cannot be captured into a graph; run it "
          "once outside capture first");
     return nullptr;
   }
-  // Drop least recently used entries until the new one fits both bounds.
-  while (!c.map.empty() && (c.map.size() >= kTableEntries || c.bytes + bytes > kTableBytes)) {
-    auto victim = c.map.begin();
+  // Drop least recently used unpinned entries until the new one fits both bounds.
+  while (c.map.size() - c.pinned_entries >= kTableEntries || c.bytes + bytes > kTableBytes) {
+    auto victim = c.map.end();
     for (auto j = c.map.begin(); j != c.map.end(); ++j)
-      if (j->second->last_use < victim->second->last_use) victim = j;
+      if (!j->second->pinned &&
+          (victim == c.map.end() || j->second->last_use < victim->second->last_use))
+        victim = j;
+    if (victim == c.map.end()) break;
     c.bytes -= victim->second->bytes;
+    evicted.push_back(std::move(victim->second));
     c.map.erase(victim);
+  }
+  hipStream_t& upload = c.upload[dev];
+  if (upload == nullptr && hipStreamCreateWithFlags(&upload, hipStreamNonBlocking) != hipSuccess) {
+    upload = nullptr;
+    fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: creating the upload stream failed");
+    return nullptr;
   }
   auto e = std::make_shared<DeviceTables>();
   e->bytes = bytes;
   if (hipHostMalloc(&e->host, bytes, hipHostMallocDefault) != hipSuccess ||
-      hipMalloc(&e->dev, bytes) != hipSuccess ||
-      hipEventCreateWithFlags(&e->ready, hipEventDisableTiming) != hipSuccess) {
+      hipMalloc(&e->dev, bytes) != hipSuccess) {
     fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: device allocation failed");
     return nullptr;
   }
   std::memset(e->host, 0, bytes);
   build(static_cast<unsigned char*>(e->host));
-  if (hipMemcpyAsync(e->dev, e->host, bytes, hipMemcpyHostToDevice, stream) != hipSuccess ||
-      hipEventRecord(e->ready, stream) != hipSuccess) {
+  if (hipMemcpyAsync(e->dev, e->host, bytes, hipMemcpyHostToDevice, upload) != hipSuccess ||
+      hipStreamSynchronize(upload) != hipSuccess) {
     fail(CONVND_HIP_LAUNCH_FAILED, "geometry tables: upload failed");
     return nullptr;
   }
-  e->filled_on = stream;
   e->last_use = ++c.clock;
   c.bytes += bytes;
   c.map.emplace(k, e);
@@ -1696,7 +1710,7 @@ int prepare(const convnd_hip_problem* problem, convnd_hip_dtype dtype, Geom* g) 
 int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, const void* input,
                 const void* weight, const void* bias, void* output, int activation, char* ws,
                 const void* tables, void* tables_at, bool timed, hipStream_t stream,
-                bool channels_last = false) {
+                bool in_cl = false, bool out_cl = false) {
   int st;
   if (f.tiny.ok) {
     TinyArgs T = f.tiny.args;
@@ -1748,9 +1762,10 @@ int run_forward(const Geom& g, convnd_hip_dtype dtype, const ForwardSetup& f, co
   A.bias = bias;
   A.out = output;
   A.act = activation;
-  // Channels-last (only with direct staging, see forward_reads_cl): stage the halo from
-  // [N][in...][C] and store [N][out...][Co].
-  A.in_cl = A.out_cl = channels_last ? 1 : 0;
+  // Channels-last (only with direct staging, see forward_reads_cl): in_cl stages the halo
+  // from [N][in...][C], out_cl stores [N][out...][Co].
+  A.in_cl = in_cl ? 1 : 0;
+  A.out_cl = out_cl ? 1 : 0;
   const auto ev = timed ? timing_begin(0, stream) : std::pair<hipEvent_t, hipEvent_t>{};
   st = hip_check(launch_igemm(dtype, f.ig.mb, f.ig.nb, A, f.ig.lds, stream),
                  "implicit GEMM forward");
@@ -2031,6 +2046,13 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
   return CONVND_HIP_SUCCESS;
 }
 
+bool valid_layout(int layout) {
+  return layout == CONVND_HIP_CHANNELS_FIRST || layout == CONVND_HIP_CHANNELS_LAST ||
+         layout == CONVND_HIP_CHANNELS_LAST_INPUT;
+}
+constexpr const char* kLayoutError =
+    "layout must be channels_first, channels_last or channels_last_input";
+
 }  // namespace
 }  // namespace convnd
 
@@ -2172,8 +2194,11 @@ size_t convnd_hip_forward_workspace_size_layout(const convnd_hip_problem* proble
   Geom g;
   if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
   const ForwardSetup f = setup_forward(g, dtype);
-  if (layout != CONVND_HIP_CHANNELS_LAST) return f.bytes;
-  return align_up(f.bytes) + cl_forward_extra(g, dtype, f);
+  if (layout == CONVND_HIP_CHANNELS_LAST)
+    return align_up(f.bytes) + cl_forward_extra(g, dtype, f);
+  if (layout == CONVND_HIP_CHANNELS_LAST_INPUT && !forward_reads_cl(f))
+    return align_up(f.bytes) + tensor_bytes(g.batch, g.channels, g.in_vol, dtype);
+  return f.bytes;
 }
 
 size_t convnd_hip_backward_workspace_size_layout(const convnd_hip_problem* problem,
@@ -2184,16 +2209,19 @@ size_t convnd_hip_backward_workspace_size_layout(const convnd_hip_problem* probl
   if (prepare(problem, dtype, &g) != CONVND_HIP_SUCCESS) return 0;
   const bool gi = need_grad_input != 0, gw = need_grad_weight != 0, gb = need_grad_bias != 0;
   const BackwardSetup b = setup_backward(g, dtype, gi, gw, gb);
-  if (layout != CONVND_HIP_CHANNELS_LAST) return b.bytes;
-  return cl_backward_plan(g, dtype, b, gi, gw, gb).bytes;
+  if (layout == CONVND_HIP_CHANNELS_LAST) return cl_backward_plan(g, dtype, b, gi, gw, gb).bytes;
+  // Channels-last input only: the weight gradient, the one consumer of the input, reads a
+  // channels-first copy of it.
+  if (layout == CONVND_HIP_CHANNELS_LAST_INPUT && gw)
+    return align_up(b.bytes) + tensor_bytes(g.batch, g.channels, g.in_vol, dtype);
+  return b.bytes;
 }
 
 int convnd_hip_forward_layout(const convnd_hip_problem* problem, convnd_hip_dtype dtype,
                               int layout, int activation, const void* input, const void* weight,
                               const void* bias, void* output, void* workspace,
                               size_t workspace_size, void* stream_ptr) {
-  if (layout != CONVND_HIP_CHANNELS_FIRST && layout != CONVND_HIP_CHANNELS_LAST)
-    return fail(CONVND_HIP_INVALID_ARGUMENT, "layout must be channels_first or channels_last");
+  if (!valid_layout(layout)) return fail(CONVND_HIP_INVALID_ARGUMENT, kLayoutError);
   if (layout == CONVND_HIP_CHANNELS_FIRST)
     return convnd_hip_forward_act(problem, dtype, input, weight, bias, output, activation,
                                   workspace, workspace_size, stream_ptr);
@@ -2205,7 +2233,7 @@ int convnd_hip_forward_layout(const convnd_hip_problem* problem, convnd_hip_dtyp
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   if (g.batch == 0) return CONVND_HIP_SUCCESS;
   const ForwardSetup f = setup_forward(g, dtype);
-  const size_t need = align_up(f.bytes) + cl_forward_extra(g, dtype, f);
+  const size_t need = convnd_hip_forward_workspace_size_layout(problem, dtype, layout);
   if (workspace_size < need || (need > 0 && workspace == nullptr))
     return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
                 "device workspace is smaller than convnd_hip_forward_workspace_size_layout");
@@ -2216,12 +2244,21 @@ int convnd_hip_forward_layout(const convnd_hip_problem* problem, convnd_hip_dtyp
   }
   char* ws = static_cast<char*>(workspace);
   const void* tab = tables ? tables->dev : nullptr;
+  const bool out_cl = layout == CONVND_HIP_CHANNELS_LAST;
   if (forward_reads_cl(f))
     return run_forward(g, dtype, f, input, weight, bias, output, activation, ws, tab, nullptr,
-                       true, stream, true);
-  // Channels-first copies: x [N][in][C] -> [N][C][in], then y [N][Co][out] -> [N][out][Co].
+                       true, stream, true, out_cl);
+  // Channels-first copies: x [N][in][C] -> [N][C][in], then (channels-last output only)
+  // y [N][Co][out] -> [N][out][Co].
   const int64_t es = element_size(dtype);
   char* x_cf = ws + align_up(f.bytes);
+  if (!out_cl) {
+    st = hip_check(launch_transpose(es, g.batch, g.in_vol, g.channels, input, x_cf, stream),
+                   "channels-last input copy");
+    if (st != CONVND_HIP_SUCCESS) return st;
+    return run_forward(g, dtype, f, x_cf, weight, bias, output, activation, ws, tab, nullptr,
+                       true, stream);
+  }
   char* y_cf = x_cf + tensor_bytes(g.batch, g.channels, g.in_vol, dtype);
   st = hip_check(launch_transpose(es, g.batch, g.in_vol, g.channels, input, x_cf, stream),
                  "channels-last input copy");
@@ -2238,8 +2275,7 @@ int convnd_hip_backward_layout(const convnd_hip_problem* problem, convnd_hip_dty
                                const void* weight, void* grad_input, void* grad_weight,
                                void* grad_bias, void* workspace, size_t workspace_size,
                                void* stream_ptr) {
-  if (layout != CONVND_HIP_CHANNELS_FIRST && layout != CONVND_HIP_CHANNELS_LAST)
-    return fail(CONVND_HIP_INVALID_ARGUMENT, "layout must be channels_first or channels_last");
+  if (!valid_layout(layout)) return fail(CONVND_HIP_INVALID_ARGUMENT, kLayoutError);
   if (layout == CONVND_HIP_CHANNELS_FIRST)
     return convnd_hip_backward(problem, dtype, grad_output, input, weight, grad_input,
                                grad_weight, grad_bias, workspace, workspace_size, stream_ptr);
@@ -2250,8 +2286,8 @@ int convnd_hip_backward_layout(const convnd_hip_problem* problem, convnd_hip_dty
   const bool gi = grad_input != nullptr, gw = grad_weight != nullptr,
              gb = grad_bias != nullptr;
   const BackwardSetup b = setup_backward(g, dtype, gi, gw, gb);
-  const ClBackward c = cl_backward_plan(g, dtype, b, gi, gw, gb);
-  if (workspace_size < c.bytes || (c.bytes > 0 && workspace == nullptr))
+  const size_t need = convnd_hip_backward_workspace_size_layout(problem, dtype, layout, gi, gw, gb);
+  if (workspace_size < need || (need > 0 && workspace == nullptr))
     return fail(CONVND_HIP_WORKSPACE_TOO_SMALL,
                 "device workspace is smaller than convnd_hip_backward_workspace_size_layout");
   char* ws = static_cast<char*>(workspace);
@@ -2259,6 +2295,21 @@ int convnd_hip_backward_layout(const convnd_hip_problem* problem, convnd_hip_dty
     return run_backward(g, dtype, b, grad_output, input, weight, grad_input, grad_weight,
                         grad_bias, ws, stream);
   const int64_t es = element_size(dtype);
+  if (layout == CONVND_HIP_CHANNELS_LAST_INPUT) {
+    // grad_output and grad_input are channels-first: the channels-first backward, with the
+    // weight gradient reading a channels-first copy of the input.
+    const void* x = input;
+    if (gw) {
+      char* x_cf = ws + align_up(b.bytes);
+      st = hip_check(launch_transpose(es, g.batch, g.in_vol, g.channels, input, x_cf, stream),
+                     "channels-last input copy");
+      if (st != CONVND_HIP_SUCCESS) return st;
+      x = x_cf;
+    }
+    return run_backward(g, dtype, b, grad_output, x, weight, grad_input, grad_weight, grad_bias,
+                        ws, stream);
+  }
+  const ClBackward c = cl_backward_plan(g, dtype, b, gi, gw, gb);
   const void* dy = grad_output;
   const void* x = input;
   if (c.dy_cf) {

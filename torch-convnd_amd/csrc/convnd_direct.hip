@@ -16,6 +16,11 @@
 namespace convnd {
 namespace {
 
+// The direct kernels take DirectGeom by value next to four pointers; with the runtime's hidden
+// arguments (256 bytes) that must stay inside the 4 KiB kernel-argument segment.
+static_assert(sizeof(DirectGeom) + 4 * sizeof(void*) + 256 <= 4096,
+              "direct kernel arguments exceed the kernel-argument segment");
+
 // Valid tap range [lo, hi] along one axis for an output coordinate whose receptive field
 // starts at input coordinate `base`: 0 <= base + t*d < in and 0 <= t < k.
 __device__ __forceinline__ void tap_range(int64_t base, int64_t d, int64_t in, int64_t k,

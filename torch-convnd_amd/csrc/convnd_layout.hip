@@ -16,6 +16,7 @@
 // Every reduction has a fixed summation order, so results are bitwise repeatable.
 
 #include "convnd_internal.h"
+#include <algorithm>
 #include <cstring>
 #include <type_traits>
 
@@ -268,29 +269,51 @@ __global__ __launch_bounds__(kThreads) void reduce_partials4_kernel(const float*
 // dst[n][b][a] = src[n][a][b] for each of `batch` matrices of rows x cols = a x b, through a
 // 64 x 64 LDS tile (one element column of padding keeps the transposed reads off one bank).
 // Channels-last to channels-first: a = positions, b = channels; the reverse swaps them.
+// Tiles are numbered t = (n * tiles_b + tile_b) * tiles_a + tile_a and handed out with a
+// grid-stride loop, so any batch and matrix size fits a one-dimensional grid.
 // Element type E: 2, 4 or 8 bytes, moved as raw bits.
+struct TransposeTiles {
+  int64_t a, b, tiles_a, tiles_b, total;
+};
+// Blocks of one transpose launch (each loops over tiles): enough to fill the GPU many times.
+constexpr int64_t kTransposeMaxBlocks = int64_t{1} << 16;
+
+__device__ inline void transpose_tile_origin(const TransposeTiles& T, int64_t t, int64_t* n,
+                                             int64_t* a0, int64_t* b0) {
+  const int64_t rest = t / T.tiles_a;
+  *a0 = (t - rest * T.tiles_a) * 64;
+  *n = rest / T.tiles_b;
+  *b0 = (rest - *n * T.tiles_b) * 64;
+}
+
 template <typename E>
 __global__ __launch_bounds__(kThreads) void transpose_kernel(const E* __restrict__ src,
-                                                             E* __restrict__ dst, int64_t a,
-                                                             int64_t b) {
+                                                             E* __restrict__ dst,
+                                                             TransposeTiles T) {
   __shared__ E tile[64][65];
-  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int64_t a = T.a, b = T.b;
   const size_t mat = static_cast<size_t>(a) * static_cast<size_t>(b);
-  const E* s = src + blockIdx.z * mat;
-  E* d = dst + blockIdx.z * mat;
   const int tx = threadIdx.x & 63;
   const int ty = threadIdx.x >> 6;  // 0..3
+  for (int64_t t = blockIdx.x; t < T.total; t += gridDim.x) {
+    int64_t n, a0, b0;
+    transpose_tile_origin(T, t, &n, &a0, &b0);
+    const E* s = src + n * mat;
+    E* d = dst + n * mat;
 #pragma unroll
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t ra = a0 + r, cb = b0 + tx;
-    if (ra < a && cb < b) tile[r][tx] = s[ra * b + cb];
-  }
-  __syncthreads();
+    for (int i = 0; i < 16; ++i) {
+      const int r = ty + 4 * i;
+      const int64_t ra = a0 + r, cb = b0 + tx;
+      if (ra < a && cb < b) tile[r][tx] = s[ra * b + cb];
+    }
+    __syncthreads();
 #pragma unroll
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t rb = b0 + r, ca = a0 + tx;
-    if (rb < b && ca < a) d[rb * a + ca] = tile[tx][r];
+    for (int i = 0; i < 16; ++i) {
+      const int r = ty + 4 * i;
+      const int64_t rb = b0 + r, ca = a0 + tx;
+      if (rb < b && ca < a) d[rb * a + ca] = tile[tx][r];
+    }
+    __syncthreads();  // the next tile overwrites the LDS tile
   }
 }
 
@@ -298,41 +321,45 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const E* __restrict
 // aligned: 16-byte loads of 8 consecutive b elements and 16-byte stores of 8 consecutive a
 // elements (gathered from the tile's column), two of each per thread.
 __global__ __launch_bounds__(kThreads) void transpose16_kernel(const uint4* __restrict__ src,
-                                                               uint4* __restrict__ dst, int64_t a,
-                                                               int64_t b) {
+                                                               uint4* __restrict__ dst,
+                                                               TransposeTiles T) {
   constexpr int kPitch = 64 + 8;  // elements per tile row
   __shared__ __align__(16) unsigned short tile[64 * kPitch];
-  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int64_t a = T.a, b = T.b;
   const size_t mat = static_cast<size_t>(a) * static_cast<size_t>(b);
-  const unsigned short* s = reinterpret_cast<const unsigned short*>(src) + blockIdx.z * mat;
-  unsigned short* d = reinterpret_cast<unsigned short*>(dst) + blockIdx.z * mat;
+  for (int64_t t = blockIdx.x; t < T.total; t += gridDim.x) {
+    int64_t n, a0, b0;
+    transpose_tile_origin(T, t, &n, &a0, &b0);
+    const unsigned short* s = reinterpret_cast<const unsigned short*>(src) + n * mat;
+    unsigned short* d = reinterpret_cast<unsigned short*>(dst) + n * mat;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int chunk = threadIdx.x + k * kThreads;  // 64 rows x 8 chunks of 8
-    const int r = chunk >> 3, c = (chunk & 7) * 8;
-    const int64_t ra = a0 + r, cb = b0 + c;
-    if (ra < a && cb < b)
-      *reinterpret_cast<uint4*>(&tile[r * kPitch + c]) =
-          *reinterpret_cast<const uint4*>(s + ra * b + cb);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int chunk = threadIdx.x + k * kThreads;  // 64 b-rows x 8 chunks of 8 a elements
-    const int r = chunk >> 3, c = (chunk & 7) * 8;
-    const int64_t rb = b0 + r, ca = a0 + c;
-    if (rb < b && ca < a) {
-      unsigned short e[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = tile[(c + i) * kPitch + r];
-      uint4 v;
-      v.x = e[0] | (static_cast<unsigned>(e[1]) << 16);
-      v.y = e[2] | (static_cast<unsigned>(e[3]) << 16);
-      v.z = e[4] | (static_cast<unsigned>(e[5]) << 16);
-      v.w = e[6] | (static_cast<unsigned>(e[7]) << 16);
-      *reinterpret_cast<uint4*>(d + rb * a + ca) = v;
+    for (int k = 0; k < 2; ++k) {
+      const int chunk = threadIdx.x + k * kThreads;  // 64 rows x 8 chunks of 8
+      const int r = chunk >> 3, c = (chunk & 7) * 8;
+      const int64_t ra = a0 + r, cb = b0 + c;
+      if (ra < a && cb < b)
+        *reinterpret_cast<uint4*>(&tile[r * kPitch + c]) =
+            *reinterpret_cast<const uint4*>(s + ra * b + cb);
     }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int chunk = threadIdx.x + k * kThreads;  // 64 b-rows x 8 chunks of 8 a elements
+      const int r = chunk >> 3, c = (chunk & 7) * 8;
+      const int64_t rb = b0 + r, ca = a0 + c;
+      if (rb < b && ca < a) {
+        unsigned short e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = tile[(c + i) * kPitch + r];
+        uint4 v;
+        v.x = e[0] | (static_cast<unsigned>(e[1]) << 16);
+        v.y = e[2] | (static_cast<unsigned>(e[3]) << 16);
+        v.z = e[4] | (static_cast<unsigned>(e[5]) << 16);
+        v.w = e[6] | (static_cast<unsigned>(e[7]) << 16);
+        *reinterpret_cast<uint4*>(d + rb * a + ca) = v;
+      }
+    }
+    __syncthreads();  // the next tile overwrites the LDS tile
   }
 }
 
@@ -341,30 +368,33 @@ __global__ __launch_bounds__(kThreads) void transpose16_kernel(const uint4* __re
 hipError_t launch_transpose(int64_t element_size, int64_t batch, int64_t a, int64_t b,
                             const void* src, void* dst, hipStream_t stream) {
   if (batch == 0 || a == 0 || b == 0) return hipSuccess;
-  if ((a + 63) / 64 > 0x7fffffff || (b + 63) / 64 > 65535 || batch > 65535)
-    return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>((a + 63) / 64), static_cast<unsigned>((b + 63) / 64),
-                  static_cast<unsigned>(batch));
+  TransposeTiles T;
+  T.a = a;
+  T.b = b;
+  T.tiles_a = (a + 63) / 64;
+  T.tiles_b = (b + 63) / 64;
+  T.total = batch * T.tiles_a * T.tiles_b;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(T.total, kTransposeMaxBlocks)));
   if (element_size == 2 && a % 8 == 0 && b % 8 == 0 &&
       reinterpret_cast<uintptr_t>(src) % 16 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
     hipLaunchKernelGGL(transpose16_kernel, grid, dim3(kThreads), 0, stream,
-                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), a, b);
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), T);
     return hipGetLastError();
   }
   switch (element_size) {
     case 2:
       hipLaunchKernelGGL((transpose_kernel<unsigned short>), grid, dim3(kThreads), 0, stream,
                          static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst),
-                         a, b);
+                         T);
       break;
     case 4:
       hipLaunchKernelGGL((transpose_kernel<unsigned>), grid, dim3(kThreads), 0, stream,
-                         static_cast<const unsigned*>(src), static_cast<unsigned*>(dst), a, b);
+                         static_cast<const unsigned*>(src), static_cast<unsigned*>(dst), T);
       break;
     case 8:
       hipLaunchKernelGGL((transpose_kernel<unsigned long long>), grid, dim3(kThreads), 0, stream,
                          static_cast<const unsigned long long*>(src),
-                         static_cast<unsigned long long*>(dst), a, b);
+                         static_cast<unsigned long long*>(dst), T);
       break;
     default:
       return hipErrorInvalidValue;

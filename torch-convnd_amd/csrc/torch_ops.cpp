@@ -142,23 +142,30 @@ void* current_stream(const at::Tensor& tensor) {
   return static_cast<void*>(c10::hip::getCurrentHIPStream(tensor.device().index()).stream());
 }
 
-// The forward on the device in the input's layout: a channels-last input gives a
-// channels-last output with no layout copy on the implicit-GEMM path
-// (convnd_hip_forward_layout); otherwise operands are made contiguous as in the reference
-// (src/torch_convnd/csrc/convnd.cpp:317-319).
+// Activation layouts of a device call. The reference operators return contiguous outputs
+// and gradients whatever the input's layout (src/torch_convnd/csrc/convnd.cpp:317-320,
+// 377-386; fake functions src/torch_convnd/_autograd.py:8-26): a channels-last input is read
+// as such (CHANNELS_LAST_INPUT, no copy on the implicit-GEMM path) and the results are
+// channels-first. The layout-following operators (conv_nd_preserve, an extension) return a
+// channels-last output and grad_input for a channels-last input (CHANNELS_LAST).
+int device_layout(const at::Tensor& input, bool follow_layout) {
+  if (!is_channels_last(input)) return CONVND_HIP_CHANNELS_FIRST;
+  return follow_layout ? CONVND_HIP_CHANNELS_LAST : CONVND_HIP_CHANNELS_LAST_INPUT;
+}
+
 at::Tensor forward_device(const convnd_hip_problem& problem, const at::Tensor& input,
                           const at::Tensor& weight, const std::optional<at::Tensor>& bias,
-                          const std::vector<int64_t>& shape, int act) {
+                          const std::vector<int64_t>& shape, int act, bool follow_layout) {
   const c10::OptionalDeviceGuard guard(input.device());
-  const bool cl = is_channels_last(input);
-  auto output = cl ? empty_channels_last(shape, input.options()) : at::empty(shape, input.options());
+  const int layout = device_layout(input, follow_layout);
+  auto output = layout == CONVND_HIP_CHANNELS_LAST ? empty_channels_last(shape, input.options())
+                                                   : at::empty(shape, input.options());
   if (problem.batch == 0) return output;
-  const auto x = cl ? input : input.contiguous();
+  const auto x = layout == CONVND_HIP_CHANNELS_FIRST ? input.contiguous() : input;
   const auto w = weight.contiguous();
   std::optional<at::Tensor> b;
   if (bias.has_value()) b = bias->contiguous();
   const auto dtype = to_dtype(input.scalar_type());
-  const int layout = cl ? CONVND_HIP_CHANNELS_LAST : CONVND_HIP_CHANNELS_FIRST;
   const size_t ws_bytes = convnd_hip_forward_workspace_size_layout(&problem, dtype, layout);
   auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
   raise_status(convnd_hip_forward_layout(&problem, dtype, layout, act, x.const_data_ptr(),
@@ -170,23 +177,28 @@ at::Tensor forward_device(const convnd_hip_problem& problem, const at::Tensor& i
   return output;
 }
 
+void check_bias(const std::optional<at::Tensor>& bias, const convnd_hip_problem& problem,
+                const at::Tensor& input) {
+  if (!bias.has_value()) return;
+  TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
+                  bias->size(0) == problem.output_channels && bias->device() == input.device() &&
+                  bias->scalar_type() == input.scalar_type(),
+              "bias must match output channels, device and dtype");
+}
+
+template <bool kFollowLayout>
 at::Tensor conv_nd_device(const at::Tensor& input, const at::Tensor& weight,
                           const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
                           at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                           int64_t workspace_bytes) {
   const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
-  if (bias.has_value()) {
-    TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
-                    bias->size(0) == problem.output_channels &&
-                    bias->device() == input.device() &&
-                    bias->scalar_type() == input.scalar_type(),
-                "bias must match output channels, device and dtype");
-  }
+  check_bias(bias, problem, input);
   const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
-  return forward_device(problem, input, weight, bias, shape, CONVND_HIP_ACT_NONE);
+  return forward_device(problem, input, weight, bias, shape, CONVND_HIP_ACT_NONE, kFollowLayout);
 }
 
+template <bool kFollowLayout>
 Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& input,
                               const at::Tensor& weight, at::IntArrayRef stride,
                               at::IntArrayRef padding, at::IntArrayRef dilation,
@@ -202,9 +214,10 @@ Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& i
   // with four-byte elements (src/torch_convnd/csrc/convnd.cpp:361).
   check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
   const c10::OptionalDeviceGuard guard(input.device());
-  // A channels-last input gets a channels-last grad_input, computed from a channels-last
-  // grad_output (converted when it comes in another layout).
-  const bool cl = is_channels_last(input);
+  // With the layout-following operator a channels-last input gets a channels-last grad_input,
+  // computed from a channels-last grad_output (converted when it comes in another layout).
+  const int layout = device_layout(input, kFollowLayout);
+  const bool cl = layout == CONVND_HIP_CHANNELS_LAST;
   std::optional<at::Tensor> grad_input, grad_weight, grad_bias;
   if (problem.batch == 0) {
     if (output_mask[0])
@@ -221,10 +234,9 @@ Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& i
   if (output_mask[2]) grad_bias = at::empty({problem.output_channels}, input.options());
   if (!output_mask[0] && !output_mask[1] && !output_mask[2]) return {};
   const auto dy = cl ? to_channels_last(grad_output) : grad_output.contiguous();
-  const auto x = cl ? input : input.contiguous();
+  const auto x = layout == CONVND_HIP_CHANNELS_FIRST ? input.contiguous() : input;
   const auto w = weight.contiguous();
   const auto dtype = to_dtype(input.scalar_type());
-  const int layout = cl ? CONVND_HIP_CHANNELS_LAST : CONVND_HIP_CHANNELS_FIRST;
   const size_t ws_bytes = convnd_hip_backward_workspace_size_layout(
       &problem, dtype, layout, output_mask[0], output_mask[1], output_mask[2]);
   auto workspace = at::empty({static_cast<int64_t>(ws_bytes)}, input.options().dtype(at::kByte));
@@ -240,26 +252,22 @@ Grads conv_nd_backward_device(const at::Tensor& grad_output, const at::Tensor& i
 // CPU tensors: the same validation as the device path, then the tap-major CPU kernels
 // (convnd_cpu.cpp), as the reference registers its CPU implementation beside the CUDA one
 // (src/torch_convnd/csrc/convnd.cpp:179-415).
+template <bool kFollowLayout>
 at::Tensor conv_nd_cpu(const at::Tensor& input, const at::Tensor& weight,
                        const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
                        at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                        int64_t workspace_bytes) {
   const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
-  if (bias.has_value()) {
-    TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
-                    bias->size(0) == problem.output_channels &&
-                    bias->device() == input.device() &&
-                    bias->scalar_type() == input.scalar_type(),
-                "bias must match output channels, device and dtype");
-  }
+  check_bias(bias, problem, input);
   const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
   auto y = torch_convnd_cpu::forward(input, weight, bias, shape, stride, padding, dilation,
                                      groups);
-  // Outputs follow the input's layout, as on the device.
-  return is_channels_last(input) ? to_channels_last(y) : y;
+  // Contiguous, as the reference's; the layout-following operator matches the input's layout.
+  return kFollowLayout && is_channels_last(input) ? to_channels_last(y) : y;
 }
 
+template <bool kFollowLayout>
 Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& input,
                            const at::Tensor& weight, at::IntArrayRef stride,
                            at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
@@ -273,7 +281,7 @@ Grads conv_nd_backward_cpu(const at::Tensor& grad_output, const at::Tensor& inpu
   check_workspace(problem, std::max<int64_t>(input.element_size(), 4), workspace_bytes);
   auto grads = torch_convnd_cpu::backward(grad_output, input, weight, stride, padding, dilation,
                                           groups, output_mask);
-  if (is_channels_last(input) && std::get<0>(grads).has_value())
+  if (kFollowLayout && is_channels_last(input) && std::get<0>(grads).has_value())
     std::get<0>(grads) = to_channels_last(*std::get<0>(grads));
   return grads;
 }
@@ -295,16 +303,10 @@ at::Tensor conv_nd_act_device(const at::Tensor& input, const at::Tensor& weight,
                               int64_t workspace_bytes, c10::string_view activation) {
   const int act = activation_code(activation);
   const auto problem = make_problem(input, weight, stride, padding, dilation, groups);
-  if (bias.has_value()) {
-    TORCH_CHECK(bias->layout() == at::kStrided && bias->dim() == 1 &&
-                    bias->size(0) == problem.output_channels &&
-                    bias->device() == input.device() &&
-                    bias->scalar_type() == input.scalar_type(),
-                "bias must match output channels, device and dtype");
-  }
+  check_bias(bias, problem, input);
   const auto shape = output_shape(problem, input);
   check_workspace(problem, input.element_size(), workspace_bytes);
-  return forward_device(problem, input, weight, bias, shape, act);
+  return forward_device(problem, input, weight, bias, shape, act, false);
 }
 
 at::Tensor conv_nd_act_cpu(const at::Tensor& input, const at::Tensor& weight,
@@ -312,7 +314,8 @@ at::Tensor conv_nd_act_cpu(const at::Tensor& input, const at::Tensor& weight,
                            at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                            int64_t workspace_bytes, c10::string_view activation) {
   const int act = activation_code(activation);
-  auto y = conv_nd_cpu(input, weight, bias, stride, padding, dilation, groups, workspace_bytes);
+  auto y = conv_nd_cpu<false>(input, weight, bias, stride, padding, dilation, groups,
+                             workspace_bytes);
   if (act == CONVND_HIP_ACT_NONE) return y;
   const auto ct = input.scalar_type() == at::kDouble ? at::kDouble : at::kFloat;
   auto v = y.to(ct);
@@ -421,7 +424,7 @@ at::Tensor conv_nd_autocast(const at::Tensor& input, const at::Tensor& weight,
   const auto dtype = at::autocast::get_autocast_dtype(kDevice);
   static const auto op = c10::Dispatcher::singleton()
                              .findSchemaOrThrow("torch_convnd::conv_nd", "")
-                             .typed<decltype(conv_nd_device)>();
+                             .typed<decltype(conv_nd_device<false>)>();
   const auto cast = [&](const at::Tensor& t) {
     return at::autocast::cached_cast(dtype, t, kDevice);
   };
@@ -444,9 +447,15 @@ using torch::autograd::variable_list;
 using ConvFn = at::Tensor(const at::Tensor&, const at::Tensor&, const std::optional<at::Tensor>&,
                           at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, int64_t);
 
+// kFollowLayout selects the layout-following operator pair (conv_nd_preserve,
+// conv_nd_backward_preserve); their derivatives are the same formulas.
+template <bool kFollowLayout>
 const c10::TypedOperatorHandle<ConvFn>& conv_op() {
   static const auto op =
-      c10::Dispatcher::singleton().findSchemaOrThrow("torch_convnd::conv_nd", "").typed<ConvFn>();
+      c10::Dispatcher::singleton()
+          .findSchemaOrThrow(
+              kFollowLayout ? "torch_convnd::conv_nd_preserve" : "torch_convnd::conv_nd", "")
+          .typed<ConvFn>();
   return op;
 }
 
@@ -454,10 +463,14 @@ const c10::TypedOperatorHandle<ConvFn>& conv_op() {
 using BackwardArrayFn = Grads(const at::Tensor&, const at::Tensor&, const at::Tensor&,
                               at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, int64_t,
                               std::array<bool, 3>);
+template <bool kFollowLayout>
 const c10::TypedOperatorHandle<BackwardArrayFn>& backward_op() {
-  static const auto op = c10::Dispatcher::singleton()
-                             .findSchemaOrThrow("torch_convnd::conv_nd_backward", "")
-                             .typed<BackwardArrayFn>();
+  static const auto op =
+      c10::Dispatcher::singleton()
+          .findSchemaOrThrow(kFollowLayout ? "torch_convnd::conv_nd_backward_preserve"
+                                           : "torch_convnd::conv_nd_backward",
+                             "")
+          .typed<BackwardArrayFn>();
   return op;
 }
 
@@ -470,7 +483,8 @@ void save_geometry(AutogradContext* ctx, at::IntArrayRef stride, at::IntArrayRef
   ctx->saved_data["workspace_bytes"] = workspace_bytes;
 }
 
-class ConvNdFunction : public torch::autograd::Function<ConvNdFunction> {
+template <bool kFollowLayout>
+class ConvNdFunction : public torch::autograd::Function<ConvNdFunction<kFollowLayout>> {
  public:
   static at::Tensor forward(AutogradContext* ctx, const at::Tensor& input, const at::Tensor& weight,
                             const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
@@ -481,7 +495,8 @@ class ConvNdFunction : public torch::autograd::Function<ConvNdFunction> {
     ctx->saved_data["has_bias"] = has_bias;
     ctx->save_for_backward({input, weight});
     at::AutoDispatchBelowADInplaceOrView below;
-    return conv_op().call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes);
+    return conv_op<kFollowLayout>().call(input, weight, bias, stride, padding, dilation, groups,
+                                         workspace_bytes);
   }
 
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
@@ -493,7 +508,7 @@ class ConvNdFunction : public torch::autograd::Function<ConvNdFunction> {
     const auto stride = ctx->saved_data["stride"].toIntVector();
     const auto padding = ctx->saved_data["padding"].toIntVector();
     const auto dilation = ctx->saved_data["dilation"].toIntVector();
-    auto [gi, gw, gb] = backward_op().call(
+    auto [gi, gw, gb] = backward_op<kFollowLayout>().call(
         grads[0], saved[0], saved[1], stride, padding, dilation, ctx->saved_data["groups"].toInt(),
         ctx->saved_data["workspace_bytes"].toInt(), mask);
     return {gi.value_or(at::Tensor()), gw.value_or(at::Tensor()), gb.value_or(at::Tensor()),
@@ -501,7 +516,9 @@ class ConvNdFunction : public torch::autograd::Function<ConvNdFunction> {
   }
 };
 
-class ConvNdBackwardFunction : public torch::autograd::Function<ConvNdBackwardFunction> {
+template <bool kFollowLayout>
+class ConvNdBackwardFunction
+    : public torch::autograd::Function<ConvNdBackwardFunction<kFollowLayout>> {
  public:
   static variable_list forward(AutogradContext* ctx, const at::Tensor& grad_output,
                                const at::Tensor& input, const at::Tensor& weight,
@@ -513,8 +530,9 @@ class ConvNdBackwardFunction : public torch::autograd::Function<ConvNdBackwardFu
         std::vector<bool>{output_mask[0], output_mask[1], output_mask[2]};
     ctx->save_for_backward({grad_output, input, weight});
     at::AutoDispatchBelowADInplaceOrView below;
-    auto [gi, gw, gb] = backward_op().call(grad_output, input, weight, stride, padding, dilation,
-                                           groups, workspace_bytes, output_mask);
+    auto [gi, gw, gb] = backward_op<kFollowLayout>().call(
+        grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes,
+        output_mask);
     // Outputs of a custom function must be defined: only the requested gradients are returned
     // (in order); the caller maps them back to the three optional results.
     variable_list out;
@@ -549,20 +567,24 @@ class ConvNdBackwardFunction : public torch::autograd::Function<ConvNdBackwardFu
     // Autocast off for these terms, on both device types the operators run on.
     c10::impl::ExcludeDispatchKeyGuard no_autocast(
         c10::DispatchKeySet({c10::DispatchKey::AutocastCUDA, c10::DispatchKey::AutocastCPU}));
+    const auto& conv = conv_op<kFollowLayout>();
+    const auto& conv_backward = backward_op<kFollowLayout>();
     if (ggi.defined()) {
-      if (need_go) add(gg_output, conv_op().call(ggi, weight, std::nullopt, stride, padding,
-                                                 dilation, groups, ws));
+      if (need_go)
+        add(gg_output,
+            conv.call(ggi, weight, std::nullopt, stride, padding, dilation, groups, ws));
       if (need_w)
-        new_weight_grad = *std::get<1>(backward_op().call(grad_output, ggi, weight, stride, padding,
-                                                          dilation, groups, ws,
+        new_weight_grad = *std::get<1>(conv_backward.call(grad_output, ggi, weight, stride,
+                                                          padding, dilation, groups, ws,
                                                           {false, true, false}));
     }
     if (ggw.defined()) {
-      if (need_go) add(gg_output, conv_op().call(input, ggw, std::nullopt, stride, padding,
-                                                 dilation, groups, ws));
+      if (need_go)
+        add(gg_output,
+            conv.call(input, ggw, std::nullopt, stride, padding, dilation, groups, ws));
       if (need_x)
-        new_input_grad = *std::get<0>(backward_op().call(grad_output, input, ggw, stride, padding,
-                                                         dilation, groups, ws,
+        new_input_grad = *std::get<0>(conv_backward.call(grad_output, input, ggw, stride,
+                                                         padding, dilation, groups, ws,
                                                          {true, false, false}));
     }
     if (ggb.defined() && need_go) {
@@ -575,20 +597,22 @@ class ConvNdBackwardFunction : public torch::autograd::Function<ConvNdBackwardFu
   }
 };
 
+template <bool kFollowLayout>
 at::Tensor conv_nd_autograd(const at::Tensor& input, const at::Tensor& weight,
                             const std::optional<at::Tensor>& bias, at::IntArrayRef stride,
                             at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                             int64_t workspace_bytes) {
-  return ConvNdFunction::apply(input, weight, bias, stride, padding, dilation, groups,
-                               workspace_bytes);
+  return ConvNdFunction<kFollowLayout>::apply(input, weight, bias, stride, padding, dilation,
+                                              groups, workspace_bytes);
 }
 
+template <bool kFollowLayout>
 Grads conv_nd_backward_autograd(const at::Tensor& grad_output, const at::Tensor& input,
                                 const at::Tensor& weight, at::IntArrayRef stride,
                                 at::IntArrayRef padding, at::IntArrayRef dilation, int64_t groups,
                                 int64_t workspace_bytes, std::array<bool, 3> output_mask) {
-  auto out = ConvNdBackwardFunction::apply(grad_output, input, weight, stride, padding, dilation,
-                                           groups, workspace_bytes, output_mask);
+  auto out = ConvNdBackwardFunction<kFollowLayout>::apply(
+      grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask);
   std::optional<at::Tensor> res[3];
   size_t at_ = 0;
   for (int i = 0; i < 3; ++i)
@@ -600,13 +624,17 @@ Grads conv_nd_backward_autograd(const at::Tensor& grad_output, const at::Tensor&
 }  // namespace torch_convnd_hip
 
 TORCH_LIBRARY_IMPL(torch_convnd, Autograd, library) {
-  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autograd);
-  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_autograd);
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_autograd<false>);
+  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_autograd<false>);
+  library.impl("conv_nd_preserve", &torch_convnd_hip::conv_nd_autograd<true>);
+  library.impl("conv_nd_backward_preserve", &torch_convnd_hip::conv_nd_backward_autograd<true>);
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, CUDA, library) {
-  library.impl("conv_nd", &torch_convnd_hip::conv_nd_device);
-  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_device);
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_device<false>);
+  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_device<false>);
+  library.impl("conv_nd_preserve", &torch_convnd_hip::conv_nd_device<true>);
+  library.impl("conv_nd_backward_preserve", &torch_convnd_hip::conv_nd_backward_device<true>);
   library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_device);
   library.impl("partial_count", &torch_convnd_hip::partial_count_device);
   library.impl("conv_nd_act", &torch_convnd_hip::conv_nd_act_device);
@@ -618,8 +646,10 @@ TORCH_LIBRARY_IMPL(torch_convnd, AutocastCUDA, library) {
 }
 
 TORCH_LIBRARY_IMPL(torch_convnd, CPU, library) {
-  library.impl("conv_nd", &torch_convnd_hip::conv_nd_cpu);
-  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_cpu);
+  library.impl("conv_nd", &torch_convnd_hip::conv_nd_cpu<false>);
+  library.impl("conv_nd_backward", &torch_convnd_hip::conv_nd_backward_cpu<false>);
+  library.impl("conv_nd_preserve", &torch_convnd_hip::conv_nd_cpu<true>);
+  library.impl("conv_nd_backward_preserve", &torch_convnd_hip::conv_nd_backward_cpu<true>);
   library.impl("partial_rescale", &torch_convnd_hip::partial_rescale_cpu);
   library.impl("conv_nd_act", &torch_convnd_hip::conv_nd_act_cpu);
 }

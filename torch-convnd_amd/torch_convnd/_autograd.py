@@ -20,8 +20,7 @@ def _spatial_output(sizes, kernels, stride, padding, dilation):
 
 
 def _is_channels_last(tensor):
-    """[N, C, *spatial] stored as [N, *spatial, C] (and not also contiguous), the layout in
-    which the native operators return channels-last outputs and input gradients."""
+    """[N, C, *spatial] stored as [N, *spatial, C] (and not also contiguous)."""
     if tensor.dim() < 3 or tensor.is_contiguous():
         return False
     return tensor.permute(0, *range(2, tensor.dim()), 1).is_contiguous()
@@ -29,7 +28,7 @@ def _is_channels_last(tensor):
 
 def _empty_like_layout(reference, shape):
     """An empty tensor of ``shape`` in ``reference``'s activation layout (channels-last or
-    contiguous), as the native operators allocate their outputs."""
+    contiguous), as the layout-following operators allocate their outputs."""
     if not _is_channels_last(reference):
         return reference.new_empty(shape)
     stored = reference.new_empty([shape[0], *shape[2:], shape[1]])
@@ -37,17 +36,34 @@ def _empty_like_layout(reference, shape):
 
 
 def _fake_forward(input, weight, bias, stride, padding, dilation, groups, workspace_bytes):
+    # Contiguous whatever the input's layout, as the reference's (_autograd.py:8-16 there).
     spatial = _spatial_output(input.shape[2:], weight.shape[2:], stride, padding, dilation)
-    return _empty_like_layout(input, [input.shape[0], weight.shape[0], *spatial])
+    return input.new_empty([input.shape[0], weight.shape[0], *spatial])
 
 
 def _fake_backward(
     grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
 ):
     contiguous = torch.contiguous_format
-    grad_input = _empty_like_layout(input, list(input.shape)) if output_mask[0] else None
+    grad_input = torch.empty_like(input, memory_format=contiguous) if output_mask[0] else None
     grad_weight = torch.empty_like(weight, memory_format=contiguous) if output_mask[1] else None
     grad_bias = input.new_empty(weight.shape[0]) if output_mask[2] else None
+    return grad_input, grad_weight, grad_bias
+
+
+def _fake_forward_preserve(input, weight, bias, stride, padding, dilation, groups, workspace_bytes):
+    spatial = _spatial_output(input.shape[2:], weight.shape[2:], stride, padding, dilation)
+    return _empty_like_layout(input, [input.shape[0], weight.shape[0], *spatial])
+
+
+def _fake_backward_preserve(
+    grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
+):
+    grad_input, grad_weight, grad_bias = _fake_backward(
+        grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
+    )
+    if output_mask[0]:
+        grad_input = _empty_like_layout(input, list(input.shape))
     return grad_input, grad_weight, grad_bias
 
 
@@ -199,6 +215,8 @@ def release_python_autograd() -> None:
 def register_training() -> None:
     torch.library.register_fake("torch_convnd::conv_nd")(_fake_forward)
     torch.library.register_fake("torch_convnd::conv_nd_backward")(_fake_backward)
+    torch.library.register_fake("torch_convnd::conv_nd_preserve")(_fake_forward_preserve)
+    torch.library.register_fake("torch_convnd::conv_nd_backward_preserve")(_fake_backward_preserve)
     torch.library.register_fake("torch_convnd::partial_rescale")(_fake_rescale)
     torch.library.register_fake("torch_convnd::partial_count")(_fake_count)
     torch.library.register_fake("torch_convnd::conv_nd_act")(_fake_act)

@@ -35,7 +35,7 @@ EXPORTED_SYMBOLS = (
     "convnd_hip_backward_layout",
 )
 
-CHANNELS_FIRST, CHANNELS_LAST = 0, 1
+CHANNELS_FIRST, CHANNELS_LAST, CHANNELS_LAST_INPUT = 0, 1, 2
 
 # Bytes of the per-GPU static scratch of convnd_hip_forward_noalloc (CONVND_HIP_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 64 << 20

@@ -46,6 +46,22 @@ def _lazy_backward(
     )
 
 
+def _lazy_preserve(input, weight, bias, stride, padding, dilation, groups, workspace_bytes):
+    _load_for(input)
+    return torch.ops.torch_convnd.conv_nd_preserve.default(
+        input, weight, bias, stride, padding, dilation, groups, workspace_bytes
+    )
+
+
+def _lazy_backward_preserve(
+    grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
+):
+    _load_for(input)
+    return torch.ops.torch_convnd.conv_nd_backward_preserve.default(
+        grad_output, input, weight, stride, padding, dilation, groups, workspace_bytes, output_mask
+    )
+
+
 def _lazy_act(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, activation):
     _load_for(input)
     return torch.ops.torch_convnd.conv_nd_act.default(
@@ -86,6 +102,20 @@ def ensure_native_definitions():
             "int[] dilation, int groups, int workspace_bytes, str activation) -> Tensor"
         )
         library.impl("conv_nd_act", _lazy_act, "CompositeExplicitAutograd")
+        # The pair above with layout-following results: a channels-last input gives a
+        # channels-last output and grad_input (conv_nd(memory_format=torch.preserve_format));
+        # no reference counterpart (its operators return contiguous tensors).
+        library.define(
+            "conv_nd_preserve(Tensor input, Tensor weight, Tensor? bias, int[] stride, "
+            "int[] padding, int[] dilation, int groups, int workspace_bytes) -> Tensor"
+        )
+        library.define(
+            "conv_nd_backward_preserve(Tensor grad_output, Tensor input, Tensor weight, "
+            "int[] stride, int[] padding, int[] dilation, int groups, int workspace_bytes, "
+            "bool[3] output_mask) -> (Tensor?, Tensor?, Tensor?)"
+        )
+        library.impl("conv_nd_preserve", _lazy_preserve, "CompositeExplicitAutograd")
+        library.impl("conv_nd_backward_preserve", _lazy_backward_preserve, "CompositeExplicitAutograd")
         # Its counting pass (window sums of the validity map), gfx950 only.
         library.define(
             "partial_count(Tensor mask, int[] kernel, int[] stride, int[] padding, "

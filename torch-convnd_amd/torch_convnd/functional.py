@@ -105,14 +105,14 @@ def _direct_geometry(rank, stride, padding, dilation, kernel):
     return value
 
 
-def _direct_call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, backend):
+def _direct_call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, backend, preserve=False):
     """The operator call of a plain batched convolution with symmetric zero padding, the
     same one the general path below ends in, without its per-call argument normalisation;
     None when any condition of that shortcut fails (the general path then handles the call,
     errors included): native library loaded, a ROCm GPU with the native or auto backend at
     rank >= 4 (or native at any rank), or a CPU tensor with the native backend; equal dtypes
     and devices, valid channels and extents; no autocast, transform, tracing, compiling or
-    ONNX export."""
+    ONNX export. ``preserve`` selects the layout-following operator."""
     if is_compiling() or not _build._LOADED:
         return None
     if workspace_bytes <= 0 or type(groups) is not int or groups <= 0:
@@ -158,9 +158,8 @@ def _direct_call(input, weight, bias, stride, padding, dilation, groups, workspa
     ):
         return None
     strides, implicit, dilations = geometry
-    return torch.ops.torch_convnd.conv_nd.default(
-        input, weight, bias, strides, implicit, dilations, groups, workspace_bytes
-    )
+    op = torch.ops.torch_convnd.conv_nd_preserve if preserve else torch.ops.torch_convnd.conv_nd
+    return op.default(input, weight, bias, strides, implicit, dilations, groups, workspace_bytes)
 
 
 def conv_nd(
@@ -176,6 +175,7 @@ def conv_nd(
     workspace_bytes: int = DEFAULT_WORKSPACE_BYTES,
     backend: str = "auto",
     activation: str | None = None,
+    memory_format: torch.memory_format = torch.contiguous_format,
 ) -> Tensor:
     """Full (non-separable) dense convolution over ``weight.ndim - 2`` spatial axes.
 
@@ -186,6 +186,13 @@ def conv_nd(
     forward epilogue (``torch_convnd::conv_nd_act``); otherwise it runs after the
     convolution.
 
+    ``memory_format`` (an extension): ``torch.contiguous_format`` (default) keeps the
+    reference operator's contract, whose outputs and input gradients are contiguous whatever
+    the input's layout; ``torch.preserve_format`` returns a channels-last output (and input
+    gradient) for a channels-last input ([N, C, *spatial] stored as [N, *spatial, C]). On the
+    gfx950 path that output is written by the kernels themselves
+    (``torch_convnd::conv_nd_preserve``); elsewhere it is a copy of the contiguous result.
+
     ``backend="auto"`` uses PyTorch convolutions for ranks 1-3 and the gfx950 kernels for
     rank >= 4 on a ROCm GPU; ``native`` forces the gfx950 kernels, ``torch`` the portable
     decomposition. Low-precision (bf16/fp16) native results accumulate in fp32.
@@ -193,10 +200,34 @@ def conv_nd(
     max(element size, 4) * channels * kernel volume bytes); the implicit-GEMM kernels
     allocate their own small scratch instead of a patch buffer.
     """
+    preserve = memory_format is torch.preserve_format
+    if not preserve and memory_format is not torch.contiguous_format:
+        raise ValueError("memory_format must be torch.contiguous_format or torch.preserve_format")
     if padding_mode == "zeros" and activation is None:
-        output = _direct_call(input, weight, bias, stride, padding, dilation, groups, workspace_bytes, backend)
+        output = _direct_call(
+            input, weight, bias, stride, padding, dilation, groups, workspace_bytes, backend, preserve
+        )
         if output is not None:
             return output
+    output = _conv_nd(
+        input, weight, bias, stride, padding, dilation, groups, padding_mode, workspace_bytes, backend, activation
+    )
+    if preserve and input.ndim == weight.ndim and _is_channels_last(input) and not _is_channels_last(output):
+        order = (0, *range(2, output.dim()), 1)
+        back = (0, output.dim() - 1, *range(1, output.dim() - 1))
+        output = output.permute(order).contiguous().permute(back)
+    return output
+
+
+def _is_channels_last(tensor):
+    if tensor.dim() < 3 or tensor.is_contiguous():
+        return False
+    return tensor.permute(0, *range(2, tensor.dim()), 1).is_contiguous()
+
+
+def _conv_nd(input, weight, bias, stride, padding, dilation, groups, padding_mode, workspace_bytes, backend, activation):
+    """conv_nd's general path: the reference's argument handling, padding modes, partial
+    convolution, the fused activation, then the backend dispatch."""
     rank = weight.ndim - 2
     if not 1 <= rank <= 62:
         raise ValueError("weight must have output/input channels and 1-62 spatial dimensions")
