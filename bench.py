@@ -231,10 +231,17 @@ def measure_configs(torch, device, iterations=30, warmup=5, only=None):
 
     lib = _build.hip_library()
     out = {}
-    # Channels-last runs of C2 and C5: x and dY stored [N, *spatial, C] (outputs and grad_input
-    # come back in that layout; same kernels, no layout copy in the forward).
-    runs = [(name, name, False) for name in CONFIGS] + [(f"{name}_channels_last", name, True) for name in CL_CONFIGS]
-    for name, base, channels_last in runs:
+    # Channels-last runs of C2 and C5, x stored [N, *spatial, C]: "_channels_last" with
+    # memory_format=torch.preserve_format (dY, output and grad_input in that layout too; the
+    # forward makes no layout copy), "_channels_last_input" with the default contract
+    # (contiguous output, grad_input and dY, as the reference operators return).
+    runs = [(name, name, None) for name in CONFIGS]
+    for name in CL_CONFIGS:
+        runs += [(f"{name}_channels_last", name, torch.preserve_format),
+                 (f"{name}_channels_last_input", name, torch.contiguous_format)]
+    for name, base, cl_format in runs:
+        channels_last = cl_format is not None
+        memory_format = cl_format if channels_last else torch.contiguous_format
         xs, ws, stride, padding, dilation, groups, bias, dtype_name, roofs = CONFIGS[base]
         if only is not None and name not in only:
             continue
@@ -248,11 +255,11 @@ def measure_configs(torch, device, iterations=30, warmup=5, only=None):
 
         def conv(*ts):
             return torch_convnd.conv_nd(ts[0], ts[1], ts[2] if len(ts) > 2 else None, stride, padding,
-                                        dilation, groups, backend="native")
+                                        dilation, groups, backend="native", memory_format=memory_format)
 
         y = conv(*leaves)
         dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(5)).to(dtype).to(device)
-        if channels_last:
+        if memory_format is torch.preserve_format:
             dy = to_channels_last(dy)
         del y
 
@@ -420,8 +427,9 @@ def main():
     parser.add_argument("--no-configs", action="store_true",
                         help="skip the per-config fwd / fwd+bwd timings of C1-C5")
     parser.add_argument("--configs", default="",
-                        help="comma-separated subset of C1,C2,C3,C4_fp32,C4_bf16,C5,"
-                        "C2_channels_last,C5_channels_last for the per-config timings (default: all)")
+                        help="comma-separated subset of C1,C2,C3,C4_fp32,C4_bf16,C5,C2_channels_last,"
+                        "C5_channels_last,C2_channels_last_input,C5_channels_last_input for the per-config "
+                        "timings (default: all)")
     parser.add_argument(
         "--calibration-copy-mib", type=int, default=0,
         help="first run a plain elementwise copy of this many MiB three times (the known-size "

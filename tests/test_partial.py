@@ -166,6 +166,35 @@ def test_modules_and_sequential():
     assert ones.shape[1] == 3
 
 
+def test_sequential_nesting_and_errors():
+    """PartialSequential: a nested container carries the same mask as a flat one; a module
+    that changes the spatial shape while a mask is carried, or that hides partial layers
+    from the mask, raises; both mask keywords at once raise; TorchScript is refused."""
+    torch.manual_seed(6)
+    first = PartialConv4d(2, 4, 3, padding=1, multi_channel=True, dtype=torch.float64)
+    second = PartialConvNd(4, 3, 3, padding=1, dimensions=4, dtype=torch.float64, multi_channel=True)
+    x = torch.randn(1, 2, 4, 4, 4, 4, dtype=torch.float64)
+    mask = (torch.rand(1, 2, 4, 4, 4, 4) > 0.4).double()
+    flat_y, flat_mask = PartialSequential(first, torch.nn.ReLU(), second)(x, mask)
+    nested_y, nested_mask = PartialSequential(first, PartialSequential(torch.nn.ReLU(), second))(x, mask)
+    torch.testing.assert_close(nested_y, flat_y, rtol=0, atol=0)
+    torch.testing.assert_close(nested_mask, flat_mask, rtol=0, atol=0)
+    assert flat_mask.shape == (1, 3, 4, 4, 4, 4)  # one mask channel per output channel
+    # mask-free: the geometry keeps every sample valid, the final mask is broadcast ones
+    y0, ones = PartialSequential(first, second)(x)
+    assert ones.shape == (1, 3, 4, 4, 4, 4) and ones.stride() == (0,) * 6 and bool((ones == 1).all())
+    with pytest.raises(ValueError, match="while a mask is carried"):
+        PartialSequential(first, torch.nn.Flatten(2, 3))(x, mask)
+    with pytest.raises(TypeError, match="cannot reach"):
+        PartialSequential(first, torch.nn.Sequential(second))(x, mask)
+    with pytest.raises(TypeError, match="not both"):
+        first(x, mask, mask_in=mask)
+    with pytest.raises(TypeError, match="bool or None"):
+        first(x, mask, return_mask=1)
+    with pytest.raises(NotImplementedError, match="TorchScript"):
+        torch.jit.script(first)
+
+
 # ---- GPU: the fused rescale and the native path ----------------------------------------
 
 @pytest.mark.gpu

@@ -177,13 +177,23 @@ class Conv4d(_FixedConvNd):
     _spatial_dimensions = 4
 
 
+def _single_mask(mask, mask_in):
+    """The call's mask: ``mask_in`` is NVIDIA's keyword for it; giving both is an error."""
+    if mask_in is None:
+        return mask
+    if mask is not None:
+        raise TypeError("pass mask or mask_in, not both")
+    return mask_in
+
+
 class PartialConvNd(ConvNd):
     """Partial convolution layer at any spatial rank, with ConvNd's parameters and state.
 
-    ``forward(input, mask=None, mask_in=None, return_mask=None)``: ``mask_in`` is NVIDIA's
-    name for ``mask``; ``return_mask`` (None: the layer's setting) selects
-    ``PartialConvOutput(output, mask)`` or the output alone. ``multi_channel`` selects one
-    mask channel per input channel. Reference: src/torch_convnd/modules.py:219-345.
+    Calls take ``(input, mask=None, mask_in=None, return_mask=None)`` and return the output,
+    or ``PartialConvOutput(output, update_mask)`` when mask returning is on (the layer's
+    ``return_mask``, overridden per call by a bool). ``multi_channel`` selects one mask channel
+    per input channel instead of one shared channel. The arithmetic is ``partial_forward``'s
+    (torch_convnd.partial). Interface: src/torch_convnd/modules.py:219-345 of the reference.
     """
 
     def __init__(
@@ -206,43 +216,54 @@ class PartialConvNd(ConvNd):
         multi_channel=False,
         return_mask=False,
     ):
+        flags = (multi_channel, return_mask)
+        if any(not isinstance(flag, bool) for flag in flags):
+            raise TypeError("multi_channel and return_mask must be bools")
+        if padding_mode == "partial":
+            raise ValueError("PartialConvNd already rescales zero padding; use padding_mode='zeros'")
         super().__init__(
             in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
             padding_mode, device, dtype, dimensions=dimensions, workspace_bytes=workspace_bytes,
             backend=backend,
         )
-        if not isinstance(multi_channel, bool) or not isinstance(return_mask, bool):
-            raise TypeError("multi_channel and return_mask must be bools")
-        if padding_mode == "partial":
-            raise ValueError("PartialConvNd already rescales zero padding; use padding_mode='zeros'")
-        self.multi_channel = multi_channel
-        self.return_mask = return_mask
+        self.multi_channel, self.return_mask = flags
+
+    def _wants_mask(self, return_mask) -> bool:
+        if return_mask is None:
+            return self.return_mask
+        if isinstance(return_mask, bool):
+            return return_mask
+        raise TypeError("return_mask must be a bool or None")
 
     def forward(self, input, mask=None, mask_in=None, return_mask=None):
-        if mask_in is not None:
-            if mask is not None:
-                raise TypeError("pass mask or mask_in, not both")
-            mask = mask_in
-        if return_mask is None:
-            return_mask = self.return_mask
-        elif not isinstance(return_mask, bool):
-            raise TypeError("return_mask must be a bool or None")
+        mask = _single_mask(mask, mask_in)
+        wants_mask = self._wants_mask(return_mask)
         output, update = partial_forward(
             input, self.weight, self.bias, self.stride, self.padding, self.dilation, self.groups,
             mask=mask, multi_channel=self.multi_channel, padding_mode=self.padding_mode,
-            workspace_bytes=self.workspace_bytes, backend=self.backend, need_update=return_mask,
+            workspace_bytes=self.workspace_bytes, backend=self.backend, need_update=wants_mask,
         )
-        return PartialConvOutput(output, update) if return_mask else output
+        return PartialConvOutput(output, update) if wants_mask else output
 
-    def keeps_every_sample_valid(self, input) -> bool:
-        """Whether this layer, without a mask, leaves every output sample valid."""
+    def update_mask_channels(self) -> int:
+        """Channels of this layer's update mask: one per output channel with multi_channel."""
+        return self.out_channels if self.multi_channel else 1
+
+    def mask_free_output_is_valid(self, spatial) -> bool:
+        """Whether, without a mask, every output sample of an input with these trailing
+        spatial sizes sees at least one valid tap (so its update mask is all ones)."""
         return mask_free_is_full(
-            tuple(input.shape[-self.dimensions :]), self.kernel_size, self.stride, self.padding,
-            self.dilation, self.padding_mode,
+            tuple(spatial), self.kernel_size, self.stride, self.padding, self.dilation, self.padding_mode
         )
 
     def extra_repr(self) -> str:
         return f"{super().extra_repr()}, multi_channel={self.multi_channel}, return_mask={self.return_mask}"
+
+    def __prepare_scriptable__(self):
+        raise NotImplementedError(
+            "PartialConvNd does not support TorchScript; use eager execution, torch.compile or "
+            "torch.jit.trace"
+        )
 
 
 class _FixedPartialConvNd(PartialConvNd):
@@ -299,73 +320,96 @@ class PartialConv4d(_FixedPartialConvNd):
     _spatial_dimensions = 4
 
 
-def _partial_rank(container):
-    for module in container.modules():
-        if isinstance(module, PartialConvNd):
-            return module.dimensions
-    return None
+def _leaf_modules(container):
+    """The children of a PartialSequential in execution order, with nested PartialSequential
+    containers expanded in place (they carry the same mask)."""
+    for module in container:
+        if isinstance(module, PartialSequential):
+            yield from _leaf_modules(module)
+        else:
+            yield module
 
 
-def _trailing(shape, rank):
-    return tuple(shape[max(len(shape) - rank, 0) :])
+def _holds_partial_layer(module) -> bool:
+    return any(isinstance(inner, PartialConvNd) for inner in module.modules())
+
+
+class _CarriedMask:
+    """The validity mask a PartialSequential carries between its modules.
+
+    ``mask`` is None while every sample is known valid (no mask given, and every partial layer
+    so far left its whole output valid); ``rank`` and ``channels`` describe the mask the last
+    partial layer would produce (the spatial rank it covers and its channel count)."""
+
+    _REAL = {torch.complex64: torch.float32, torch.complex128: torch.float64}
+
+    def __init__(self, mask, rank, channels=1):
+        self.mask, self.rank, self.channels = mask, rank, channels
+
+    def spatial(self, shape):
+        return tuple(shape[max(len(shape) - self.rank, 0):])
+
+    def through_partial(self, layer, tensor):
+        self.rank, self.channels = layer.dimensions, layer.update_mask_channels()
+        if self.mask is None and layer.mask_free_output_is_valid(self.spatial(tensor.shape)):
+            return layer(tensor, return_mask=False)
+        tensor, self.mask = layer(tensor, self.mask, return_mask=True)
+        return tensor
+
+    def through_other(self, module, tensor):
+        if _holds_partial_layer(module):
+            raise TypeError(
+                f"{type(module).__name__} holds partial layers the mask cannot reach; use PartialSequential"
+            )
+        if self.mask is None:
+            return module(tensor)
+        before = tensor.shape  # the shape only: keeping the tensor would hold its memory
+        tensor = module(tensor)
+        if tensor.ndim != len(before) or self.spatial(tensor.shape) != self.spatial(before):
+            raise ValueError(
+                f"{type(module).__name__} changed the shape {tuple(before)} to {tuple(tensor.shape)} "
+                "while a mask is carried; keep the spatial shape or resample the mask around it"
+            )
+        return tensor
+
+    def final(self, output):
+        """The carried mask, or for an all-valid result a broadcast view of ones in the layout
+        of the last partial layer's update mask."""
+        if self.mask is not None:
+            return self.mask
+        if not has_rank(output.ndim, self.rank):
+            raise ValueError(
+                f"the {output.ndim}-dimensional output has lost the {self.rank} spatial axes "
+                "a validity mask describes"
+            )
+        batch = (output.shape[0],) if output.ndim == self.rank + 2 else ()
+        shape = (*batch, self.channels, *self.spatial(output.shape))
+        dtype = self._REAL.get(output.dtype, output.dtype)
+        return torch.ones((), dtype=dtype, device=output.device).expand(shape)
 
 
 class PartialSequential(nn.Sequential):
     """Run modules in order, carrying the validity mask through the partial layers.
 
-    ``forward(input, mask=None)`` returns ``PartialConvOutput(output, mask)``. Partial
-    layers (also inside nested PartialSequential containers) consume the current mask and
-    replace it with their update mask; other modules see only the tensor and must keep the
-    spatial shape while a mask is carried. Without a mask, layers whose geometry keeps every
-    sample valid run mask-free and an all-valid result is reported as a broadcast view of
-    ones. Reference: src/torch_convnd/modules.py:442-506.
+    ``forward(input, mask=None)`` returns ``PartialConvOutput(output, mask)``. Partial layers
+    (also inside nested PartialSequential containers) consume the carried mask and replace it
+    with their update mask; any other module sees only the tensor and must keep the spatial
+    shape while a mask is carried (a module that hides partial layers inside it is an error).
+    Without a mask, partial layers whose geometry leaves every sample valid run mask-free, and
+    an all-valid result is reported as a broadcast view of ones. Interface:
+    src/torch_convnd/modules.py:442-506 of the reference.
     """
 
     def forward(self, input, mask=None):
-        rank = _partial_rank(self)
-        layout = (max(input.ndim - 2, 0) if rank is None else rank, 1)
-        output, mask, layout = self._carry(input, mask, layout)
-        if mask is None:
-            mask = self._all_valid(output, *layout)
-        return PartialConvOutput(output, mask)
-
-    @staticmethod
-    def _all_valid(output, rank, channels):
-        if not has_rank(output.ndim, rank):
-            raise ValueError(
-                f"the {output.ndim}-dimensional output has lost the {rank} spatial axes "
-                "a validity mask describes"
-            )
-        level = {torch.complex64: torch.float32, torch.complex128: torch.float64}.get(output.dtype, output.dtype)
-        shape = (channels, *_trailing(output.shape, rank))
-        if output.ndim == rank + 2:
-            shape = (output.shape[0], *shape)
-        return torch.ones((), dtype=level, device=output.device).expand(shape)
-
-    def _carry(self, input, mask, layout):
-        for module in self:
-            if isinstance(module, PartialSequential):
-                input, mask, layout = module._carry(input, mask, layout)
-            elif isinstance(module, PartialConvNd):
-                layout = module.dimensions, module.out_channels if module.multi_channel else 1
-                if mask is None and module.keeps_every_sample_valid(input):
-                    input = module(input, return_mask=False)
-                else:
-                    input, mask = module(input, mask, return_mask=True)
-            elif _partial_rank(module) is not None:
-                raise TypeError(
-                    f"{type(module).__name__} holds partial layers the mask cannot reach; "
-                    "use PartialSequential"
-                )
-            elif mask is None:
-                input = module(input)
+        leaves = list(_leaf_modules(self))
+        first = next((m for m in leaves if isinstance(m, PartialConvNd)), None)
+        carried = _CarriedMask(mask, max(input.ndim - 2, 0) if first is None else first.dimensions)
+        for module in leaves:
+            if isinstance(module, PartialConvNd):
+                input = carried.through_partial(module, input)
             else:
-                shape, rank = input.shape, layout[0]
-                input = module(input)
-                if input.ndim != len(shape) or _trailing(input.shape, rank) != _trailing(shape, rank):
-                    raise ValueError(
-                        f"{type(module).__name__} changed the shape {tuple(shape)} to "
-                        f"{tuple(input.shape)} while a mask is carried; keep the spatial "
-                        "shape or resample the mask around it"
-                    )
-        return input, mask, layout
+                input = carried.through_other(module, input)
+        return PartialConvOutput(input, carried.final(input))
+
+    def __prepare_scriptable__(self):
+        raise NotImplementedError("PartialSequential does not support TorchScript")
