@@ -250,3 +250,27 @@ def test_plan_check_baseline_and_random_geometries(lib):
                 case, dtype, lib.convnd_hip_last_error().decode())
     bad = problem((1, 4, 6), (6, 2, 3), groups=3)
     assert lib.convnd_hip_plan_check(ctypes.byref(bad), _capi.BFLOAT16) == _capi.INVALID_ARGUMENT
+
+
+def test_unmatched_plan_override_is_ignored():
+    """CONVND_HIP_FWD_PLAN / _DGRAD_PLAN / _WGRAD_PLAN restrict the planners' search (a tuning
+    aid); an override that no plan of a problem matches is ignored rather than sending the
+    problem to the 64-bit direct kernels. The variables are read once per process."""
+    import os
+    import subprocess
+    import sys
+
+    code = (
+        "import sys; sys.path.insert(0, 'torch-convnd_amd')\n"
+        "import torch\n"
+        "from torch_convnd import _build, _capi\n"
+        "lib = _build.hip_library()\n"
+        "print(','.join(_capi.plan_names(lib, (1, 8, 8, 8, 8, 8, 8, 8), (16, 8) + (3,) * 6, (1,) * 6,\n"
+        "                               (1,) * 6, (1,) * 6, 1, torch.bfloat16)))\n"
+    )
+    env = dict(os.environ, CONVND_HIP_FWD_PLAN="waves=8,cc=8,nbuf=2", CONVND_HIP_DGRAD_PLAN="waves=8,cc=8,nbuf=2",
+               CONVND_HIP_WGRAD_PLAN="waves=16")
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == "mfma,mfma,mfma"

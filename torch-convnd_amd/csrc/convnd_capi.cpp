@@ -416,7 +416,20 @@ const PlanFilter& plan_filter(int mode) {
 constexpr int kSplit = 6;
 constexpr int kSplitMaxChannels = 64;
 
+IgemmPlan plan_igemm_filtered(const Geom& g, convnd_hip_dtype dt, int mode,
+                               const PlanFilter& filter);
+
+// The implicit-GEMM plan; an override (CONVND_HIP_FWD_PLAN / CONVND_HIP_DGRAD_PLAN) that no
+// plan of this problem matches is ignored.
 IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
+  const PlanFilter& filter = plan_filter(mode);
+  IgemmPlan plan = plan_igemm_filtered(g, dt, mode, filter);
+  if (!plan.ok && filter.active) plan = plan_igemm_filtered(g, dt, mode, PlanFilter{});
+  return plan;
+}
+
+IgemmPlan plan_igemm_filtered(const Geom& g, convnd_hip_dtype dt, int mode,
+                               const PlanFilter& filter) {
   IgemmPlan plan;
   const bool split = dt == CONVND_HIP_FLOAT32;
   if ((!is_half(dt) && !split) || g.rank > kFastRank || !fits_int32(g)) return plan;
@@ -460,7 +473,6 @@ IgemmPlan plan_igemm(const Geom& g, convnd_hip_dtype dt, int mode) {
     }
   }
   const int mtiles = (gemm_cout + 15) / 16;
-  const PlanFilter& filter = plan_filter(mode);
   // Direct staging (16-bit data): the kernel reads the caller's channels-first tensor and
   // double-buffers the chunk halos; otherwise (split-precision fp32, or halos too large to
   // double-buffer) a prologue copies the operand octet-major first, which costs its HBM
@@ -780,7 +792,8 @@ struct WgradPlan {
 
 // Channel-major weight-gradient plan: 16-bit data and a unit stride along the last axis
 // (the runs of a halo row are contiguous in the padded input).
-bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
+bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
+                   WgradPlan* out) {
   if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g) || g.batch == 0) return false;
   const int R = g.rank;
   if (g.s[R - 1] != 1) return false;
@@ -792,7 +805,6 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
   const int mgroups = (mtiles + mb - 1) / mb;
   const int ncol = cin_g * k_vol;
   const int ntiles = (ncol + 15) / 16;
-  const PlanFilter& filter = plan_filter(2);
   // LDS past the two item buffers (static): run table and item records.
   const int64_t dyn_budget = 160 * 1024 - 2 * kWgradCmBuffer;
   double best = -1.0;
@@ -1011,18 +1023,24 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, WgradPlan* out) {
   return true;
 }
 
-WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt);
+WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter);
 
 // The channel-major kernel where it applies (CONVND_HIP_WGRAD_PLAN=cm=0 forces the
-// octet-major one), else the octet-major kernel.
+// octet-major one), else the octet-major kernel; an override that no plan of this problem
+// matches is ignored.
 WgradPlan plan_wgrad(const Geom& g, convnd_hip_dtype dt) {
+  auto search = [&](const PlanFilter& filter) {
+    WgradPlan cm;
+    if (filter.cm != 0 && plan_wgrad_cm(g, dt, filter, &cm)) return cm;
+    return plan_wgrad_octets(g, dt, filter);
+  };
   const PlanFilter& filter = plan_filter(2);
-  WgradPlan cm;
-  if (filter.cm != 0 && plan_wgrad_cm(g, dt, &cm)) return cm;
-  return plan_wgrad_octets(g, dt);
+  WgradPlan plan = search(filter);
+  if (!plan.ok && filter.active) plan = search(PlanFilter{});
+  return plan;
 }
 
-WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt) {
+WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter) {
   WgradPlan plan;
   // Split-precision fp32: kSplit images of bf16 parts per image (see convnd_types.h).
   const bool split = dt == CONVND_HIP_FLOAT32;
@@ -1047,7 +1065,6 @@ WgradPlan plan_wgrad_octets(const Geom& g, convnd_hip_dtype dt) {
     max_oct = std::max(max_oct, (p1 - 1) / k_vol - p0 / k_vol + 1);
   }
   const int out_last = static_cast<int>(g.out[R - 1]);
-  const PlanFilter& filter = plan_filter(2);
   double best = -1.0;
   for (int box_vol : {512, 256, 128}) {
     int limit[kFastRank];
