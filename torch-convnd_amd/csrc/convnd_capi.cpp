@@ -790,11 +790,17 @@ struct WgradPlan {
   PlanarPadArgs ppad{};  // the zero-padded channels-first input it reads (staged_elems)
 };
 
-// Channel-major weight-gradient plan: 16-bit data and a unit stride along the last axis
-// (the runs of a halo row are contiguous in the padded input).
+// Channel-major weight-gradient plan: 16-bit data, or split-precision fp32 (kSplit bf16 part
+// images per image, both operands read from part copies), and a unit stride along the last
+// axis (the runs of a halo row are contiguous in the padded input).
 bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
                    WgradPlan* out) {
-  if (!is_half(dt) || g.rank > kFastRank || !fits_int32(g) || g.batch == 0) return false;
+  const bool split = dt == CONVND_HIP_FLOAT32;
+  if ((!is_half(dt) && !split) || g.rank > kFastRank || !fits_int32(g) || g.batch == 0)
+    return false;
+  // The planar copy's source is addressed by 32-bit byte offsets.
+  if (g.batch * g.channels * g.in_vol * element_size(dt) > 0xffffffe0ll) return false;
+  const int64_t batch = split ? g.batch * kSplit : g.batch;
   const int R = g.rank;
   if (g.s[R - 1] != 1) return false;
   const int cin_g = static_cast<int>(g.cin_g), cout_g = static_cast<int>(g.cout_g);
@@ -850,13 +856,13 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
         if (pvol > kI32Safe) return;
       }
       // The padded copy must stay int32-addressable and not dwarf the input.
-      if (pvol * g.batch * g.channels * 2 > kI32Safe || pvol > 8 * g.in_vol + (1 << 20)) return;
+      if (pvol * batch * g.channels * 2 > kI32Safe || pvol > 8 * g.in_vol + (1 << 20)) return;
       const int bl8 = bl / 8;
       const int nrho = kl * bl8;
       const int runpitch = nrho * 16;
       const int64_t chpitch = rows_h * runpitch;
-      if (dvol * g.batch * g.out_channels > kI32Safe / 2) return;
-      const int64_t items = boxes * g.batch;
+      if (dvol * batch * g.out_channels > kI32Safe / 2) return;
+      const int64_t items = boxes * batch;
       if (items > (int64_t{1} << 22)) return;
       const int64_t dyt_bytes = (int64_t)mb * 16 * box_vol * 2;
       const int ksteps = box_vol / 32;
@@ -937,13 +943,14 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
         plan.mb = mb;
         plan.cost = cost;
         plan.lds = static_cast<size_t>(lds);
-        plan.exact = dvol == g.out_vol;
-        plan.staged_elems = (size_t)g.batch * g.channels * pvol;
+        // Split precision always reads grad_output's padded part copy.
+        plan.exact = dvol == g.out_vol && !split;
+        plan.staged_elems = (size_t)batch * g.channels * pvol;
         WgradCmArgs& C = plan.cm_args;
         std::memset(&C, 0, sizeof(C));
         C.x_bytes = static_cast<unsigned>(plan.staged_elems * 2);
         C.rank = R;
-        C.batch = static_cast<int>(g.batch);
+        C.batch = static_cast<int>(batch);
         C.groups = static_cast<int>(g.groups);
         C.cin_g = cin_g;
         C.cout_g = cout_g;
@@ -980,7 +987,7 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
         P.channels = static_cast<int>(g.channels);
         P.in_vol = static_cast<int>(g.in_vol);
         P.pvol = static_cast<int>(pvol);
-        P.src_bytes = static_cast<unsigned>(g.batch * g.channels * g.in_vol * 2);
+        P.src_bytes = static_cast<unsigned>(g.batch * g.channels * g.in_vol * element_size(dt));
         for (int a = 0; a < R; ++a) {
           C.box[a] = b[a];
           C.nbox[a] = nbox[a];
@@ -1017,7 +1024,8 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
   }
   if (!plan.ok) return false;
   if (wgrad_cm_table_layout(plan.cm_args) > (size_t)kI32Safe) return false;
-  plan.dy_pad_elems = plan.exact ? 0 : (size_t)g.batch * plan.cm_args.dvol * g.out_channels;
+  plan.dy_pad_elems =
+      plan.exact ? 0 : (size_t)plan.cm_args.batch * plan.cm_args.dvol * g.out_channels;
   plan.partial_elems = (size_t)plan.cm_args.npc * wgrad_cm_partial_slots(plan.mb, plan.cm_args) * 4;
   *out = plan;
   return true;
@@ -1944,7 +1952,9 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
     pp.pp = &b.wg.ppad;
     pp.x = input;
     pp.x_pp = ws + b.off_x_stage;
-    pp.pp_batch = g.batch;
+    pp.pp_batch = CA.batch;
+    // Split-precision fp32: part images of both operands (kSplit x batch of each).
+    pp.split_batch = dtype == CONVND_HIP_FLOAT32 ? static_cast<int>(g.batch) : 0;
     CA.partial = reinterpret_cast<float*>(ws + b.off_partial);
     CA.dy_bytes = static_cast<unsigned>(g.batch * g.out_channels * g.out_vol * 2);
     // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the

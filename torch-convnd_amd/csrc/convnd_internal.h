@@ -408,7 +408,9 @@ int64_t prologue_sum_blocks(int64_t batch, int64_t volume);
 //   octets:     zero-padded octet-major input for the weight gradient (pad);
 //   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg);
 //   planar pad: zero-padded channels-first input for the channel-major weight gradient
-//               (pp, 16-bit data);
+//               (pp; an fp32 source gives pp_batch = 6 x split_batch bf16 part images,
+//               image n holding part split_data_part(n / split_batch) of image
+//               n % split_batch);
 //   sums:       channel partial sums of a channels-first 16-bit tensor (bias gradient).
 struct IgemmArgs;
 struct WgradArgs;
@@ -428,7 +430,7 @@ struct PrologueParts {
   const WgradArgs* wg = nullptr;
   const void* dy = nullptr;
   void* dy_pad = nullptr;
-  int split_batch = 0;
+  int split_batch = 0;  // fp32 source: images per part block (dy_pad and planar pad)
   const PlanarPadArgs* pp = nullptr;  // zero-padded channels-first input (x -> x_pp)
   void* x_pp = nullptr;
   int64_t pp_batch = 0;

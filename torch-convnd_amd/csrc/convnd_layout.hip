@@ -62,6 +62,7 @@ struct DevPrologue {
   void* x_pp;
   int64_t e_total;
   int e_blocks;
+  int e_split_nc;  // split precision: source (image, channel) rows of each part block
   // Channel partial sums of a channels-first 16-bit tensor (bias gradient): block (image,
   // channel, run of kSumRun positions) -> f_sums[c * (batch * f_nrun) + n * f_nrun + run].
   const void* f_src;
@@ -162,10 +163,15 @@ void prologue_kernel(DevPrologue P) {
     return;
   }
   b -= P.d_blocks;
-  if constexpr (!SPLIT) {
-    if (b < P.e_blocks)
+  if (b < P.e_blocks) {
+    if constexpr (SPLIT) {
+      stage::pad_planar_split_blocks(static_cast<const float*>(P.xpp_src),
+                                     static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total,
+                                     P.e_split_nc, b);
+    } else {
       stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
                                  static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b);
+    }
   }
 }
 
@@ -477,7 +483,10 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     total += P.d_blocks;
   }
   if (p.x_pp != nullptr && p.pp != nullptr) {
-    if (split) return hipErrorInvalidValue;
+    // Split precision: pp_batch = kSplitProducts x split_batch part images.
+    if (split && (p.split_batch <= 0 || p.pp_batch != (int64_t)kSplitProducts * p.split_batch))
+      return hipErrorInvalidValue;
+    P.e_split_nc = split ? p.split_batch * p.pp->channels : 0;
     P.ppa = *p.pp;
     P.xpp_src = p.x;
     P.x_pp = p.x_pp;

@@ -491,6 +491,90 @@ __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
   }
 }
 
+// Split-precision form of the zero-padded channels-first copy: an fp32 source of split_nc
+// (image, channel) rows gives kSplitProducts x split_nc destination rows, destination row
+// block s holding bf16 part split_data_part(s) of every source element. Run t (8 elements, one
+// 16-byte store) loads the three aligned 16-byte chunks that cover its source elements (the
+// buffer's per-dword range check reads zero past the source's end, and an offset before its
+// start is sent out of range); elements outside the source row are zero.
+__device__ __forceinline__ void pad_planar_split_blocks(const float* src, unsigned short* dst,
+                                                        const PlanarPadArgs& P, int64_t total,
+                                                        int split_nc, int block) {
+  const int R = P.rank;
+  int in_last = 1, pad_last = 0;
+#pragma unroll
+  for (int a = 0; a < kFastRank; ++a) {
+    if (a == R - 1) {
+      in_last = P.in[a];
+      pad_last = P.pad[a];
+    }
+  }
+  const int chunks = P.pe[R - 1] >> 3;
+  const int rows_per_img = P.pvol / P.pe[R - 1];
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes), 0x00020000);
+  // 32-bit index arithmetic: the planner keeps the copy and the source below 2^31 elements.
+  const int ntotal = static_cast<int>(total);
+  u32x4 w[kPlanarRuns];
+#pragma unroll
+  for (int q = 0; q < kPlanarRuns; ++q) {
+    const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
+    w[q] = u32x4{0u, 0u, 0u, 0u};
+    if (t >= ntotal) continue;
+    const int row = fast_div(t, P.div_chunks);
+    const int u0 = (t - row * chunks) * 8 - pad_last;
+    const int nc = fast_div(row, P.div_rows);
+    const int s = nc / split_nc;
+    const int snc = nc - s * split_nc;
+    const int part = split_data_part(s);
+    int rem = row - nc * rows_per_img;
+    int srow = 0, istr = in_last;
+    bool ok = true;
+#pragma unroll
+    for (int a = kFastRank - 2; a >= 0; --a) {
+      if (a < R - 1) {
+        const int qa = fast_div(rem, P.div_pe[a]);
+        const int u = rem - qa * P.pe[a] - P.pad[a];
+        rem = qa;
+        ok = ok && u >= 0 && u < P.in[a];
+        srow += u * istr;
+        istr *= P.in[a];
+      }
+    }
+    const int lo_i = -u0 < 0 ? 0 : (-u0 > 8 ? 8 : -u0);
+    const int hi_i = in_last - u0 < 0 ? 0 : (in_last - u0 > 8 ? 8 : in_last - u0);
+    if (!ok || lo_i >= hi_i) continue;
+    const int64_t first = (int64_t)snc * P.in_vol + srow + u0;
+    const int64_t chunk = first >= 0 ? first >> 2 : -((3 - first) >> 2);  // floor(first / 4)
+    const int o = static_cast<int>(first - chunk * 4);                   // 0 .. 3
+    const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
+    auto load16 = [&](int64_t c) {
+      const unsigned off = c >= 0 && c * 16 < nbytes ? static_cast<unsigned>(c * 16) : 0xfffffff0u;
+      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
+    };
+    const u32x4 c0 = load16(chunk), c1 = load16(chunk + 1);
+    const u32x4 c2 = o > 0 ? load16(chunk + 2) : u32x4{0u, 0u, 0u, 0u};
+    const unsigned d[12] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1],
+                            c1[2], c1[3], c2[0], c2[1], c2[2], c2[3]};
+    unsigned h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      unsigned x = d[e];
+#pragma unroll
+      for (int k = 1; k < 4; ++k)
+        if (o == k) x = d[e + k];
+      h[e] = e >= lo_i && e < hi_i ? bf16_part_bits(__builtin_bit_cast(float, x), part) : 0u;
+    }
+    w[q] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                 h[6] | (h[7] << 16)};
+  }
+#pragma unroll
+  for (int q = 0; q < kPlanarRuns; ++q) {
+    const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
+    if (t < ntotal) *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = w[q];
+  }
+}
+
 // Bias gradient from the fp32 channel sums of a staging pass: db[c] = sum of the nsum
 // partial sums of channel c, one workgroup per channel, fixed-order tree.
 struct BiasSums {

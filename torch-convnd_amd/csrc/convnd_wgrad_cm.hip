@@ -470,6 +470,8 @@ hipError_t launch_wgrad_cm(convnd_hip_dtype dtype, int mb, const WgradCmArgs& a,
   if (a.items == 0) return hipSuccess;
   if (dtype == CONVND_HIP_BFLOAT16) return wgrad_cm_dispatch<__bf16>(mb, a, lds_bytes, stream);
   if (dtype == CONVND_HIP_FLOAT16) return wgrad_cm_dispatch<_Float16>(mb, a, lds_bytes, stream);
+  // Split-precision fp32: the operands are bf16 part images.
+  if (dtype == CONVND_HIP_FLOAT32) return wgrad_cm_dispatch<__bf16>(mb, a, lds_bytes, stream);
   return hipErrorInvalidValue;
 }
 
@@ -497,6 +499,9 @@ hipError_t launch_wgrad_cm_reduce(convnd_hip_dtype dtype, int mb, const WgradCmA
   } else if (dtype == CONVND_HIP_FLOAT16) {
     hipLaunchKernelGGL(wgrad_cm_reduce_kernel<_Float16>, grid, dim3(kThreads), 0, stream, part,
                        static_cast<_Float16*>(dw), a, mb, nslots, rb, bs);
+  } else if (dtype == CONVND_HIP_FLOAT32) {
+    hipLaunchKernelGGL(wgrad_cm_reduce_kernel<float>, grid, dim3(kThreads), 0, stream, part,
+                       static_cast<float*>(dw), a, mb, nslots, rb, bs);
   } else {
     return hipErrorInvalidValue;
   }
