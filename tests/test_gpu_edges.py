@@ -53,6 +53,10 @@ SHAPES = {
     "cout_not_multiple_of_16": ((1, 8, 4, 4, 5, 12), (20, 8, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True),
     "rank5_dilated": ((1, 16, 5, 4, 6, 5, 9), (16, 16, 2, 3, 2, 2, 3), (1,) * 5, (1, 2, 1, 0, 2), (2, 1, 2, 1, 2),
                       1, True),
+    # Odd element counts: the weight gradient's zero-padded input copy ends in a partial
+    # 16-byte chunk (the source's last dword straddles its end for 16-bit data).
+    "odd_volume_rank3": ((1, 5, 7, 9, 11), (8, 5, 3, 3, 3), (1,) * 3, (1,) * 3, (1,) * 3, 1, True),
+    "odd_volume_rank4": ((1, 3, 5, 7, 13, 3), (16, 3, 3, 3, 3, 3), (1,) * 4, (1,) * 4, (1,) * 4, 1, True),
 }
 
 

@@ -997,13 +997,20 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
           C.k[a] = static_cast<int>(g.k[a]);
           C.s[a] = static_cast<int>(g.s[a]);
           C.d[a] = static_cast<int>(g.d[a]);
-          P.in[a] = static_cast<int>(g.in[a]);
-          P.pe[a] = pe[a];
-          P.pad[a] = static_cast<int>(g.p[a]);
-          P.div_pe[a] = make_fast_div(static_cast<unsigned>(pe[a]));
         }
+        for (int a = 0; a < kFastRank; ++a) {
+          const bool outer = a < R - 1;
+          P.in[a] = outer ? static_cast<int>(g.in[a]) : 1;
+          P.pe[a] = outer ? pe[a] : 1;
+          P.pad[a] = outer ? static_cast<int>(g.p[a]) : 0;
+          P.div_pe[a] = make_fast_div(static_cast<unsigned>(P.pe[a]));
+        }
+        P.last_in = static_cast<int>(g.in[R - 1]);
+        P.last_pe = pe[R - 1];
+        P.last_pad = static_cast<int>(g.p[R - 1]);
+        P.rows_per_img = static_cast<int>(pvol / pe[R - 1]);
         P.div_chunks = make_fast_div(static_cast<unsigned>(pe[R - 1] / 8));
-        P.div_rows = make_fast_div(static_cast<unsigned>(pvol / pe[R - 1]));
+        P.div_rows = make_fast_div(static_cast<unsigned>(P.rows_per_img));
         // grad_output as the padded copy's source/destination sees it.
         WgradArgs& D = plan.args;
         std::memset(&D, 0, sizeof(D));

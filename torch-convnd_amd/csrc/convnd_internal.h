@@ -343,11 +343,14 @@ struct PartialRescaleArgs {
 // multiple of 8).
 struct PlanarPadArgs {
   int rank, channels;
+  // Outer axes a < rank - 1: input extent, padded extent, leading padding; entries from
+  // rank - 1 on are identities (1, 1, 0) so the kernels walk all of them without a rank test.
   int in[kFastRank], pe[kFastRank], pad[kFastRank];
-  int in_vol, pvol;
+  int last_in, last_pe, last_pad;  // the last axis (last_pe a multiple of 8)
+  int in_vol, pvol, rows_per_img;  // rows_per_img = pvol / last_pe
   unsigned src_bytes;  // size of the source tensor (loads past it read zero)
-  // Divisions of the copy's run index: by pe[a] (a < rank - 1), by the runs per row
-  // (pe[rank-1] / 8) and by the rows per (image, channel) (pvol / pe[rank-1]).
+  // Divisions of the copy's run index: by pe[a], by the runs per row (last_pe / 8) and by
+  // the rows per (image, channel).
   FastDiv div_pe[kFastRank];
   FastDiv div_chunks, div_rows;
 };

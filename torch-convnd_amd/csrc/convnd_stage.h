@@ -367,211 +367,176 @@ __device__ __forceinline__ void pad_dy16_blocks(const Src* src, unsigned short* 
   }
 }
 
-// Zero-padded channels-first copy (PlanarPadArgs), 16-bit elements: run t of 8 consecutive
-// elements of a destination row (pe[rank-1] is a multiple of 8) is one 16-byte store. A block
-// covers 2 kThreads consecutive runs, two per thread (both loads in flight before the stores;
-// consecutive threads write consecutive runs); the index divisions are multiply-shifts.
-constexpr int kPlanarRuns = 2;
+// Zero-padded channels-first copies (PlanarPadArgs): run t of 8 consecutive elements of a
+// destination row (last_pe is a multiple of 8) is one 16-byte store; consecutive threads
+// write consecutive runs, kPlanarRuns per thread, kPlanarRuns * kThreads per block. Every
+// run's loads are issued before the first run is shifted and stored, and the axis walk has
+// no rank test (entries past the outer axes are identities), so its scalar parameter loads
+// issue together instead of one dependent wait per axis.
+constexpr int kPlanarRuns = 4;
+
+// Source of run t: (image, channel) row nc, the element offset of the run's first element
+// from the source's start (negative before it), and its elements [lo, hi) inside the input
+// (lo >= hi: none, the run lies in the padding).
+struct PlanarRunSrc {
+  int nc;
+  int64_t first;
+  int lo, hi;
+};
+
+__device__ __forceinline__ PlanarRunSrc planar_run_src(const PlanarPadArgs& P, int t) {
+  const int row = fast_div(t, P.div_chunks);  // (image, channel, padded row)
+  const int u0 = (t - row * (P.last_pe >> 3)) * 8 - P.last_pad;
+  const int nc = fast_div(row, P.div_rows);
+  int rem = row - nc * P.rows_per_img;
+  int srow = 0, istr = P.last_in;
+  bool ok = true;
+#pragma unroll
+  for (int a = kFastRank - 2; a >= 0; --a) {
+    const int qa = fast_div(rem, P.div_pe[a]);
+    const int u = rem - qa * P.pe[a] - P.pad[a];
+    rem = qa;
+    ok = ok && u >= 0 && u < P.in[a];
+    srow += u * istr;
+    istr *= P.in[a];
+  }
+  PlanarRunSrc r;
+  r.nc = nc;
+  r.first = (int64_t)nc * P.in_vol + srow + u0;
+  r.lo = -u0 < 0 ? 0 : (-u0 > 8 ? 8 : -u0);
+  r.hi = ok ? (P.last_in - u0 < 0 ? 0 : (P.last_in - u0 > 8 ? 8 : P.last_in - u0)) : 0;
+  return r;
+}
+
+// 16-byte chunk c of a buffer of nbytes (offset 0xfffffff0, past every buffer, for a chunk
+// outside it: reads zero).
+__device__ __forceinline__ u32x4 planar_chunk(__amdgpu_buffer_rsrc_t sr, int64_t c,
+                                              int64_t nbytes, bool live) {
+  const unsigned off =
+      live && c >= 0 && c * 16 < nbytes ? static_cast<unsigned>(c * 16) : 0xfffffff0u;
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
+}
+
+// A 16-bit chunk that straddles the buffer's end, element by element (the buffer's range check
+// is per dword: a straddling dword would read zero, valid half included).
+__device__ __forceinline__ u32x4 planar_chunk16_tail(__amdgpu_buffer_rsrc_t sr, int64_t c) {
+  u32x4 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const unsigned off = static_cast<unsigned>(c * 16 + 4 * k);
+    const unsigned lo = __builtin_amdgcn_raw_buffer_load_b16(sr, off, 0, 0);
+    const unsigned hi = __builtin_amdgcn_raw_buffer_load_b16(sr, off + 2u, 0, 0);
+    r[k] = lo | (hi << 16);
+  }
+  return r;
+}
+
 __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
                                                     unsigned short* dst,
                                                     const PlanarPadArgs& P, int64_t total,
                                                     int block) {
-  const int R = P.rank;
-  int in_last = 1, pad_last = 0;
-#pragma unroll
-  for (int a = 0; a < kFastRank; ++a) {
-    if (a == R - 1) {
-      in_last = P.in[a];
-      pad_last = P.pad[a];
-    }
-  }
-  const int chunks = P.pe[R - 1] >> 3;
-  const int rows_per_img = P.pvol / P.pe[R - 1];
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<unsigned short*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes),
       0x00020000);
-  // 32-bit index arithmetic: the padded copy and the source hold fewer than 2^31 elements
-  // (the planner checks both).
+  const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
+  // 32-bit run indices: the planner keeps the copy and the source below 2^31 elements.
   const int ntotal = static_cast<int>(total);
-  u32x4 w[kPlanarRuns];
+  // The two aligned 16-byte chunks that cover each run's 8 source elements (starting at
+  // element o of the first).
+  u32x4 c0[kPlanarRuns], c1[kPlanarRuns];
+  int o[kPlanarRuns], lo[kPlanarRuns], hi[kPlanarRuns];
 #pragma unroll
   for (int q = 0; q < kPlanarRuns; ++q) {
     const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
-    w[q] = u32x4{0u, 0u, 0u, 0u};
-    if (t >= ntotal) continue;
-    const int row = fast_div(t, P.div_chunks);  // (image, channel, padded row)
-    const int u0 = (t - row * chunks) * 8 - pad_last;
-    const int nc = fast_div(row, P.div_rows);
-    int rem = row - nc * rows_per_img;
-    int srow = 0, istr = in_last;
-    bool ok = true;
-#pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        const int qa = fast_div(rem, P.div_pe[a]);
-        const int u = rem - qa * P.pe[a] - P.pad[a];
-        rem = qa;
-        ok = ok && u >= 0 && u < P.in[a];
-        srow += u * istr;
-        istr *= P.in[a];
-      }
-    }
-    // The run's 8 source elements start at `first` (any element offset): the two aligned
-    // 16-byte chunks that cover them are loaded (a chunk before the source or past its end
-    // reads zero) and the run is shifted out of them; elements outside the row are masked to
-    // zero.
-    const int64_t first = (int64_t)nc * P.in_vol + srow + u0;
-    const int lo_i = -u0 < 0 ? 0 : (-u0 > 8 ? 8 : -u0);
-    const int hi_i = in_last - u0 < 0 ? 0 : (in_last - u0 > 8 ? 8 : in_last - u0);
-    if (ok && lo_i < hi_i) {
-      const int64_t chunk = first >= 0 ? first >> 3 : -((7 - first) >> 3);  // floor(first / 8)
-      const int o = static_cast<int>(first - chunk * 8);                   // 0 .. 7
-      // A chunk that straddles the source's end loads element by element (the buffer's range
-      // check is per dword: a dword straddling the end would read zero, valid half included).
-      auto load16 = [&](int64_t c) {
-        const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
-        if (c >= 0 && (c + 1) * 16 > nbytes && c * 16 < nbytes) {
-          u32x4 r;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const unsigned off = static_cast<unsigned>(c * 16 + 4 * k);
-            const unsigned lo = __builtin_amdgcn_raw_buffer_load_b16(sr, off, 0, 0);
-            const unsigned hi = __builtin_amdgcn_raw_buffer_load_b16(sr, off + 2u, 0, 0);
-            r[k] = lo | (hi << 16);
-          }
-          return r;
-        }
-        const unsigned off = c >= 0 && c * 16 < nbytes ? static_cast<unsigned>(c * 16) : 0xfffffff0u;
-        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
-      };
-      const u32x4 c0 = load16(chunk);
-      const u32x4 c1 = o > 0 ? load16(chunk + 1) : u32x4{0u, 0u, 0u, 0u};
-      const unsigned d[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-      // Dword j of the run: bytes 2 o + 4 j .. +3 of the 32 loaded bytes.
-      u32x4 v;
-      const int dw = o >> 1;
-      if (o & 1) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          unsigned lo = d[0], hi = d[1];
-#pragma unroll
-          for (int k = 1; k < 4; ++k)
-            if (dw == k) {
-              lo = d[k + j];
-              hi = d[k + j + 1];
-            }
-          if (dw == 0) {
-            lo = d[j];
-            hi = d[j + 1];
-          }
-          v[j] = __builtin_amdgcn_alignbyte(hi, lo, 2);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          unsigned x = d[j];
-#pragma unroll
-          for (int k = 1; k < 4; ++k)
-            if (dw == k) x = d[k + j];
-          v[j] = x;
-        }
-      }
-      const unsigned bits = ((1u << hi_i) - 1u) & ~((1u << lo_i) - 1u);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        v[j] &= ((bits >> (2 * j)) & 1u ? 0x0000ffffu : 0u) |
-                ((bits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
-      w[q] = v;
-    }
+    const PlanarRunSrc r = planar_run_src(P, t < ntotal ? t : 0);
+    const bool live = t < ntotal && r.lo < r.hi;
+    const int64_t chunk = r.first >= 0 ? r.first >> 3 : -((7 - r.first) >> 3);  // floor(/8)
+    o[q] = static_cast<int>(r.first - chunk * 8);
+    lo[q] = live ? r.lo : 0;
+    hi[q] = live ? r.hi : 0;
+    const bool tail0 = live && chunk >= 0 && chunk * 16 < nbytes && (chunk + 1) * 16 > nbytes;
+    const bool tail1 = live && o[q] > 0 && (chunk + 1) * 16 < nbytes && (chunk + 2) * 16 > nbytes;
+    c0[q] = tail0 ? planar_chunk16_tail(sr, chunk) : planar_chunk(sr, chunk, nbytes, live);
+    c1[q] = tail1 ? planar_chunk16_tail(sr, chunk + 1)
+                  : planar_chunk(sr, chunk + 1, nbytes, live && o[q] > 0);
   }
 #pragma unroll
   for (int q = 0; q < kPlanarRuns; ++q) {
     const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
-    if (t < ntotal) *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = w[q];
+    if (t >= ntotal) continue;
+    const unsigned d[8] = {c0[q][0], c0[q][1], c0[q][2], c0[q][3],
+                           c1[q][0], c1[q][1], c1[q][2], c1[q][3]};
+    // Dword j of the run: bytes 2 o + 4 j .. +3 of the 32 loaded bytes.
+    const int dw = o[q] >> 1;
+    u32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      unsigned a = d[j], b = d[j + 1];
+#pragma unroll
+      for (int k = 1; k < 4; ++k)
+        if (dw == k) {
+          a = d[k + j];
+          b = d[k + j + 1];
+        }
+      v[j] = (o[q] & 1) ? __builtin_amdgcn_alignbyte(b, a, 2) : a;
+    }
+    const unsigned bits = ((1u << hi[q]) - 1u) & ~((1u << lo[q]) - 1u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] &= ((bits >> (2 * j)) & 1u ? 0x0000ffffu : 0u) |
+              ((bits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+    *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = v;
   }
 }
 
-// Split-precision form of the zero-padded channels-first copy: an fp32 source of split_nc
-// (image, channel) rows gives kSplitProducts x split_nc destination rows, destination row
-// block s holding bf16 part split_data_part(s) of every source element. Run t (8 elements, one
-// 16-byte store) loads the three aligned 16-byte chunks that cover its source elements (the
-// buffer's per-dword range check reads zero past the source's end, and an offset before its
-// start is sent out of range); elements outside the source row are zero.
+// Split-precision form: an fp32 source of split_nc (image, channel) rows gives
+// kSplitProducts x split_nc destination rows, destination row block s holding bf16 part
+// split_data_part(s) of every source element. A run's 8 fp32 elements start at element o of
+// the first of three aligned 16-byte chunks (the buffer's per-dword range check reads zero
+// past the source's end).
 __device__ __forceinline__ void pad_planar_split_blocks(const float* src, unsigned short* dst,
                                                         const PlanarPadArgs& P, int64_t total,
                                                         int split_nc, int block) {
-  const int R = P.rank;
-  int in_last = 1, pad_last = 0;
-#pragma unroll
-  for (int a = 0; a < kFastRank; ++a) {
-    if (a == R - 1) {
-      in_last = P.in[a];
-      pad_last = P.pad[a];
-    }
-  }
-  const int chunks = P.pe[R - 1] >> 3;
-  const int rows_per_img = P.pvol / P.pe[R - 1];
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes), 0x00020000);
-  // 32-bit index arithmetic: the planner keeps the copy and the source below 2^31 elements.
+  const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
   const int ntotal = static_cast<int>(total);
-  u32x4 w[kPlanarRuns];
+  u32x4 c0[kPlanarRuns], c1[kPlanarRuns], c2[kPlanarRuns];
+  int o[kPlanarRuns], lo[kPlanarRuns], hi[kPlanarRuns], part[kPlanarRuns];
 #pragma unroll
   for (int q = 0; q < kPlanarRuns; ++q) {
     const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
-    w[q] = u32x4{0u, 0u, 0u, 0u};
-    if (t >= ntotal) continue;
-    const int row = fast_div(t, P.div_chunks);
-    const int u0 = (t - row * chunks) * 8 - pad_last;
-    const int nc = fast_div(row, P.div_rows);
-    const int s = nc / split_nc;
-    const int snc = nc - s * split_nc;
-    const int part = split_data_part(s);
-    int rem = row - nc * rows_per_img;
-    int srow = 0, istr = in_last;
-    bool ok = true;
+    PlanarRunSrc r = planar_run_src(P, t < ntotal ? t : 0);
+    // Destination row block s reads source row nc - s * split_nc.
+    const int s = r.nc / split_nc;
+    r.first -= (int64_t)s * split_nc * P.in_vol;
+    part[q] = split_data_part(s);
+    const bool live = t < ntotal && r.lo < r.hi;
+    const int64_t chunk = r.first >= 0 ? r.first >> 2 : -((3 - r.first) >> 2);  // floor(/4)
+    o[q] = static_cast<int>(r.first - chunk * 4);
+    lo[q] = live ? r.lo : 0;
+    hi[q] = live ? r.hi : 0;
+    c0[q] = planar_chunk(sr, chunk, nbytes, live);
+    c1[q] = planar_chunk(sr, chunk + 1, nbytes, live);
+    c2[q] = planar_chunk(sr, chunk + 2, nbytes, live && o[q] > 0);
+  }
 #pragma unroll
-    for (int a = kFastRank - 2; a >= 0; --a) {
-      if (a < R - 1) {
-        const int qa = fast_div(rem, P.div_pe[a]);
-        const int u = rem - qa * P.pe[a] - P.pad[a];
-        rem = qa;
-        ok = ok && u >= 0 && u < P.in[a];
-        srow += u * istr;
-        istr *= P.in[a];
-      }
-    }
-    const int lo_i = -u0 < 0 ? 0 : (-u0 > 8 ? 8 : -u0);
-    const int hi_i = in_last - u0 < 0 ? 0 : (in_last - u0 > 8 ? 8 : in_last - u0);
-    if (!ok || lo_i >= hi_i) continue;
-    const int64_t first = (int64_t)snc * P.in_vol + srow + u0;
-    const int64_t chunk = first >= 0 ? first >> 2 : -((3 - first) >> 2);  // floor(first / 4)
-    const int o = static_cast<int>(first - chunk * 4);                   // 0 .. 3
-    const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
-    auto load16 = [&](int64_t c) {
-      const unsigned off = c >= 0 && c * 16 < nbytes ? static_cast<unsigned>(c * 16) : 0xfffffff0u;
-      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
-    };
-    const u32x4 c0 = load16(chunk), c1 = load16(chunk + 1);
-    const u32x4 c2 = o > 0 ? load16(chunk + 2) : u32x4{0u, 0u, 0u, 0u};
-    const unsigned d[12] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1],
-                            c1[2], c1[3], c2[0], c2[1], c2[2], c2[3]};
+  for (int q = 0; q < kPlanarRuns; ++q) {
+    const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
+    if (t >= ntotal) continue;
+    const unsigned d[12] = {c0[q][0], c0[q][1], c0[q][2], c0[q][3], c1[q][0], c1[q][1],
+                            c1[q][2], c1[q][3], c2[q][0], c2[q][1], c2[q][2], c2[q][3]};
     unsigned h[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       unsigned x = d[e];
 #pragma unroll
       for (int k = 1; k < 4; ++k)
-        if (o == k) x = d[e + k];
-      h[e] = e >= lo_i && e < hi_i ? bf16_part_bits(__builtin_bit_cast(float, x), part) : 0u;
+        if (o[q] == k) x = d[e + k];
+      h[e] = e >= lo[q] && e < hi[q] ? bf16_part_bits(__builtin_bit_cast(float, x), part[q]) : 0u;
     }
-    w[q] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                 h[6] | (h[7] << 16)};
-  }
-#pragma unroll
-  for (int q = 0; q < kPlanarRuns; ++q) {
-    const int t = (block * kPlanarRuns + q) * kThreads + static_cast<int>(threadIdx.x);
-    if (t < ntotal) *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) = w[q];
+    *reinterpret_cast<u32x4*>(dst + (size_t)t * 8) =
+        u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
   }
 }
 
