@@ -1399,6 +1399,15 @@ TinyPlan plan_tiny(const Geom& g, convnd_hip_dtype dt, int mode) {
     ivol *= in_size[a];
     ovol *= out_size[a];
   }
+  // Axes past the rank: identities (one position, one tap), so the kernels' axis walks need
+  // no rank test.
+  for (int a = R; a < kFastRank; ++a) {
+    A.k[a] = A.s[a] = A.d[a] = A.in_size[a] = A.out_size[a] = A.box[a] = A.nbox[a] = 1;
+    A.hext[a] = 1;
+    A.p[a] = A.box_shift[a] = A.hpitch[a] = 0;
+    A.div_hext[a] = make_fast_div(1u);
+    A.div_k[a] = make_fast_div(1u);
+  }
   A.box_vol = static_cast<int>(box_vol);
   A.halo_vol = static_cast<int>(halo);
   A.k_vol = static_cast<int>(g.k_vol);

@@ -67,6 +67,7 @@ struct TinyArgs {
   int csplit, red_at;           // input-channel slices per workgroup (waves = slots x slices)
                                 // and the LDS element offset of their sums
   int cot;                      // weight gradient: output channels per workgroup (4, 8, 16)
+  // Per axis; entries past `rank` are identities (extent 1, one tap, no padding, box 1).
   int k[kFastRank], s[kFastRank], p[kFastRank], d[kFastRank];
   int in_size[kFastRank], out_size[kFastRank];
   int box[kFastRank], box_shift[kFastRank], nbox[kFastRank];
