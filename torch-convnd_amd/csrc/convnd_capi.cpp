@@ -1312,7 +1312,7 @@ TinyPlan plan_tiny(const Geom& g, convnd_hip_dtype dt, int mode) {
   // gradient: all output channels of the group in one tile of cot.
   // Forward kernel: jw waves of cpw output channels each, times csplit slices of the input
   // channels (their sums added through LDS), at most 8 waves.
-  const int cpw = cog >= 16 ? 4 : (cog >= 8 ? 2 : 1);
+  const int cpw = cog >= 16 ? 4 : (cog >= 2 ? 2 : 1);
   const int64_t jw = std::min<int64_t>(8, (cog + cpw - 1) / cpw);
   int64_t csplit = 1;
   while (csplit * 2 <= cig && jw * csplit * 2 <= 8) csplit *= 2;
@@ -1396,6 +1396,7 @@ TinyPlan plan_tiny(const Geom& g, convnd_hip_dtype dt, int mode) {
     A.nbox[a] = static_cast<int>((out_size[a] + b[a] - 1) / b[a]);
     A.div_hext[a] = make_fast_div(static_cast<unsigned>(A.hext[a]));
     A.div_k[a] = make_fast_div(static_cast<unsigned>(A.k[a]));
+    A.div_nbox[a] = make_fast_div(static_cast<unsigned>(A.nbox[a]));
     ivol *= in_size[a];
     ovol *= out_size[a];
   }
@@ -1407,6 +1408,7 @@ TinyPlan plan_tiny(const Geom& g, convnd_hip_dtype dt, int mode) {
     A.p[a] = A.box_shift[a] = A.hpitch[a] = 0;
     A.div_hext[a] = make_fast_div(1u);
     A.div_k[a] = make_fast_div(1u);
+    A.div_nbox[a] = make_fast_div(1u);
   }
   A.box_vol = static_cast<int>(box_vol);
   A.halo_vol = static_cast<int>(halo);

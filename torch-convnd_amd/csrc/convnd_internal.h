@@ -73,7 +73,7 @@ struct TinyArgs {
   int box[kFastRank], box_shift[kFastRank], nbox[kFastRank];
   int hext[kFastRank], hpitch[kFastRank];
   int box_vol, halo_vol, k_vol, in_vol, out_vol, boxes;
-  FastDiv div_halo, div_hext[kFastRank], div_k[kFastRank];
+  FastDiv div_halo, div_hext[kFastRank], div_k[kFastRank], div_nbox[kFastRank];
   // Halo offset (positions) of every tap, sum over the axes of t_a d_a hpitch_a: read by the
   // forward kernel with uniform (scalar) loads from the kernel arguments.
   int toff[kTinyMaxTaps];

@@ -44,43 +44,53 @@ __device__ __forceinline__ void tiny_box_coords(const TinyArgs& A, int q, int* c
 }
 
 // Stages the input halo of box bx of image n, input channels [c0, c0 + cig) of the tensor, into
-// xh[c][h] (h over the halo, last axis fastest). Four elements per thread and pass, their loads
-// all issued before the first store (a load outside the input reads element 0 and is replaced
-// by zero), so each thread waits for memory once per pass.
+// xh[c][h] (h over the halo, last axis fastest). A thread takes kPos halo positions per pass:
+// their input offsets come from one axis walk each, and the loads of up to 8 channels at each
+// (a load outside the input reads element 0 and is replaced by zero) are all issued before the
+// first store, so a pass waits for memory once. Most tiny layers stage in a single pass.
 template <typename T, int NA>
 __device__ __forceinline__ void tiny_stage_halo(const TinyArgs& A, const T* in, int n, int c0,
                                                 const int* origin, TinyAcc<T>* xh) {
   using Acc = TinyAcc<T>;
-  constexpr int kBatch = 4;
-  const int total = A.cig * A.halo_vol;
+  constexpr int kPos = 2, kCh = 8;
   const int nt = blockDim.x;
-  for (int e0 = threadIdx.x; e0 < total; e0 += kBatch * nt) {
-    T raw[kBatch];
-    bool keep[kBatch];
+  const int hv = A.halo_vol;
+  const size_t iv = static_cast<size_t>(A.in_vol);
+  const T* src = in + ((size_t)n * A.cin_total + c0) * iv;
+  for (int h0 = threadIdx.x; h0 < hv; h0 += kPos * nt) {
+    int off[kPos];
+    bool ok[kPos];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int e = e0 + u * nt;
-      const int c = fast_div(e, A.div_halo);
-      int h = e - c * A.halo_vol;
-      int off = 0, stride = 1;
-      bool ok = e < total;
+    for (int u = 0; u < kPos; ++u) {
+      int h = h0 + u * nt;
+      ok[u] = h < hv;
+      int o = 0, stride = 1;
 #pragma unroll
       for (int a = NA - 1; a >= 0; --a) {
         const int q = fast_div(h, A.div_hext[a]);
-        const int ha = h - q * A.hext[a];
+        const int x = origin[a] * A.s[a] - A.p[a] + (h - q * A.hext[a]);
         h = q;
-        const int x = origin[a] * A.s[a] - A.p[a] + ha;
-        ok = ok && x >= 0 && x < A.in_size[a];
-        off += x * stride;
+        ok[u] = ok[u] && x >= 0 && x < A.in_size[a];
+        o += x * stride;
         stride *= A.in_size[a];
       }
-      keep[u] = ok;
-      raw[u] = in[ok ? ((size_t)n * A.cin_total + c0 + c) * A.in_vol + off : 0];
+      off[u] = ok[u] ? o : 0;
     }
+    for (int cb = 0; cb < A.cig; cb += kCh) {
+      T raw[kPos][kCh];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int e = e0 + u * nt;
-      if (e < total) xh[e] = keep[u] ? widen<Acc>(raw[u]) : Acc(0);
+      for (int u = 0; u < kPos; ++u)
+#pragma unroll
+        for (int k = 0; k < kCh; ++k)
+          if (cb + k < A.cig) raw[u][k] = src[(size_t)(cb + k) * iv + off[u]];
+#pragma unroll
+      for (int u = 0; u < kPos; ++u) {
+        const int h = h0 + u * nt;
+#pragma unroll
+        for (int k = 0; k < kCh; ++k)
+          if (cb + k < A.cig && h < hv)
+            xh[(size_t)(cb + k) * hv + h] = ok[u] ? widen<Acc>(raw[u][k]) : Acc(0);
+      }
     }
   }
 }
@@ -108,8 +118,7 @@ __global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
     int r = bx;
 #pragma unroll
     for (int a = NA - 1; a >= 0; --a) {
-      origin[a] = 0;
-      const int q = r / A.nbox[a];
+      const int q = fast_div(r, A.div_nbox[a]);
       origin[a] = (r - q * A.nbox[a]) * A.box[a];
       r = q;
     }
@@ -138,25 +147,32 @@ __global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
     ostride *= A.out_size[a];
   }
   const bool wave_live = j0 < A.cog;
+  // Lanes past the box compute on halo position 0 and store nothing: the channel loop then
+  // has wave-uniform bounds, so its weight loads stay scalar.
+  if (!inside) posoff = 0;
   const int c_lo = cs * A.cig / A.csplit;
   const int c_hi = (cs + 1) * A.cig / A.csplit;
   // Weights W(j, c, t): forward w[g cog + j][c][t]; input gradient w[g cig + c][j][K - 1 - t]
   // (the kernel's reduction channels are the convolution's output channels). A channel past
-  // the group's reads channel j0 and is not stored. Taps go in chunks of 8: the chunk's tap
+  // the group's reads channel j0 and is not stored. Taps go in chunks of 16: the chunk's tap
   // offsets (kernel arguments) and weights are uniform scalar loads, then 8 LDS reads of the
   // lane's input values, then the 8 x CPW FMAs.
-  const T* w = static_cast<const T*>(A.w);
+  // Weights through the scalar cache: the constant address space makes the wave-uniform loads
+  // scalar loads (s_load, 8 taps at a time), which take neither the LDS nor the vector memory
+  // path that the lanes' input reads use.
+  using CT = __attribute__((address_space(4))) const T;
+  CT* w = (CT*)A.w;  // address-space conversion (a C-style cast: no C++ cast performs it)
   int jj[CPW];
 #pragma unroll
   for (int i = 0; i < CPW; ++i) jj[i] = j0 + i < A.cog ? j0 + i : j0;
   Acc acc[CPW];
 #pragma unroll
   for (int i = 0; i < CPW; ++i) acc[i] = 0;
-  constexpr int kChunk = 8;
+  constexpr int kChunk = 16;
   const int kv = A.k_vol;
-  for (int c = wave_live && inside ? c_lo : c_hi; c < c_hi; ++c) {
+  for (int c = wave_live ? c_lo : c_hi; c < c_hi; ++c) {
     const Acc* xc = xh + (size_t)c * A.halo_vol + posoff;
-    const T* wr[CPW];
+    CT* wr[CPW];
 #pragma unroll
     for (int i = 0; i < CPW; ++i)
       wr[i] = A.mode == 0 ? w + ((size_t)(g * A.cog + jj[i]) * A.cig + c) * kv
@@ -239,8 +255,7 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
     int r = bx;
 #pragma unroll
     for (int a = NA - 1; a >= 0; --a) {
-      origin[a] = 0;
-      const int q = r / A.nbox[a];
+      const int q = fast_div(r, A.div_nbox[a]);
       origin[a] = (r - q * A.nbox[a]) * A.box[a];
       r = q;
     }
@@ -294,6 +309,9 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
 #pragma unroll
     for (int j = 0; j < COG; ++j) acc[j] = 0;
     typedef Acc acc4 __attribute__((ext_vector_type(4)));
+    // Unrolled so that the position offsets (uniform), the input values and the grad_output
+    // rows of several positions are in flight together.
+#pragma unroll 8
     for (int q = 0; q < A.box_vol; ++q) {
       const Acc v = xc[posl[q]];
       const acc4* dq = reinterpret_cast<const acc4*>(dyt + q * COG);
