@@ -489,103 +489,122 @@ void igemm_kernel(IgemmArgs A) {
   // 4*lg .. 4*lg+3 of its position block. In a box inside the output whose rows have at
   // least 4 positions on a unit output step they are adjacent: one 8-byte store for 16-bit
   // O, 16 bytes for float. Otherwise every position has its own offset and bounds check.
-  O* out = static_cast<O*>(A.out);
-  const int act = A.act;
-  const size_t chan0 = (size_t)n * A.cout_total + (size_t)g * A.cout_g;
-  O* obox = out + box.out_origin;
-  if (A.out_cl) {
-    // Channels-last output: output channel m of position q at
-    // ((n*out_vol + q)*cout_total + g*cout_g + m); sixteen lanes write one position's 16
-    // consecutive channels.
-    const size_t ostride = static_cast<size_t>(A.cout_total);
-    O* ocl = out + ((size_t)n * A.out_vol + box.out_origin) * ostride + (size_t)g * A.cout_g;
-    const bool inside = A.packed_ok && (flags & 2);
-    int off[NB][4];
-    {
+  // The activation is a compile-time constant of each epilogue copy, dispatched once: every
+  // copy's code is contiguous (a launch starts on a cold instruction cache, and per-element
+  // branches over the activations' code would spread the executed instructions over many
+  // more cache lines).
+  auto epilogue = [&](auto act_c) {
+    constexpr int kAct = decltype(act_c)::value;
+    O* out = static_cast<O*>(A.out);
+    const size_t chan0 = (size_t)n * A.cout_total + (size_t)g * A.cout_g;
+    O* obox = out + box.out_origin;
+    if (A.out_cl) {
+      // Channels-last output: output channel m of position q at
+      // ((n*out_vol + q)*cout_total + g*cout_g + m); sixteen lanes write one position's 16
+      // consecutive channels.
+      const size_t ostride = static_cast<size_t>(A.cout_total);
+      O* ocl = out + ((size_t)n * A.out_vol + box.out_origin) * ostride + (size_t)g * A.cout_g;
+      const bool inside = A.packed_ok && (flags & 2);
+      int off[NB][4];
+      {
+        const unsigned long long lim = box.lim;
+        const unsigned long long guard = A.coord_bits == 16 ? kGuard16 : kGuard8;
+        const unsigned long long ones = A.coord_bits == 16 ? kOnes16 : kOnes8;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int q = (wn * NB + nb) * 16 + 4 * lg + i;
+            if (inside) {
+              off[nb][i] = posout[q];
+            } else {
+              const int4 e = pt[q];
+              const unsigned long long c = static_cast<unsigned>(e.z) |
+                                           (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
+              off[nb][i] = swar_all_less(c, lim, guard, ones) ? e.y : -1;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = (mt0 + mb) * 16 + (lane & 15);
+        if (m >= A.cout_g) continue;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (off[nb][i] >= 0)
+              ocl[(size_t)off[nb][i] * ostride + m] =
+                  static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], kAct));
+        }
+      }
+    } else if (A.packed_ok && (flags & 2)) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = (mt0 + mb) * 16 + (lane & 15);
+        if (m >= A.cout_g) continue;
+        O* orow = obox + (chan0 + m) * A.out_vol;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          O v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], kAct));
+          O* dst = orow + posout[(wn * NB + nb) * 16 + 4 * lg];
+          if constexpr (sizeof(O) == 2) {
+            uint2 w;
+            w.x = __builtin_bit_cast(unsigned short, v[0]) |
+                  ((unsigned)__builtin_bit_cast(unsigned short, v[1]) << 16);
+            w.y = __builtin_bit_cast(unsigned short, v[2]) |
+                  ((unsigned)__builtin_bit_cast(unsigned short, v[3]) << 16);
+            *reinterpret_cast<uint2*>(dst) = w;
+          } else {
+            *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+          }
+        }
+      }
+    } else {
       const unsigned long long lim = box.lim;
       const unsigned long long guard = A.coord_bits == 16 ? kGuard16 : kGuard8;
       const unsigned long long ones = A.coord_bits == 16 ? kOnes16 : kOnes8;
+      int off[NB][4];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int q = (wn * NB + nb) * 16 + 4 * lg + i;
-          if (inside) {
-            off[nb][i] = posout[q];
-          } else {
-            const int4 e = pt[q];
-            const unsigned long long c = static_cast<unsigned>(e.z) |
-                                         (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
-            off[nb][i] = swar_all_less(c, lim, guard, ones) ? e.y : -1;
-          }
+          const int4 e = pt[(wn * NB + nb) * 16 + 4 * lg + i];
+          const unsigned long long c =
+              static_cast<unsigned>(e.z) | (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
+          off[nb][i] = swar_all_less(c, lim, guard, ones) ? e.y : -1;
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int m = (mt0 + mb) * 16 + (lane & 15);
+        if (m >= A.cout_g) continue;
+        O* orow = obox + (chan0 + m) * A.out_vol;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (off[nb][i] >= 0)
+              orow[off[nb][i]] = static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], kAct));
         }
       }
     }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int m = (mt0 + mb) * 16 + (lane & 15);
-      if (m >= A.cout_g) continue;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (off[nb][i] >= 0)
-            ocl[(size_t)off[nb][i] * ostride + m] =
-                static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], act));
-      }
-    }
-  } else if (A.packed_ok && (flags & 2)) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int m = (mt0 + mb) * 16 + (lane & 15);
-      if (m >= A.cout_g) continue;
-      O* orow = obox + (chan0 + m) * A.out_vol;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        O v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], act));
-        O* dst = orow + posout[(wn * NB + nb) * 16 + 4 * lg];
-        if constexpr (sizeof(O) == 2) {
-          uint2 w;
-          w.x = __builtin_bit_cast(unsigned short, v[0]) |
-                ((unsigned)__builtin_bit_cast(unsigned short, v[1]) << 16);
-          w.y = __builtin_bit_cast(unsigned short, v[2]) |
-                ((unsigned)__builtin_bit_cast(unsigned short, v[3]) << 16);
-          *reinterpret_cast<uint2*>(dst) = w;
-        } else {
-          *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-        }
-      }
-    }
-  } else {
-    const unsigned long long lim = box.lim;
-    const unsigned long long guard = A.coord_bits == 16 ? kGuard16 : kGuard8;
-    const unsigned long long ones = A.coord_bits == 16 ? kOnes16 : kOnes8;
-    int off[NB][4];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int4 e = pt[(wn * NB + nb) * 16 + 4 * lg + i];
-        const unsigned long long c =
-            static_cast<unsigned>(e.z) | (static_cast<unsigned long long>(static_cast<unsigned>(e.w)) << 32);
-        off[nb][i] = swar_all_less(c, lim, guard, ones) ? e.y : -1;
-      }
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int m = (mt0 + mb) * 16 + (lane & 15);
-      if (m >= A.cout_g) continue;
-      O* orow = obox + (chan0 + m) * A.out_vol;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (off[nb][i] >= 0)
-            orow[off[nb][i]] = static_cast<O>(epilogue_act(acc[mb][nb][i] + bias_v[mb], act));
-      }
-    }
+  };
+  switch (A.act) {
+    case CONVND_HIP_ACT_RELU:
+      epilogue(std::integral_constant<int, CONVND_HIP_ACT_RELU>{});
+      break;
+    case CONVND_HIP_ACT_GELU:
+      epilogue(std::integral_constant<int, CONVND_HIP_ACT_GELU>{});
+      break;
+    case CONVND_HIP_ACT_GELU_TANH:
+      epilogue(std::integral_constant<int, CONVND_HIP_ACT_GELU_TANH>{});
+      break;
+    default:
+      epilogue(std::integral_constant<int, CONVND_HIP_ACT_NONE>{});
   }
 }
 
