@@ -288,21 +288,33 @@ void igemm_kernel(IgemmArgs A) {
       const unsigned chan = img_chan + static_cast<unsigned>(ck * A.cc + o * 8);
       const unsigned pos = static_cast<unsigned>(ro + (jlo + jj) * 8);
       const unsigned cl_chan = static_cast<unsigned>(g * A.cin_g + ck * A.cc + o * 8);
+      unsigned offs[8];
+      bool straddle = false;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const unsigned off =
             ro < 0 ? kPast
                    : (in_cl ? ((cl_img + pos + i) * cl_stride + cl_chan) * 2u
                             : ((chan + i) * in_vol + pos) * 2u);
+        offs[i] = off;
         v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
-        // The buffer's range check is per dword: a dword straddling the tensor's end reads
-        // zero, valid half included. A run that crosses the end loads element by element.
-        if (off < in_bytes && off + 16u > in_bytes) {
+        straddle = straddle || (off < in_bytes && off + 16u > in_bytes);
+      }
+      // The buffer's range check is per dword: a dword straddling the tensor's end reads
+      // zero, valid half included. A run that crosses the end loads element by element (one
+      // rarely taken branch per task, so the common path's code stays contiguous).
+      if (straddle) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const unsigned lo = __builtin_amdgcn_raw_buffer_load_b16(srsrc, off + 4u * k, 0, 0);
-            const unsigned hi = __builtin_amdgcn_raw_buffer_load_b16(srsrc, off + 4u * k + 2u, 0, 0);
-            v[i][k] = lo | (hi << 16);
+        for (int i = 0; i < 8; ++i) {
+          const unsigned off = offs[i];
+          if (off < in_bytes && off + 16u > in_bytes) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const unsigned lo = __builtin_amdgcn_raw_buffer_load_b16(srsrc, off + 4u * k, 0, 0);
+              const unsigned hi =
+                  __builtin_amdgcn_raw_buffer_load_b16(srsrc, off + 4u * k + 2u, 0, 0);
+              v[i][k] = lo | (hi << 16);
+            }
           }
         }
       }
@@ -340,10 +352,13 @@ void igemm_kernel(IgemmArgs A) {
     };
     // Tasks past the ones held in registers: loaded and written in place (not overlapped).
     auto stage_rest = [&](int ck, unsigned char* buf) {
-      for (int t = tid + kPf * kWT; t < ntask; t += kWT) {
-        u32x4 v[8];
-        task_load(ck, t, v);
-        task_store(t, v, buf);
+      // Two tasks per pass, both tasks' loads in flight before the stores.
+      for (int t = tid + kPf * kWT; t < ntask; t += 2 * kWT) {
+        u32x4 v0[8], v1[8];
+        task_load(ck, t, v0);
+        task_load(ck, t + kWT, v1);
+        task_store(t, v0, buf);
+        task_store(t + kWT, v1, buf);
       }
     };
     __syncthreads();  // row tables in LDS
