@@ -800,7 +800,10 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
     return false;
   // The planar copy's source is addressed by 32-bit byte offsets.
   if (g.batch * g.channels * g.in_vol * element_size(dt) > 0xffffffe0ll) return false;
+  // Split precision: the GEMM runs over kSplit part products per image, read from copies that
+  // hold each of the three bf16 parts once (of the input and of grad_output).
   const int64_t batch = split ? g.batch * kSplit : g.batch;
+  const int64_t sbatch = split ? g.batch * 3 : g.batch;
   const int R = g.rank;
   if (g.s[R - 1] != 1) return false;
   const int cin_g = static_cast<int>(g.cin_g), cout_g = static_cast<int>(g.cout_g);
@@ -856,12 +859,12 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
         if (pvol > kI32Safe) return;
       }
       // The padded copy must stay int32-addressable and not dwarf the input.
-      if (pvol * batch * g.channels * 2 > kI32Safe || pvol > 8 * g.in_vol + (1 << 20)) return;
+      if (pvol * sbatch * g.channels * 2 > kI32Safe || pvol > 8 * g.in_vol + (1 << 20)) return;
       const int bl8 = bl / 8;
       const int nrho = kl * bl8;
       const int runpitch = nrho * 16;
       const int64_t chpitch = rows_h * runpitch;
-      if (dvol * batch * g.out_channels > kI32Safe / 2) return;
+      if (dvol * sbatch * g.out_channels > kI32Safe / 2) return;
       const int64_t items = boxes * batch;
       if (items > (int64_t{1} << 22)) return;
       const int64_t dyt_bytes = (int64_t)mb * 16 * box_vol * 2;
@@ -945,12 +948,13 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
         plan.lds = static_cast<size_t>(lds);
         // Split precision always reads grad_output's padded part copy.
         plan.exact = dvol == g.out_vol && !split;
-        plan.staged_elems = (size_t)batch * g.channels * pvol;
+        plan.staged_elems = (size_t)sbatch * g.channels * pvol;
         WgradCmArgs& C = plan.cm_args;
         std::memset(&C, 0, sizeof(C));
         C.x_bytes = static_cast<unsigned>(plan.staged_elems * 2);
         C.rank = R;
         C.batch = static_cast<int>(batch);
+        C.split_n = split ? static_cast<int>(g.batch) : 0;
         C.groups = static_cast<int>(g.groups);
         C.cin_g = cin_g;
         C.cout_g = cout_g;
@@ -1015,7 +1019,7 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
         WgradArgs& D = plan.args;
         std::memset(&D, 0, sizeof(D));
         D.rank = R;
-        D.batch = C.batch;
+        D.batch = static_cast<int>(sbatch);
         D.cout_total = C.cout_total;
         D.dvol = C.dvol;
         int ovol = 1;
@@ -1031,8 +1035,7 @@ bool plan_wgrad_cm(const Geom& g, convnd_hip_dtype dt, const PlanFilter& filter,
   }
   if (!plan.ok) return false;
   if (wgrad_cm_table_layout(plan.cm_args) > (size_t)kI32Safe) return false;
-  plan.dy_pad_elems =
-      plan.exact ? 0 : (size_t)plan.cm_args.batch * plan.cm_args.dvol * g.out_channels;
+  plan.dy_pad_elems = plan.exact ? 0 : (size_t)plan.args.batch * plan.cm_args.dvol * g.out_channels;
   plan.partial_elems = (size_t)plan.cm_args.npc * wgrad_cm_partial_slots(plan.mb, plan.cm_args) * 4;
   *out = plan;
   return true;
@@ -1970,9 +1973,15 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
     pp.pp = &b.wg.ppad;
     pp.x = input;
     pp.x_pp = ws + b.off_x_stage;
-    pp.pp_batch = CA.batch;
-    // Split-precision fp32: part images of both operands (kSplit x batch of each).
-    pp.split_batch = dtype == CONVND_HIP_FLOAT32 ? static_cast<int>(g.batch) : 0;
+    pp.pp_batch = WA.batch;
+    // Split-precision fp32: the three bf16 part images of both operands (the item table pairs
+    // them into the six products).
+    if (dtype == CONVND_HIP_FLOAT32) {
+      pp.split_batch = static_cast<int>(g.batch);
+      pp.pp_blocks = 3;
+      pp.pp_part_map = kSplitPartsMap;
+      pp.dy_part_map = kSplitPartsMap;
+    }
     CA.partial = reinterpret_cast<float*>(ws + b.off_partial);
     CA.dy_bytes = static_cast<unsigned>(g.batch * g.out_channels * g.out_vol * 2);
     // grad_output is read in 16-byte runs of whole boxes: pad it to whole boxes unless the

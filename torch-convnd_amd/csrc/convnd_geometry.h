@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "convnd_internal.h"
+#include "convnd_types.h"
 
 namespace convnd {
 
@@ -672,8 +673,16 @@ inline void wgrad_cm_build_tables(const WgradCmArgs& A, unsigned char* tab) {
   for (int it = 0; it < A.items; ++it) {
     const int n = it / boxes;
     int bb = it - n * boxes;
-    long long xbase = (long long)n * A.cin_total * A.pvol;
-    long long dbase = (long long)n * A.cout_total * A.dvol;
+    // Split precision: batch block s pairs part split_data_part(s) of the input with part
+    // split_other_part(s) of grad_output, each copy holding the three parts once.
+    int xn = n, dn = n;
+    if (A.split_n > 0) {
+      const int s = n / A.split_n, i = n - s * A.split_n;
+      xn = split_data_part(s) * A.split_n + i;
+      dn = split_other_part(s) * A.split_n + i;
+    }
+    long long xbase = (long long)xn * A.cin_total * A.pvol;
+    long long dbase = (long long)dn * A.cout_total * A.dvol;
     for (int a = R - 1; a >= 0; --a) {
       const int j0 = (bb % A.nbox[a]) * A.box[a];
       bb /= A.nbox[a];

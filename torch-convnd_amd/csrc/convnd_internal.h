@@ -271,6 +271,10 @@ struct WgradCmArgs {
   // channel cq / cpc only, so it stages one channel's runs.
   int kvp, tpc, cpc;
   int npc, items, items_per_pc;
+  // Split-precision fp32: images per part block (0 otherwise). Item n of batch block s reads
+  // part split_data_part(s) of image n % split_n from the padded input's part copies and
+  // part split_other_part(s) from grad_output's (three part images each).
+  int split_n;
   int lds_items;        // dynamic LDS byte offset of the item records (after the run table)
   int box[kFastRank], nbox[kFastRank], dext[kFastRank], hext[kFastRank], pe[kFastRank];
   int k[kFastRank], s[kFastRank], d[kFastRank];
@@ -412,10 +416,18 @@ int64_t prologue_sum_blocks(int64_t batch, int64_t volume);
 //   octets:     zero-padded octet-major input for the weight gradient (pad);
 //   dy_pad:     grad_output padded to whole boxes for the weight gradient (wg);
 //   planar pad: zero-padded channels-first input for the channel-major weight gradient
-//               (pp; an fp32 source gives pp_batch = 6 x split_batch bf16 part images,
-//               image n holding part split_data_part(n / split_batch) of image
-//               n % split_batch);
+//               (pp; an fp32 source gives pp_batch = pp_blocks x split_batch bf16 part
+//               images, image n holding part split_map_part(pp_part_map, n / split_batch)
+//               of image n % split_batch);
 //   sums:       channel partial sums of a channels-first 16-bit tensor (bias gradient).
+// Split-precision part maps: 4 bits per image block, block s of a copy holding bf16 part
+// (map >> 4 s) & 15 of every source image. kSplitDataMap / kSplitOtherMap: the six products'
+// parts of the data and the other operand (blocks 0..5, the order of split_data_part /
+// split_other_part); kSplitPartsMap: a copy of the three parts themselves.
+constexpr int kSplitBlocks = 6;
+constexpr unsigned kSplitDataMap = 0x120100u;   // 0, 0, 1, 0, 2, 1
+constexpr unsigned kSplitOtherMap = 0x102010u;  // 0, 1, 0, 2, 0, 1
+constexpr unsigned kSplitPartsMap = 0x210u;     // 0, 1, 2
 struct IgemmArgs;
 struct WgradArgs;
 struct PrologueParts {
@@ -435,9 +447,12 @@ struct PrologueParts {
   const void* dy = nullptr;
   void* dy_pad = nullptr;
   int split_batch = 0;  // fp32 source: images per part block (dy_pad and planar pad)
+  unsigned dy_part_map = kSplitOtherMap;  // part of each block of dy_pad
   const PlanarPadArgs* pp = nullptr;  // zero-padded channels-first input (x -> x_pp)
   void* x_pp = nullptr;
   int64_t pp_batch = 0;
+  int pp_blocks = kSplitBlocks;       // fp32 source: part blocks of x_pp
+  unsigned pp_part_map = kSplitDataMap;  // and the part each holds
   // Channel partial sums of a channels-first 16-bit tensor [sum_batch][sum_channels]
   // [sum_volume] in the layout of the GEMM-input copy's sums (octet_sum_blocks per channel).
   const void* sum_src = nullptr;

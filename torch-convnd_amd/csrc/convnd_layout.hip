@@ -54,6 +54,7 @@ struct DevPrologue {
   const void* dy;
   void* dy_pad;
   int split_batch;
+  unsigned dy_part_map;  // split precision: part of each image block of dy_pad
   int64_t runs;
   int d_blocks;
   // Zero-padded channels-first input for the channel-major weight gradient.
@@ -63,6 +64,7 @@ struct DevPrologue {
   int64_t e_total;
   int e_blocks;
   int e_split_nc;  // split precision: source (image, channel) rows of each part block
+  unsigned e_part_map;  // and the part each block holds
   // Channel partial sums of a channels-first 16-bit tensor (bias gradient): block (image,
   // channel, run of kSumRun positions) -> f_sums[c * (batch * f_nrun) + n * f_nrun + run].
   const void* f_src;
@@ -159,7 +161,7 @@ void prologue_kernel(DevPrologue P) {
   b -= P.c_blocks;
   if (b < P.d_blocks) {
     stage::pad_dy16_blocks<S>(static_cast<const S*>(P.dy), static_cast<unsigned short*>(P.dy_pad),
-                              P.wg, P.split_batch, P.runs, b, P.d_blocks);
+                              P.wg, P.split_batch, P.dy_part_map, P.runs, b, P.d_blocks);
     return;
   }
   b -= P.d_blocks;
@@ -167,7 +169,7 @@ void prologue_kernel(DevPrologue P) {
     if constexpr (SPLIT) {
       stage::pad_planar_split_blocks(static_cast<const float*>(P.xpp_src),
                                      static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total,
-                                     P.e_split_nc, b);
+                                     P.e_split_nc, P.e_part_map, b);
     } else {
       stage::pad_planar16_blocks(static_cast<const unsigned short*>(P.xpp_src),
                                  static_cast<unsigned short*>(P.x_pp), P.ppa, P.e_total, b);
@@ -474,6 +476,7 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     P.dy = p.dy;
     P.dy_pad = p.dy_pad;
     P.split_batch = p.split_batch;
+    P.dy_part_map = p.dy_part_map;
     int dlast = 8;
     for (int i = 0; i < a.rank; ++i)
       if (i == a.rank - 1) dlast = a.dext[i];
@@ -483,10 +486,12 @@ hipError_t launch_prologue(convnd_hip_dtype dtype, const PrologueParts& p, hipSt
     total += P.d_blocks;
   }
   if (p.x_pp != nullptr && p.pp != nullptr) {
-    // Split precision: pp_batch = kSplitProducts x split_batch part images.
-    if (split && (p.split_batch <= 0 || p.pp_batch != (int64_t)kSplitProducts * p.split_batch))
+    // Split precision: pp_batch = pp_blocks x split_batch part images.
+    if (split && (p.split_batch <= 0 || p.pp_blocks < 1 || p.pp_blocks > kSplitProducts ||
+                  p.pp_batch != (int64_t)p.pp_blocks * p.split_batch))
       return hipErrorInvalidValue;
     P.e_split_nc = split ? p.split_batch * p.pp->channels : 0;
+    P.e_part_map = p.pp_part_map;
     P.ppa = *p.pp;
     P.xpp_src = p.x;
     P.x_pp = p.x_pp;

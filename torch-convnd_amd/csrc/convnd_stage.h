@@ -309,11 +309,12 @@ __device__ __forceinline__ void octets16_block(const Src* src, unsigned short* d
 // Zero-padded copy of grad_output: dst[nc][u...] = src[nc][u...] for u inside the output
 // extents, else zero; each thread writes 8 consecutive elements of the last axis (whose
 // padded extent is a multiple of 8). Src = float (split precision): destination image n of
-// A.batch = kSplitProducts x split_batch holds part split_other_part(n / split_batch) of
+// A.batch = blocks x split_batch holds part split_map_part(part_map, n / split_batch) of
 // source image n % split_batch.
 template <typename Src>
 __device__ __forceinline__ void pad_dy16_blocks(const Src* src, unsigned short* dst,
                                                 const WgradArgs& A, int split_batch,
+                                                unsigned part_map,
                                                 int64_t total_runs, int block, int nblocks) {
   const int R = A.rank;
   int dlast = 8, olast = 1;
@@ -337,7 +338,7 @@ __device__ __forceinline__ void pad_dy16_blocks(const Src* src, unsigned short* 
     if constexpr (sizeof(Src) == 4) {
       const int64_t n = nc / A.cout_total, c = nc - n * A.cout_total;
       snc = (n % split_batch) * A.cout_total + c;
-      part = split_other_part(static_cast<int>(n / split_batch));
+      part = split_map_part(part_map, static_cast<int>(n / split_batch));
     }
     int srow = 0, istr = olast;
     bool ok = true;
@@ -489,14 +490,16 @@ __device__ __forceinline__ void pad_planar16_blocks(const unsigned short* src,
   }
 }
 
-// Split-precision form: an fp32 source of split_nc (image, channel) rows gives
-// kSplitProducts x split_nc destination rows, destination row block s holding bf16 part
-// split_data_part(s) of every source element. A run's 8 fp32 elements start at element o of
+// Split-precision form: an fp32 source of split_nc (image, channel) rows gives blocks of
+// split_nc destination rows, destination row block s holding bf16 part
+// split_map_part(part_map, s) of every source element. A run's 8 fp32 elements start at
+// element o of
 // the first of three aligned 16-byte chunks (the buffer's per-dword range check reads zero
 // past the source's end).
 __device__ __forceinline__ void pad_planar_split_blocks(const float* src, unsigned short* dst,
                                                         const PlanarPadArgs& P, int64_t total,
-                                                        int split_nc, int block) {
+                                                        int split_nc, unsigned part_map,
+                                                        int block) {
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(src), static_cast<short>(0), static_cast<int>(P.src_bytes), 0x00020000);
   const int64_t nbytes = static_cast<int64_t>(P.src_bytes);
@@ -510,7 +513,7 @@ __device__ __forceinline__ void pad_planar_split_blocks(const float* src, unsign
     // Destination row block s reads source row nc - s * split_nc.
     const int s = r.nc / split_nc;
     r.first -= (int64_t)s * split_nc * P.in_vol;
-    part[q] = split_data_part(s);
+    part[q] = split_map_part(part_map, s);
     const bool live = t < ntotal && r.lo < r.hi;
     const int64_t chunk = r.first >= 0 ? r.first >> 2 : -((3 - r.first) >> 2);  // floor(/4)
     o[q] = static_cast<int>(r.first - chunk * 4);

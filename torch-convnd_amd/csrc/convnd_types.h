@@ -45,11 +45,16 @@ __device__ __forceinline__ T narrow(A v) {
 // every product that meets an infinity carries the sign of x*w and a zero only meets it
 // where w or x itself is zero -- as in an fp32 GEMM (inf * 0 = NaN; inf * w = +-inf).
 constexpr int kSplitProducts = 6;
-__device__ __forceinline__ int split_data_part(int s) {
+__host__ __device__ __forceinline__ int split_data_part(int s) {
   return s == 2 || s == 5 ? 1 : (s == 4 ? 2 : 0);
 }
-__device__ __forceinline__ int split_other_part(int s) {
+__host__ __device__ __forceinline__ int split_other_part(int s) {
   return s == 1 || s == 5 ? 1 : (s == 3 ? 2 : 0);
+}
+// Part of image block s of a split-precision copy with part map `map` (kSplitDataMap ... in
+// convnd_internal.h).
+__host__ __device__ __forceinline__ int split_map_part(unsigned map, int s) {
+  return static_cast<int>((map >> (4 * s)) & 15u);
 }
 __host__ __device__ __forceinline__ unsigned short bf16_part_bits(float v, int part) {
   const unsigned bits = __builtin_bit_cast(unsigned, v);
