@@ -158,7 +158,7 @@ struct IgemmArgs {
   FastDiv div_mt, div_kc, div_nchunk, div_groups;
 };
 
-constexpr int kTapPad = 8;
+constexpr int kTapPad = 16;  // tap-table entries past the last step (prefetch distance)
 
 // Per (phase, box) state of the implicit GEMM (64 bytes).
 struct IgemmBox {
