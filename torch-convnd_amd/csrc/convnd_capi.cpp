@@ -2031,12 +2031,30 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
                    "bias gradient");
     if (st != CONVND_HIP_SUCCESS) return st;
   }
+  // Both gradients on the tiny-channel kernels: the weight gradient's partial sums first, and
+  // their reduction as extra workgroups of the input-gradient launch (one launch fewer).
+  const bool tiny_fused = gi && b.tdx.ok && gw && b.tdw.ok && b.tdx.args.waves >= 4;
+  TinyReduceArgs carried{};
+  if (tiny_fused) {
+    TinyArgs T = b.tdw.args;
+    T.in = input;
+    T.w = weight;
+    T.dy = grad_output;
+    const auto ev = timing_begin(2, stream);
+    st = hip_check(launch_tiny_wgrad_partials(dtype, T, b.tdw.wlds, ws + b.off_tpart,
+                                              ws + b.off_tbpart, grad_weight,
+                                              tiny_bias ? grad_bias : nullptr, &carried, stream),
+                   "tiny-channel weight gradient");
+    timing_end(ev, stream);
+    if (st != CONVND_HIP_SUCCESS) return st;
+  }
   if (gi && b.tdx.ok) {
     TinyArgs T = b.tdx.args;
     T.in = grad_output;
     T.w = weight;
     T.bias = nullptr;
     T.out = grad_input;
+    if (tiny_fused) T.red = carried;
     const auto ev = timing_begin(1, stream);
     st = hip_check(launch_tiny_conv(dtype, T, b.tdx.lds, stream), "tiny-channel input gradient");
     timing_end(ev, stream);
@@ -2054,7 +2072,7 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
     }
     if (st != CONVND_HIP_SUCCESS) return st;
   }
-  if (gw && b.tdw.ok) {
+  if (gw && b.tdw.ok && !tiny_fused) {
     TinyArgs T = b.tdw.args;
     T.in = input;
     T.w = weight;
@@ -2065,7 +2083,7 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
                    "tiny-channel weight gradient");
     timing_end(ev, stream);
     if (st != CONVND_HIP_SUCCESS) return st;
-  } else if (gw) {
+  } else if (gw && !b.tdw.ok) {
     if (mfma_dw) {
       const auto ev = timing_begin(2, stream);
       st = hip_check(b.wg.cm ? launch_wgrad_cm(dtype, b.wg.mb, CA, b.wg.lds, stream)

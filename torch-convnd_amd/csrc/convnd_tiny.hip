@@ -100,6 +100,66 @@ __device__ __forceinline__ void tiny_tap_offsets(const TinyArgs& A, int* toff) {
   for (int t = threadIdx.x; t < A.k_vol; t += blockDim.x) toff[t] = A.toff[t];
 }
 
+// dW[g cog + co][c][t] = sum over the workgroups blk of image/box of part[blk][co][c][t] (blocks
+// of group g only), and db likewise from bpart. Reduction block `block` covers 16 consecutive
+// output elements (the thread's low 4 bits) and splits the workgroups into 16 interleaved sets
+// (threads 16 .. 255's high bits; threads past 256 idle), eight loads in flight per thread;
+// the 16 set sums are added in order through LDS (fixed order: deterministic, the same in the
+// stand-alone kernel and inside the input-gradient launch).
+template <typename T>
+__device__ __forceinline__ void tiny_reduce_block(const TinyReduceArgs& R, int block) {
+  using Acc = TinyAcc<T>;
+  __shared__ Acc red[16][16];
+  const int ncol = R.cig * R.k_vol;
+  const int per_group = R.cog * ncol;
+  const int nw = R.groups * per_group;
+  const int nb = R.db != nullptr ? R.groups * R.cog : 0;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int el = tid & 15;
+  const int set = tid >> 4;
+  const int e = block * 16 + el;
+  const int nblk = R.nblk;
+  // Element e: a weight (e < nw) or a bias channel; its partials are at stride `stride` from
+  // `base`, one per workgroup blk = b * groups + g.
+  const Acc* src = nullptr;
+  size_t stride = 0;
+  if (tid < 256) {
+    if (e < nw) {
+      const int g = e / per_group;
+      src = static_cast<const Acc*>(R.part) + (size_t)g * per_group + (e - g * per_group);
+      stride = (size_t)R.groups * per_group;
+    } else if (e < nw + nb) {
+      const int f = e - nw;
+      const int g = f / R.cog;
+      src = static_cast<const Acc*>(R.bpart) + (size_t)g * R.cog + (f - g * R.cog);
+      stride = (size_t)R.groups * R.cog;
+    }
+  }
+  Acc acc = 0;
+  if (src != nullptr) {
+    for (int b0 = set; b0 < nblk; b0 += 16 * 8) {
+      Acc v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int b = b0 + 16 * k;
+        v[k] = b < nblk ? src[(size_t)b * stride] : Acc(0);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (b0 + 16 * k < nblk) acc += v[k];
+    }
+  }
+  if (tid < 256) red[set][el] = acc;
+  __syncthreads();
+  if (tid >= 16 || src == nullptr) return;
+  for (int k = 1; k < 16; ++k) acc += red[k][el];
+  if (e < nw) {
+    static_cast<T*>(R.dw)[e] = narrow<T>(acc);
+  } else {
+    static_cast<T*>(R.db)[e - nw] = narrow<T>(acc);
+  }
+}
+
 // One lane per box position (box_vol <= 64) and one wave per CPW output channels: the
 // wave's weights are the same for all its lanes, so they come through the scalar cache
 // (uniform loads), and each (input channel, tap) costs one LDS read of the lane's input value
@@ -110,6 +170,14 @@ __global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
   extern __shared__ __align__(16) unsigned char smem[];
   Acc* xh = reinterpret_cast<Acc*>(smem);  // [cig][halo_vol]
   const int bx = blockIdx.x;
+  if (bx >= A.boxes) {
+    // Extra columns of the grid: a weight-gradient reduction riding in this launch.
+    const int extra = static_cast<int>(gridDim.x) - A.boxes;
+    const int rb = (static_cast<int>(blockIdx.z) * static_cast<int>(gridDim.y) +
+                    static_cast<int>(blockIdx.y)) * extra + (bx - A.boxes);
+    if (rb < A.red.blocks) tiny_reduce_block<T>(A.red, rb);
+    return;
+  }
   const int g = blockIdx.y / A.ctiles;
   const int tile = blockIdx.y - g * A.ctiles;
   const int n = blockIdx.z;
@@ -335,62 +403,9 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
   }
 }
 
-// dW[g cog + co][c][t] = sum over the workgroups blk of image/box of part[blk][co][c][t] (blocks
-// of group g only), and db likewise from bpart. A block covers 16 consecutive output elements
-// (the lane's low 4 bits) and splits the workgroups into 16 interleaved sets (the thread's high
-// bits), eight loads in flight per thread; the 16 set sums are added in order through LDS
-// (fixed order: deterministic).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void tiny_reduce_kernel(TinyArgs A, const TinyAcc<T>* part,
-                                                               const TinyAcc<T>* bpart, T* dw,
-                                                               T* db) {
-  using Acc = TinyAcc<T>;
-  __shared__ Acc red[16][16];
-  const int ncol = A.cig * A.k_vol;
-  const int per_group = A.cog * ncol;
-  const int nw = A.groups * per_group;
-  const int nb = db != nullptr ? A.groups * A.cog : 0;
-  const int el = threadIdx.x & 15;
-  const int set = threadIdx.x >> 4;
-  const int e = blockIdx.x * 16 + el;
-  const int nblk = A.batch * A.boxes;
-  // Element e: a weight (e < nw) or a bias channel; its partials are at stride `stride` from
-  // `base`, one per workgroup blk = b * groups + g.
-  const Acc* src = nullptr;
-  size_t stride = 0;
-  if (e < nw) {
-    const int g = e / per_group;
-    src = part + (size_t)g * per_group + (e - g * per_group);
-    stride = (size_t)A.groups * per_group;
-  } else if (e < nw + nb) {
-    const int f = e - nw;
-    const int g = f / A.cog;
-    src = bpart + (size_t)g * A.cog + (f - g * A.cog);
-    stride = (size_t)A.groups * A.cog;
-  }
-  Acc acc = 0;
-  if (src != nullptr) {
-    for (int b0 = set; b0 < nblk; b0 += 16 * 8) {
-      Acc v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int b = b0 + 16 * k;
-        v[k] = b < nblk ? src[(size_t)b * stride] : Acc(0);
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (b0 + 16 * k < nblk) acc += v[k];
-    }
-  }
-  red[set][el] = acc;
-  __syncthreads();
-  if (set != 0 || src == nullptr) return;
-  for (int k = 1; k < 16; ++k) acc += red[k][el];
-  if (e < nw) {
-    dw[e] = narrow<T>(acc);
-  } else {
-    db[e - nw] = narrow<T>(acc);
-  }
+__global__ __launch_bounds__(kThreads) void tiny_reduce_kernel(TinyReduceArgs R) {
+  tiny_reduce_block<T>(R, static_cast<int>(blockIdx.x));
 }
 
 template <typename T, int CPW, int NA>
@@ -399,7 +414,15 @@ hipError_t tiny_launch_na(const TinyArgs& a, size_t lds, hipStream_t s) {
     const hipError_t err = ensure_dynamic_lds<tiny_conv_kernel<T, CPW, NA>>(lds);
     if (err != hipSuccess) return err;
   }
-  hipLaunchKernelGGL((tiny_conv_kernel<T, CPW, NA>), dim3(a.boxes, a.groups * a.ctiles, a.batch),
+  // Extra grid columns for a carried weight-gradient reduction (at least 256 threads a block).
+  unsigned extra = 0;
+  if (a.red.blocks > 0) {
+    if (a.waves < 4) return hipErrorInvalidValue;
+    const int64_t per_col = (int64_t)a.groups * a.ctiles * a.batch;
+    extra = static_cast<unsigned>((a.red.blocks + per_col - 1) / per_col);
+  }
+  hipLaunchKernelGGL((tiny_conv_kernel<T, CPW, NA>),
+                     dim3(static_cast<unsigned>(a.boxes) + extra, a.groups * a.ctiles, a.batch),
                      dim3(64 * a.waves), lds, s, a);
   return hipGetLastError();
 }
@@ -424,21 +447,10 @@ hipError_t tiny_wgrad_part_launch(const TinyArgs& a, size_t lds, void* part, voi
 }
 
 template <typename T, int COG>
-hipError_t tiny_wgrad_launch(const TinyArgs& a, size_t lds, void* part, void* bpart, void* dw,
-                             void* db, hipStream_t s) {
-  using Acc = TinyAcc<T>;
-  {
-    const hipError_t err = a.rank <= 4 ? tiny_wgrad_part_launch<T, COG, 4>(a, lds, part, bpart, s)
-                                       : tiny_wgrad_part_launch<T, COG, kFastRank>(a, lds, part, bpart, s);
-    if (err != hipSuccess) return err;
-  }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  const int64_t n = (int64_t)a.groups * a.cog * a.cig * a.k_vol + (db != nullptr ? a.groups * a.cog : 0);
-  hipLaunchKernelGGL((tiny_reduce_kernel<T>), dim3(static_cast<unsigned>((n + 15) / 16)),
-                     dim3(kThreads), 0, s, a, static_cast<const Acc*>(part),
-                     static_cast<const Acc*>(bpart), static_cast<T*>(dw), static_cast<T*>(db));
-  return hipGetLastError();
+hipError_t tiny_wgrad_launch(const TinyArgs& a, size_t lds, void* part, void* bpart,
+                             hipStream_t s) {
+  return a.rank <= 4 ? tiny_wgrad_part_launch<T, COG, 4>(a, lds, part, bpart, s)
+                     : tiny_wgrad_part_launch<T, COG, kFastRank>(a, lds, part, bpart, s);
 }
 
 template <typename T>
@@ -452,12 +464,12 @@ hipError_t tiny_dispatch(const TinyArgs& a, size_t lds, hipStream_t s) {
 }
 
 template <typename T>
-hipError_t tiny_wgrad_dispatch(const TinyArgs& a, size_t lds, void* part, void* bpart, void* dw,
-                               void* db, hipStream_t s) {
+hipError_t tiny_wgrad_dispatch(const TinyArgs& a, size_t lds, void* part, void* bpart,
+                               hipStream_t s) {
   switch (a.cot) {
-    case 4: return tiny_wgrad_launch<T, 4>(a, lds, part, bpart, dw, db, s);
-    case 8: return tiny_wgrad_launch<T, 8>(a, lds, part, bpart, dw, db, s);
-    case 16: return tiny_wgrad_launch<T, 16>(a, lds, part, bpart, dw, db, s);
+    case 4: return tiny_wgrad_launch<T, 4>(a, lds, part, bpart, s);
+    case 8: return tiny_wgrad_launch<T, 8>(a, lds, part, bpart, s);
+    case 16: return tiny_wgrad_launch<T, 16>(a, lds, part, bpart, s);
   }
   return hipErrorInvalidValue;
 }
@@ -475,16 +487,54 @@ hipError_t launch_tiny_conv(convnd_hip_dtype dtype, const TinyArgs& a, size_t ld
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, void* part,
-                             void* bpart, void* dw, void* db, hipStream_t s) {
+hipError_t launch_tiny_wgrad_partials(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds,
+                                      void* part, void* bpart, void* dw, void* db,
+                                      TinyReduceArgs* reduce, hipStream_t s) {
+  TinyReduceArgs& R = *reduce;
+  R.part = part;
+  R.bpart = bpart;
+  R.dw = dw;
+  R.db = db;
+  R.groups = a.groups;
+  R.cog = a.cog;
+  R.cig = a.cig;
+  R.k_vol = a.k_vol;
+  R.nblk = a.batch * a.boxes;
+  const int64_t n = (int64_t)a.groups * a.cog * a.cig * a.k_vol + (db != nullptr ? a.groups * a.cog : 0);
+  R.blocks = static_cast<int>((n + 15) / 16);
   if (a.boxes == 0 || a.batch == 0) return hipSuccess;
   switch (dtype) {
-    case CONVND_HIP_FLOAT32: return tiny_wgrad_dispatch<float>(a, lds, part, bpart, dw, db, s);
-    case CONVND_HIP_FLOAT64: return tiny_wgrad_dispatch<double>(a, lds, part, bpart, dw, db, s);
-    case CONVND_HIP_FLOAT16: return tiny_wgrad_dispatch<_Float16>(a, lds, part, bpart, dw, db, s);
-    case CONVND_HIP_BFLOAT16: return tiny_wgrad_dispatch<__bf16>(a, lds, part, bpart, dw, db, s);
+    case CONVND_HIP_FLOAT32: return tiny_wgrad_dispatch<float>(a, lds, part, bpart, s);
+    case CONVND_HIP_FLOAT64: return tiny_wgrad_dispatch<double>(a, lds, part, bpart, s);
+    case CONVND_HIP_FLOAT16: return tiny_wgrad_dispatch<_Float16>(a, lds, part, bpart, s);
+    case CONVND_HIP_BFLOAT16: return tiny_wgrad_dispatch<__bf16>(a, lds, part, bpart, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, void* part,
+                             void* bpart, void* dw, void* db, hipStream_t s) {
+  TinyReduceArgs R{};
+  hipError_t err = launch_tiny_wgrad_partials(dtype, a, lds, part, bpart, dw, db, &R, s);
+  if (err != hipSuccess || a.boxes == 0 || a.batch == 0 || R.blocks == 0) return err;
+  const dim3 grid(static_cast<unsigned>(R.blocks));
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32:
+      hipLaunchKernelGGL((tiny_reduce_kernel<float>), grid, dim3(kThreads), 0, s, R);
+      break;
+    case CONVND_HIP_FLOAT64:
+      hipLaunchKernelGGL((tiny_reduce_kernel<double>), grid, dim3(kThreads), 0, s, R);
+      break;
+    case CONVND_HIP_FLOAT16:
+      hipLaunchKernelGGL((tiny_reduce_kernel<_Float16>), grid, dim3(kThreads), 0, s, R);
+      break;
+    case CONVND_HIP_BFLOAT16:
+      hipLaunchKernelGGL((tiny_reduce_kernel<__bf16>), grid, dim3(kThreads), 0, s, R);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace convnd
