@@ -2031,35 +2031,38 @@ int run_backward(const Geom& g, convnd_hip_dtype dtype, const BackwardSetup& b,
                    "bias gradient");
     if (st != CONVND_HIP_SUCCESS) return st;
   }
-  // Both gradients on the tiny-channel kernels: the weight gradient's partial sums first, and
-  // their reduction as extra workgroups of the input-gradient launch (one launch fewer).
+  // Both gradients on the tiny-channel kernels: one launch runs the weight gradient's partial
+  // sums and the input gradient side by side, then the reduction.
   const bool tiny_fused = gi && b.tdx.ok && gw && b.tdw.ok && b.tdx.args.waves >= 4;
-  TinyReduceArgs carried{};
   if (tiny_fused) {
-    TinyArgs T = b.tdw.args;
-    T.in = input;
-    T.w = weight;
-    T.dy = grad_output;
-    const auto ev = timing_begin(2, stream);
-    st = hip_check(launch_tiny_wgrad_partials(dtype, T, b.tdw.wlds, ws + b.off_tpart,
-                                              ws + b.off_tbpart, grad_weight,
-                                              tiny_bias ? grad_bias : nullptr, &carried, stream),
-                   "tiny-channel weight gradient");
+    TinyArgs D = b.tdx.args;
+    D.in = grad_output;
+    D.w = weight;
+    D.bias = nullptr;
+    D.out = grad_input;
+    TinyGeom W = b.tdw.args;
+    W.in = input;
+    W.w = weight;
+    W.dy = grad_output;
+    const auto ev = timing_begin(1, stream);
+    st = hip_check(launch_tiny_backward(dtype, D, b.tdx.lds, W, b.tdw.wlds, ws + b.off_tpart,
+                                        ws + b.off_tbpart, grad_weight,
+                                        tiny_bias ? grad_bias : nullptr, stream),
+                   "tiny-channel gradients");
     timing_end(ev, stream);
     if (st != CONVND_HIP_SUCCESS) return st;
   }
-  if (gi && b.tdx.ok) {
+  if (gi && b.tdx.ok && !tiny_fused) {
     TinyArgs T = b.tdx.args;
     T.in = grad_output;
     T.w = weight;
     T.bias = nullptr;
     T.out = grad_input;
-    if (tiny_fused) T.red = carried;
     const auto ev = timing_begin(1, stream);
     st = hip_check(launch_tiny_conv(dtype, T, b.tdx.lds, stream), "tiny-channel input gradient");
     timing_end(ev, stream);
     if (st != CONVND_HIP_SUCCESS) return st;
-  } else if (gi) {
+  } else if (gi && !b.tdx.ok) {
     if (mfma_dx) {
       const auto ev = timing_begin(1, stream);
       st = hip_check(launch_igemm(dtype, b.dg.mb, b.dg.nb, DA, b.dg.lds, stream),

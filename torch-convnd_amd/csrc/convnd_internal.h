@@ -47,26 +47,15 @@ __host__ __device__ __forceinline__ int fast_div(int x, FastDiv f) {
   return static_cast<int>((static_cast<unsigned long long>(static_cast<unsigned>(x)) * f.m) >> f.p);
 }
 
-// Fixed-order reduction of a tiny-channel weight gradient's partial sums into dW and db (see
-// tiny_reduce_kernel): part[blk][co][c][t] and bpart[blk][co] over nblk workgroups, 16 output
-// elements per reduction block. It runs either on its own or as extra workgroups of the
-// input-gradient launch that follows (blocks > 0 there), in the same summation order.
-struct TinyReduceArgs {
-  const void* part;
-  const void* bpart;
-  void* dw;
-  void* db;  // null: no bias gradient
-  int groups, cog, cig, k_vol, nblk;
-  int blocks;
-};
-
 constexpr int kTinyMaxTaps = 512;
 // Tiny-channel convolution on the vector ALUs (convnd_tiny.hip): a workgroup per (box of
 // output positions, group and tile of output channels, image); halo of the group's cig input
 // channels in LDS. Mode 0: forward convolution (also the weight
 // gradient's geometry, with dy set); mode 1: input gradient of a stride-1 convolution as a
 // convolution of grad_output (in) with the flipped, transposed weights. All sizes int32.
-struct TinyArgs {
+// TinyGeom is everything but the tap table; the weight-gradient kernel computes its tap
+// offsets itself, so its arguments fit beside a full TinyArgs in one launch.
+struct TinyGeom {
   const void* in;    // [batch][cin_total][in_vol]
   const void* w;     // the convolution's weight [cout][cin_g][k_vol] (both modes)
   const void* bias;  // [cout_total] or null (mode 0)
@@ -87,9 +76,8 @@ struct TinyArgs {
   int hext[kFastRank], hpitch[kFastRank];
   int box_vol, halo_vol, k_vol, in_vol, out_vol, boxes;
   FastDiv div_halo, div_hext[kFastRank], div_k[kFastRank], div_nbox[kFastRank];
-  // Forward kernel: a weight-gradient reduction carried as extra workgroups past the boxes
-  // (red.blocks > 0; its grid gets ceil(blocks / (groups * ctiles * batch)) more columns).
-  TinyReduceArgs red;
+};
+struct TinyArgs : TinyGeom {
   // Halo offset (positions) of every tap, sum over the axes of t_a d_a hpitch_a: read by the
   // forward kernel with uniform (scalar) loads from the kernel arguments.
   int toff[kTinyMaxTaps];
@@ -98,13 +86,14 @@ hipError_t launch_tiny_conv(convnd_hip_dtype dtype, const TinyArgs& a, size_t ld
 // Weight gradient (and bias gradient when db is set) of a mode-0 TinyArgs: per-workgroup
 // partial sums into part / bpart (tiny_wgrad_part_elems accumulation-type elements), then a
 // fixed-order reduction into dw / db.
-hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, void* part,
+hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyGeom& a, size_t lds, void* part,
                              void* bpart, void* dw, void* db, hipStream_t s);
-// The partial sums only (reduce: the reduction to run later, e.g. inside the input-gradient
-// launch through TinyArgs::red).
-hipError_t launch_tiny_wgrad_partials(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds,
-                                      void* part, void* bpart, void* dw, void* db,
-                                      TinyReduceArgs* reduce, hipStream_t s);
+// Both gradients of one layer: the input gradient (mode-1 args dx, dx_lds, at least four
+// waves) and the weight gradient's partial sums (mode-0 args dw_args, dw_lds) as the two
+// halves of one launch, then the fixed-order reduction into dw / db.
+hipError_t launch_tiny_backward(convnd_hip_dtype dtype, const TinyArgs& dx, size_t dx_lds,
+                                const TinyGeom& dw_args, size_t dw_lds, void* part, void* bpart,
+                                void* dw, void* db, hipStream_t s);
 
 // Arguments of the box-tiled implicit GEMM (forward, or one family of stride phases of
 // the input gradient). All sizes fit int32; the planner checks that.

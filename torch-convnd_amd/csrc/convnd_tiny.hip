@@ -16,6 +16,9 @@
 //     tap) column, accumulating all output channels over the box's positions; it writes these
 //     partial sums (and the grad_output sums of the box, for the bias gradient) per workgroup.
 //   * tiny_reduce_kernel: adds the workgroups' partial sums in a fixed order into dW and db.
+//   * tiny_bwd_kernel: both gradients of a layer in one launch, its first workgroups running the
+//     weight-gradient partial sums and the rest the input gradient (the two are independent and
+//     each alone leaves most of the GPU idle); the reduction follows as its own launch.
 // Every sum has a fixed order, so results are bitwise repeatable. Semantics follow the
 // reference's im2col map (src/torch_convnd/csrc/convnd.h:57-104): input coordinate =
 // o*stride - pad + t*dilation, out-of-range coordinates read as zero.
@@ -35,7 +38,7 @@ using TinyAcc = typename Acc<T>::type;
 // line on gfx950): the shorter walk and batches of 4 elements cut the halo staging of a rank-4
 // launch to well under half.
 template <int NA>
-__device__ __forceinline__ void tiny_box_coords(const TinyArgs& A, int q, int* c) {
+__device__ __forceinline__ void tiny_box_coords(const TinyGeom& A, int q, int* c) {
 #pragma unroll
   for (int a = NA - 1; a >= 0; --a) {
     c[a] = q & (A.box[a] - 1);
@@ -49,7 +52,7 @@ __device__ __forceinline__ void tiny_box_coords(const TinyArgs& A, int q, int* c
 // (a load outside the input reads element 0 and is replaced by zero) are all issued before the
 // first store, so a pass waits for memory once. Most tiny layers stage in a single pass.
 template <typename T, int NA>
-__device__ __forceinline__ void tiny_stage_halo(const TinyArgs& A, const T* in, int n, int c0,
+__device__ __forceinline__ void tiny_stage_halo(const TinyGeom& A, const T* in, int n, int c0,
                                                 const int* origin, TinyAcc<T>* xh) {
   using Acc = TinyAcc<T>;
   constexpr int kPos = 2, kCh = 8;
@@ -95,17 +98,39 @@ __device__ __forceinline__ void tiny_stage_halo(const TinyArgs& A, const T* in, 
   }
 }
 
-// LDS offset (in the halo, positions) of every tap (the plan's table A.toff) into toff.
-__device__ __forceinline__ void tiny_tap_offsets(const TinyArgs& A, int* toff) {
-  for (int t = threadIdx.x; t < A.k_vol; t += blockDim.x) toff[t] = A.toff[t];
+// LDS offset (in the halo, positions) of every tap into toff: sum over the axes of
+// t_a d_a hpitch_a, tap t's axis indices t_a taken last axis fastest.
+template <int NA>
+__device__ __forceinline__ void tiny_tap_offsets(const TinyGeom& A, int* toff) {
+  for (int t = threadIdx.x; t < A.k_vol; t += blockDim.x) {
+    int r = t, off = 0;
+#pragma unroll
+    for (int a = NA - 1; a >= 0; --a) {
+      const int q = fast_div(r, A.div_k[a]);
+      off += (r - q * A.k[a]) * A.d[a] * A.hpitch[a];
+      r = q;
+    }
+    toff[t] = off;
+  }
 }
+
+// Fixed-order reduction of a weight gradient's partial sums into dW and db:
+// part[blk][co][c][t] and bpart[blk][co] over nblk workgroups, 16 output elements per
+// reduction block.
+struct TinyReduceArgs {
+  const void* part;
+  const void* bpart;
+  void* dw;
+  void* db;  // null: no bias gradient
+  int groups, cog, cig, k_vol, nblk;
+  int blocks;
+};
 
 // dW[g cog + co][c][t] = sum over the workgroups blk of image/box of part[blk][co][c][t] (blocks
 // of group g only), and db likewise from bpart. Reduction block `block` covers 16 consecutive
 // output elements (the thread's low 4 bits) and splits the workgroups into 16 interleaved sets
 // (threads 16 .. 255's high bits; threads past 256 idle), eight loads in flight per thread;
-// the 16 set sums are added in order through LDS (fixed order: deterministic, the same in the
-// stand-alone kernel and inside the input-gradient launch).
+// the 16 set sums are added in order through LDS (fixed order: deterministic).
 template <typename T>
 __device__ __forceinline__ void tiny_reduce_block(const TinyReduceArgs& R, int block) {
   using Acc = TinyAcc<T>;
@@ -164,23 +189,14 @@ __device__ __forceinline__ void tiny_reduce_block(const TinyReduceArgs& R, int b
 // wave's weights are the same for all its lanes, so they come through the scalar cache
 // (uniform loads), and each (input channel, tap) costs one LDS read of the lane's input value
 // and CPW FMAs.
+// Workgroup (box bx, group and channel tile by, image n) of the convolution.
 template <typename T, int CPW, int NA>
-__global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
+__device__ __forceinline__ void tiny_conv_body(const TinyArgs& A, int bx, int by, int n) {
   using Acc = TinyAcc<T>;
   extern __shared__ __align__(16) unsigned char smem[];
   Acc* xh = reinterpret_cast<Acc*>(smem);  // [cig][halo_vol]
-  const int bx = blockIdx.x;
-  if (bx >= A.boxes) {
-    // Extra columns of the grid: a weight-gradient reduction riding in this launch.
-    const int extra = static_cast<int>(gridDim.x) - A.boxes;
-    const int rb = (static_cast<int>(blockIdx.z) * static_cast<int>(gridDim.y) +
-                    static_cast<int>(blockIdx.y)) * extra + (bx - A.boxes);
-    if (rb < A.red.blocks) tiny_reduce_block<T>(A.red, rb);
-    return;
-  }
-  const int g = blockIdx.y / A.ctiles;
-  const int tile = blockIdx.y - g * A.ctiles;
-  const int n = blockIdx.z;
+  const int g = by / A.ctiles;
+  const int tile = by - g * A.ctiles;
   int origin[kFastRank];
   {
     int r = bx;
@@ -302,12 +318,17 @@ __global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
   }
 }
 
+template <typename T, int CPW, int NA>
+__global__ __launch_bounds__(512) void tiny_conv_kernel(TinyArgs A) {
+  tiny_conv_body<T, CPW, NA>(A, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
 // Partial sums of one workgroup (image n, box bx, group g): part[blk][co][c][t] for the group's
 // output channels co, input channels c, taps t, and bpart[blk][co] (grad_output summed over the
-// box) where blk = (n * boxes + bx) * groups + g.
+// box) where blk = (n * boxes + bx) * groups + g. Any workgroup size of at least 256 threads.
 template <typename T, int COG, int NA>
-__global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAcc<T>* part,
-                                                              TinyAcc<T>* bpart) {
+__device__ __forceinline__ void tiny_wgrad_body(const TinyGeom& A, int bx, int g, int n,
+                                                TinyAcc<T>* part, TinyAcc<T>* bpart) {
   using Acc = TinyAcc<T>;
   extern __shared__ __align__(16) unsigned char smem[];
   // [box_vol][COG] grad_output tile first (16-byte aligned rows of COG), then the halo.
@@ -315,9 +336,7 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
   Acc* xh = dyt + (size_t)A.box_vol * COG;                // [cig][halo_vol]
   int* toff = reinterpret_cast<int*>(xh + (size_t)A.cig * A.halo_vol);  // [k_vol]
   int* posl = toff + A.k_vol;                             // [box_vol]
-  const int bx = blockIdx.x;
-  const int g = blockIdx.y;
-  const int n = blockIdx.z;
+  const int nt = blockDim.x;
   int origin[kFastRank];
   {
     int r = bx;
@@ -331,17 +350,17 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
   const T* x = static_cast<const T*>(A.in);
   const T* dy = static_cast<const T*>(A.dy);
   tiny_stage_halo<T, NA>(A, x, n, g * A.cig, origin, xh);
-  tiny_tap_offsets(A, toff);
+  tiny_tap_offsets<NA>(A, toff);
   // grad_output tile [q][co] (zero outside the output and past the group's channels) and the
   // halo offset of every box position.
   // (box_vol * COG <= 64 * 16 entries: at most four per thread, loads first.)
   {
-    constexpr int kPer = (64 * COG + kThreads - 1) / kThreads;
+    constexpr int kPer = (64 * COG + kThreads - 1) / kThreads;  // blockDim.x >= kThreads
     T raw[kPer];
     bool keep[kPer];
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int e = threadIdx.x + u * kThreads;
+      const int e = threadIdx.x + u * nt;
       const int q = e / COG;
       const int j = e - q * COG;
       int bc[kFastRank];
@@ -362,14 +381,14 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
     }
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int e = threadIdx.x + u * kThreads;
+      const int e = threadIdx.x + u * nt;
       if (e < A.box_vol * COG) dyt[e] = keep[u] ? widen<Acc>(raw[u]) : Acc(0);
     }
   }
   __syncthreads();
   const int blk = (n * A.boxes + bx) * A.groups + g;
   const int ncol = A.cig * A.k_vol;
-  for (int col = threadIdx.x; col < ncol; col += kThreads) {
+  for (int col = threadIdx.x; col < ncol; col += nt) {
     const int c = col / A.k_vol;
     const int t = col - c * A.k_vol;
     const Acc* xc = xh + (size_t)c * A.halo_vol + toff[t];
@@ -403,6 +422,31 @@ __global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyArgs A, TinyAc
   }
 }
 
+template <typename T, int COG, int NA>
+__global__ __launch_bounds__(kThreads) void tiny_wgrad_kernel(TinyGeom A, TinyAcc<T>* part,
+                                                              TinyAcc<T>* bpart) {
+  tiny_wgrad_body<T, COG, NA>(A, blockIdx.x, blockIdx.y, blockIdx.z, part, bpart);
+}
+
+// Both gradients: workgroups [0, nw) are the weight gradient's (box, group, image), the rest
+// the input gradient's (box, group and channel tile, image), each workgroup decoding its own
+// coordinates from the flat index.
+template <typename T, int CPW, int COG, int NA>
+__global__ __launch_bounds__(512) void tiny_bwd_kernel(TinyArgs D, TinyGeom W, TinyAcc<T>* part,
+                                                       TinyAcc<T>* bpart) {
+  const int nw = W.boxes * W.groups * W.batch;
+  int b = static_cast<int>(blockIdx.x);
+  if (b < nw) {
+    const int r = b / W.boxes;
+    tiny_wgrad_body<T, COG, NA>(W, b - r * W.boxes, r % W.groups, r / W.groups, part, bpart);
+    return;
+  }
+  b -= nw;
+  const int ny = D.groups * D.ctiles;
+  const int r = b / D.boxes;
+  tiny_conv_body<T, CPW, NA>(D, b - r * D.boxes, r % ny, r / ny);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void tiny_reduce_kernel(TinyReduceArgs R) {
   tiny_reduce_block<T>(R, static_cast<int>(blockIdx.x));
@@ -414,15 +458,8 @@ hipError_t tiny_launch_na(const TinyArgs& a, size_t lds, hipStream_t s) {
     const hipError_t err = ensure_dynamic_lds<tiny_conv_kernel<T, CPW, NA>>(lds);
     if (err != hipSuccess) return err;
   }
-  // Extra grid columns for a carried weight-gradient reduction (at least 256 threads a block).
-  unsigned extra = 0;
-  if (a.red.blocks > 0) {
-    if (a.waves < 4) return hipErrorInvalidValue;
-    const int64_t per_col = (int64_t)a.groups * a.ctiles * a.batch;
-    extra = static_cast<unsigned>((a.red.blocks + per_col - 1) / per_col);
-  }
   hipLaunchKernelGGL((tiny_conv_kernel<T, CPW, NA>),
-                     dim3(static_cast<unsigned>(a.boxes) + extra, a.groups * a.ctiles, a.batch),
+                     dim3(static_cast<unsigned>(a.boxes), a.groups * a.ctiles, a.batch),
                      dim3(64 * a.waves), lds, s, a);
   return hipGetLastError();
 }
@@ -434,7 +471,7 @@ hipError_t tiny_launch(const TinyArgs& a, size_t lds, hipStream_t s) {
 }
 
 template <typename T, int COG, int NA>
-hipError_t tiny_wgrad_part_launch(const TinyArgs& a, size_t lds, void* part, void* bpart,
+hipError_t tiny_wgrad_part_launch(const TinyGeom& a, size_t lds, void* part, void* bpart,
                                   hipStream_t s) {
   using Acc = TinyAcc<T>;
   if (lds > 64 * 1024) {
@@ -447,7 +484,7 @@ hipError_t tiny_wgrad_part_launch(const TinyArgs& a, size_t lds, void* part, voi
 }
 
 template <typename T, int COG>
-hipError_t tiny_wgrad_launch(const TinyArgs& a, size_t lds, void* part, void* bpart,
+hipError_t tiny_wgrad_launch(const TinyGeom& a, size_t lds, void* part, void* bpart,
                              hipStream_t s) {
   return a.rank <= 4 ? tiny_wgrad_part_launch<T, COG, 4>(a, lds, part, bpart, s)
                      : tiny_wgrad_part_launch<T, COG, kFastRank>(a, lds, part, bpart, s);
@@ -464,7 +501,7 @@ hipError_t tiny_dispatch(const TinyArgs& a, size_t lds, hipStream_t s) {
 }
 
 template <typename T>
-hipError_t tiny_wgrad_dispatch(const TinyArgs& a, size_t lds, void* part, void* bpart,
+hipError_t tiny_wgrad_dispatch(const TinyGeom& a, size_t lds, void* part, void* bpart,
                                hipStream_t s) {
   switch (a.cot) {
     case 4: return tiny_wgrad_launch<T, 4>(a, lds, part, bpart, s);
@@ -474,23 +511,54 @@ hipError_t tiny_wgrad_dispatch(const TinyArgs& a, size_t lds, void* part, void* 
   return hipErrorInvalidValue;
 }
 
-}  // namespace
+template <typename T, int CPW, int COG, int NA>
+hipError_t tiny_bwd_launch_na(const TinyArgs& d, const TinyGeom& w, size_t lds, void* part,
+                              void* bpart, hipStream_t s) {
+  using Acc = TinyAcc<T>;
+  if (lds > 64 * 1024) {
+    const hipError_t err = ensure_dynamic_lds<tiny_bwd_kernel<T, CPW, COG, NA>>(lds);
+    if (err != hipSuccess) return err;
+  }
+  const int64_t nw = (int64_t)w.boxes * w.groups * w.batch;
+  const int64_t nd = (int64_t)d.boxes * d.groups * d.ctiles * d.batch;
+  if (nw + nd > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((tiny_bwd_kernel<T, CPW, COG, NA>), dim3(static_cast<unsigned>(nw + nd)),
+                     dim3(64 * d.waves), lds, s, d, w, static_cast<Acc*>(part),
+                     static_cast<Acc*>(bpart));
+  return hipGetLastError();
+}
 
-hipError_t launch_tiny_conv(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, hipStream_t s) {
-  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
-  switch (dtype) {
-    case CONVND_HIP_FLOAT32: return tiny_dispatch<float>(a, lds, s);
-    case CONVND_HIP_FLOAT64: return tiny_dispatch<double>(a, lds, s);
-    case CONVND_HIP_FLOAT16: return tiny_dispatch<_Float16>(a, lds, s);
-    case CONVND_HIP_BFLOAT16: return tiny_dispatch<__bf16>(a, lds, s);
+template <typename T, int CPW, int COG>
+hipError_t tiny_bwd_launch(const TinyArgs& d, const TinyGeom& w, size_t lds, void* part,
+                           void* bpart, hipStream_t s) {
+  return d.rank <= 4 ? tiny_bwd_launch_na<T, CPW, COG, 4>(d, w, lds, part, bpart, s)
+                     : tiny_bwd_launch_na<T, CPW, COG, kFastRank>(d, w, lds, part, bpart, s);
+}
+
+template <typename T, int CPW>
+hipError_t tiny_bwd_cog(const TinyArgs& d, const TinyGeom& w, size_t lds, void* part,
+                        void* bpart, hipStream_t s) {
+  switch (w.cot) {
+    case 4: return tiny_bwd_launch<T, CPW, 4>(d, w, lds, part, bpart, s);
+    case 8: return tiny_bwd_launch<T, CPW, 8>(d, w, lds, part, bpart, s);
+    case 16: return tiny_bwd_launch<T, CPW, 16>(d, w, lds, part, bpart, s);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_tiny_wgrad_partials(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds,
-                                      void* part, void* bpart, void* dw, void* db,
-                                      TinyReduceArgs* reduce, hipStream_t s) {
-  TinyReduceArgs& R = *reduce;
+template <typename T>
+hipError_t tiny_bwd_dispatch(const TinyArgs& d, const TinyGeom& w, size_t lds, void* part,
+                             void* bpart, hipStream_t s) {
+  switch (d.cpw) {
+    case 1: return tiny_bwd_cog<T, 1>(d, w, lds, part, bpart, s);
+    case 2: return tiny_bwd_cog<T, 2>(d, w, lds, part, bpart, s);
+    case 4: return tiny_bwd_cog<T, 4>(d, w, lds, part, bpart, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+TinyReduceArgs reduce_args(const TinyGeom& a, void* part, void* bpart, void* dw, void* db) {
+  TinyReduceArgs R{};
   R.part = part;
   R.bpart = bpart;
   R.dw = dw;
@@ -502,21 +570,11 @@ hipError_t launch_tiny_wgrad_partials(convnd_hip_dtype dtype, const TinyArgs& a,
   R.nblk = a.batch * a.boxes;
   const int64_t n = (int64_t)a.groups * a.cog * a.cig * a.k_vol + (db != nullptr ? a.groups * a.cog : 0);
   R.blocks = static_cast<int>((n + 15) / 16);
-  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
-  switch (dtype) {
-    case CONVND_HIP_FLOAT32: return tiny_wgrad_dispatch<float>(a, lds, part, bpart, s);
-    case CONVND_HIP_FLOAT64: return tiny_wgrad_dispatch<double>(a, lds, part, bpart, s);
-    case CONVND_HIP_FLOAT16: return tiny_wgrad_dispatch<_Float16>(a, lds, part, bpart, s);
-    case CONVND_HIP_BFLOAT16: return tiny_wgrad_dispatch<__bf16>(a, lds, part, bpart, s);
-  }
-  return hipErrorInvalidValue;
+  return R;
 }
 
-hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, void* part,
-                             void* bpart, void* dw, void* db, hipStream_t s) {
-  TinyReduceArgs R{};
-  hipError_t err = launch_tiny_wgrad_partials(dtype, a, lds, part, bpart, dw, db, &R, s);
-  if (err != hipSuccess || a.boxes == 0 || a.batch == 0 || R.blocks == 0) return err;
+hipError_t launch_tiny_reduce(convnd_hip_dtype dtype, const TinyReduceArgs& R, hipStream_t s) {
+  if (R.blocks == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>(R.blocks));
   switch (dtype) {
     case CONVND_HIP_FLOAT32:
@@ -535,6 +593,52 @@ hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyArgs& a, size_t l
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_tiny_conv(convnd_hip_dtype dtype, const TinyArgs& a, size_t lds, hipStream_t s) {
+  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32: return tiny_dispatch<float>(a, lds, s);
+    case CONVND_HIP_FLOAT64: return tiny_dispatch<double>(a, lds, s);
+    case CONVND_HIP_FLOAT16: return tiny_dispatch<_Float16>(a, lds, s);
+    case CONVND_HIP_BFLOAT16: return tiny_dispatch<__bf16>(a, lds, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_tiny_wgrad(convnd_hip_dtype dtype, const TinyGeom& a, size_t lds, void* part,
+                             void* bpart, void* dw, void* db, hipStream_t s) {
+  if (a.boxes == 0 || a.batch == 0) return hipSuccess;
+  hipError_t err = hipErrorInvalidValue;
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32: err = tiny_wgrad_dispatch<float>(a, lds, part, bpart, s); break;
+    case CONVND_HIP_FLOAT64: err = tiny_wgrad_dispatch<double>(a, lds, part, bpart, s); break;
+    case CONVND_HIP_FLOAT16: err = tiny_wgrad_dispatch<_Float16>(a, lds, part, bpart, s); break;
+    case CONVND_HIP_BFLOAT16: err = tiny_wgrad_dispatch<__bf16>(a, lds, part, bpart, s); break;
+  }
+  if (err != hipSuccess) return err;
+  return launch_tiny_reduce(dtype, reduce_args(a, part, bpart, dw, db), s);
+}
+
+hipError_t launch_tiny_backward(convnd_hip_dtype dtype, const TinyArgs& dx, size_t dx_lds,
+                                const TinyGeom& dw_args, size_t dw_lds, void* part, void* bpart,
+                                void* dw, void* db, hipStream_t s) {
+  // The weight-gradient half runs with the input gradient's workgroup size (at least 256).
+  if (dx.waves < 4 || dx.rank != dw_args.rank || dx.boxes < 1 || dw_args.boxes < 1)
+    return hipErrorInvalidValue;
+  if (dw_args.batch == 0) return hipSuccess;
+  const size_t lds = dx_lds > dw_lds ? dx_lds : dw_lds;
+  hipError_t err = hipErrorInvalidValue;
+  switch (dtype) {
+    case CONVND_HIP_FLOAT32: err = tiny_bwd_dispatch<float>(dx, dw_args, lds, part, bpart, s); break;
+    case CONVND_HIP_FLOAT64: err = tiny_bwd_dispatch<double>(dx, dw_args, lds, part, bpart, s); break;
+    case CONVND_HIP_FLOAT16: err = tiny_bwd_dispatch<_Float16>(dx, dw_args, lds, part, bpart, s); break;
+    case CONVND_HIP_BFLOAT16: err = tiny_bwd_dispatch<__bf16>(dx, dw_args, lds, part, bpart, s); break;
+  }
+  if (err != hipSuccess) return err;
+  return launch_tiny_reduce(dtype, reduce_args(dw_args, part, bpart, dw, db), s);
 }
 
 }  // namespace convnd
