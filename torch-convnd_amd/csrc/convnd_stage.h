@@ -374,7 +374,7 @@ __device__ __forceinline__ void pad_dy16_blocks(const Src* src, unsigned short* 
 // run's loads are issued before the first run is shifted and stored, and the axis walk has
 // no rank test (entries past the outer axes are identities), so its scalar parameter loads
 // issue together instead of one dependent wait per axis.
-constexpr int kPlanarRuns = 4;
+constexpr int kPlanarRuns = 2;
 
 // Source of run t: (image, channel) row nc, the element offset of the run's first element
 // from the source's start (negative before it), and its elements [lo, hi) inside the input
