@@ -129,8 +129,8 @@ struct TinyReduceArgs {
 // dW[g cog + co][c][t] = sum over the workgroups blk of image/box of part[blk][co][c][t] (blocks
 // of group g only), and db likewise from bpart. Reduction block `block` covers 16 consecutive
 // output elements (the thread's low 4 bits) and splits the workgroups into 16 interleaved sets
-// (threads 16 .. 255's high bits; threads past 256 idle), eight loads in flight per thread;
-// the 16 set sums are added in order through LDS (fixed order: deterministic).
+// (the thread's high 4 bits; 256 threads), eight loads in flight per thread; the 16 set sums
+// are added in order through LDS (fixed order: deterministic).
 template <typename T>
 __device__ __forceinline__ void tiny_reduce_block(const TinyReduceArgs& R, int block) {
   using Acc = TinyAcc<T>;
