@@ -91,3 +91,29 @@ def test_activation_with_autograd_gpu():
     helpers.assert_close(y.detach().cpu(), yr.detach(), torch.float32, "y")
     for g, r in zip(grads, ref_grads):
         helpers.assert_close(g.cpu(), r, torch.float32, "grad")
+
+
+@pytest.mark.gpu
+def test_fused_activation_random_problems_gpu():
+    """Every fourth seeded random problem of tests/random_cases.py (every kernel family and
+    dtype) with an activation chosen per case: the fused result matches the activation of the
+    oracle's float64 convolution, and the activation of the unfused call up to one rounding."""
+    import random_cases
+
+    names = list(ACTS)
+    for index, case in enumerate(random_cases.cases()):
+        if index % 4:
+            continue
+        x_shape, w_shape, stride, padding, dilation, groups, bias, dtype = case
+        act = names[(index // 4) % len(names)]
+        print(f"[epilogue random {index}] {act} x={x_shape} w={w_shape} {dtype}", flush=True)
+        x, w, b = helpers.seeded_problem(x_shape, w_shape, bias, dtype, seed=index)
+        want = ACTS[act](helpers.oracle_forward(x, w, b, stride, padding, dilation, groups))
+        xc, wc = x.cuda(), w.cuda()
+        bc = b.cuda() if b is not None else None
+        with torch.no_grad():
+            got = conv_nd(xc, wc, bc, stride, padding, dilation, groups, backend="native", activation=act)
+            plain = conv_nd(xc, wc, bc, stride, padding, dilation, groups, backend="native")
+        assert got.dtype == dtype
+        helpers.assert_close(got.cpu(), want, dtype, f"random {index} fused {act}")
+        helpers.assert_close(got.cpu(), ACTS[act](plain.double()).cpu(), dtype, f"random {index} vs unfused")

@@ -108,3 +108,23 @@ def test_noalloc_rejects_problems_beyond_its_scratch(lib):
     assert st == _capi.WORKSPACE_TOO_SMALL
     message = lib.convnd_hip_last_error().decode()
     assert "device scratch" in message and str(_capi.NOALLOC_SCRATCH_BYTES) in message, message
+
+
+def test_noalloc_random_problems_in_sequence(lib):
+    """Every fifth seeded random problem of tests/random_cases.py, one after another on the
+    shared scratch array (sizes, dtypes and plans change from call to call): each output equals
+    convnd_hip_forward's bit for bit and matches the oracle."""
+    import random_cases
+
+    for index, case in enumerate(random_cases.cases()):
+        if index % 5:
+            continue
+        x_shape, w_shape, stride, padding, dilation, groups, bias, dtype = case
+        problem = _capi.Problem.make(x_shape, w_shape, stride, padding, dilation, groups)
+        assert lib.convnd_hip_forward_workspace_size(ctypes.byref(problem), _capi.dtype_code(dtype)) \
+            <= _capi.NOALLOC_SCRATCH_BYTES
+        print(f"[noalloc random {index}] x={x_shape} w={w_shape} {dtype}", flush=True)
+        got, want, ref = _forward_pair(lib, x_shape, w_shape, stride, padding, dilation, groups, bias,
+                                       dtype, seed=index)
+        assert torch.equal(got, want), index
+        helpers.assert_close(got, ref, dtype, f"noalloc random {index}")
