@@ -63,3 +63,51 @@ def test_graph_replay_after_cache_eviction():
         _other_geometries(140 if round_ == 0 else 8)
     helpers.assert_close(captured[0], helpers.oracle_forward(x, w, b, (1,) * 4, (1,) * 4, (1,) * 4, 1),
                          torch.bfloat16, "graph replay forward")
+
+
+def test_graph_replay_random_problems():
+    """Every 27th seeded random problem of tests/random_cases.py (tiny, implicit-GEMM and
+    direct plans, every dtype): forward and full backward captured after an eager first call,
+    replayed three times with another problem's eager step between replays, each replay equal
+    to the eager result bit for bit."""
+    import random_cases
+
+    cases = [c for i, c in enumerate(random_cases.cases()) if i % 27 == 0]
+    conv_back = torch.ops.torch_convnd.conv_nd_backward.default
+
+    def make_step(index, case):
+        x_shape, w_shape, stride, padding, dilation, groups, bias, dtype = case
+        x, w, b = helpers.seeded_problem(x_shape, w_shape, bias, dtype, seed=index)
+        x, w = x.cuda(), w.cuda()
+        b = b.cuda() if b is not None else None
+        y0 = conv_nd(x, w, b, stride, padding, dilation, groups, backend="native")
+        dy = torch.randn(y0.shape, generator=torch.Generator().manual_seed(500 + index)).to(dtype).cuda()
+        params = (list(stride), list(padding), list(dilation), groups, 1 << 26)
+
+        def step():
+            y = conv_nd(x, w, b, stride, padding, dilation, groups, backend="native")
+            return (y, *conv_back(dy, x, w, *params, [True, True, b is not None]))
+        return step
+
+    steps = [make_step(i, c) for i, c in enumerate(cases)]
+    for i, step in enumerate(steps):
+        print(f"[graph random {i}] x={cases[i][0]} w={cases[i][1]} {cases[i][7]}", flush=True)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            eager = step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = step()
+        for round_ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            for k, (got, want) in enumerate(zip(captured, eager)):
+                if want is None:
+                    continue
+                assert torch.equal(got, want), f"case {i} replay {round_}: result {k} differs from eager"
+            steps[(i + round_ + 1) % len(steps)]()
+            torch.cuda.synchronize()
+        del graph
